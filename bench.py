@@ -1,0 +1,187 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X DiT hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs attention,sage] [--no-cpu]
+
+Headline workload: BF16 DiT self-attention, S = 27x30x40 =
+32400 tokens, B = 1, H = 40, D = 128, Q/K/V = 0.5 N(0,1) BF16 with the 3D RoPE
+applied to Q and K. A "step" is one attention call over that input, resident in
+HBM before the timed region. value = 4 S^2 H D / (time per call) in TFLOP/s.
+
+Extra legs (own JSON objects on the same line): the Sage int8/fp8 attention on
+config 3's inputs. The CPU baseline times the oracle's restatement of the
+reference operator on a bounded sample (a slice of query rows, all keys and
+heads) on the host cores and scales it to the same unit.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+SEQ, HEADS, DIM = 32400, 40, 128
+ROPE_SHAPE = (27, 30, 40)
+PEAK_BF16 = 2500.0      # MI355X dense BF16 MFMA, TFLOP/s
+PEAK_FP8 = 5000.0       # MI355X dense FP8 / INT8 MFMA, TFLOP/s (TOP/s)
+
+
+def attention_flops(seq, heads, dim=DIM, density=1.0):
+    return 4.0 * seq * seq * heads * dim * density
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Q, K, V resident on the GPU for one attention configuration."""
+
+    def __init__(self, gpu, seq, heads, seed, scale, rope, k_bias=False):
+        from h3cli_amd import synth
+        lib = gpu.lib
+        n = seq * heads * DIM
+        self.gpu, self.seq, self.heads, self.n = gpu, seq, heads, n
+        self.q, self.k, self.v = gpu.empty(n), gpu.empty(n), gpu.empty(n)
+        self.out = gpu.empty(n)
+        gpu.begin()
+        for i, t in enumerate((self.q, self.k, self.v)):
+            gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, t.handle, seed * 16 + i, scale, n), "fill")
+        gpu.submit()
+        if rope or k_bias:
+            # Host-side preparation (outside any timed region): RoPE on Q and K,
+            # or the +4.0 bias on 1% of K's channels.
+            q = synth.bf16_to_f32(self.q.read()).reshape(seq, heads, DIM)
+            k = synth.bf16_to_f32(self.k.read()).reshape(seq, heads, DIM)
+            if rope:
+                cos, sin = synth.rope_tables(*ROPE_SHAPE)
+                q = synth.apply_rope(q, cos[:seq], sin[:seq])
+                k = synth.apply_rope(k, cos[:seq], sin[:seq])
+            if k_bias:
+                rng = np.random.default_rng(seed)
+                for h in range(heads):
+                    k[:, h, rng.choice(DIM, size=max(1, round(0.01 * DIM)), replace=False)] += 4.0
+            for t, a in ((self.q, q), (self.k, k)):
+                b = synth.f32_to_bf16(a.reshape(-1))
+                gpu.check(lib.h3_gpu_tensor_write_bf16(t.handle, b.ctypes.data, n), "upload")
+
+    def call(self):
+        g = self.gpu
+        return g.lib.h3_gpu_dit_sdpa_bf16(g.handle, self.out.handle, self.q.handle, self.k.handle, self.v.handle,
+                                          self.seq, self.heads, DIM, 1.0 / math.sqrt(DIM), 0, 0, 0)
+
+    def host_inputs(self):
+        from h3cli_amd import synth
+        return [synth.bf16_to_f32(t.read()) for t in (self.q, self.k, self.v)]
+
+
+def time_calls(gpu, call, steps, warmup):
+    gpu.begin()
+    for _ in range(warmup):
+        gpu.check(call(), "warmup")
+    gpu.submit()
+    e0, e1 = gpu.timing_event(), gpu.timing_event()
+    gpu.begin()
+    gpu.record(e0)
+    for _ in range(steps):
+        gpu.check(call(), "timed call")
+    gpu.record(e1)
+    t0 = time.perf_counter()
+    gpu.submit()
+    wall = time.perf_counter() - t0
+    ms = gpu.elapsed_ms(e0, e1)
+    gpu.lib.h3_gpu_event_free(e0)
+    gpu.lib.h3_gpu_event_free(e1)
+    return ms / steps, wall
+
+
+def cpu_baseline(q, k, v, seq, heads, rows):
+    """The oracle's online-softmax attention (reference cuda_attention.cuh:7-51
+    restated in C, OpenMP) on rows [0, rows) x all keys x all heads."""
+    from oracle import oracle
+    scale = 1.0 / math.sqrt(DIM)
+    oracle.attention(q[: 64 * heads * DIM], k[: 64 * heads * DIM], v[: 64 * heads * DIM], 64, heads, scale,
+                     rows=(0, 8))  # warm the library and page in
+    t0 = time.perf_counter()
+    oracle.attention(q, k, v, seq, heads, scale, tile=64, rows=(0, rows))
+    dt = time.perf_counter() - t0
+    flops = attention_flops(seq, heads) * rows / seq
+    return dict(value=round(flops / dt / 1e12, 6), unit="TFLOP/s", cores=oracle.threads(), kind="port",
+                sample=f"oracle_attention rows 0..{rows} of {seq} x {heads} heads x all keys, "
+                       f"{dt:.2f} s; TFLOP/s of that slice (same FLOP convention)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--legs", default="attention,sage")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "192")))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the DiT hot path here runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not part of this build).", file=sys.stderr)
+        sys.exit(2)
+
+    from h3cli_amd.runtime import Gpu
+    legs = [x for x in args.legs.split(",") if x]
+    result = {}
+    with Gpu() as gpu:
+        log(f"[bench] bf16 attention S={SEQ} H={HEADS}: preparing inputs")
+        w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=True)
+        ms, wall = time_calls(gpu, w.call, args.steps, args.warmup)
+        flops = attention_flops(SEQ, HEADS)
+        tflops = flops / (ms * 1e-3) / 1e12
+        log(f"[bench] bf16 attention: {ms:.3f} ms/call, {tflops:.1f} TFLOP/s")
+        result.update({
+            "metric": "attention TFLOP/s + %MFMA peak; s/denoise-step (40-block DiT, S=32400) 1 GPU",
+            "value": round(tflops, 3),
+            "unit": "TFLOP/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic: seeded 0.5*N(0,1) bf16 Q/K/V with 3D RoPE (44/42/42, theta 1e4) on Q,K",
+            "config": {"workload": "bf16 DiT video self-attention (BASELINE config 2)", "seq": SEQ,
+                       "heads": HEADS, "head_dim": DIM, "batch": 1, "flop_convention": "4*S^2*H*D"},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16, "unit": "TFLOP/s",
+                         "frac": round(tflops / PEAK_BF16, 4), "traffic": None,
+                         "kernel": "attn_bf16_kernel<4,false>"},
+        })
+        if not args.no_cpu:
+            log(f"[bench] CPU baseline on {args.cpu_rows} rows")
+            q, k, v = w.host_inputs()
+            result["cpu_baseline"] = cpu_baseline(q, k, v, SEQ, HEADS, args.cpu_rows)
+            del q, k, v
+        for t in (w.q, w.k, w.v, w.out):
+            gpu.free(t)
+
+    if "sage" in legs:
+        with Gpu() as gpu:
+            gpu.check(gpu.lib.h3_gpu_dit_attention_configure(gpu.handle, 1), "configure sage2++")
+            log("[bench] sage attention: preparing inputs")
+            w = Workload(gpu, SEQ, HEADS, seed=3, scale=1.0, rope=False, k_bias=True)
+            ms_s, _ = time_calls(gpu, w.call, args.steps, args.warmup)
+            eff = attention_flops(SEQ, HEADS) / (ms_s * 1e-3) / 1e12
+            log(f"[bench] sage attention: {ms_s:.3f} ms/call, {eff:.1f} effective TFLOP/s")
+            result["sage"] = {"workload": "Sage int8-QK / fp8-PV attention (BASELINE config 3), incl. quantization",
+                              "ms_per_call": round(ms_s, 4), "effective_tflops": round(eff, 3),
+                              "speedup_vs_bf16": round(ms / ms_s, 3),
+                              "frac_of_fp8_peak": round(eff / PEAK_FP8, 4)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

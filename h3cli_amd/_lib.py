@@ -1,0 +1,108 @@
+"""ctypes binding of libh3hip.so (the C ABI declared in include/h3_gpu.h and
+include/h3_hip_ext.h). Loading fails loudly when the library has not been built:
+there is no fallback path."""
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libh3hip.so"
+
+F32, BF16, I8, U32, F16 = 0, 1, 2, 3, 4
+HOST_VISIBLE, DEVICE_ONLY, HOST_PINNED = 0, 1, 2
+
+_p = C.c_void_p
+_u32 = C.c_uint32
+_i = C.c_int
+_f = C.c_float
+_sz = C.c_size_t
+
+# name: (restype, [argtypes])
+_SIGNATURES = {
+    # context
+    "h3_gpu_create": (_p, [C.c_char_p, C.c_char_p, _sz]),
+    "h3_gpu_free": (None, [_p]),
+    "h3_gpu_cancel": (None, [_p]),
+    "h3_gpu_backend_name": (C.c_char_p, [_p]),
+    "h3_gpu_begin": (_i, [_p]),
+    "h3_gpu_continue": (_i, [_p]),
+    "h3_gpu_submit": (_i, [_p]),
+    "h3_gpu_synchronize": (_i, [_p]),
+    "h3_gpu_error": (C.c_char_p, [_p]),
+    "h3_gpu_get_stats": (_i, [_p, _p]),
+    # tensors
+    "h3_gpu_tensor_alloc": (_p, [_p, _sz, _i, _i]),
+    "h3_gpu_tensor_contents": (_p, [_p]),
+    "h3_gpu_tensor_new_f32": (_p, [_p, _sz]),
+    "h3_gpu_tensor_new_bf16": (_p, [_p, _sz]),
+    "h3_gpu_tensor_new_i8": (_p, [_p, _sz]),
+    "h3_gpu_tensor_from_f32": (_p, [_p, _p, _sz]),
+    "h3_gpu_tensor_from_bf16": (_p, [_p, _p, _sz]),
+    "h3_gpu_tensor_from_u32": (_p, [_p, _p, _sz]),
+    "h3_gpu_tensor_read_file_bf16": (_i, [_p, C.c_char_p, C.c_uint64, _sz, C.c_char_p, _sz]),
+    "h3_gpu_tensor_stream_file_bf16": (_i, [_p, C.c_char_p, C.c_uint64, _sz, C.c_char_p, _sz]),
+    "h3_gpu_tensor_free": (None, [_p]),
+    "h3_gpu_tensor_elements": (_sz, [_p]),
+    "h3_gpu_tensor_dtype": (_i, [_p]),
+    "h3_gpu_tensor_read_f32": (_i, [_p, _p, _sz]),
+    "h3_gpu_tensor_read_f32_range": (_i, [_p, _sz, _p, _sz]),
+    "h3_gpu_tensor_read_bf16": (_i, [_p, _p, _sz]),
+    "h3_gpu_tensor_read_u32": (_i, [_p, _p, _sz]),
+    "h3_gpu_tensor_write_f32": (_i, [_p, _p, _sz]),
+    "h3_gpu_tensor_write_f32_range": (_i, [_p, _sz, _p, _sz]),
+    "h3_gpu_tensor_write_bf16": (_i, [_p, _p, _sz]),
+    "h3_gpu_tensor_write_bf16_range": (_i, [_p, _sz, _p, _sz]),
+    # events
+    "h3_gpu_event_new": (_p, [_p]),
+    "h3_gpu_event_record": (_i, [_p, _p]),
+    "h3_gpu_event_wait": (_i, [_p, _p]),
+    "h3_gpu_event_free": (None, [_p]),
+    # attention
+    "h3_gpu_dit_attention_configure": (_i, [_p, _i]),
+    "h3_gpu_dit_sdpa_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f, _i, C.c_uint, _i]),
+    "h3_gpu_dit_attention_noise": (_i, [_p, _i, _f, _f]),
+    "h3_gpu_sdpa_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f]),
+    "h3_gpu_sdpa_bf16_head_major_output": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f]),
+    # extensions
+    "h3_hip_version": (C.c_char_p, []),
+    "h3_hip_dit_block_mask": (_i, [_p, _p, _u32, _u32, _u32]),
+    "h3_hip_sage_pack": (_i, [_p, _p, _p, _p, _u32, _u32, _p, _p, _p, _p, _p, _p, _p]),
+    "h3_hip_sage_v_position": (C.c_uint, [C.c_uint]),
+    "h3_hip_timing_event_new": (_p, [_p]),
+    "h3_hip_event_elapsed_ms": (_i, [_p, _p, _p, C.POINTER(_f)]),
+    "h3_hip_host_alloc": (_p, [_p, _sz]),
+    "h3_hip_host_free": (None, [_p, _p, _sz]),
+    "h3_hip_tensor_stream_host": (_i, [_p, _p, _sz]),
+    "h3_hip_tensor_read_bytes": (_i, [_p, _p, _sz]),
+    "h3_hip_fill_normal_bf16": (_i, [_p, _p, C.c_uint64, _f, _sz]),
+    "h3_hip_synthetic_block_mask": (C.c_uint, [_p, C.c_uint, C.c_uint, C.c_uint, C.c_double, C.c_uint64]),
+}
+
+# Declared in include/*.h but optional for this module's loader (added as the
+# backend grows); listed so the export test can check them when present.
+_OPTIONAL = set()
+
+_lib = None
+
+
+def load():
+    """Load libh3hip.so and bind every known signature. Raises if not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m h3cli_amd.build` "
+                           "(the HIP backend has no fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            if name in _OPTIONAL:
+                continue
+            raise RuntimeError(f"libh3hip.so does not export {name}")
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def signatures():
+    return dict(_SIGNATURES)

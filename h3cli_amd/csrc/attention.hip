@@ -1,0 +1,195 @@
+// Main-DiT attention boundary: mode configuration, block-sparse mask binding and
+// dispatch to the BF16 or Sage kernels. Contract of the reference's
+// h3_gpu_dit_sdpa_bf16 (src/cuda/gpu_cuda.cu:1599-1668): sequence-major BF16
+// Q/K/V [seq, heads, 128] after norm/RoPE, disjoint output (sequence- or
+// head-major), positive finite scale rounded to BF16, deferred faults.
+#include "common.h"
+#include "internal.h"
+#include "sage.h"
+#include <cmath>
+#include <new>
+#include <vector>
+
+enum { MODE_DEFAULT = 0, MODE_SAGE2 = 1, MODE_SAGE3 = 2, MODE_SOL = 3, MODE_SUBBLOCK = 4 };
+
+struct h3_attention_state {
+    bool configured = false;
+    int mode = MODE_DEFAULT;
+    int step = -1;
+    // Bound block-sparse mask (128 x 128 tiles), compacted to kept 64-key tiles.
+    bool masked = false;
+    uint32_t mask_q_blocks = 0, mask_k_blocks = 0, mask_block = 0;
+    uint32_t *kv_list = nullptr, *kv_count = nullptr;
+    uint32_t list_stride = 0;
+    uint64_t kept_tiles = 0, total_tiles = 0;  // over 128-query blocks x 64-key tiles
+    h3_sage_workspace sage;
+    // Per-dispatch timing (H3_PROFILE): pairs of events collected at synchronize.
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+};
+
+int h3_attention_init(h3_gpu *g) {
+    g->attention = new (std::nothrow) h3_attention_state();
+    return g->attention ? 1 : h3_set_error(g, "attention: out of host memory");
+}
+
+void h3_attention_destroy(h3_gpu *g) {
+    auto *s = g->attention;
+    if (!s) return;
+    if (s->kv_list) hipFree(s->kv_list);
+    if (s->kv_count) hipFree(s->kv_count);
+    h3_sage_workspace_free(&s->sage);
+    for (auto &p : s->pending) { hipEventDestroy(p.first); hipEventDestroy(p.second); }
+    delete s; g->attention = nullptr;
+}
+
+void h3_attention_collect_timing(h3_gpu *g) {
+    auto *s = g->attention;
+    if (!s) return;
+    for (auto &p : s->pending) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, p.first, p.second) == hipSuccess) {
+            g->stats.attention_seconds += ms * 1e-3; g->stats.main_attention_seconds += ms * 1e-3;
+            g->stats.attention_timing_samples++;
+        } else g->stats.attention_timing_missed++;
+        hipEventDestroy(p.first); hipEventDestroy(p.second);
+    }
+    s->pending.clear();
+}
+
+extern "C" int h3_gpu_dit_attention_configure(h3_gpu *g, int mode) {
+    if (!g) return 0;
+    auto *s = g->attention;
+    if (s->configured) return h3_set_error(g, "attention context is already configured");
+    if (mode < 0 || mode > 4) return h3_set_error(g, "cuda-attention must be default, sage2++, sage3, sol or subblock");
+    if (mode == MODE_SAGE3) return h3_set_error(g, "sage3 (NVFP4) attention is unsupported on the HIP backend");
+    if (mode == MODE_SOL) return h3_set_error(g, "SOL attention is unsupported on the HIP backend");
+    s->mode = mode; s->configured = true;
+    return 1;
+}
+
+extern "C" int h3_gpu_dit_attention_noise(h3_gpu *g, int step, float video, float audio) {
+    if (!g) return 0;
+    auto *s = g->attention;
+    if (s->mode != MODE_SUBBLOCK) return 1;
+    if (step < 0 || !std::isfinite(video) || !std::isfinite(audio) || video < 0 || video > 1 || audio < 0 || audio > 1)
+        return h3_set_error(g, "invalid HIP attention absolute step/noise");
+    s->step = step;
+    return 1;
+}
+
+extern "C" int h3_hip_dit_block_mask(h3_gpu *g, const uint8_t *mask, uint32_t qb, uint32_t kb, uint32_t block) {
+    if (!g) return 0;
+    auto *s = g->attention;
+    if (g->active && !h3_hip_check(g, hipStreamSynchronize(g->compute), "mask rebind fence")) return 0;
+    if (s->kv_list) { hipFree(s->kv_list); s->kv_list = nullptr; }
+    if (s->kv_count) { hipFree(s->kv_count); s->kv_count = nullptr; }
+    s->masked = false; s->kept_tiles = s->total_tiles = 0;
+    if (!mask) return 1;
+    if (block != 128) return h3_set_error(g, "block mask: block must be 128");
+    if (!qb || !kb || qb > (1u << 20) || kb > (1u << 20)) return h3_set_error(g, "block mask: invalid shape");
+    // The kernel walks 128-query blocks over 64-key tiles: each kept 128-key
+    // block contributes its two 64-key tiles.
+    const uint32_t q_rows = qb, tiles = kb * 2;
+    std::vector<uint32_t> count(q_rows, 0), list((size_t)q_rows * tiles, 0);
+    for (uint32_t r = 0; r < q_rows; r++) {
+        uint32_t c = 0;
+        for (uint32_t t = 0; t < tiles; t++)
+            if (mask[(size_t)r * kb + t / 2]) list[(size_t)r * tiles + c++] = t;
+        count[r] = c;
+        s->kept_tiles += c;
+    }
+    s->total_tiles = (uint64_t)q_rows * tiles;
+    if (!h3_hip_check(g, hipMalloc(&s->kv_list, list.size() * 4), "mask list") ||
+        !h3_hip_check(g, hipMalloc(&s->kv_count, count.size() * 4), "mask counts") ||
+        !h3_hip_check(g, hipMemcpy(s->kv_list, list.data(), list.size() * 4, hipMemcpyHostToDevice), "mask list upload") ||
+        !h3_hip_check(g, hipMemcpy(s->kv_count, count.data(), count.size() * 4, hipMemcpyHostToDevice), "mask count upload"))
+        return 0;
+    s->mask_q_blocks = q_rows; s->mask_k_blocks = kb; s->mask_block = block; s->list_stride = tiles;
+    s->masked = true;
+    return 1;
+}
+
+static float round_scale_bf16(float scale) {
+    uint32_t bits; memcpy(&bits, &scale, 4);
+    bits = (bits + 0x7fffu + ((bits >> 16) & 1u)) & 0xffff0000u;
+    memcpy(&scale, &bits, 4);
+    return scale;
+}
+
+static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                    const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
+                    int mode, bool masked) {
+    auto *s = g->attention;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (g->profiling) {
+        hipEventCreate(&t0); hipEventCreate(&t1);
+        hipEventRecord(t0, g->compute);
+    }
+    const uint32_t *list = masked ? s->kv_list : nullptr;
+    const uint32_t *cnt = masked ? s->kv_count : nullptr;
+    int ok;
+    if (mode == MODE_SAGE2) {
+        ok = h3_sage_attention(g, &s->sage, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
+                               (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
+        if (ok) g->stats.sage2_attention_dispatches++;
+        g->stats.attention_workspace_bytes = s->sage.bytes;
+    } else {
+        ok = h3_launch_attention_bf16(g, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
+                                      (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
+    }
+    if (g->profiling) {
+        hipEventRecord(t1, g->compute);
+        s->pending.emplace_back(t0, t1);
+    }
+    if (ok) {
+        g->stats.attention_dispatches++;
+        if (masked) { g->stats.subblock_calls++; g->stats.subblock_selected += s->kept_tiles; g->stats.subblock_possible += s->total_tiles; }
+        else if (mode == MODE_DEFAULT) g->stats.main_dense_calls++;
+    }
+    return ok;
+}
+
+static int validate(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                    const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, uint32_t dim, float scale) {
+    size_t n = (size_t)seq * heads * dim;
+    if (!h3_launch_ready(g)) return 0;
+    if (!seq || seq > INT32_MAX / 128 || !heads || heads > 65535 || dim != 128 || !std::isfinite(scale) || scale <= 0 ||
+        !out || !q || !k || !v || out == q || out == k || out == v)
+        return h3_set_error(g, "DiT attention requires disjoint BF16 output, S>0, H>0, D=128 and a positive FP32 scale");
+    return h3_require(g, q, H3_GPU_BF16, n, "DiT attention Q") && h3_require(g, k, H3_GPU_BF16, n, "DiT attention K") &&
+           h3_require(g, v, H3_GPU_BF16, n, "DiT attention V") && h3_require(g, out, H3_GPU_BF16, n, "DiT attention output");
+}
+
+extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                                    const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, uint32_t dim, float scale,
+                                    int head_major, unsigned block, int step) {
+    (void)block;
+    if (!g) return 0;
+    if (!validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
+    if ((head_major != 0 && head_major != 1) || step < 0)
+        return h3_set_error(g, "DiT attention: head_major must be 0/1 and step >= 0");
+    auto *s = g->attention;
+    if (s->mode == MODE_SUBBLOCK) {
+        if (step != s->step) return h3_set_error(g, "SubBlock absolute step was not bound");
+        if (!s->masked) return h3_set_error(g, "SubBlock attention on HIP needs a bound block mask (h3_hip_dit_block_mask)");
+    }
+    // A kept last 128-key block may list a 64-key tile wholly past the sequence
+    // end; the kernels load zeros there and mask keys >= seq to -inf.
+    if (s->masked && (s->mask_q_blocks != (seq + 127) / 128 || s->mask_k_blocks != (seq + 127) / 128))
+        return h3_set_error(g, "bound block mask does not match sequence %u", seq);
+    return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), head_major != 0,
+                    s->mode == MODE_SAGE2 ? MODE_SAGE2 : MODE_DEFAULT, s->masked);
+}
+
+extern "C" int h3_gpu_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                                const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, uint32_t dim, float scale) {
+    if (!g || !validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
+    return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), false, MODE_DEFAULT, false);
+}
+
+extern "C" int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q,
+                                                  const h3_gpu_tensor *k, const h3_gpu_tensor *v, uint32_t seq,
+                                                  uint32_t heads, uint32_t dim, float scale) {
+    if (!g || !validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
+    return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), true, MODE_DEFAULT, false);
+}

@@ -1,0 +1,94 @@
+// Internal definitions shared by the gfx950 backend translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <cstdio>
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+#include "../../include/h3_gpu.h"
+#include "../../include/h3_hip_ext.h"
+
+// ---------------------------------------------------------------- vector types
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- bf16 helpers
+__host__ __device__ inline float bf16_to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+// Round-to-nearest-even; NaN stays a quiet NaN.
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------- objects
+struct h3_gpu_tensor {
+    h3_gpu *owner;
+    void *data;             // device (or pinned host) pointer
+    size_t elements;
+    size_t bytes;           // logical bytes (elements * item size)
+    size_t bytes_alloc;     // allocated bytes (with tail slack)
+    h3_gpu_dtype dtype;
+    h3_gpu_storage storage;
+    // W8A16 weight: data holds int8 codes [rows, cols]; scales fp32 [rows, groups].
+    int q8;
+    uint32_t q8_rows, q8_cols, q8_group;
+    float *q8_scales;
+    // Streaming fences (copy stream fills, compute stream reads).
+    hipEvent_t ready, released;
+    bool ready_pending, release_recorded;
+};
+
+struct h3_gpu_event { hipEvent_t event; };
+
+struct h3_attention_state;  // attention.hip
+struct h3_stream_state;     // context.hip (weight streaming bounce buffers)
+
+struct h3_gpu {
+    int device;
+    hipStream_t compute, copy;
+    bool active, deferred_error;
+    char error[1024];
+    h3_gpu_stats stats;
+    unsigned *fault;        // device flags: [0] nonfinite attention, [1] quantizer nonfinite
+    int quant_mode;
+    h3_attention_state *attention;
+    h3_stream_state *streaming;
+    std::mutex copy_mutex;
+    // optional event timing of attention / linear dispatches (H3_PROFILE)
+    bool profiling;
+};
+
+// ---------------------------------------------------------------- helpers
+int h3_set_error(h3_gpu *g, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int h3_hip_check(h3_gpu *g, hipError_t e, const char *what);
+int h3_launch_ready(h3_gpu *g);
+int h3_launch_status(h3_gpu *g, const char *what);
+int h3_require(h3_gpu *g, const h3_gpu_tensor *t, h3_gpu_dtype dtype, size_t elements, const char *name);
+void h3_stats_track_alloc(h3_gpu *g, size_t bytes, int sign);
+
+// Number of XCDs on MI355X; workgroups are dispatched round-robin across them.
+constexpr int kXcds = 8;
+
+// Bijective remap of a linear workgroup id so that consecutive logical ids land
+// on the same XCD (and its L2): hardware id i runs on XCD i % 8.
+__device__ inline unsigned xcd_remap(unsigned pid, unsigned total) {
+    unsigned per = (total + kXcds - 1) / kXcds;
+    unsigned tall = total % kXcds; if (tall == 0) tall = kXcds;
+    unsigned xcd = pid % kXcds, local = pid / kXcds;
+    if (xcd < tall) return xcd * per + local;
+    return tall * per + (xcd - tall) * (per - 1) + local;
+}

@@ -1,0 +1,87 @@
+/* h3_hip_ext.h — entry points of the gfx950 backend with no counterpart in the
+ * reference operator surface. They exist for callers that need to drive parts
+ * of the DiT hot path the reference drives internally (a fixed block-sparse
+ * mask instead of its learned router, pre-packed W8A16 weights instead of a
+ * checkpoint file), and for measurement and parity tests. */
+#ifndef H3_HIP_EXT_H
+#define H3_HIP_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "h3_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library build identity ("h3hip gfx950 <version>"). */
+const char *h3_hip_version(void);
+
+/* W8A16 weight from already-packed codes: int8 [rows, columns] row-major and
+ * fp32 scales [rows, ceil(columns/group)]. group = columns gives one scale per
+ * output channel; group = 64 is the reference q8 recipe (src/weights/q8.h:6-12).
+ * The tensor dequantizes as w = bf16(code * scale) (src/metal/shaders.metal:825-827). */
+h3_gpu_tensor *h3_hip_q8_from_packed(h3_gpu *gpu, const int8_t *codes, const float *scales,
+                                     uint32_t rows, uint32_t columns, uint32_t group);
+
+/* Fixed block-sparse mask for main-DiT attention. mask is u8 [q_blocks, k_blocks]
+ * (nonzero = keep) over block x block tiles; block must be 128 (or 64). While a
+ * mask is bound, h3_gpu_dit_sdpa_bf16 computes softmax over the kept key tiles
+ * only, in the configured precision (dense BF16 or sage2++). NULL unbinds. The
+ * mask is copied; rows with no kept tile produce zeros. */
+int h3_hip_dit_block_mask(h3_gpu *gpu, const uint8_t *mask, uint32_t q_blocks,
+                          uint32_t k_blocks, uint32_t block);
+
+/* Synthetic block mask of the benchmark's joint sequence (video rows first, then
+ * audio): mask[qb * B + kb], B = ceil(seq/block), is 1 on the diagonal, for every
+ * pair of blocks that both hold audio rows (rows >= video_rows), and otherwise
+ * when splitmix64((seed << 40) + qb*B + kb) >> 11, times 2^-53, is < density.
+ * Returns the number of kept blocks (0 on invalid arguments). Host only. */
+unsigned h3_hip_synthetic_block_mask(uint8_t *mask, unsigned seq, unsigned video_rows,
+                                     unsigned block, double density, uint64_t seed);
+
+/* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
+ * layouts the quantized attention kernel consumes (all head-major, rows padded
+ * to a multiple of 64, padded rows zero):
+ *   q8, k8   int8 [heads, padded, 128]; K is smoothed first: k' = bf16(k - mean)
+ *   q_scale, k_scale fp32 [heads, padded/64]: fmaf(max|x| over the 64x128 block, 1/127, 1e-7)
+ *   v8       fp8 e4m3 (OCP) [heads, 128, padded], key order permuted within each
+ *            64-key tile as the kernel reads it (h3_hip_sage_v_position)
+ *   v_scale  fp32 [heads, 128]: max|v| over the sequence / 448
+ *   k_mean   bf16 [heads, 128]: bf16(sum / seq), sum in fp32 over rows in a fixed order:
+ *            partial p sums rows [256p, 256p+256) in row order, partials summed in p order.
+ * Requires an active command. Used by parity tests; the attention path calls the
+ * same kernels on its own workspace. */
+int h3_hip_sage_pack(h3_gpu *gpu, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                     const h3_gpu_tensor *v, uint32_t seq, uint32_t heads,
+                     h3_gpu_tensor *q8, h3_gpu_tensor *k8, h3_gpu_tensor *v8,
+                     h3_gpu_tensor *q_scale, h3_gpu_tensor *k_scale,
+                     h3_gpu_tensor *v_scale, h3_gpu_tensor *k_mean);
+/* Position of key j (0..63) of a 64-key tile inside the packed fp8 V row. */
+unsigned h3_hip_sage_v_position(unsigned j);
+
+/* Pinned host memory for streamed weights, and an asynchronous fill of a device
+ * tensor from it on the copy stream (the streamed-weight path of reference
+ * src/cuda/gpu_cuda.cu:761-840, with the source already in pinned memory).
+ * For a q8 weight, src holds the int8 codes followed by the fp32 scales. Kernels
+ * that read the tensor wait for the fill; the next fill waits for those kernels. */
+void *h3_hip_host_alloc(h3_gpu *gpu, size_t bytes);
+void h3_hip_host_free(h3_gpu *gpu, void *pointer, size_t bytes);
+int h3_hip_tensor_stream_host(h3_gpu_tensor *tensor, const void *src, size_t bytes);
+
+/* Raw device contents of a tensor (any dtype), for reading int8/fp8 codes. */
+int h3_hip_tensor_read_bytes(const h3_gpu_tensor *tensor, void *dst, size_t bytes);
+/* Fill count BF16 elements with seeded N(0,1) * scale values: the splitmix64 +
+ * Box-Muller stream documented in h3cli_amd/synth.py. Requires an active command. */
+int h3_hip_fill_normal_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor, uint64_t seed, float scale, size_t count);
+
+/* Kernel timing on the compute stream: record a timing event (created with
+ * timing enabled) and read the elapsed milliseconds between two of them after
+ * h3_gpu_submit/synchronize. */
+h3_gpu_event *h3_hip_timing_event_new(h3_gpu *gpu);
+int h3_hip_event_elapsed_ms(h3_gpu *gpu, h3_gpu_event *start, h3_gpu_event *end, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,139 @@
+"""BF16 DiT attention on the GPU vs the CPU oracle (reference
+src/cuda/cuda_attention.cuh:7-51 restated in oracle/attention.c), through the C ABI."""
+import math
+
+import numpy as np
+import pytest
+
+from h3cli_amd import synth
+from h3cli_amd.runtime import Gpu
+from oracle import oracle
+from tests.helpers import ATTN_COSINE, ATTN_MAX_ABS, bf16, metrics, scale_bf16, sdpa
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = Gpu()
+    yield g
+    g.close()
+
+
+def _check(gpu, q, k, v, seq, heads, head_major=False, dit=True, rows=None):
+    print(f"[attention] seq={seq} heads={heads} head_major={head_major} dit={dit}", flush=True)
+    out = sdpa(gpu, q, k, v, seq, heads, head_major=head_major, dit=dit)
+    scale = scale_bf16(1 / math.sqrt(128))
+    r0, r1 = rows if rows else (0, seq)
+    ref = oracle.attention(bf16(q), bf16(k), bf16(v), seq, heads, scale, tile=64, rows=(r0, r1))
+    got = bf16(out)[r0:r1]
+    m = metrics(got, ref)
+    assert np.all(np.isfinite(got))
+    assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+    return m
+
+
+@pytest.mark.parametrize("seq,heads,head_major", [(19, 4, False), (513, 3, False), (1025, 4, True),
+                                                  (2048, 8, False), (1, 2, False), (64, 1, False),
+                                                  (65, 1, True), (300, 40, False)])
+def test_reference_patterns(gpu, seq, heads, head_major):
+    """Shapes and the xorshift input pattern of the reference's
+    tests/cuda_attention.c:14-18,52 (D fixed at 128 on this path)."""
+    st = np.array([123], np.uint32)
+    n = seq * heads * 128
+    q, k, v = (oracle.xorshift_bf16(n, st) for _ in range(3))
+    m = _check(gpu, q, k, v, seq, heads, head_major)
+    # The reference's own gate for its tiled kernel (tests/cuda_attention.c:43).
+    assert m["max_abs"] < 0.016, m
+
+
+@pytest.mark.parametrize("seq,heads", [(1000, 2), (4096, 4)])
+def test_gaussian_rope_inputs(gpu, seq, heads):
+    """BASELINE config 2 input distribution (0.5 N(0,1), 3D RoPE) at small S."""
+    q, k, v = synth.attention_inputs(seq, heads, seed=2, scale=0.5, rope_shape=(27, 30, 40))
+    _check(gpu, q, k, v, seq, heads)
+
+
+def test_plain_entry_points(gpu):
+    seq, heads = 700, 3
+    q, k, v = synth.attention_inputs(seq, heads, seed=5)
+    _check(gpu, q, k, v, seq, heads, dit=False)
+    _check(gpu, q, k, v, seq, heads, head_major=True, dit=False)
+
+
+def test_f64_bruteforce_rows(gpu):
+    """Sampled rows against a direct FP64 softmax (tests/metal_attention.c:55-67)."""
+    seq, heads = 3000, 2
+    q, k, v = synth.attention_inputs(seq, heads, seed=9, scale=1.0)
+    out = bf16(sdpa(gpu, q, k, v, seq, heads))
+    scale = scale_bf16(1 / math.sqrt(128))
+    for r0 in (0, 1234, 2990):
+        ref = oracle.attention_f64(bf16(q), bf16(k), bf16(v), seq, heads, scale, rows=(r0, r0 + 10))
+        m = metrics(out[r0:r0 + 10], ref)
+        assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+
+
+def test_invariants(gpu):
+    """Zero input -> zero output; constant V -> V (tests/attention_native.c:79-80)."""
+    seq, heads = 777, 2
+    n = seq * heads * 128
+    z = np.zeros(n, np.uint16)
+    assert np.all((sdpa(gpu, z, z, z, seq, heads) & 0x7FFF) == 0)
+    q, k, _ = synth.attention_inputs(seq, heads, seed=11)
+    c = np.full(n, synth.f32_to_bf16(np.float32(0.5)), np.uint16)
+    out = bf16(sdpa(gpu, q, k, c, seq, heads))
+    assert np.max(np.abs(out - 0.5)) < 0.02
+
+
+def test_nonfinite_rejected(gpu):
+    """NaN input must fail the submit with an error naming 'nonfinite'
+    (tests/attention_native.c:71)."""
+    seq, heads = 200, 2
+    q, k, v = synth.attention_inputs(seq, heads, seed=3)
+    q = q.copy()
+    q[0] = 0x7FC0
+    with pytest.raises(Exception) as e:
+        sdpa(gpu, q, k, v, seq, heads)
+    assert "nonfinite" in str(e.value)
+    gpu.cancel()
+    # The context recovers after cancel.
+    q, k, v = synth.attention_inputs(seq, heads, seed=4)
+    _check(gpu, q, k, v, seq, heads)
+
+
+def test_inputs_unchanged_and_guards(gpu):
+    """Inputs are not modified and nothing is written past the output
+    (tests/attention_native.c:57-66,74-77 guard words)."""
+    lib = gpu.lib
+    seq, heads = 333, 3
+    n = seq * heads * 128
+    q, k, v = synth.attention_inputs(seq, heads, seed=6)
+    guard = np.full(256, 0x7F7F, np.uint16)
+    tq, tk, tv = (gpu.from_bf16(np.concatenate([a, guard])) for a in (q, k, v))
+    out = gpu.from_bf16(np.concatenate([np.full(n, 0xFFFF, np.uint16), guard]))
+    gpu.begin()
+    gpu.check(lib.h3_gpu_dit_sdpa_bf16(gpu.handle, out.handle, tq.handle, tk.handle, tv.handle, seq, heads, 128,
+                                       1 / math.sqrt(128), 0, 0, 0), "sdpa")
+    gpu.submit()
+    for t, a in ((tq, q), (tk, k), (tv, v)):
+        assert np.array_equal(t.read()[:n], a)
+    o = out.read()
+    assert np.all(o[n:] == 0x7F7F)
+    assert np.all((o[:n] & 0x7F80) != 0x7F80)
+
+
+def test_contract_errors(gpu):
+    lib = gpu.lib
+    seq, heads = 64, 1
+    n = seq * heads * 128
+    t = gpu.from_bf16(np.zeros(n, np.uint16))
+    o = gpu.empty(n)
+    # Not inside begin/submit.
+    assert not lib.h3_gpu_dit_sdpa_bf16(gpu.handle, o.handle, t.handle, t.handle, t.handle, seq, heads, 128, 0.1, 0, 0, 0)
+    gpu.begin()
+    # Output aliases an input; D != 128; non-positive scale; short tensor.
+    assert not lib.h3_gpu_dit_sdpa_bf16(gpu.handle, t.handle, t.handle, t.handle, t.handle, seq, heads, 128, 0.1, 0, 0, 0)
+    assert not lib.h3_gpu_dit_sdpa_bf16(gpu.handle, o.handle, t.handle, t.handle, t.handle, seq, heads * 2, 64, 0.1, 0, 0, 0)
+    assert not lib.h3_gpu_dit_sdpa_bf16(gpu.handle, o.handle, t.handle, t.handle, t.handle, seq, heads, 128, -1.0, 0, 0, 0)
+    assert not lib.h3_gpu_dit_sdpa_bf16(gpu.handle, o.handle, t.handle, t.handle, t.handle, seq + 1, heads, 128, 0.1, 0, 0, 0)
+    gpu.submit()

@@ -1,0 +1,165 @@
+"""Pins of the CPU oracle against checks independent of its own formulas:
+FP64 brute force, invariants, torch's float8 cast, closed forms, brute-force
+enumeration and the reference's own known-answer cases."""
+import math
+
+import numpy as np
+import pytest
+
+from h3cli_amd import synth
+from oracle import oracle
+from tests.helpers import bf16, metrics
+
+torch = pytest.importorskip("torch")
+
+
+def test_attention_matches_f64_bruteforce():
+    seq, heads = 300, 3
+    q, k, v = (bf16(a) for a in synth.attention_inputs(seq, heads, seed=1, scale=1.0))
+    scale = 1 / math.sqrt(128)
+    got = oracle.attention(q, k, v, seq, heads, scale, tile=64)
+    ref = oracle.attention_f64(q, k, v, seq, heads, scale)
+    m = metrics(got, ref)
+    assert m["max_abs"] < 1e-5 and m["rel_l2"] < 1e-5, m
+
+
+def test_attention_matches_torch_sdpa():
+    """Against the textbook routine (torch's math SDPA in float64)."""
+    seq, heads = 257, 2
+    q, k, v = (bf16(a).reshape(seq, heads, 128) for a in synth.attention_inputs(seq, heads, seed=2))
+    scale = 0.0883
+    got = oracle.attention(q, k, v, seq, heads, scale, tile=16)
+    t = lambda a: torch.from_numpy(a.astype(np.float64)).permute(1, 0, 2)
+    ref = torch.softmax(t(q) @ t(k).transpose(1, 2) * scale, -1) @ t(v)
+    m = metrics(got, ref.permute(1, 0, 2).numpy())
+    assert m["max_abs"] < 1e-5, m
+
+
+def test_attention_tile_size_and_invariants():
+    seq, heads = 130, 2
+    q, k, v = (bf16(a) for a in synth.attention_inputs(seq, heads, seed=3))
+    scale = 0.1
+    a = oracle.attention(q, k, v, seq, heads, scale, tile=16)
+    b = oracle.attention(q, k, v, seq, heads, scale, tile=64)
+    assert metrics(a, b)["max_abs"] < 1e-5
+    c = np.full_like(v, 0.75)
+    assert np.allclose(oracle.attention(q, k, c, seq, heads, scale), 0.75, atol=1e-6)
+    z = np.zeros_like(q)
+    assert np.all(oracle.attention(z, z, z, seq, heads, scale) == 0)
+    # Permuting heads permutes outputs.
+    perm = [1, 0]
+    qp, kp, vp = (x.reshape(seq, heads, 128)[:, perm].copy() for x in (q, k, v))
+    assert np.array_equal(oracle.attention(qp, kp, vp, seq, heads, scale, tile=16), a.reshape(seq, heads, 128)[:, perm])
+
+
+def test_masked_attention_equals_dense_on_full_mask_and_bruteforce():
+    seq, heads = 300, 2
+    q, k, v = (bf16(a) for a in synth.attention_inputs(seq, heads, seed=4))
+    blocks = (seq + 127) // 128
+    full = np.ones((blocks, blocks), np.uint8)
+    a = oracle.attention(q, k, v, seq, heads, 0.1, tile=128)
+    b = oracle.attention(q, k, v, seq, heads, 0.1, mask=full, block=128)
+    assert metrics(a, b)["max_abs"] < 1e-6
+    # Brute force: masked keys get -inf in an FP64 softmax.
+    mask = np.array([[1, 0, 1], [0, 1, 0], [1, 1, 0]], np.uint8)
+    got = oracle.attention(q, k, v, seq, heads, 0.1, mask=mask, block=128)
+    qq, kk, vv = (x.reshape(seq, heads, 128).astype(np.float64) for x in (q, k, v))
+    s = np.einsum("qhd,khd->hqk", qq, kk) * 0.1
+    allow = mask[np.arange(seq)[:, None] // 128, np.arange(seq)[None, :] // 128].astype(bool)
+    s[:, ~allow] = -np.inf
+    p = np.exp(s - s.max(-1, keepdims=True))
+    ref = np.einsum("hqk,khd->qhd", p / p.sum(-1, keepdims=True), vv)
+    assert metrics(got, ref)["max_abs"] < 1e-5
+
+
+def test_e4m3_encoder_matches_torch_cast():
+    """The brute-force e4m3 encoder equals torch's float8_e4m3fn cast (RNE) for
+    every in-range value class: all codes, midpoints, subnormals, random values."""
+    codes = np.arange(0x7F, dtype=np.uint8)
+    vals = oracle.e4m3_decode(codes)
+    mids = (vals[:-1] + vals[1:]) / 2
+    rng = np.random.default_rng(0)
+    rand = rng.uniform(-448, 448, 2000).astype(np.float32)
+    tiny = rng.uniform(-0.02, 0.02, 500).astype(np.float32)
+    xs = np.concatenate([vals, -vals, mids, -mids, rand, tiny, np.float32([448.0, -448.0, 1e-9, 0.0])])
+    ref = torch.from_numpy(xs).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = oracle.e4m3_encode(xs)
+    bad = np.flatnonzero(got != ref)
+    assert bad.size == 0, (xs[bad[:5]], got[bad[:5]], ref[bad[:5]])
+    # Decoding agrees with torch as well.
+    back = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(vals, back)
+
+
+def test_e4m3_saturates_above_448():
+    assert oracle.e4m3_encode([500.0, 463.9, 1e6])[0] == 0x7E
+    assert oracle.e4m3_encode([463.9])[0] == 0x7E
+
+
+def test_sage_pack_closed_forms():
+    """Scale = fmaf(amax, 1/127, 1e-7); codes within one step of x/scale; a
+    block's extreme value codes to +/-127; zero blocks code to 0 with scale 1e-7;
+    K mean within one BF16 ulp of the FP64 mean; V codes are the nearest e4m3."""
+    seq, heads = 200, 2
+    n = seq * heads * 128
+    q = synth.normal_bf16(1, n)
+    k = synth.normal_bf16(2, n, scale=2.0)
+    v = synth.normal_bf16(3, n)
+    q[: heads * 128 * 64] = 0  # first 64-row block of Q is all zeros
+    p = oracle.sage_pack(q, k, v, seq, heads)
+    padded, blocks = 256, 4
+    q3 = bf16(q).reshape(seq, heads, 128)
+    assert np.all(p["q_scale"].reshape(heads, blocks)[:, 0] == np.float32(1e-7))
+    for h in range(heads):
+        for b in range(1, blocks):
+            x = q3[b * 64:min(seq, b * 64 + 64), h]
+            amax = np.float32(np.abs(x).max())
+            assert p["q_scale"][h * blocks + b] == np.float32(np.fma(amax, np.float32(1 / 127), np.float32(1e-7))) \
+                if hasattr(np, "fma") else True
+            s = p["q_scale"][h * blocks + b]
+            codes = p["q8"].reshape(heads, padded, 128)[h, b * 64:b * 64 + x.shape[0]]
+            assert np.all(np.abs(codes - x / s) <= 0.5 + 1e-6)
+            assert np.abs(codes).max() == 127
+    m64 = oracle.k_mean_f64(k, seq, heads)
+    mean = bf16(p["k_mean"]).astype(np.float64)
+    assert np.all(np.abs(mean - m64) <= np.abs(m64) * 2.0 ** -7 + 1e-12)
+    # V: decode(code) * v_scale approximates v; code is the nearest e4m3 of v * 448 / vmax.
+    v3 = bf16(v).reshape(seq, heads, 128)
+    vmax = np.abs(v3).max(0)
+    assert np.array_equal(p["v_scale"].reshape(heads, 128), (vmax / np.float32(448)).astype(np.float32))
+    pos = np.array([oracle.sage_v_position(j) for j in range(64)])
+    assert sorted(pos) == list(range(64))
+    v8 = p["v8"].reshape(heads, 128, padded)
+    for h in range(heads):
+        for j in (0, 17, 63, 64, 199):
+            codes = v8[h, :, (j // 64) * 64 + pos[j % 64]]
+            want = torch.from_numpy((v3[j, h] * (np.float32(448) / vmax[h])).astype(np.float32)).to(
+                torch.float8_e4m3fn).view(torch.uint8).numpy()
+            assert np.array_equal(codes, want)
+
+
+def test_sage_attention_oracle_close_to_fp_reference():
+    # Quantization error averages over keys: the BASELINE gate is met from a
+    # few thousand keys on (max-abs falls roughly as 1/sqrt(seq)).
+    seq, heads = 2048, 2
+    q, k, v = synth.attention_inputs(seq, heads, seed=8, scale=1.0)
+    p = oracle.sage_pack(q, k, v, seq, heads)
+    a = oracle.sage_attention(p, seq, heads, 0.0884, rows=(0, 128))
+    b = oracle.attention_f64(bf16(q), bf16(k), bf16(v), seq, heads, 0.0884, rows=(0, 128))
+    m = metrics(a, b)
+    assert m["cosine"] > 0.999 and m["max_abs"] < 2e-2, m
+
+
+def test_reference_input_generator_known_values():
+    """tests/cuda_attention.c:14-18 from seed 123: first values by hand."""
+    st = np.array([123], np.uint32)
+    out = oracle.xorshift_bf16(3, st)
+    s = 123
+    vals = []
+    for _ in range(3):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        vals.append(((s % 4097) - 2048) / 1024.0)
+    assert np.array_equal(out, synth.f32_to_bf16(np.float32(vals)))
+    assert st[0] == s

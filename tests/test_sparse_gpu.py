@@ -1,0 +1,80 @@
+"""Block-sparse DiT attention (BF16 and Sage) on the GPU vs the masked CPU oracle;
+the synthetic mask builder bit-exact vs its numpy restatement."""
+import math
+
+import numpy as np
+import pytest
+
+from h3cli_amd import synth
+from h3cli_amd.runtime import Gpu
+from oracle import oracle
+from tests.helpers import ATTN_COSINE, ATTN_MAX_ABS, bf16, metrics, scale_bf16, sdpa
+from tests.test_sage_gpu import sage_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def bind_mask(gpu, mask):
+    qb, kb = mask.shape
+    m = np.ascontiguousarray(mask, np.uint8)
+    gpu.check(gpu.lib.h3_hip_dit_block_mask(gpu.handle, m.ctypes.data, qb, kb, 128), "bind mask")
+
+
+def make_gpu(mode):
+    g = Gpu()
+    g.check(g.lib.h3_gpu_dit_attention_configure(g.handle, mode), "configure")
+    return g
+
+
+@pytest.mark.parametrize("mode", [0, 4])
+@pytest.mark.parametrize("seq,video", [(1000, 900), (2100, 1700)])
+def test_masked_bf16(mode, seq, video):
+    print(f"[sparse bf16] mode={mode} seq={seq}", flush=True)
+    g = make_gpu(mode)
+    try:
+        if mode == 4:
+            g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.5, 0.5), "noise")
+        mask = oracle.block_mask(seq, video, 128, 0.25, seed=seq)
+        bind_mask(g, mask)
+        q, k, v = synth.attention_inputs(seq, 2, seed=seq, scale=1.0)
+        out = bf16(sdpa(g, q, k, v, seq, 2))
+        scale = scale_bf16(1 / math.sqrt(128))
+        ref = oracle.attention(bf16(q), bf16(k), bf16(v), seq, 2, scale, mask=mask, block=128)
+        m = metrics(out, ref)
+        assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+    finally:
+        g.close()
+
+
+def test_masked_sage():
+    seq, video, heads = 1500, 1200, 2
+    print(f"[sparse sage] seq={seq}", flush=True)
+    g = make_gpu(1)
+    try:
+        mask = oracle.block_mask(seq, video, 128, 0.25, seed=3)
+        bind_mask(g, mask)
+        q, k, v = sage_inputs(seq, heads, seed=13)
+        out = bf16(sdpa(g, q, k, v, seq, heads))
+        scale = scale_bf16(1 / math.sqrt(128))
+        ref = oracle.attention(bf16(q), bf16(k), bf16(v), seq, heads, scale, mask=mask, block=128)
+        m = metrics(out, ref)
+        assert m["cosine"] >= ATTN_COSINE, m
+        pack = oracle.sage_pack(q, k, v, seq, heads)
+        mq = metrics(out, oracle.sage_attention(pack, seq, heads, scale, mask=mask, block=128))
+        assert mq["cosine"] >= 0.9995, mq
+    finally:
+        g.close()
+
+
+def test_subblock_requires_mask_and_step():
+    g = make_gpu(4)
+    try:
+        seq = 256
+        q, k, v = synth.attention_inputs(seq, 1, seed=1)
+        with pytest.raises(RuntimeError):
+            sdpa(g, q, k, v, seq, 1, step=0)  # step not bound
+        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.5, 0.5), "noise")
+        with pytest.raises(RuntimeError):
+            sdpa(g, q, k, v, seq, 1, step=0)  # no mask bound
+    finally:
+        g.close()
