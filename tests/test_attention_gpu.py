@@ -109,6 +109,7 @@ def test_inputs_unchanged_and_guards(gpu):
     n = seq * heads * 128
     q, k, v = synth.attention_inputs(seq, heads, seed=6)
     guard = np.full(256, 0x7F7F, np.uint16)
+    q, k, v = (a.reshape(-1) for a in (q, k, v))
     tq, tk, tv = (gpu.from_bf16(np.concatenate([a, guard])) for a in (q, k, v))
     out = gpu.from_bf16(np.concatenate([np.full(n, 0xFFFF, np.uint16), guard]))
     gpu.begin()
