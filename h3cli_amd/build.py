@@ -25,6 +25,9 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # Packed-FP32 instructions are disabled for device code on this pool.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # No IEEE NaN quieting around min/max (it doubles the score-max work);
+    # kernels test finiteness on bit patterns instead of with isfinite().
+    "-mno-amdgpu-ieee", "-fno-honor-nans",
     "-Wno-unused-result", "-Wno-unused-value", "-Wno-unused-command-line-argument",
     f"-I{ROOT / 'include'}",
 ]

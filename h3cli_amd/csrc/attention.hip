@@ -23,6 +23,7 @@ struct h3_attention_state {
     uint32_t list_stride = 0;
     uint64_t kept_tiles = 0, total_tiles = 0;  // over 128-query blocks x 64-key tiles
     h3_sage_workspace sage;
+    h3_device_buffer bf16_ws;              // transposed V of the BF16 kernel
     // Per-dispatch timing (H3_PROFILE): pairs of events collected at synchronize.
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
 };
@@ -38,6 +39,7 @@ void h3_attention_destroy(h3_gpu *g) {
     if (s->kv_list) hipFree(s->kv_list);
     if (s->kv_count) hipFree(s->kv_count);
     h3_sage_workspace_free(&s->sage);
+    h3_buffer_free(&s->bf16_ws);
     for (auto &p : s->pending) { hipEventDestroy(p.first); hipEventDestroy(p.second); }
     delete s; g->attention = nullptr;
 }
@@ -71,7 +73,7 @@ extern "C" int h3_gpu_dit_attention_noise(h3_gpu *g, int step, float video, floa
     if (!g) return 0;
     auto *s = g->attention;
     if (s->mode != MODE_SUBBLOCK) return 1;
-    if (step < 0 || !std::isfinite(video) || !std::isfinite(audio) || video < 0 || video > 1 || audio < 0 || audio > 1)
+    if (step < 0 || !finite_f32(video) || !finite_f32(audio) || video < 0 || video > 1 || audio < 0 || audio > 1)
         return h3_set_error(g, "invalid HIP attention absolute step/noise");
     s->step = step;
     return 1;
@@ -132,11 +134,12 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
         ok = h3_sage_attention(g, &s->sage, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
                                (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
         if (ok) g->stats.sage2_attention_dispatches++;
-        g->stats.attention_workspace_bytes = s->sage.bytes;
     } else {
-        ok = h3_launch_attention_bf16(g, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
+        ok = h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") &&
+             h3_launch_attention_bf16(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
                                       (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
     }
+    g->stats.attention_workspace_bytes = s->sage.bytes + s->bf16_ws.bytes;
     if (g->profiling) {
         hipEventRecord(t1, g->compute);
         s->pending.emplace_back(t0, t1);
@@ -153,7 +156,7 @@ static int validate(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
                     const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, uint32_t dim, float scale) {
     size_t n = (size_t)seq * heads * dim;
     if (!h3_launch_ready(g)) return 0;
-    if (!seq || seq > INT32_MAX / 128 || !heads || heads > 65535 || dim != 128 || !std::isfinite(scale) || scale <= 0 ||
+    if (!seq || seq > INT32_MAX / 128 || !heads || heads > 65535 || dim != 128 || !finite_f32(scale) || scale <= 0 ||
         !out || !q || !k || !v || out == q || out == k || out == v)
         return h3_set_error(g, "DiT attention requires disjoint BF16 output, S>0, H>0, D=128 and a positive FP32 scale");
     return h3_require(g, q, H3_GPU_BF16, n, "DiT attention Q") && h3_require(g, k, H3_GPU_BF16, n, "DiT attention K") &&

@@ -11,12 +11,16 @@
 //    fragments of a wave stay in VGPRs for the whole key sweep;
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
 //    each lane then owns one query column, so the row max is a register max
-//    plus one exchange between the two 32-lane halves, and the FP32 score
-//    accumulator is already laid out as the B operand of O^T += V^T P^T;
-//  * K tiles (64 keys) are staged row-major in LDS, V tiles transposed in LDS
-//    with a key permutation matching the score accumulator, both double
-//    buffered with one barrier per tile; global loads of tile t+1 are issued
-//    before the MFMAs of tile t;
+//    plus one v_permlane32_swap between the two 32-lane halves, and the FP32
+//    score accumulator is already laid out as the B operand of O^T += V^T P^T;
+//  * V is transposed once per call by a bandwidth-bound pre-pass into
+//    [head, channel, key] with the key order the score accumulator produces, so
+//    the main loop stages both K and V^T tiles with plain 16-byte copies;
+//  * K / V^T tiles (64 keys) are double buffered in LDS with one barrier per
+//    tile; global loads of tile t+1 are issued before the MFMAs of tile t;
+//  * the running max is only raised when a tile's max exceeds it by more than
+//    2^8 (P then stays below 256, exact in BF16/FP32 range), so the FP32
+//    accumulator rescale runs a handful of times per row instead of per tile;
 //  * workgroup ids are remapped so that the workgroups of one head share an XCD
 //    (and its L2), which is where their K/V tiles are re-read.
 #include "common.h"
@@ -27,16 +31,21 @@ namespace {
 
 constexpr int D = 128;
 constexpr int BN = 64;                     // keys per tile
-constexpr int K_STRIDE = D + 8;            // LDS row stride of the K tile (elements)
-constexpr int V_STRIDE = BN + 8;           // LDS row stride of the transposed V tile
-constexpr int K_ELEMS = BN * K_STRIDE;
-constexpr int V_ELEMS = D * V_STRIDE;
-constexpr int STAGE_ELEMS = K_ELEMS + V_ELEMS;
+constexpr int K_BYTES = BN * D * 2;        // K tile: 64 rows x 256 B, 16-byte chunks XOR-swizzled
+constexpr int V_BYTES = D * BN * 2;        // V^T tile: 128 rows x 128 B, 16-byte chunks XOR-swizzled
+constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
+constexpr float RESCALE_SLACK = 8.0f;      // log2 units the running max may lag
+
+// LDS chunk swizzles (16-byte chunks): every 16-lane group of a ds_read_b128
+// touches 16 distinct 4-bank groups for both operand reads.
+__device__ inline unsigned k_chunk(unsigned key, unsigned ch) { return ch ^ (key & 15); }
+__device__ inline unsigned v_chunk(unsigned d, unsigned ch) { return ch ^ ((d >> 1) & 7); }
 
 struct Args {
     uint16_t *out;
-    const uint16_t *q, *k, *v;
-    unsigned seq, heads;
+    const uint16_t *q, *k;
+    const uint16_t *vt;                    // [heads, 128, padded] permuted keys
+    unsigned seq, heads, padded;
     float scale_log2;                      // softmax scale * log2(e)
     int head_major;
     const uint32_t *kv_list;               // sparse: per 128-query block, kept 64-key tile ids (all heads)
@@ -48,9 +57,43 @@ struct Args {
 // Position of key j (0..63) inside a transposed V row: keys are grouped by 16
 // and, inside a group, ordered the way a lane half holds them in the S^T
 // accumulator (rows (r/4)*8 + half*4 + r%4 of a 32x32 MFMA output).
-__device__ inline unsigned v_position(unsigned j) {
+__host__ __device__ inline unsigned v_position(unsigned j) {
     unsigned k16 = j & 15;
     return (j & ~15u) + ((k16 >> 2) & 1) * 8 + (k16 >> 3) * 4 + (k16 & 3);
+}
+
+// V [seq, heads, 128] -> Vt [heads, 128, padded]; one workgroup per (64-key tile,
+// head). The pass also screens this tile's K and V rows for Inf/NaN.
+__global__ __launch_bounds__(256) void transpose_v(const uint16_t *v, const uint16_t *k, uint16_t *vt, unsigned seq,
+                                                  unsigned heads, unsigned padded, unsigned *fault) {
+    __shared__ uint16_t tile[BN][D + 8];
+    const unsigned blk = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+    const size_t stride = (size_t)heads * D;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned c = t + 256 * i, key = c / 16, ch = c % 16, row = blk * BN + key;
+        u16x8 raw = row < seq ? *reinterpret_cast<const u16x8 *>(v + row * stride + (size_t)head * D + ch * 8) : u16x8{};
+        u16x8 kraw = row < seq ? *reinterpret_cast<const u16x8 *>(k + row * stride + (size_t)head * D + ch * 8) : u16x8{};
+        bad |= bf16_vec_nonfinite(raw) | bf16_vec_nonfinite(kraw);
+        *reinterpret_cast<u16x8 *>(&tile[key][ch * 8]) = raw;
+    }
+    if (bad) fault[0] = 1u;
+    __syncthreads();
+    // Thread t writes channel d = t / 2, positions half*32 .. half*32+31.
+    const unsigned d = t / 2, half = t % 2;
+    u16x8 w[4];
+#pragma unroll
+    for (int p = 0; p < 32; p++) {
+        unsigned pos = half * 32 + p;
+        // Inverse of v_position inside the 16-key group.
+        unsigned p16 = pos & 15, hf = p16 >> 3, i = p16 & 7;
+        unsigned key = (pos & ~15u) + (i >> 2) * 8 + hf * 4 + (i & 3);
+        w[p / 8][p % 8] = tile[key][d];
+    }
+    uint16_t *dst = vt + ((size_t)head * D + d) * padded + blk * BN + half * 32;
+#pragma unroll
+    for (int j = 0; j < 4; j++) *reinterpret_cast<u16x8 *>(dst + j * 8) = w[j];
 }
 
 template <int WAVES, bool SPARSE>
@@ -58,10 +101,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), a
 void attn_bf16_kernel(Args a) {
     constexpr int T = 64 * WAVES;
     constexpr int BM = 64 * WAVES;
-    constexpr int KCH = (BN * D / 8) / T;  // 16-byte K chunks per thread per tile
-    constexpr int VU = (BN / 4) * (D / 8) / T;  // 4-key x 8-channel V units per thread
-    static_assert(KCH * T == BN * D / 8 && VU * T == (BN / 4) * (D / 8), "tile split");
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    constexpr int LOADS = (K_BYTES / 1024) / WAVES;  // 1 KB direct-to-LDS loads per wave per operand
+    static_assert(LOADS * WAVES * 1024 == K_BYTES && K_BYTES == V_BYTES, "tile split");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
@@ -72,7 +114,8 @@ void attn_bf16_kernel(Args a) {
     const size_t stride = (size_t)a.heads * D;
     const uint16_t *qh = a.q + (size_t)head * D;
     const uint16_t *kh = a.k + (size_t)head * D;
-    const uint16_t *vh = a.v + (size_t)head * D;
+    const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
+    const float c = a.scale_log2;
 
     unsigned count;
     const uint32_t *list = nullptr;
@@ -93,6 +136,14 @@ void attn_bf16_kernel(Args a) {
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) qf[nb][ks] = *reinterpret_cast<const bf16x8 *>(p + ks * 16);
     }
+    {
+        bool bad = false;
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) bad |= bf16_vec_nonfinite(qf[nb][ks]);
+        if (bad) a.fault[0] = 1u;
+    }
 
     f32x16 o[4][2];
 #pragma unroll
@@ -101,61 +152,36 @@ void attn_bf16_kernel(Args a) {
         for (int nb = 0; nb < 2; nb++) o[md][nb] = f32x16{};
     float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
 
-    u16x8 rk[KCH];
-    u16x8 rv[VU][4];
-    auto load_tile = [&](unsigned tile) {
+    // Tile loads go straight from global memory to LDS (global_load_lds_dwordx4):
+    // each wave instruction fills one contiguous KB, lane i writing bytes
+    // [16i, 16i+16), so each lane fetches the logical chunk that the swizzle
+    // places there. Keys past the end are clamped (their scores are masked) and
+    // the transposed V is zero-padded to a whole tile.
+    auto load_tile = [&](unsigned tile, int stage) {
         const unsigned key0 = tile * BN;
+        uint8_t *ks = smem + stage * STAGE_BYTES;
+        uint8_t *vs = ks + K_BYTES;
 #pragma unroll
-        for (int j = 0; j < KCH; j++) {
-            unsigned c = tid + T * j, key = key0 + c / 16, ch = c % 16;
-            rk[j] = key < a.seq ? *reinterpret_cast<const u16x8 *>(kh + (size_t)key * stride + ch * 8) : u16x8{};
-        }
-#pragma unroll
-        for (int j = 0; j < VU; j++) {
-            unsigned u = tid + T * j, kg = u % 16, dc = u / 16;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                unsigned key = key0 + kg * 4 + i;
-                rv[j][i] = key < a.seq ? *reinterpret_cast<const u16x8 *>(vh + (size_t)key * stride + dc * 8) : u16x8{};
-            }
-        }
-    };
-    auto store_tile = [&](int stage) {
-        uint16_t *ks = smem + stage * STAGE_ELEMS;
-        uint16_t *vs = ks + K_ELEMS;
-#pragma unroll
-        for (int j = 0; j < KCH; j++) {
-            unsigned c = tid + T * j, key = c / 16, ch = c % 16;
-            *reinterpret_cast<u16x8 *>(ks + key * K_STRIDE + ch * 8) = rk[j];
-        }
-#pragma unroll
-        for (int j = 0; j < VU; j++) {
-            unsigned u = tid + T * j, kg = u % 16, dc = u / 16;
-            unsigned pos = v_position(kg * 4);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                u16x4 col = {rv[j][0][e], rv[j][1][e], rv[j][2][e], rv[j][3][e]};
-                *reinterpret_cast<u16x4 *>(vs + (dc * 8 + e) * V_STRIDE + pos) = col;
-            }
+        for (int j = 0; j < LOADS; j++) {
+            const unsigned b = wave * LOADS + j;
+            // K block b: keys 4b .. 4b+3, lane -> (key, physical chunk).
+            unsigned key = 4 * b + lane / 16, phys = lane % 16;
+            unsigned row = min(key0 + key, a.seq - 1);
+            const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
+            // V^T block b: channels 8b .. 8b+7.
+            unsigned d = 8 * b + lane / 8, vph = lane % 8;
+            unsigned col = min(key0, a.padded - BN);
+            const uint16_t *vsrc = vth + (size_t)d * a.padded + col + v_chunk(d, vph) * 8;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vsrc,
+                                             (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
         }
     };
 
-    if (count) {
-        load_tile(SPARSE ? list[0] : 0);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (unsigned it = 0; it < count; it++) {
-        const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        const bool more = it + 1 < count;
-        if (more) load_tile(SPARSE ? list[it + 1] : it + 1);
-
-        const uint16_t *ks = smem + cur * STAGE_ELEMS;
-        const uint16_t *vs = ks + K_ELEMS;
-
-        // S^T[mb][nb]: 32 keys x 32 queries.
+    // One key tile: scores, online softmax, P.V. MASKED handles keys >= seq.
+    auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile) {
+        const bool MASKED = tile * BN + BN > a.seq;
         f32x16 s[2][2];
 #pragma unroll
         for (int mb = 0; mb < 2; mb++)
@@ -165,13 +191,14 @@ void attn_bf16_kernel(Args a) {
         for (int kstep = 0; kstep < 8; kstep++) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
-                bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + (mb * 32 + n) * K_STRIDE + kstep * 16 + hf * 8);
+                const unsigned key = mb * 32 + n;
+                bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, kstep * 2 + hf) * 16);
 #pragma unroll
                 for (int nb = 0; nb < 2; nb++)
                     s[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[nb][kstep], s[mb][nb], 0, 0, 0);
             }
         }
-        if (tile * BN + BN > a.seq) {
+        if (MASKED) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
@@ -180,47 +207,61 @@ void attn_bf16_kernel(Args a) {
                     if (key >= a.seq) { s[mb][0][r] = -INFINITY; s[mb][1][r] = -INFINITY; }
                 }
         }
-
-        // Online softmax in the log2 domain; P rounded to BF16 as the PV operand.
         bf16x8 pb[2][4];
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
-            float mx = -INFINITY;
+            float mx = fmaxf(s[0][nb][0], s[1][nb][0]);
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
+            for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s[0][nb][r], s[1][nb][r]));
+            mx = half_max(mx) * c;
+            // Raise the running max only when this tile exceeds it by the slack.
+            if (__builtin_amdgcn_ballot_w64(mx > m[nb] + RESCALE_SLACK)) {
+                const float mnew = fmaxf(m[nb], mx);
+                const float alpha = exp2f_fast(m[nb] - mnew);
+                m[nb] = mnew;
+                l[nb] *= alpha;
 #pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[mb][nb][r]);
-            mx = fmaxf(mx, half_swap(mx));
-            const float mnew = fmaxf(m[nb], mx * a.scale_log2);
-            const float alpha = exp2f_fast(m[nb] - mnew);
-            m[nb] = mnew;
+                for (int md = 0; md < 4; md++) o[md][nb] *= alpha;
+            }
+            const float neg = -m[nb];
             float psum = 0.f;
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float p = exp2f_fast(fmaf(s[mb][nb][r], a.scale_log2, -mnew));
-                    psum += p;
-                    pb[nb][mb * 2 + r / 8][r % 8] = (__bf16)p;
+                for (int r = 0; r < 16; r += 2) {
+                    float p0 = exp2f_fast(fmaf(s[mb][nb][r], c, neg));
+                    float p1 = exp2f_fast(fmaf(s[mb][nb][r + 1], c, neg));
+                    psum += p0 + p1;
+                    pb[nb][mb * 2 + r / 8][r % 8] = (__bf16)p0;
+                    pb[nb][mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
                 }
-            l[nb] = fmaf(l[nb], alpha, psum);
-#pragma unroll
-            for (int md = 0; md < 4; md++) o[md][nb] *= alpha;
+            l[nb] += psum;
         }
-
         // O^T[md][nb] += V^T[md] P^T[nb]: 32 channels x 32 queries, 4 k-steps of 16 keys.
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
 #pragma unroll
             for (int md = 0; md < 4; md++) {
-                bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + (md * 32 + n) * V_STRIDE + kk * 16 + hf * 8);
+                const unsigned d = md * 32 + n;
+                bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, kk * 2 + hf) * 16);
 #pragma unroll
                 for (int nb = 0; nb < 2; nb++)
                     o[md][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[nb][kk], o[md][nb], 0, 0, 0);
             }
         }
+    };
 
-        if (more) store_tile(cur ^ 1);
+    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    wait_vm_loads();
+    __syncthreads();
+
+    for (unsigned it = 0; it < count; it++) {
+        const int cur = it & 1;
+        const unsigned tile = SPARSE ? list[it] : it;
+        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        const uint8_t *ks = smem + cur * STAGE_BYTES;
+        process(ks, ks + K_BYTES, tile);
+        wait_vm_loads();
         __syncthreads();
     }
 
@@ -228,7 +269,7 @@ void attn_bf16_kernel(Args a) {
     bool bad = false;
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-        const float total = l[nb] + half_swap(l[nb]);
+        const float total = half_sum(l[nb]);
         const float inv = total > 0.f ? 1.f / total : 0.f;
         const unsigned q = q0 + wave * 64 + nb * 32 + n;
         if (q >= a.seq) continue;
@@ -241,7 +282,7 @@ void attn_bf16_kernel(Args a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     float x = o[md][nb][g4 * 4 + i] * inv;
-                    bad |= !__builtin_isfinite(x);
+                    bad |= !finite_f32(x);
                     w[i] = f32_to_bf16(x);
                 }
                 *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
@@ -252,7 +293,7 @@ void attn_bf16_kernel(Args a) {
 
 template <int WAVES, bool SPARSE>
 int launch(h3_gpu *g, const Args &a, unsigned groups) {
-    constexpr size_t shared = 2 * STAGE_ELEMS * sizeof(uint16_t);
+    constexpr size_t shared = 2 * STAGE_BYTES;
     static bool configured = false;
     auto kernel = attn_bf16_kernel<WAVES, SPARSE>;
     if (!configured) {
@@ -267,17 +308,23 @@ int launch(h3_gpu *g, const Args &a, unsigned groups) {
 
 }  // namespace
 
-unsigned h3_attention_query_block(bool sparse) { return sparse ? 128u : 256u; }
+size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads) {
+    return (size_t)heads * D * ((seq + 63) / 64 * 64) * sizeof(uint16_t);
+}
 
-int h3_launch_attention_bf16(h3_gpu *g, uint16_t *out, const uint16_t *q, const uint16_t *k, const uint16_t *v,
-                             uint32_t seq, uint32_t heads, float scale, bool head_major,
+int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                             const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
                              const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride) {
     Args a;
-    a.out = out; a.q = q; a.k = k; a.v = v; a.seq = seq; a.heads = heads;
+    a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
+    a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride;
     a.fault = g->fault;
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+                       seq, heads, a.padded, g->fault);
+    if (!h3_launch_status(g, "V transpose")) return 0;
     if (kv_list) {
         unsigned nqb = (seq + 127) / 128;
         return launch<2, true>(g, a, nqb * heads);

@@ -34,6 +34,39 @@ __host__ __device__ inline uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Finite test on the bit pattern. The library is built with relaxed NaN
+// semantics, so the bits pass through an opaque step that keeps the compiler
+// from turning the test back into a floating-point compare it may fold.
+__host__ __device__ inline bool finite_f32(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+#ifdef __HIP_DEVICE_COMPILE__
+    asm volatile("" : "+v"(u));
+#else
+    volatile uint32_t opaque = u;
+    u = opaque;
+#endif
+    return (u & 0x7f800000u) != 0x7f800000u;
+}
+
+// Non-finite test on raw BF16 bits (exponent all ones = Inf or NaN), two
+// values per 32-bit word. Integer-only, so it holds under any FP assumptions.
+__host__ __device__ inline bool bf16x2_nonfinite(uint32_t w) {
+    return ((w & 0x7f80u) == 0x7f80u) | ((w & 0x7f800000u) == 0x7f800000u);
+}
+template <class V>
+__device__ inline bool bf16_vec_nonfinite(const V &v) {
+    static_assert(sizeof(V) % 4 == 0, "vector of BF16 pairs");
+    bool bad = false;
+#pragma unroll
+    for (unsigned i = 0; i < sizeof(V) / 4; i++)
+        bad |= bf16x2_nonfinite(reinterpret_cast<const uint32_t *>(&v)[i]);
+    return bad;
+}
+
+// Wait for this wave's outstanding vector-memory loads, including direct
+// global->LDS loads, before a barrier publishes their LDS contents.
+__device__ inline void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ---------------------------------------------------------------- objects
 struct h3_gpu_tensor {
     h3_gpu *owner;

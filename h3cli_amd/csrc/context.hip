@@ -480,3 +480,17 @@ extern "C" int h3_hip_tensor_read_bytes(const h3_gpu_tensor *t, void *dst, size_
     if (!t || !dst) return 0;
     return read_bytes(t, 0, dst, bytes);
 }
+
+int h3_buffer_reserve(h3_gpu *g, h3_device_buffer *b, size_t bytes, const char *what) {
+    if (b->bytes >= bytes) return 1;
+    if (b->ptr && !h3_hip_check(g, hipStreamSynchronize(g->compute), what)) return 0;
+    h3_buffer_free(b);
+    if (!h3_hip_check(g, hipMalloc(&b->ptr, bytes), what)) { b->ptr = nullptr; return 0; }
+    b->bytes = bytes;
+    return 1;
+}
+
+void h3_buffer_free(h3_device_buffer *b) {
+    if (b->ptr) hipFree(b->ptr);
+    b->ptr = nullptr; b->bytes = 0;
+}

@@ -11,7 +11,16 @@ int h3_tensor_acquire(h3_gpu *g, const h3_gpu_tensor *t);
 int h3_tensor_release(h3_gpu *g, const h3_gpu_tensor *t);
 
 // Launch helpers of the kernel translation units (all enqueue on g->compute).
-int h3_launch_attention_bf16(h3_gpu *g, uint16_t *out, const uint16_t *q, const uint16_t *k,
+size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads);
+int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale,
                              bool head_major, const uint32_t *kv_list, const uint32_t *kv_count,
                              uint32_t list_stride);
+
+// Grow-only device buffer; growing waits for queued work that may read the old one.
+struct h3_device_buffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+int h3_buffer_reserve(h3_gpu *g, h3_device_buffer *b, size_t bytes, const char *what);
+void h3_buffer_free(h3_device_buffer *b);

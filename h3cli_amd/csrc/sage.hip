@@ -81,10 +81,10 @@ __global__ __launch_bounds__(256) void sage_reduce_partials(const uint16_t *k, c
     for (unsigned row = p * PARTIAL_ROWS; row < end; row++) {
         u16x8 kx = *reinterpret_cast<const u16x8 *>(k + row * stride + col);
         u16x8 vx = *reinterpret_cast<const u16x8 *>(v + row * stride + col);
+        bad |= bf16_vec_nonfinite(kx) | bf16_vec_nonfinite(vx);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             float x = bf16_to_f32(kx[e]), y = bf16_to_f32(vx[e]);
-            bad |= !__builtin_isfinite(x) || !__builtin_isfinite(y);
             sum[e] = __fadd_rn(sum[e], x);
             vmax[e] = fmaxf(vmax[e], fabsf(y));
         }
@@ -133,10 +133,10 @@ __global__ __launch_bounds__(256) void sage_quant_int8(const uint16_t *x, const 
     for (int i = 0; i < 4; i++) {
         unsigned row = blk * 64 + r0 + 16 * i;
         u16x8 raw = row < seq ? *reinterpret_cast<const u16x8 *>(x + row * stride + (size_t)head * D + chunk * 8) : u16x8{};
+        if (!KEY) bad |= bf16_vec_nonfinite(raw);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             float f = bf16_to_f32(raw[e]);
-            if (!KEY) bad |= !__builtin_isfinite(f);
             if (KEY && row < seq) f = bf16_to_f32(f32_to_bf16(__fsub_rn(f, mu[e])));
             val[i][e] = f;
             amax = fmaxf(amax, fabsf(f));
@@ -354,7 +354,7 @@ void sage_attn_kernel(SArgs a) {
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[mb][nb][r]);
-            mx = fmaxf(mx, half_swap(mx));
+            mx = half_max(mx);
             const float mnew = fmaxf(m[nb], mx);
             const float alpha = exp2f_fast(m[nb] - mnew);
             m[nb] = mnew;
@@ -393,7 +393,7 @@ void sage_attn_kernel(SArgs a) {
     const float *vsc = a.v_scale + head * D;
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-        const float total = l[nb] + half_swap(l[nb]);
+        const float total = half_sum(l[nb]);
         const float inv = total > 0.f ? 1.f / total : 0.f;
         const unsigned q = q0 + wave * 64 + nb * 32 + n;
         if (q >= a.seq) continue;
@@ -407,7 +407,7 @@ void sage_attn_kernel(SArgs a) {
                 for (int i = 0; i < 4; i++) {
                     unsigned d = md * 32 + g4 * 8 + hf * 4 + i;
                     float x = o[md][nb][g4 * 4 + i] * (vsc[d] * inv);
-                    bad |= !__builtin_isfinite(x);
+                    bad |= !finite_f32(x);
                     w[i] = f32_to_bf16(x);
                 }
                 *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
