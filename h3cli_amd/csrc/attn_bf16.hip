@@ -96,11 +96,15 @@ __global__ __launch_bounds__(256) void transpose_v(const uint16_t *v, const uint
     for (int j = 0; j < 4; j++) *reinterpret_cast<u16x8 *>(dst + j * 8) = w[j];
 }
 
-template <int WAVES, bool SPARSE>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(1, 1)))
+// WAVES wavefronts per workgroup, each owning NB x 32 queries; OCC waves share a
+// SIMD (register budget 512 / OCC), so the hardware overlaps one wave's softmax
+// with another's MFMAs.
+template <int WAVES, int NB, int OCC, bool SPARSE>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(OCC, OCC)))
 void attn_bf16_kernel(Args a) {
     constexpr int T = 64 * WAVES;
-    constexpr int BM = 64 * WAVES;
+    constexpr int BM = 32 * NB * WAVES;
+    constexpr int WQ = 32 * NB;             // queries per wave
     constexpr int LOADS = (K_BYTES / 1024) / WAVES;  // 1 KB direct-to-LDS loads per wave per operand
     static_assert(LOADS * WAVES * 1024 == K_BYTES && K_BYTES == V_BYTES, "tile split");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -127,10 +131,10 @@ void attn_bf16_kernel(Args a) {
     }
 
     // Query fragments: B operand of S^T = K Q^T, 8 k-steps of 16 channels.
-    bf16x8 qf[2][8];
+    bf16x8 qf[NB][8];
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-        unsigned row = q0 + wave * 64 + nb * 32 + n;
+    for (int nb = 0; nb < NB; nb++) {
+        unsigned row = q0 + wave * WQ + nb * 32 + n;
         row = row < a.seq ? row : a.seq - 1;
         const uint16_t *p = qh + (size_t)row * stride + hf * 8;
 #pragma unroll
@@ -139,18 +143,24 @@ void attn_bf16_kernel(Args a) {
     {
         bool bad = false;
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++)
+        for (int nb = 0; nb < NB; nb++)
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) bad |= bf16_vec_nonfinite(qf[nb][ks]);
         if (bad) a.fault[0] = 1u;
     }
 
-    f32x16 o[4][2];
+    f32x16 o[4][NB];
 #pragma unroll
     for (int md = 0; md < 4; md++)
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) o[md][nb] = f32x16{};
-    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
+        for (int nb = 0; nb < NB; nb++) o[md][nb] = f32x16{};
+    float m[NB];
+    f32x16 lsum[NB];                         // every element holds the query's running sum
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) { m[nb] = -1e30f; lsum[nb] = f32x16{}; }
+    bf16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
 
     // Tile loads go straight from global memory to LDS (global_load_lds_dwordx4):
     // each wave instruction fills one contiguous KB, lane i writing bytes
@@ -182,11 +192,11 @@ void attn_bf16_kernel(Args a) {
     // One key tile: scores, online softmax, P.V. MASKED handles keys >= seq.
     auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile) {
         const bool MASKED = tile * BN + BN > a.seq;
-        f32x16 s[2][2];
+        f32x16 s[2][NB];
 #pragma unroll
         for (int mb = 0; mb < 2; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) s[mb][nb] = f32x16{};
+            for (int nb = 0; nb < NB; nb++) s[mb][nb] = f32x16{};
 #pragma unroll
         for (int kstep = 0; kstep < 8; kstep++) {
 #pragma unroll
@@ -194,7 +204,7 @@ void attn_bf16_kernel(Args a) {
                 const unsigned key = mb * 32 + n;
                 bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, kstep * 2 + hf) * 16);
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < NB; nb++)
                     s[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[nb][kstep], s[mb][nb], 0, 0, 0);
             }
         }
@@ -204,38 +214,42 @@ void attn_bf16_kernel(Args a) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
-                    if (key >= a.seq) { s[mb][0][r] = -INFINITY; s[mb][1][r] = -INFINITY; }
+                    if (key >= a.seq) {
+#pragma unroll
+                        for (int nb = 0; nb < NB; nb++) s[mb][nb][r] = -INFINITY;
+                    }
                 }
         }
-        bf16x8 pb[2][4];
+        bf16x8 pb[NB][4];
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            float mx = fmaxf(s[0][nb][0], s[1][nb][0]);
+        for (int nb = 0; nb < NB; nb++) {
+            // Two chains of 3-input maxima over the lane's 32 scores.
+            float mx0 = fmaxf(s[0][nb][0], s[0][nb][1]), mx1 = fmaxf(s[1][nb][0], s[1][nb][1]);
 #pragma unroll
-            for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s[0][nb][r], s[1][nb][r]));
-            mx = half_max(mx) * c;
+            for (int r = 2; r < 16; r += 2) {
+                mx0 = fmaxf(fmaxf(mx0, s[0][nb][r]), s[0][nb][r + 1]);
+                mx1 = fmaxf(fmaxf(mx1, s[1][nb][r]), s[1][nb][r + 1]);
+            }
+            const float mx = half_max(fmaxf(mx0, mx1)) * c;
             // Raise the running max only when this tile exceeds it by the slack.
             if (__builtin_amdgcn_ballot_w64(mx > m[nb] + RESCALE_SLACK)) {
                 const float mnew = fmaxf(m[nb], mx);
                 const float alpha = exp2f_fast(m[nb] - mnew);
                 m[nb] = mnew;
-                l[nb] *= alpha;
+                lsum[nb] *= alpha;
 #pragma unroll
                 for (int md = 0; md < 4; md++) o[md][nb] *= alpha;
             }
             const float neg = -m[nb];
-            float psum = 0.f;
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
                     float p0 = exp2f_fast(fmaf(s[mb][nb][r], c, neg));
                     float p1 = exp2f_fast(fmaf(s[mb][nb][r + 1], c, neg));
-                    psum += p0 + p1;
                     pb[nb][mb * 2 + r / 8][r % 8] = (__bf16)p0;
                     pb[nb][mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
                 }
-            l[nb] += psum;
         }
         // O^T[md][nb] += V^T[md] P^T[nb]: 32 channels x 32 queries, 4 k-steps of 16 keys.
 #pragma unroll
@@ -245,9 +259,14 @@ void attn_bf16_kernel(Args a) {
                 const unsigned d = md * 32 + n;
                 bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, kk * 2 + hf) * 16);
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < NB; nb++)
                     o[md][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[nb][kk], o[md][nb], 0, 0, 0);
             }
+            // Row sums of the BF16 P actually multiplied into V, on the matrix
+            // core: ones(32 x 16) . P^T gives every row the 16-key sum per query.
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                lsum[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[nb][kk], lsum[nb], 0, 0, 0);
         }
     };
 
@@ -268,10 +287,10 @@ void attn_bf16_kernel(Args a) {
     // Normalize and store. Lane holds query column n, channels (r/4)*8 + hf*4 + r%4.
     bool bad = false;
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-        const float total = half_sum(l[nb]);
+    for (int nb = 0; nb < NB; nb++) {
+        const float total = lsum[nb][0];
         const float inv = total > 0.f ? 1.f / total : 0.f;
-        const unsigned q = q0 + wave * 64 + nb * 32 + n;
+        const unsigned q = q0 + wave * WQ + nb * 32 + n;
         if (q >= a.seq) continue;
         uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
 #pragma unroll
@@ -291,11 +310,11 @@ void attn_bf16_kernel(Args a) {
     if (bad) a.fault[0] = 1u;
 }
 
-template <int WAVES, bool SPARSE>
+template <int WAVES, int NB, int OCC, bool SPARSE>
 int launch(h3_gpu *g, const Args &a, unsigned groups) {
     constexpr size_t shared = 2 * STAGE_BYTES;
     static bool configured = false;
-    auto kernel = attn_bf16_kernel<WAVES, SPARSE>;
+    auto kernel = attn_bf16_kernel<WAVES, NB, OCC, SPARSE>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
                           "attention shared memory"))
@@ -325,10 +344,8 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
-    if (kv_list) {
-        unsigned nqb = (seq + 127) / 128;
-        return launch<2, true>(g, a, nqb * heads);
-    }
-    unsigned nqb = (seq + 255) / 256;
-    return launch<4, false>(g, a, nqb * heads);
+    // Sparse lists are per 128-query block: 4 waves per workgroup, two
+    // workgroups per CU. Dense: 8 waves x 32 queries, two waves per SIMD.
+    if (kv_list) return launch<4, 1, 2, true>(g, a, (seq + 127) / 128 * heads);
+    return launch<8, 1, 2, false>(g, a, (seq + 255) / 256 * heads);
 }

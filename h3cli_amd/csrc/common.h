@@ -103,6 +103,9 @@ struct h3_gpu {
     std::mutex copy_mutex;
     // optional event timing of attention / linear dispatches (H3_PROFILE)
     bool profiling;
+    // Kernel-shape selector for measurement (H3_HIP_ATTENTION_VARIANT): 0 is the
+    // default shape, other values pick the alternatives each kernel documents.
+    int attention_variant;
 };
 
 // ---------------------------------------------------------------- helpers
