@@ -99,14 +99,15 @@ __global__ __launch_bounds__(256) void transpose_v(const uint16_t *v, const uint
 // WAVES wavefronts per workgroup, each owning NB x 32 queries; OCC waves share a
 // SIMD (register budget 512 / OCC), so the hardware overlaps one wave's softmax
 // with another's MFMAs.
-template <int WAVES, int NB, int OCC, bool SPARSE>
+// MSUM: row sums of P on the matrix core (ones . P^T) instead of VALU adds.
+template <int WAVES, int NB, int OCC, bool SPARSE, bool MSUM>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(OCC, OCC)))
 void attn_bf16_kernel(Args a) {
     constexpr int T = 64 * WAVES;
     constexpr int BM = 32 * NB * WAVES;
     constexpr int WQ = 32 * NB;             // queries per wave
-    constexpr int LOADS = (K_BYTES / 1024) / WAVES;  // 1 KB direct-to-LDS loads per wave per operand
-    static_assert(LOADS * WAVES * 1024 == K_BYTES && K_BYTES == V_BYTES, "tile split");
+    constexpr int BLOCKS = K_BYTES / 1024;  // 1 KB direct-to-LDS load blocks per operand tile
+    static_assert(K_BYTES == V_BYTES, "tile split");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -154,10 +155,12 @@ void attn_bf16_kernel(Args a) {
     for (int md = 0; md < 4; md++)
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) o[md][nb] = f32x16{};
-    float m[NB];
-    f32x16 lsum[NB];                         // every element holds the query's running sum
+    float m[NB], l[NB];
+    f32x16 lsum[MSUM ? NB : 1];              // MSUM: every element holds the query's running sum
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) { m[nb] = -1e30f; lsum[nb] = f32x16{}; }
+    for (int nb = 0; nb < NB; nb++) { m[nb] = -1e30f; l[nb] = 0.f; }
+#pragma unroll
+    for (int nb = 0; nb < (MSUM ? NB : 1); nb++) lsum[nb] = f32x16{};
     bf16x8 ones;
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
@@ -172,8 +175,7 @@ void attn_bf16_kernel(Args a) {
         uint8_t *ks = smem + stage * STAGE_BYTES;
         uint8_t *vs = ks + K_BYTES;
 #pragma unroll
-        for (int j = 0; j < LOADS; j++) {
-            const unsigned b = wave * LOADS + j;
+        for (unsigned b = wave; b < BLOCKS; b += WAVES) {
             // K block b: keys 4b .. 4b+3, lane -> (key, physical chunk).
             unsigned key = 4 * b + lane / 16, phys = lane % 16;
             unsigned row = min(key0 + key, a.seq - 1);
@@ -236,20 +238,24 @@ void attn_bf16_kernel(Args a) {
                 const float mnew = fmaxf(m[nb], mx);
                 const float alpha = exp2f_fast(m[nb] - mnew);
                 m[nb] = mnew;
-                lsum[nb] *= alpha;
+                if constexpr (MSUM) lsum[nb] *= alpha;
+                else l[nb] *= alpha;
 #pragma unroll
                 for (int md = 0; md < 4; md++) o[md][nb] *= alpha;
             }
             const float neg = -m[nb];
+            float psum = 0.f;
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
                     float p0 = exp2f_fast(fmaf(s[mb][nb][r], c, neg));
                     float p1 = exp2f_fast(fmaf(s[mb][nb][r + 1], c, neg));
+                    if constexpr (!MSUM) psum += p0 + p1;
                     pb[nb][mb * 2 + r / 8][r % 8] = (__bf16)p0;
                     pb[nb][mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
                 }
+            if constexpr (!MSUM) l[nb] += psum;
         }
         // O^T[md][nb] += V^T[md] P^T[nb]: 32 channels x 32 queries, 4 k-steps of 16 keys.
 #pragma unroll
@@ -264,9 +270,11 @@ void attn_bf16_kernel(Args a) {
             }
             // Row sums of the BF16 P actually multiplied into V, on the matrix
             // core: ones(32 x 16) . P^T gives every row the 16-key sum per query.
+            if constexpr (MSUM) {
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++)
-                lsum[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[nb][kk], lsum[nb], 0, 0, 0);
+                for (int nb = 0; nb < NB; nb++)
+                    lsum[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[nb][kk], lsum[nb], 0, 0, 0);
+            }
         }
     };
 
@@ -288,7 +296,7 @@ void attn_bf16_kernel(Args a) {
     bool bad = false;
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        const float total = lsum[nb][0];
+        const float total = MSUM ? lsum[nb][0] : half_sum(l[nb]);
         const float inv = total > 0.f ? 1.f / total : 0.f;
         const unsigned q = q0 + wave * WQ + nb * 32 + n;
         if (q >= a.seq) continue;
@@ -310,11 +318,11 @@ void attn_bf16_kernel(Args a) {
     if (bad) a.fault[0] = 1u;
 }
 
-template <int WAVES, int NB, int OCC, bool SPARSE>
+template <int WAVES, int NB, int OCC, bool SPARSE, bool MSUM>
 int launch(h3_gpu *g, const Args &a, unsigned groups) {
     constexpr size_t shared = 2 * STAGE_BYTES;
     static bool configured = false;
-    auto kernel = attn_bf16_kernel<WAVES, NB, OCC, SPARSE>;
+    auto kernel = attn_bf16_kernel<WAVES, NB, OCC, SPARSE, MSUM>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
                           "attention shared memory"))
@@ -346,6 +354,7 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     if (!h3_launch_status(g, "V transpose")) return 0;
     // Sparse lists are per 128-query block: 4 waves per workgroup, two
     // workgroups per CU. Dense: 8 waves x 32 queries, two waves per SIMD.
-    if (kv_list) return launch<4, 1, 2, true>(g, a, (seq + 127) / 128 * heads);
-    return launch<8, 1, 2, false>(g, a, (seq + 255) / 256 * heads);
+    if (kv_list) return launch<4, 1, 2, true, true>(g, a, (seq + 127) / 128 * heads);
+    if (g->attention_variant == 2) return launch<12, 1, 3, false, false>(g, a, (seq + 383) / 384 * heads);
+    return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
 }

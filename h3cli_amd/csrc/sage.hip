@@ -24,11 +24,6 @@ namespace {
 constexpr int D = 128;
 constexpr int BN = 64;
 constexpr unsigned PARTIAL_ROWS = 256;     // rows per partial K sum
-constexpr int K8_STRIDE = D + 16;          // LDS bytes per K row
-constexpr int V8_STRIDE = BN + 16;         // LDS bytes per transposed V row
-constexpr int K8_BYTES = BN * K8_STRIDE;
-constexpr int V8_BYTES = D * V8_STRIDE;
-constexpr int SAGE_STAGE = K8_BYTES + V8_BYTES;
 constexpr float LOG2_448 = 8.807354922057604f;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -233,14 +228,24 @@ struct SArgs {
     unsigned *fault;
 };
 
-template <int WAVES, bool SPARSE>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(1, 1)))
+constexpr int Q8_TILE = BN * D;             // K8 tile bytes: 64 rows x 128 B
+constexpr int V8_TILE = D * BN;             // V8 tile bytes: 128 rows x 64 B
+constexpr int SAGE_TILE = Q8_TILE + V8_TILE;
+constexpr float P_SLACK = 2.0f;             // log2 units the running max may lag (P <= 448)
+
+// 16-byte chunk swizzles of the LDS tiles: each 16-lane group of a
+// ds_read_b128 hits 16 distinct 4-bank groups.
+__device__ inline unsigned k8_chunk(unsigned key, unsigned ch) { return ch ^ ((key >> 1) & 7); }
+__device__ inline unsigned v8_chunk(unsigned d, unsigned ch) { return ch ^ ((d >> 2) & 3); }
+
+// WAVES wavefronts of 32 queries; OCC waves per SIMD overlap softmax with MFMA.
+template <int WAVES, int OCC, bool SPARSE>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(OCC, OCC)))
 void sage_attn_kernel(SArgs a) {
-    constexpr int T = 64 * WAVES, BM = 64 * WAVES;
-    constexpr int KC = (BN * D / 16) / T;        // 16-byte K8 chunks per thread
-    constexpr int VC = (D * BN / 16) / T;        // 16-byte V8 chunks per thread
-    static_assert(KC * T == BN * D / 16 && VC * T == D * BN / 16, "tile split");
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int BM = 32 * WAVES;
+    constexpr int BLOCKS = Q8_TILE / 1024;  // 1 KB load blocks per operand tile
+    static_assert(Q8_TILE == V8_TILE, "tile split");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n = lane % 32, hf = lane / 32;
     const unsigned nqb = (a.seq + BM - 1) / BM;
@@ -256,147 +261,126 @@ void sage_attn_kernel(SArgs a) {
     if constexpr (SPARSE) { count = a.kv_count[qb]; list = a.kv_list + (size_t)qb * a.list_stride; }
     else count = ntiles;
 
-    i32x4 qf[2][4];
+    // Query fragments (B operand of S^T = K Q^T): 4 k-steps of 32 channels.
+    i32x4 qf[4];
+    const unsigned qrow = min(q0 + wave * 32 + n, a.padded - 1);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-        unsigned row = min(q0 + wave * 64 + nb * 32 + n, a.padded - 1);
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) qf[nb][ks] = *reinterpret_cast<const i32x4 *>(qh + (size_t)row * D + ks * 32 + hf * 16);
-    }
-    const unsigned qblk = min((q0 + wave * 64) / 64, a.blocks - 1);
+    for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const i32x4 *>(qh + (size_t)qrow * D + ks * 32 + hf * 16);
+    const unsigned qblk = min((q0 + wave * 32) / 64, a.blocks - 1);
     const float qs = a.q_scale[head * a.blocks + qblk] * a.scale_log2;
 
-    f32x16 o[4][2];
+    f32x16 o[4];
 #pragma unroll
-    for (int md = 0; md < 4; md++)
+    for (int md = 0; md < 4; md++) o[md] = f32x16{};
+    f32x16 lsum = f32x16{};                 // every element holds the query's running sum of P
+    float m = -1e30f;
+    i32x8 ones;                              // fp8 e4m3 1.0 = 0x38
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) o[md][nb] = f32x16{};
-    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
+    for (int i = 0; i < 8; i++) ones[i] = 0x38383838;
 
-    i32x4 rk[KC], rv[VC];
-    auto load_tile = [&](unsigned tile) {
-        const bool ok = tile < ntiles;
+    // Direct global->LDS tile loads, one contiguous KB per wave instruction.
+    auto load_tile = [&](unsigned tile, int stage) {
+        const unsigned t = min(tile, ntiles - 1);
+        uint8_t *ks = lds + stage * SAGE_TILE;
+        uint8_t *vs = ks + Q8_TILE;
 #pragma unroll
-        for (int j = 0; j < KC; j++) {
-            unsigned c = tid + T * j, row = c / 8, ch = c % 8;
-            rk[j] = ok ? *reinterpret_cast<const i32x4 *>(kh + ((size_t)tile * BN + row) * D + ch * 16) : i32x4{};
-        }
-#pragma unroll
-        for (int j = 0; j < VC; j++) {
-            unsigned c = tid + T * j, d = c / 4, ch = c % 4;
-            rv[j] = ok ? *reinterpret_cast<const i32x4 *>(vh + (size_t)d * a.padded + (size_t)tile * BN + ch * 16) : i32x4{};
-        }
-    };
-    auto store_tile = [&](int stage) {
-        uint8_t *ks = lds + stage * SAGE_STAGE;
-        uint8_t *vs = ks + K8_BYTES;
-#pragma unroll
-        for (int j = 0; j < KC; j++) {
-            unsigned c = tid + T * j, row = c / 8, ch = c % 8;
-            *reinterpret_cast<i32x4 *>(ks + row * K8_STRIDE + ch * 16) = rk[j];
-        }
-#pragma unroll
-        for (int j = 0; j < VC; j++) {
-            unsigned c = tid + T * j, d = c / 4, ch = c % 4;
-            *reinterpret_cast<i32x4 *>(vs + d * V8_STRIDE + ch * 16) = rv[j];
+        for (unsigned b = wave; b < BLOCKS; b += WAVES) {
+            unsigned key = 8 * b + lane / 8, ph = lane % 8;
+            const int8_t *src = kh + ((size_t)t * BN + key) * D + k8_chunk(key, ph) * 16;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
+            unsigned d = 16 * b + lane / 4, vp = lane % 4;
+            const uint8_t *vsrc = vh + (size_t)d * a.padded + (size_t)t * BN + v8_chunk(d, vp) * 16;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vsrc,
+                                             (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
         }
     };
 
-    if (count) { load_tile(SPARSE ? list[0] : 0); store_tile(0); }
-    __syncthreads();
-
-    for (unsigned it = 0; it < count; it++) {
-        const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        const bool more = it + 1 < count;
-        if (more) load_tile(SPARSE ? list[it + 1] : it + 1);
-        const uint8_t *ks = lds + cur * SAGE_STAGE;
-        const uint8_t *vs = ks + K8_BYTES;
-
-        i32x16 si[2][2];
-#pragma unroll
-        for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-            for (int nb = 0; nb < 2; nb++) si[mb][nb] = i32x16{};
+    auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile) {
+        i32x16 si[2];
+        si[0] = i32x16{}; si[1] = i32x16{};
 #pragma unroll
         for (int kstep = 0; kstep < 4; kstep++) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
-                i32x4 kf = *reinterpret_cast<const i32x4 *>(ks + (mb * 32 + n) * K8_STRIDE + kstep * 32 + hf * 16);
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++)
-                    si[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[nb][kstep], si[mb][nb], 0, 0, 0);
+                const unsigned key = mb * 32 + n;
+                i32x4 kf = *reinterpret_cast<const i32x4 *>(ks + key * D + k8_chunk(key, kstep * 2 + hf) * 16);
+                si[mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kstep], si[mb], 0, 0, 0);
             }
         }
         const float c = qs * a.k_scale[head * a.blocks + min(tile, a.blocks - 1)];
-        f32x16 s[2][2];
-#pragma unroll
-        for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[mb][nb][r] = (float)si[mb][nb][r] * c;
-        if (tile * BN + BN > a.seq) {
+        const bool masked = tile * BN + BN > a.seq;
+        if (masked) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
-                    if (key >= a.seq) { s[mb][0][r] = -INFINITY; s[mb][1][r] = -INFINITY; }
+                    if (key >= a.seq) si[mb][r] = INT32_MIN / 2;
                 }
         }
-
-        i32x8 pf[2];
+        // Integer row max (3-input), then one scale.
+        int mi0 = max(si[0][0], si[0][1]), mi1 = max(si[1][0], si[1][1]);
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[mb][nb][r]);
-            mx = half_max(mx);
-            const float mnew = fmaxf(m[nb], mx);
-            const float alpha = exp2f_fast(m[nb] - mnew);
-            m[nb] = mnew;
-            const float bias = LOG2_448 - mnew;
-            float psum = 0.f;
-            float p[32];
-#pragma unroll
-            for (int i = 0; i < 32; i++) {
-                p[i] = exp2f_fast(s[i / 16][nb][i % 16] + bias);
-                psum += p[i];
-            }
-#pragma unroll
-            for (int w = 0; w < 8; w++) {
-                int packed = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * w], p[4 * w + 1], 0, false);
-                packed = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * w + 2], p[4 * w + 3], packed, true);
-                pf[nb][w] = packed;
-            }
-            l[nb] = fmaf(l[nb], alpha, psum);
-#pragma unroll
-            for (int md = 0; md < 4; md++) o[md][nb] *= alpha;
+        for (int r = 2; r < 16; r += 2) {
+            mi0 = max(max(mi0, si[0][r]), si[0][r + 1]);
+            mi1 = max(max(mi1, si[1][r]), si[1][r + 1]);
         }
-
+        const float mx = half_max((float)max(mi0, mi1)) * c;
+        if (__builtin_amdgcn_ballot_w64(mx > m + P_SLACK)) {
+            const float mnew = fmaxf(m, mx);
+            const float alpha = exp2f_fast(m - mnew);
+            m = mnew;
+            lsum *= alpha;
+#pragma unroll
+            for (int md = 0; md < 4; md++) o[md] *= alpha;
+        }
+        // P = 2^(s - m + log2 448 - slack) <= 448, rounded to fp8 e4m3. Masked
+        // keys (huge negative score) give exactly 0.
+        const float bias = LOG2_448 - P_SLACK - m;
+        i32x8 pf;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int idx = 4 * w + i;
+                p[i] = exp2f_fast(fmaf((float)si[idx / 16][idx % 16], c, bias));
+            }
+            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false);
+            pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], packed, true);
+        }
+        // O^T[md] += V^T[md] P^T (fp8, K = 64 keys); row sums from ones . P^T.
 #pragma unroll
         for (int md = 0; md < 4; md++) {
-            i32x8 vf = *reinterpret_cast<const i32x8 *>(vs + (md * 32 + n) * V8_STRIDE + hf * 32);
-#pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-                o[md][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf[nb], o[md][nb], 0, 0, 0, 0, 0, 0);
+            const unsigned d = md * 32 + n;
+            i32x4 lo = *reinterpret_cast<const i32x4 *>(vs + d * BN + v8_chunk(d, hf * 2) * 16);
+            i32x4 hi = *reinterpret_cast<const i32x4 *>(vs + d * BN + v8_chunk(d, hf * 2 + 1) * 16);
+            i32x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[md] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[md], 0, 0, 0, 0, 0, 0);
         }
+        lsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, lsum, 0, 0, 0, 0, 0, 0);
+    };
 
-        if (more) store_tile(cur ^ 1);
+    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    wait_vm_loads();
+    __syncthreads();
+    for (unsigned it = 0; it < count; it++) {
+        const int cur = it & 1;
+        const unsigned tile = SPARSE ? list[it] : it;
+        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        const uint8_t *ks = lds + cur * SAGE_TILE;
+        process(ks, ks + Q8_TILE, tile);
+        wait_vm_loads();
         __syncthreads();
     }
 
     bool bad = false;
     const float *vsc = a.v_scale + head * D;
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-        const float total = half_sum(l[nb]);
-        const float inv = total > 0.f ? 1.f / total : 0.f;
-        const unsigned q = q0 + wave * 64 + nb * 32 + n;
-        if (q >= a.seq) continue;
+    const float total = lsum[0];
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const unsigned q = q0 + wave * 32 + n;
+    if (q < a.seq) {
         uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
 #pragma unroll
         for (int md = 0; md < 4; md++)
@@ -406,7 +390,7 @@ void sage_attn_kernel(SArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     unsigned d = md * 32 + g4 * 8 + hf * 4 + i;
-                    float x = o[md][nb][g4 * 4 + i] * (vsc[d] * inv);
+                    float x = o[md][g4 * 4 + i] * (vsc[d] * inv);
                     bad |= !finite_f32(x);
                     w[i] = f32_to_bf16(x);
                 }
@@ -416,10 +400,10 @@ void sage_attn_kernel(SArgs a) {
     if (bad) a.fault[0] = 1u;
 }
 
-template <int WAVES, bool SPARSE>
+template <int WAVES, int OCC, bool SPARSE>
 int launch_sage(h3_gpu *g, const SArgs &a, unsigned groups) {
-    constexpr size_t shared = 2 * SAGE_STAGE;
-    hipLaunchKernelGGL((sage_attn_kernel<WAVES, SPARSE>), dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
+    constexpr size_t shared = 2 * SAGE_TILE;
+    hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE>), dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
     return h3_launch_status(g, "Sage attention");
 }
 }  // namespace
@@ -445,8 +429,10 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride; a.fault = g->fault;
-    if (kv_list) return launch_sage<2, true>(g, a, (seq + 127) / 128 * heads);
-    return launch_sage<4, false>(g, a, (seq + 255) / 256 * heads);
+    if (kv_list) return launch_sage<4, 2, true>(g, a, (seq + 127) / 128 * heads);
+    // 12 waves x 32 queries: three waves per SIMD (166 VGPRs each).
+    if (g->attention_variant == 1) return launch_sage<8, 2, false>(g, a, (seq + 255) / 256 * heads);
+    return launch_sage<12, 3, false>(g, a, (seq + 383) / 384 * heads);
 }
 
 extern "C" unsigned h3_hip_sage_v_position(unsigned j) { return sage_v_position(j & 63); }
