@@ -61,7 +61,25 @@ _SIGNATURES = {
     "h3_gpu_dit_attention_noise": (_i, [_p, _i, _f, _f]),
     "h3_gpu_sdpa_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f]),
     "h3_gpu_sdpa_bf16_head_major_output": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f]),
+    # DiT block operators
+    "h3_gpu_linear_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32]),
+    "h3_gpu_mlp_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _u32]),
+    "h3_gpu_swiglu_bf16": (_i, [_p, _p, _p, _u32, _u32]),
+    "h3_gpu_gelu_bf16": (_i, [_p, _p, _p, _u32, _i]),
+    "h3_gpu_adaln_bf16": (_i, [_p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _f]),
+    "h3_gpu_gate_bf16": (_i, [_p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32]),
+    "h3_gpu_gate_adaln_bf16": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _u32, _f]),
+    "h3_gpu_qkv_rope_bf16": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _f]),
+    "h3_gpu_grouped_qkv_rope_bf16": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _f]),
+    "h3_gpu_grouped_qkv_linear_rope_bf16": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32,
+                                                 _u32, _f]),
+    "h3_gpu_euler_bf16": (_i, [_p, _p, _sz, _p, _p, _u32, _f, _f]),
+    "h3_gpu_quant_configure": (_i, [_p, _i, C.c_char_p, C.c_uint64, C.c_uint64, _i]),
+    "h3_gpu_quant_load": (_p, [_p, C.c_char_p, C.c_uint64, _u32, _u32]),
+    "h3_gpu_q8_load": (_p, [_p, C.c_char_p, C.c_uint64, _u32, _u32]),
     # extensions
+    "h3_hip_q8_from_packed": (_p, [_p, _p, _p, _u32, _u32, _u32]),
+    "h3_hip_linear_gelu_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32]),
     "h3_hip_version": (C.c_char_p, []),
     "h3_hip_dit_block_mask": (_i, [_p, _p, _u32, _u32, _u32]),
     "h3_hip_sage_pack": (_i, [_p, _p, _p, _p, _u32, _u32, _p, _p, _p, _p, _p, _p, _p]),

@@ -1,0 +1,342 @@
+// DiT block elementwise operators for gfx950: AdaLN-modulated RMSNorm, gates,
+// Q/K RMSNorm + rotate-half RoPE split, GELU, SwiGLU and the Euler update.
+// Arithmetic follows the reference kernels (src/cuda/cuda_kernels.cuh:879-1059,
+// 1242-1254); these are HBM-bound, so every kernel moves 16-byte vectors and
+// keeps a row (or a head) in registers between its reduction and its output.
+#include "common.h"
+#include "internal.h"
+#include <cmath>
+
+namespace {
+
+constexpr int MAX_CHUNKS = 16;  // 8-element chunks per lane: rows up to 64*16*8 = 8192 wide
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ inline void unpack8(const u16x8 &r, float *f) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) f[e] = bf16_to_f32(r[e]);
+}
+
+struct AdaLNArgs {
+    uint16_t *out;          // AdaLN output
+    uint16_t *gated;        // gate_adaln: gated residual output (nullptr for plain AdaLN)
+    const uint16_t *x;      // AdaLN input, or the residual for gate_adaln
+    const uint16_t *branch; // gate_adaln branch
+    const uint16_t *weight, *mod, *gate_mod;
+    const uint32_t *row_map;
+    unsigned rows, width, slots, shift_slot, scale_slot, gate_slot;
+    float eps;
+};
+
+// One wave per row. With GATE, the row is first gated (residual + branch * gate,
+// rounded to BF16 and stored) and the AdaLN then normalizes that BF16 row, as the
+// reference's two-kernel composition does (src/cuda/gpu_cuda.cu:1118-1120).
+template <bool GATE>
+__global__ __launch_bounds__(256) void adaln_kernel(AdaLNArgs a) {
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const unsigned row = blockIdx.x * 4 + wave;
+    if (row >= a.rows) return;
+    const unsigned chunks = a.width / 8;
+    const size_t base = (size_t)row * a.width;
+    const size_t mbase = (size_t)a.row_map[row] * a.slots * a.width;
+    float v[MAX_CHUNKS][8];
+    float sumsq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAX_CHUNKS; i++) {
+        unsigned c = lane + 64 * i;
+        if (c >= chunks) break;
+        u16x8 xr = *reinterpret_cast<const u16x8 *>(a.x + base + c * 8);
+        unpack8(xr, v[i]);
+        if constexpr (GATE) {
+            u16x8 br = *reinterpret_cast<const u16x8 *>(a.branch + base + c * 8);
+            u16x8 gr = *reinterpret_cast<const u16x8 *>(a.gate_mod + mbase + (size_t)a.gate_slot * a.width + c * 8);
+            u16x8 outr;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                outr[e] = f32_to_bf16(fmaf(bf16_to_f32(br[e]), bf16_to_f32(gr[e]), v[i][e]));
+                v[i][e] = bf16_to_f32(outr[e]);
+            }
+            *reinterpret_cast<u16x8 *>(a.gated + base + c * 8) = outr;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) sumsq = fmaf(v[i][e], v[i][e], sumsq);
+    }
+    const float inv = rsqrtf(wave_sum(sumsq) / (float)a.width + a.eps);
+#pragma unroll
+    for (int i = 0; i < MAX_CHUNKS; i++) {
+        unsigned c = lane + 64 * i;
+        if (c >= chunks) break;
+        u16x8 wr = *reinterpret_cast<const u16x8 *>(a.weight + c * 8);
+        u16x8 sh = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.shift_slot * a.width + c * 8);
+        u16x8 sc = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.scale_slot * a.width + c * 8);
+        u16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float normalized = v[i][e] * inv * bf16_to_f32(wr[e]);
+            o[e] = f32_to_bf16(fmaf(normalized, 1.0f + bf16_to_f32(sc[e]), bf16_to_f32(sh[e])));
+        }
+        *reinterpret_cast<u16x8 *>(a.out + base + c * 8) = o;
+    }
+}
+
+// out = bf16(residual + branch * gate), 8 elements per thread.
+__global__ __launch_bounds__(256) void gate_kernel(uint16_t *out, const uint16_t *res, const uint16_t *branch,
+                                                  const uint16_t *mod, const uint32_t *row_map, unsigned rows,
+                                                  unsigned width, unsigned slots, unsigned gate_slot) {
+    const size_t chunk = (size_t)blockIdx.x * 256 + threadIdx.x, chunks = (size_t)rows * width / 8;
+    if (chunk >= chunks) return;
+    const size_t at = chunk * 8;
+    const unsigned row = at / width, col = at % width;
+    const size_t g = (size_t)row_map[row] * slots * width + (size_t)gate_slot * width + col;
+    u16x8 r = *reinterpret_cast<const u16x8 *>(res + at), b = *reinterpret_cast<const u16x8 *>(branch + at);
+    u16x8 gv = *reinterpret_cast<const u16x8 *>(mod + g), o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = f32_to_bf16(fmaf(bf16_to_f32(b[e]), bf16_to_f32(gv[e]), bf16_to_f32(r[e])));
+    *reinterpret_cast<u16x8 *>(out + at) = o;
+}
+
+struct QkvArgs {
+    uint16_t *q, *k, *v;
+    const uint16_t *qkv, *qw, *kw, *cos_t, *sin_t;
+    unsigned seq, heads, dim, half;
+    float eps;
+    int grouped;
+};
+
+// One wave per (row, head): optional per-head RMSNorm of Q and K (weights
+// qw/kw; null skips the norm), rotate-half RoPE on the first 2*half channels
+// (pair d <-> d + half, cos/sin [seq, half]), V copied.
+__global__ __launch_bounds__(256) void qkv_rope_kernel(QkvArgs a) {
+    __shared__ float stage[4][2][256];
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const size_t items = (size_t)a.seq * a.heads;
+    const size_t item = min((size_t)blockIdx.x * 4 + wave, items - 1);  // tail waves redo the last item
+    const bool store = (size_t)blockIdx.x * 4 + wave < items;
+    const unsigned row = item / a.heads, head = item % a.heads;
+    const size_t inner = (size_t)a.heads * a.dim, row_base = (size_t)row * inner * 3;
+    size_t qb = row_base + (size_t)head * a.dim, kb = qb + inner, vb = qb + 2 * inner;
+    if (a.grouped) { qb = row_base + (size_t)head * a.dim * 3; kb = qb + a.dim; vb = kb + a.dim; }
+    float qv[4], kv[4];
+    float qs = 0.f, ks = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned d = lane + 64 * i;
+        qv[i] = kv[i] = 0.f;
+        if (d < a.dim) {
+            qv[i] = bf16_to_f32(a.qkv[qb + d]);
+            kv[i] = bf16_to_f32(a.qkv[kb + d]);
+            qs = fmaf(qv[i], qv[i], qs);
+            ks = fmaf(kv[i], kv[i], ks);
+        }
+    }
+    float qi = 1.f, ki = 1.f;
+    if (a.qw) {
+        qi = rsqrtf(wave_sum(qs) / (float)a.dim + a.eps);
+        ki = rsqrtf(wave_sum(ks) / (float)a.dim + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned d = lane + 64 * i;
+        if (d < a.dim) {
+            float wq = a.qw ? bf16_to_f32(a.qw[d]) : 1.f, wk = a.kw ? bf16_to_f32(a.kw[d]) : 1.f;
+            qv[i] = a.qw ? qv[i] * qi * wq : qv[i];
+            kv[i] = a.qw ? kv[i] * ki * wk : kv[i];
+            stage[wave][0][d] = qv[i];
+            stage[wave][1][d] = kv[i];
+        }
+    }
+    __syncthreads();  // partner channels come from other lanes through LDS
+    if (!store) return;
+    const size_t out_base = ((size_t)row * a.heads + head) * a.dim;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned d = lane + 64 * i;
+        if (d >= a.dim) continue;
+        float q0 = qv[i], k0 = kv[i];
+        if (d < a.half) {
+            float c = bf16_to_f32(a.cos_t[(size_t)row * a.half + d]), s = bf16_to_f32(a.sin_t[(size_t)row * a.half + d]);
+            float q1 = stage[wave][0][d + a.half], k1 = stage[wave][1][d + a.half];
+            q0 = q0 * c - q1 * s;
+            k0 = k0 * c - k1 * s;
+        } else if (d < 2 * a.half) {
+            unsigned p = d - a.half;
+            float c = bf16_to_f32(a.cos_t[(size_t)row * a.half + p]), s = bf16_to_f32(a.sin_t[(size_t)row * a.half + p]);
+            float q1 = stage[wave][0][p], k1 = stage[wave][1][p];
+            q0 = q0 * c + q1 * s;
+            k0 = k0 * c + k1 * s;
+        }
+        a.q[out_base + d] = f32_to_bf16(q0);
+        a.k[out_base + d] = f32_to_bf16(k0);
+        a.v[out_base + d] = a.qkv[vb + d];
+    }
+}
+
+__device__ inline float gelu_value(float v, int approximate) {
+    if (approximate) {
+        float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+        return inner <= -10.0f ? 0.0f : inner >= 10.0f ? v : 0.5f * v * (1.0f + tanhf(inner));
+    }
+    return v <= -10.0f ? 0.0f : v >= 10.0f ? v : 0.5f * v * (1.0f + erff(v * 0.7071067811865475f));
+}
+
+__global__ __launch_bounds__(256) void gelu_kernel(uint16_t *out, const uint16_t *in, size_t n, int approximate) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(gelu_value(bf16_to_f32(in[i]), approximate));
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(uint16_t *out, const uint16_t *fused, unsigned rows, unsigned width) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)rows * width) return;
+    size_t row = i / width, col = i % width, base = row * width * 2;
+    float gate = bf16_to_f32(fused[base + col]), up = bf16_to_f32(fused[base + width + col]);
+    out[i] = f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+}
+
+__global__ __launch_bounds__(256) void euler_kernel(float *sample, const uint16_t *last, const uint16_t *prev, unsigned n,
+                                                   float delta, float ratio) {
+    unsigned i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float l = bf16_to_f32(last[i]);
+    float velocity = fmaf(ratio, l - bf16_to_f32(prev[i]), l);
+    sample[i] = fmaf(delta, velocity, sample[i]);
+}
+
+unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+int check_map(h3_gpu *g, const h3_gpu_tensor *map, uint32_t rows, const char *what) {
+    if (!map || map->dtype != H3_GPU_U32 || map->elements < rows) return h3_set_error(g, "%s row map: need %u U32 entries", what, rows);
+    return 1;
+}
+
+}  // namespace
+
+extern "C" int h3_gpu_adaln_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w,
+                                 const h3_gpu_tensor *mod, const h3_gpu_tensor *map, uint32_t rows, uint32_t width,
+                                 uint32_t slots, uint32_t shift, uint32_t scale, float eps) {
+    size_t n = (size_t)rows * width;
+    if (!h3_launch_ready(g)) return 0;
+    if (!rows || !width || width % 8 || width > 64 * MAX_CHUNKS * 8 || shift >= slots || scale >= slots)
+        return h3_set_error(g, "AdaLN: width must be a multiple of 8 up to 8192 and slots valid");
+    if (!h3_require(g, in, H3_GPU_BF16, n, "AdaLN input") || !h3_require(g, w, H3_GPU_BF16, width, "AdaLN norm") ||
+        !h3_require(g, mod, H3_GPU_BF16, (size_t)slots * width, "AdaLN modulation") || !check_map(g, map, rows, "AdaLN") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "AdaLN output"))
+        return 0;
+    AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data, nullptr, (const uint16_t *)w->data,
+                (const uint16_t *)mod->data, nullptr, (const uint32_t *)map->data, rows, width, slots, shift, scale, 0, eps};
+    hipLaunchKernelGGL(adaln_kernel<false>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    return h3_launch_status(g, "AdaLN");
+}
+
+extern "C" int h3_gpu_gate_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *res, const h3_gpu_tensor *branch,
+                                const h3_gpu_tensor *mod, const h3_gpu_tensor *map, uint32_t rows, uint32_t width,
+                                uint32_t slots, uint32_t gate_slot) {
+    size_t n = (size_t)rows * width;
+    if (!h3_launch_ready(g)) return 0;
+    if (!rows || !width || width % 8 || gate_slot >= slots) return h3_set_error(g, "gate: width must be a multiple of 8");
+    if (!h3_require(g, res, H3_GPU_BF16, n, "gate residual") || !h3_require(g, branch, H3_GPU_BF16, n, "gate branch") ||
+        !h3_require(g, mod, H3_GPU_BF16, (size_t)slots * width, "gate modulation") || !check_map(g, map, rows, "gate") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "gate output"))
+        return 0;
+    hipLaunchKernelGGL(gate_kernel, dim3(blocks_for(n / 8, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)res->data, (const uint16_t *)branch->data, (const uint16_t *)mod->data,
+                       (const uint32_t *)map->data, rows, width, slots, gate_slot);
+    return h3_launch_status(g, "gate");
+}
+
+extern "C" int h3_gpu_gate_adaln_bf16(h3_gpu *g, h3_gpu_tensor *gated, h3_gpu_tensor *out, const h3_gpu_tensor *res,
+                                      const h3_gpu_tensor *branch, const h3_gpu_tensor *w, const h3_gpu_tensor *gate_mod,
+                                      const h3_gpu_tensor *norm_mod, const h3_gpu_tensor *map, uint32_t rows,
+                                      uint32_t width, uint32_t slots, uint32_t gate_slot, uint32_t shift,
+                                      uint32_t scale, float eps) {
+    size_t n = (size_t)rows * width;
+    if (!h3_launch_ready(g)) return 0;
+    if (!rows || !width || width % 8 || width > 64 * MAX_CHUNKS * 8 || gate_slot >= slots || shift >= slots || scale >= slots)
+        return h3_set_error(g, "gate AdaLN: width must be a multiple of 8 up to 8192 and slots valid");
+    if (!h3_require(g, res, H3_GPU_BF16, n, "gate residual") || !h3_require(g, branch, H3_GPU_BF16, n, "gate branch") ||
+        !h3_require(g, w, H3_GPU_BF16, width, "AdaLN norm") ||
+        !h3_require(g, gate_mod, H3_GPU_BF16, (size_t)slots * width, "gate modulation") ||
+        !h3_require(g, norm_mod, H3_GPU_BF16, (size_t)slots * width, "AdaLN modulation") ||
+        !check_map(g, map, rows, "gate AdaLN") || !h3_require(g, gated, H3_GPU_BF16, n, "gated residual") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "AdaLN output"))
+        return 0;
+    if (gated == out || gated == branch || out == res || out == branch)
+        return h3_set_error(g, "gate AdaLN: outputs must not alias the branch or each other");
+    AdaLNArgs a{(uint16_t *)out->data, (uint16_t *)gated->data, (const uint16_t *)res->data, (const uint16_t *)branch->data,
+                (const uint16_t *)w->data, (const uint16_t *)norm_mod->data, (const uint16_t *)gate_mod->data,
+                (const uint32_t *)map->data, rows, width, slots, shift, scale, gate_slot, eps};
+    hipLaunchKernelGGL(adaln_kernel<true>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    return h3_launch_status(g, "gate AdaLN");
+}
+
+static int qkv_rope(h3_gpu *g, h3_gpu_tensor *q, h3_gpu_tensor *k, h3_gpu_tensor *v, const h3_gpu_tensor *qkv,
+                    const h3_gpu_tensor *qw, const h3_gpu_tensor *kw, const h3_gpu_tensor *c, const h3_gpu_tensor *s,
+                    uint32_t seq, uint32_t heads, uint32_t dim, uint32_t half, float eps, int grouped) {
+    size_t n = (size_t)seq * heads * dim;
+    if (!h3_launch_ready(g)) return 0;
+    if (!seq || !heads || !dim || dim > 256 || half * 2 > dim || (!qw) != (!kw))
+        return h3_set_error(g, "QKV RoPE: need dim <= 256, 2*rope_half <= dim, both or neither norm weights");
+    if (!h3_require(g, qkv, H3_GPU_BF16, n * 3, "QKV") || !h3_require(g, q, H3_GPU_BF16, n, "Q") ||
+        !h3_require(g, k, H3_GPU_BF16, n, "K") || !h3_require(g, v, H3_GPU_BF16, n, "V") ||
+        (qw && (!h3_require(g, qw, H3_GPU_BF16, dim, "Q norm") || !h3_require(g, kw, H3_GPU_BF16, dim, "K norm"))) ||
+        (half && (!h3_require(g, c, H3_GPU_BF16, (size_t)seq * half, "RoPE cos") ||
+                  !h3_require(g, s, H3_GPU_BF16, (size_t)seq * half, "RoPE sin"))))
+        return 0;
+    QkvArgs a{(uint16_t *)q->data, (uint16_t *)k->data, (uint16_t *)v->data, (const uint16_t *)qkv->data,
+              qw ? (const uint16_t *)qw->data : nullptr, kw ? (const uint16_t *)kw->data : nullptr,
+              half ? (const uint16_t *)c->data : nullptr, half ? (const uint16_t *)s->data : nullptr,
+              seq, heads, dim, half, eps, grouped};
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3(blocks_for((size_t)seq * heads, 4)), dim3(256), 0, g->compute, a);
+    return h3_launch_status(g, "QKV norm/RoPE");
+}
+
+extern "C" int h3_gpu_qkv_rope_bf16(h3_gpu *g, h3_gpu_tensor *q, h3_gpu_tensor *k, h3_gpu_tensor *v, const h3_gpu_tensor *qkv,
+                                    const h3_gpu_tensor *qw, const h3_gpu_tensor *kw, const h3_gpu_tensor *c,
+                                    const h3_gpu_tensor *s, uint32_t seq, uint32_t heads, uint32_t dim, uint32_t half,
+                                    float eps) {
+    return g && qkv_rope(g, q, k, v, qkv, qw, kw, c, s, seq, heads, dim, half, eps, 0);
+}
+
+extern "C" int h3_gpu_grouped_qkv_rope_bf16(h3_gpu *g, h3_gpu_tensor *q, h3_gpu_tensor *k, h3_gpu_tensor *v,
+                                            const h3_gpu_tensor *qkv, const h3_gpu_tensor *qw, const h3_gpu_tensor *kw,
+                                            const h3_gpu_tensor *c, const h3_gpu_tensor *s, uint32_t seq,
+                                            uint32_t heads, uint32_t dim, uint32_t half, float eps) {
+    return g && qkv_rope(g, q, k, v, qkv, qw, kw, c, s, seq, heads, dim, half, eps, 1);
+}
+
+extern "C" int h3_gpu_gelu_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, uint32_t n, int approximate) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, in, H3_GPU_BF16, n, "GELU input") || !h3_require(g, out, H3_GPU_BF16, n, "GELU output")) return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(gelu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)in->data, (size_t)n, approximate ? 1 : 0);
+    return h3_launch_status(g, "GELU");
+}
+
+extern "C" int h3_gpu_swiglu_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *fused, uint32_t rows, uint32_t width) {
+    if (!h3_launch_ready(g)) return 0;
+    size_t n = (size_t)rows * width;
+    if (!h3_require(g, fused, H3_GPU_BF16, n * 2, "SwiGLU input") || !h3_require(g, out, H3_GPU_BF16, n, "SwiGLU output"))
+        return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)fused->data, rows, width);
+    return h3_launch_status(g, "SwiGLU");
+}
+
+extern "C" int h3_gpu_euler_bf16(h3_gpu *g, h3_gpu_tensor *sample, size_t offset, const h3_gpu_tensor *last,
+                                 const h3_gpu_tensor *previous, uint32_t n, float delta, float ratio) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!sample || sample->dtype != H3_GPU_F32 || offset > sample->elements || n > sample->elements - offset)
+        return h3_set_error(g, "Euler: sample range out of bounds");
+    if (!h3_require(g, last, H3_GPU_BF16, n, "Euler last") || !h3_require(g, previous, H3_GPU_BF16, n, "Euler previous"))
+        return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(euler_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (float *)sample->data + offset,
+                       (const uint16_t *)last->data, (const uint16_t *)previous->data, n, delta, ratio);
+    return h3_launch_status(g, "Euler");
+}

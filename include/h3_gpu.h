@@ -210,7 +210,8 @@ int h3_gpu_gate_adaln_bf16(h3_gpu *gpu, h3_gpu_tensor *gated_residual, h3_gpu_te
                            uint32_t shift_slot, uint32_t scale_slot, float epsilon);
 /* gpu.h:643. qkv [seq, 3, heads, dim] -> per-head RMSNorm of Q and K (weights
  * q_norm/k_norm [dim]) then rotate-half RoPE on the first 2*rope_half dims
- * (pair d <-> d+rope_half, cos/sin [seq, rope_half]); V copied. */
+ * (pair d <-> d+rope_half, cos/sin [seq, rope_half]); V copied. dim <= 256.
+ * Extension: q_norm = k_norm = NULL skips the Q/K RMSNorm (RoPE only). */
 int h3_gpu_qkv_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *query, h3_gpu_tensor *key,
                          h3_gpu_tensor *value, const h3_gpu_tensor *qkv,
                          const h3_gpu_tensor *q_norm, const h3_gpu_tensor *k_norm,

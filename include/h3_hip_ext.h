@@ -24,6 +24,13 @@ const char *h3_hip_version(void);
 h3_gpu_tensor *h3_hip_q8_from_packed(h3_gpu *gpu, const int8_t *codes, const float *scales,
                                      uint32_t rows, uint32_t columns, uint32_t group);
 
+/* h3_gpu_linear_bf16 followed by the tanh GELU of h3_gpu_gelu_bf16(approximate=1),
+ * fused into the GEMM epilogue: y = bf16(gelu(bf16(x . W^T + bias))). The MLP
+ * up-projection of the synthetic DiT block. */
+int h3_hip_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *input,
+                            const h3_gpu_tensor *weight, const h3_gpu_tensor *bias,
+                            uint32_t rows, uint32_t input_dim, uint32_t output_dim);
+
 /* Fixed block-sparse mask for main-DiT attention. mask is u8 [q_blocks, k_blocks]
  * (nonzero = keep) over block x block tiles; block must be 128 (or 64). While a
  * mask is bound, h3_gpu_dit_sdpa_bf16 computes softmax over the kept key tiles

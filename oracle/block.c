@@ -1,0 +1,196 @@
+/* CPU oracle — TEST INFRASTRUCTURE ONLY (see oracle.h). DiT block operators:
+ * q8 packing, W8A16 / BF16 projections (FP64 accumulation), AdaLN, gates,
+ * Q/K norm + RoPE, activations and the Euler update. */
+#include "oracle.h"
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+
+/* src/weights/q8.c:26-56 with a group parameter (64 = the reference recipe;
+ * group = cols = one scale per output channel): scale = max|w|/127 (1 for an
+ * all-zero group, floored at FLT_MIN), code = nearest integer to w/scale with
+ * ties to even (nearbyintf in the default rounding mode), clamped to +-127. */
+int oracle_q8_pack(const uint16_t *w, int8_t *codes, float *scales, unsigned rows, unsigned cols,
+                   unsigned group) {
+    if (!rows || !cols || !group) return 0;
+    unsigned groups = (cols + group - 1) / group;
+    for (unsigned r = 0; r < rows; r++)
+        for (unsigned gi = 0; gi < groups; gi++) {
+            unsigned b = gi * group, e = b + group < cols ? b + group : cols;
+            float amax = 0.f;
+            for (unsigned c = b; c < e; c++) {
+                float x = oracle_bf16_to_f32(w[(size_t)r * cols + c]);
+                if (isnan(x) || isinf(x)) return 0;
+                amax = fmaxf(amax, fabsf(x));
+            }
+            float s = amax == 0.f ? 1.f : fmaxf(amax / 127.f, FLT_MIN);
+            scales[(size_t)r * groups + gi] = s;
+            for (unsigned c = b; c < e; c++) {
+                float q = nearbyintf(oracle_bf16_to_f32(w[(size_t)r * cols + c]) / s);
+                codes[(size_t)r * cols + c] = (int8_t)(q > 127.f ? 127 : q < -127.f ? -127 : (int)q);
+            }
+        }
+    return 1;
+}
+
+static float gelu_tanh_f(float v) {
+    /* src/cuda/cuda_kernels.cuh:886-895 */
+    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return inner <= -10.0f ? 0.0f : inner >= 10.0f ? v : 0.5f * v * (1.0f + tanhf(inner));
+}
+float oracle_gelu_tanh(float x) { return gelu_tanh_f(x); }
+
+static void linear_rows(uint16_t *y, double *y64, const uint16_t *x, const float *wrow_f, const uint16_t *bias,
+                        unsigned k, unsigned n, unsigned col, int gelu, unsigned row0, unsigned row1) {
+    for (unsigned r = row0; r < row1; r++) {
+        double s = bias ? (double)oracle_bf16_to_f32(bias[col]) : 0.0;
+        const uint16_t *xr = x + (size_t)r * k;
+        for (unsigned c = 0; c < k; c++) s += (double)oracle_bf16_to_f32(xr[c]) * wrow_f[c];
+        size_t at = (size_t)(r - row0) * n + col;
+        uint16_t b = oracle_f32_to_bf16((float)s);
+        if (gelu) b = oracle_f32_to_bf16(gelu_tanh_f(oracle_bf16_to_f32(b)));
+        if (y) y[at] = b;
+        if (y64) y64[at] = gelu ? (double)gelu_tanh_f((float)s) : s;
+    }
+}
+
+/* W8A16 (src/metal/shaders.metal:799-855, tests/metal_q8.c:125-132): every
+ * weight is reconstructed as bf16(code * scale); sums in FP64. Output rows
+ * [row0, row1) into y/y64 [row1-row0, n]. */
+void oracle_linear_q8(uint16_t *y, double *y64, const uint16_t *x, const int8_t *codes, const float *scales,
+                      const uint16_t *bias, unsigned rows, unsigned k, unsigned n, unsigned group, int gelu,
+                      unsigned row0, unsigned row1) {
+    unsigned groups = (k + group - 1) / group;
+#pragma omp parallel
+    {
+        float *wf = malloc(sizeof(float) * k);
+#pragma omp for schedule(dynamic, 8)
+        for (unsigned col = 0; col < n; col++) {
+            for (unsigned c = 0; c < k; c++)
+                wf[c] = oracle_bf16_to_f32(oracle_f32_to_bf16((float)codes[(size_t)col * k + c] *
+                                                              scales[(size_t)col * groups + c / group]));
+            linear_rows(y, y64, x, wf, bias, k, n, col, gelu, row0, row1);
+        }
+        free(wf);
+    }
+}
+
+void oracle_linear_bf16(uint16_t *y, double *y64, const uint16_t *x, const uint16_t *w, const uint16_t *bias,
+                        unsigned rows, unsigned k, unsigned n, int gelu, unsigned row0, unsigned row1) {
+#pragma omp parallel
+    {
+        float *wf = malloc(sizeof(float) * k);
+#pragma omp for schedule(dynamic, 8)
+        for (unsigned col = 0; col < n; col++) {
+            for (unsigned c = 0; c < k; c++) wf[c] = oracle_bf16_to_f32(w[(size_t)col * k + c]);
+            linear_rows(y, y64, x, wf, bias, k, n, col, gelu, row0, row1);
+        }
+        free(wf);
+    }
+}
+
+/* src/cuda/cuda_kernels.cuh:936-971: per row, sum of squares by fmaf in column
+ * order, inv = 1/sqrt(mean + eps), y = bf16(fmaf(x*inv*w, 1+scale, shift)). */
+void oracle_adaln(uint16_t *y, const uint16_t *x, const uint16_t *w, const uint16_t *mod, const uint32_t *row_map,
+                  unsigned rows, unsigned width, unsigned slots, unsigned shift_slot, unsigned scale_slot, float eps) {
+#pragma omp parallel for
+    for (unsigned r = 0; r < rows; r++) {
+        const uint16_t *xr = x + (size_t)r * width;
+        float sum = 0.f;
+        for (unsigned c = 0; c < width; c++) {
+            float v = oracle_bf16_to_f32(xr[c]);
+            sum = fmaf(v, v, sum);
+        }
+        float inv = 1.0f / sqrtf(sum / (float)width + eps);
+        size_t base = (size_t)row_map[r] * slots * width;
+        for (unsigned c = 0; c < width; c++) {
+            float normalized = oracle_bf16_to_f32(xr[c]) * inv * oracle_bf16_to_f32(w[c]);
+            float shift = oracle_bf16_to_f32(mod[base + (size_t)shift_slot * width + c]);
+            float scale = oracle_bf16_to_f32(mod[base + (size_t)scale_slot * width + c]);
+            y[(size_t)r * width + c] = oracle_f32_to_bf16(fmaf(normalized, 1.0f + scale, shift));
+        }
+    }
+}
+
+/* src/cuda/cuda_kernels.cuh:973-986 (residual + branch*gate, one rounding). */
+void oracle_gate(uint16_t *y, const uint16_t *residual, const uint16_t *branch, const uint16_t *mod,
+                 const uint32_t *row_map, unsigned rows, unsigned width, unsigned slots, unsigned gate_slot) {
+    for (unsigned r = 0; r < rows; r++)
+        for (unsigned c = 0; c < width; c++) {
+            size_t i = (size_t)r * width + c;
+            float gate = oracle_bf16_to_f32(mod[(size_t)row_map[r] * slots * width + (size_t)gate_slot * width + c]);
+            y[i] = oracle_f32_to_bf16(fmaf(oracle_bf16_to_f32(branch[i]), gate, oracle_bf16_to_f32(residual[i])));
+        }
+}
+
+/* src/cuda/cuda_kernels.cuh:988-1045 (grouped rows when grouped != 0). With
+ * qw == NULL the Q/K RMSNorm is skipped (RoPE only). */
+void oracle_qkv_rope(uint16_t *q, uint16_t *k, uint16_t *v, const uint16_t *qkv, const uint16_t *qw,
+                     const uint16_t *kw, const uint16_t *cos_t, const uint16_t *sin_t, unsigned seq,
+                     unsigned heads, unsigned dim, unsigned half, float eps, int grouped) {
+    for (unsigned row = 0; row < seq; row++)
+        for (unsigned h = 0; h < heads; h++) {
+            size_t inner = (size_t)heads * dim, rb = (size_t)row * inner * 3;
+            size_t qb = rb + (size_t)h * dim, kb = qb + inner, vb = qb + 2 * inner;
+            if (grouped) { qb = rb + (size_t)h * dim * 3; kb = qb + dim; vb = kb + dim; }
+            float qs = 0.f, ks = 0.f;
+            for (unsigned d = 0; d < dim; d++) {
+                float a = oracle_bf16_to_f32(qkv[qb + d]), b = oracle_bf16_to_f32(qkv[kb + d]);
+                qs = fmaf(a, a, qs);
+                ks = fmaf(b, b, ks);
+            }
+            float qi = qw ? 1.0f / sqrtf(qs / (float)dim + eps) : 1.f;
+            float ki = qw ? 1.0f / sqrtf(ks / (float)dim + eps) : 1.f;
+#define NQ(d) (qw ? oracle_bf16_to_f32(qkv[qb + (d)]) * qi * oracle_bf16_to_f32(qw[d]) : oracle_bf16_to_f32(qkv[qb + (d)]))
+#define NK(d) (qw ? oracle_bf16_to_f32(qkv[kb + (d)]) * ki * oracle_bf16_to_f32(kw[d]) : oracle_bf16_to_f32(qkv[kb + (d)]))
+            size_t ob = ((size_t)row * heads + h) * dim;
+            for (unsigned d = 0; d < dim; d++) {
+                float q0 = NQ(d), k0 = NK(d);
+                if (d < half) {
+                    float c = oracle_bf16_to_f32(cos_t[(size_t)row * half + d]);
+                    float s = oracle_bf16_to_f32(sin_t[(size_t)row * half + d]);
+                    q0 = q0 * c - NQ(d + half) * s;
+                    k0 = k0 * c - NK(d + half) * s;
+                } else if (d < 2 * half) {
+                    unsigned p = d - half;
+                    float c = oracle_bf16_to_f32(cos_t[(size_t)row * half + p]);
+                    float s = oracle_bf16_to_f32(sin_t[(size_t)row * half + p]);
+                    q0 = q0 * c + NQ(p) * s;
+                    k0 = k0 * c + NK(p) * s;
+                }
+                q[ob + d] = oracle_f32_to_bf16(q0);
+                k[ob + d] = oracle_f32_to_bf16(k0);
+                v[ob + d] = qkv[vb + d];
+            }
+#undef NQ
+#undef NK
+        }
+}
+
+void oracle_gelu(uint16_t *y, const uint16_t *x, size_t n, int approximate) {
+    for (size_t i = 0; i < n; i++) {
+        float v = oracle_bf16_to_f32(x[i]), r;
+        if (approximate) r = gelu_tanh_f(v);
+        else r = v <= -10.0f ? 0.0f : v >= 10.0f ? v : 0.5f * v * (1.0f + erff(v * 0.7071067811865475f));
+        y[i] = oracle_f32_to_bf16(r);
+    }
+}
+
+/* src/cuda/cuda_kernels.cuh:1047-1059 */
+void oracle_swiglu(uint16_t *y, const uint16_t *fused, unsigned rows, unsigned width) {
+    for (unsigned r = 0; r < rows; r++)
+        for (unsigned c = 0; c < width; c++) {
+            float gate = oracle_bf16_to_f32(fused[(size_t)r * width * 2 + c]);
+            float up = oracle_bf16_to_f32(fused[(size_t)r * width * 2 + width + c]);
+            y[(size_t)r * width + c] = oracle_f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+        }
+}
+
+/* src/cuda/cuda_kernels.cuh:1242-1254 */
+void oracle_euler(float *sample, const uint16_t *last, const uint16_t *previous, size_t n, float delta, float ratio) {
+    for (size_t i = 0; i < n; i++) {
+        float l = oracle_bf16_to_f32(last[i]);
+        float velocity = fmaf(ratio, l - oracle_bf16_to_f32(previous[i]), l);
+        sample[i] = fmaf(delta, velocity, sample[i]);
+    }
+}

@@ -43,6 +43,17 @@ def load():
         lib.oracle_threads.restype = C.c_int
         lib.oracle_xorshift_bf16.argtypes = [_p, C.c_size_t, _p]
         lib.oracle_xorshift_native_bf16.argtypes = [_p, C.c_size_t, _p]
+        lib.oracle_q8_pack.argtypes = [_p, _p, _p, _u, _u, _u]
+        lib.oracle_linear_q8.argtypes = [_p, _p, _p, _p, _p, _p, _u, _u, _u, _u, C.c_int, _u, _u]
+        lib.oracle_linear_bf16.argtypes = [_p, _p, _p, _p, _p, _u, _u, _u, C.c_int, _u, _u]
+        lib.oracle_adaln.argtypes = [_p, _p, _p, _p, _p, _u, _u, _u, _u, _u, _f]
+        lib.oracle_gate.argtypes = [_p, _p, _p, _p, _p, _u, _u, _u, _u]
+        lib.oracle_qkv_rope.argtypes = [_p, _p, _p, _p, _p, _p, _p, _p, _u, _u, _u, _u, _f, C.c_int]
+        lib.oracle_gelu.argtypes = [_p, _p, C.c_size_t, C.c_int]
+        lib.oracle_gelu_tanh.argtypes = [_f]
+        lib.oracle_gelu_tanh.restype = _f
+        lib.oracle_swiglu.argtypes = [_p, _p, _u, _u]
+        lib.oracle_euler.argtypes = [_p, _p, _p, C.c_size_t, _f, _f]
         _lib = lib
     return _lib
 
@@ -169,3 +180,79 @@ def block_mask(seq, video_rows, block, density, seed):
     audio = (last >= video_rows) & (video_rows < seq)
     keep = (qb == kb) | (audio[:, None] & audio[None, :]) | (u < density)
     return keep.astype(np.uint8)
+
+
+def _u16(a):
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def q8_pack(w, rows, cols, group=64):
+    """Reference q8 packing (src/weights/q8.c:26-56) with a group parameter."""
+    w = _u16(w)
+    groups = (cols + group - 1) // group
+    codes = np.zeros(rows * cols, np.int8)
+    scales = np.zeros(rows * groups, np.float32)
+    ok = load().oracle_q8_pack(_ptr(w), _ptr(codes), _ptr(scales), rows, cols, group)
+    return (codes, scales) if ok else None
+
+
+def linear_q8(x, codes, scales, rows, k, n, group, bias=None, gelu=False, rows_range=None):
+    r0, r1 = rows_range if rows_range else (0, rows)
+    y = np.zeros((r1 - r0) * n, np.uint16)
+    y64 = np.zeros((r1 - r0) * n, np.float64)
+    b = None if bias is None else _u16(bias)
+    load().oracle_linear_q8(_ptr(y), _ptr(y64), _ptr(_u16(x)), _ptr(np.ascontiguousarray(codes, np.int8)),
+                            _ptr(np.ascontiguousarray(scales, np.float32)), _ptr(b), rows, k, n, group,
+                            int(gelu), r0, r1)
+    return y, y64
+
+
+def linear_bf16(x, w, rows, k, n, bias=None, gelu=False, rows_range=None):
+    r0, r1 = rows_range if rows_range else (0, rows)
+    y = np.zeros((r1 - r0) * n, np.uint16)
+    y64 = np.zeros((r1 - r0) * n, np.float64)
+    b = None if bias is None else _u16(bias)
+    load().oracle_linear_bf16(_ptr(y), _ptr(y64), _ptr(_u16(x)), _ptr(_u16(w)), _ptr(b), rows, k, n, int(gelu), r0, r1)
+    return y, y64
+
+
+def adaln(x, w, mod, row_map, rows, width, slots, shift, scale, eps):
+    y = np.zeros(rows * width, np.uint16)
+    load().oracle_adaln(_ptr(y), _ptr(_u16(x)), _ptr(_u16(w)), _ptr(_u16(mod)),
+                        _ptr(np.ascontiguousarray(row_map, np.uint32)), rows, width, slots, shift, scale, eps)
+    return y
+
+
+def gate(res, branch, mod, row_map, rows, width, slots, gate_slot):
+    y = np.zeros(rows * width, np.uint16)
+    load().oracle_gate(_ptr(y), _ptr(_u16(res)), _ptr(_u16(branch)), _ptr(_u16(mod)),
+                       _ptr(np.ascontiguousarray(row_map, np.uint32)), rows, width, slots, gate_slot)
+    return y
+
+
+def qkv_rope(qkv, qw, kw, cos_t, sin_t, seq, heads, dim, half, eps, grouped):
+    n = seq * heads * dim
+    q, k, v = (np.zeros(n, np.uint16) for _ in range(3))
+    load().oracle_qkv_rope(_ptr(q), _ptr(k), _ptr(v), _ptr(_u16(qkv)), _ptr(None if qw is None else _u16(qw)),
+                           _ptr(None if kw is None else _u16(kw)), _ptr(_u16(cos_t)), _ptr(_u16(sin_t)),
+                           seq, heads, dim, half, eps, int(grouped))
+    return q, k, v
+
+
+def gelu(x, approximate=True):
+    x = _u16(x)
+    y = np.zeros(x.size, np.uint16)
+    load().oracle_gelu(_ptr(y), _ptr(x), x.size, int(approximate))
+    return y
+
+
+def swiglu(fused, rows, width):
+    y = np.zeros(rows * width, np.uint16)
+    load().oracle_swiglu(_ptr(y), _ptr(_u16(fused)), rows, width)
+    return y
+
+
+def euler(sample, last, previous, delta, ratio):
+    s = np.array(sample, np.float32, copy=True)
+    load().oracle_euler(_ptr(s), _ptr(_u16(last)), _ptr(_u16(previous)), s.size, delta, ratio)
+    return s
