@@ -23,12 +23,15 @@ def gpu():
     g.close()
 
 
-def ulp_diff(a, b):
-    """Distance in BF16 units in the last place (sign-magnitude order)."""
-    def key(x):
-        x = np.asarray(x, np.uint16).astype(np.int32)
-        return np.where(x & 0x8000, -(x & 0x7FFF), x & 0x7FFF)
-    return np.abs(key(a) - key(b))
+def ulp_diff(a, b, floor=2.0 ** -17):
+    """|a - b| in units of the BF16 ulp at the larger magnitude of the pair, with
+    the ulp floored at `floor`: outputs that cancel to near zero (fma(x, 1+scale,
+    shift) with x*(1+scale) ~ -shift) inherit the absolute error of the O(1) terms,
+    not the tiny ulp of the result."""
+    fa, fb = bf16(a).astype(np.float64), bf16(b).astype(np.float64)
+    mag = np.maximum(np.maximum(np.abs(fa), np.abs(fb)), 2.0 ** -126)
+    ulp = np.maximum(2.0 ** (np.floor(np.log2(mag)) - 7), floor)
+    return np.abs(fa - fb) / ulp
 
 
 def run(gpu, fn, *args):
