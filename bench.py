@@ -117,12 +117,54 @@ def cpu_baseline(q, k, v, seq, heads, rows):
                        f"{dt:.2f} s; TFLOP/s of that slice (same FLOP convention)")
 
 
+GEMM_SHAPES = [("qkv", 5120, 15360, False), ("out", 5120, 5120, False), ("up_gelu", 5120, 13824, True),
+               ("down", 13824, 5120, False)]
+
+
+def gemm_leg(steps, warmup, m=32400, seed=4):
+    """W8A16 GEMMs of one DiT block at M = 32400 rows, int8
+    weights U[-127,127] with per-output-channel fp32 scales U[1e-3,1e-2]."""
+    from h3cli_amd.runtime import Gpu, Tensor
+    out = {"workload": "W8A16 GEMM set of one DiT block (BASELINE config 4)", "rows": m, "shapes": {}}
+    total_flops, total_ms = 0.0, 0.0
+    with Gpu() as gpu:
+        lib = gpu.lib
+        x = gpu.empty(m * 13824)
+        gpu.begin()
+        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, seed * 16, 1.0, m * 13824), "fill")
+        gpu.submit()
+        rng = np.random.default_rng(seed)
+        for name, k, n, gelu in GEMM_SHAPES:
+            codes = rng.integers(-127, 128, size=n * k, dtype=np.int8)
+            scales = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+            h = lib.h3_hip_q8_from_packed(gpu.handle, codes.ctypes.data, scales.ctypes.data, n, k, k)
+            if not h:
+                raise RuntimeError(gpu.error())
+            w = Tensor(gpu, h, n * k, 2)
+            gpu.tensors.append(w)
+            y = gpu.empty(m * n)
+            fn = lib.h3_hip_linear_gelu_bf16 if gelu else lib.h3_gpu_linear_bf16
+            call = lambda: fn(gpu.handle, y.handle, x.handle, w.handle, None, m, k, n)
+            ms, _ = time_calls(gpu, call, steps, warmup)
+            flops = 2.0 * m * k * n
+            total_flops += flops
+            total_ms += ms
+            out["shapes"][name] = {"k": k, "n": n, "ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2)}
+            log(f"[bench] gemm {name} {m}x{k}x{n}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s")
+            gpu.free(y)
+            gpu.free(w)
+    out["ms_total"] = round(total_ms, 4)
+    out["tflops"] = round(total_flops / total_ms / 1e9, 2)
+    out["frac_of_bf16_peak"] = round(total_flops / total_ms / 1e9 / PEAK_BF16, 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage")
+    ap.add_argument("--legs", default="attention,sage,gemm")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "192")))
     args = ap.parse_args()
@@ -180,6 +222,8 @@ def main():
                               "ms_per_call": round(ms_s, 4), "effective_tflops": round(eff, 3),
                               "speedup_vs_bf16": round(ms / ms_s, 3),
                               "frac_of_fp8_peak": round(eff / PEAK_FP8, 4)}
+    if "gemm" in legs:
+        result["gemm"] = gemm_leg(args.steps, args.warmup)
     print(json.dumps(result), flush=True)
 
 

@@ -11,8 +11,9 @@
 // MI355X design:
 //  * C^T = W . X^T on v_mfma_f32_32x32x16_bf16, so a lane owns one output row and
 //    four consecutive columns per register group (8-byte row-major stores);
-//  * 256 x 256 output tile per workgroup of 4 waves (each 128 x 128, 16
-//    accumulator blocks), K staged 64 at a time, double buffered in LDS;
+//  * 256 x 256 output tile per workgroup of 8 waves (each 128 x 64, 8
+//    accumulator blocks, two waves per SIMD), K staged 64 at a time, double
+//    buffered in LDS, operand fragments of the next k-step read during MFMAs;
 //  * X tiles go global -> LDS directly (global_load_lds_dwordx4, XOR-swizzled
 //    16-byte chunks); int8 weight tiles are loaded into registers one tile ahead,
 //    dequantized in registers (w = bf16(code * scale)) and written to LDS as BF16,
@@ -44,13 +45,23 @@ struct GemmArgs {
 };
 
 __device__ inline float gelu_tanh(float v) {
-    // Reference h3_gelu_bf16, approximate form (src/cuda/cuda_kernels.cuh:879-902).
+    // Reference h3_gelu_bf16, approximate form (src/cuda/cuda_kernels.cuh:879-902);
+    // tanh(t) = 1 - 2 / (exp(2t) + 1) on the exp unit, |t| < 10 here.
     float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    return inner <= -10.0f ? 0.0f : inner >= 10.0f ? v : 0.5f * v * (1.0f + tanhf(inner));
+    if (inner <= -10.0f) return 0.0f;
+    if (inner >= 10.0f) return v;
+    float t = 1.0f - 2.0f / (__expf(2.0f * inner) + 1.0f);
+    return 0.5f * v * (1.0f + t);
 }
 
-template <bool Q8>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// 8 waves as 2 (M) x 4 (N); each wave owns a 128 x 64 output tile (8 MFMA
+// blocks), two waves per SIMD. CHANNEL: one scale per output row (group == K),
+// loaded once. EPI bit 0: bias, bit 1: GELU.
+template <bool Q8, bool CHANNEL, int EPI>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
@@ -62,28 +73,31 @@ void gemm_kernel(GemmArgs a) {
     const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
     const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
     const unsigned m0 = tm * TM, n0 = tn * TN;
-    // Wave (wm, wn) owns output rows m0 + wm*128 .. +128 and columns n0 + wn*128 .. +128.
-    const unsigned wm = wave / 2, wn = wave % 2;
+    const unsigned wm = wave / 4, wn = wave % 4;   // wave rows m0 + wm*128, columns n0 + wn*64
     const unsigned ksteps = a.k / TK;
 
-    f32x16 acc[4][4];   // [n block][m block], C^T layout: lane = output row, regs = columns
+    f32x16 acc[2][4];   // [n block][m block], C^T layout: lane = output row, regs = columns
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
 
-    // Weight staging (q8): 256 rows x 64 int8 = 1024 16-byte chunks, 4 per thread.
-    i32x4 wq[4];
-    float wscale[4];
+    // Weight staging (q8): 256 rows x 64 int8 = 1024 16-byte chunks, 2 per thread.
+    i32x4 wq[2];
+    float wscale[2];
+    if constexpr (Q8 && CHANNEL) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) wscale[j] = a.scales[n0 + (tid + 512 * j) / 4];
+    }
     auto load_w = [&](unsigned kt) {
         if constexpr (Q8) {
             const int8_t *w8 = reinterpret_cast<const int8_t *>(a.w);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                unsigned c = tid + 256 * j, row = c / 4, part = c % 4;
-                size_t off = (size_t)(n0 + row) * a.k + kt * TK + part * 16;
-                wq[j] = *reinterpret_cast<const i32x4 *>(w8 + off);
-                wscale[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
+            for (int j = 0; j < 2; j++) {
+                unsigned c = tid + 512 * j, row = c / 4, part = c % 4;
+                wq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
+                if constexpr (!CHANNEL)
+                    wscale[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
             }
         }
     };
@@ -91,17 +105,20 @@ void gemm_kernel(GemmArgs a) {
         if constexpr (Q8) {
             uint8_t *ws = lds + stage * STAGE + TILE_BYTES;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                unsigned c = tid + 256 * j, row = c / 4, part = c % 4;
-                bf16x8 lo, hi;
+            for (int j = 0; j < 2; j++) {
+                unsigned c = tid + 512 * j, row = c / 4, part = c % 4;
+                bf16x8 half[2];
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    int q = (int)(int8_t)((wq[j][e / 4] >> (8 * (e % 4))) & 0xff);
-                    __bf16 v = (__bf16)((float)q * wscale[j]);
-                    if (e < 8) lo[e] = v; else hi[e - 8] = v;
+                for (int e = 0; e < 16; e += 2) {
+                    int word = wq[j][e / 4];
+                    f32x2 f = {(float)(int8_t)(word >> (8 * (e % 4))) * wscale[j],
+                               (float)(int8_t)(word >> (8 * (e % 4 + 1))) * wscale[j]};
+                    bf16x2 b = __builtin_convertvector(f, bf16x2);
+                    half[e / 8][e % 8] = b[0];
+                    half[e / 8][e % 8 + 1] = b[1];
                 }
-                *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, part * 2) * 16) = lo;
-                *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, part * 2 + 1) * 16) = hi;
+                *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, part * 2) * 16) = half[0];
+                *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, part * 2 + 1) * 16) = half[1];
             }
         }
     };
@@ -109,7 +126,7 @@ void gemm_kernel(GemmArgs a) {
     auto load_direct = [&](unsigned kt, int stage) {
         uint8_t *xs = lds + stage * STAGE;
 #pragma unroll
-        for (unsigned b = wave; b < 32; b += 4) {
+        for (unsigned b = wave; b < 32; b += 8) {
             unsigned row = 8 * b + lane / 8, ph = lane % 8;
             unsigned gm = min(m0 + row, a.m - 1);
             const uint16_t *src = a.x + (size_t)gm * a.k + kt * TK + swz(row, ph) * 8;
@@ -120,6 +137,18 @@ void gemm_kernel(GemmArgs a) {
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)wsrc,
                                                  (__attribute__((address_space(3))) void *)(xs + TILE_BYTES + b * 1024), 16, 0, 0);
             }
+        }
+    };
+    auto frags = [&](const uint8_t *xs, const uint8_t *ws, int ks, bf16x8 *wf, bf16x8 *xf) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            unsigned wr = wn * 64 + i * 32 + n32;
+            wf[i] = *reinterpret_cast<const bf16x8 *>(ws + wr * ROW_BYTES + swz(wr, ks * 2 + hf) * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            unsigned xr = wm * 128 + j * 32 + n32;
+            xf[j] = *reinterpret_cast<const bf16x8 *>(xs + xr * ROW_BYTES + swz(xr, ks * 2 + hf) * 16);
         }
     };
 
@@ -135,20 +164,17 @@ void gemm_kernel(GemmArgs a) {
         if (more) { load_direct(kt + 1, cur ^ 1); load_w(kt + 1); }
         const uint8_t *xs = lds + cur * STAGE;
         const uint8_t *ws = xs + TILE_BYTES;
+        // Fragments of k-step ks+1 are read while the MFMAs of ks run.
+        bf16x8 wf[2][2], xf[2][4];
+        frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ks++) {
-            bf16x8 wf[4], xf[4];
+            if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                unsigned wr = wn * 128 + i * 32 + n32, xr = wm * 128 + i * 32 + n32;
-                wf[i] = *reinterpret_cast<const bf16x8 *>(ws + wr * ROW_BYTES + swz(wr, ks * 2 + hf) * 16);
-                xf[i] = *reinterpret_cast<const bf16x8 *>(xs + xr * ROW_BYTES + swz(xr, ks * 2 + hf) * 16);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
         }
         if (more) store_w(cur ^ 1);
         wait_vm_loads();
@@ -156,24 +182,26 @@ void gemm_kernel(GemmArgs a) {
     }
 
     // Epilogue: lane holds output row m = m0 + wm*128 + j*32 + n32 and columns
-    // n0 + wn*128 + i*32 + g*8 + hf*4 + 0..3 for register group g.
+    // n0 + wn*64 + i*32 + g*8 + hf*4 + 0..3 for register group g.
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const unsigned row = m0 + wm * 128 + j * 32 + n32;
         if (row >= a.m) continue;
         uint16_t *dst = a.y + (size_t)row * a.n;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
-                const unsigned col = n0 + wn * 128 + i * 32 + g4 * 8 + hf * 4;
+                const unsigned col = n0 + wn * 64 + i * 32 + g4 * 8 + hf * 4;
                 u16x4 out;
+                u16x4 bias4 = {};
+                if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float v = acc[i][j][g4 * 4 + e];
-                    if (a.bias) v += bf16_to_f32(a.bias[col + e]);
+                    if constexpr (EPI & 1) v += bf16_to_f32(bias4[e]);
                     uint16_t b = f32_to_bf16(v);
-                    if (a.gelu) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
+                    if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
                     out[e] = b;
                 }
                 *reinterpret_cast<u16x4 *>(dst + col) = out;
@@ -205,19 +233,31 @@ __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
     a.y[idx] = b;
 }
 
-template <bool Q8>
+template <bool Q8, bool CHANNEL, int EPI>
 int launch_tiled(h3_gpu *g, const GemmArgs &a) {
     constexpr size_t shared = 2 * STAGE;
     static bool configured = false;
+    auto kernel = gemm_kernel<Q8, CHANNEL, EPI>;
     if (!configured) {
-        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)gemm_kernel<Q8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)shared), "GEMM shared memory"))
             return 0;
         configured = true;
     }
     unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
-    hipLaunchKernelGGL(gemm_kernel<Q8>, dim3(tiles), dim3(256), shared, g->compute, a);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(512), shared, g->compute, a);
     return h3_launch_status(g, Q8 ? "W8A16 GEMM" : "BF16 GEMM");
+}
+
+template <bool Q8, bool CHANNEL>
+int launch_epi(h3_gpu *g, const GemmArgs &a) {
+    const int epi = (a.bias ? 1 : 0) | (a.gelu ? 2 : 0);
+    switch (epi) {
+    case 0: return launch_tiled<Q8, CHANNEL, 0>(g, a);
+    case 1: return launch_tiled<Q8, CHANNEL, 1>(g, a);
+    case 2: return launch_tiled<Q8, CHANNEL, 2>(g, a);
+    default: return launch_tiled<Q8, CHANNEL, 3>(g, a);
+    }
 }
 
 }  // namespace
@@ -232,7 +272,11 @@ int h3_gemm(h3_gpu *g, uint16_t *y, const uint16_t *x, const h3_gpu_tensor *w, c
     if (!h3_tensor_acquire(g, w)) return 0;
     int ok;
     const bool tiled = n % TN == 0 && k % TK == 0 && m >= 32 && (!w->q8 || a.group % 16 == 0);
-    if (tiled) ok = w->q8 ? launch_tiled<true>(g, a) : launch_tiled<false>(g, a);
+    if (tiled) {
+        if (!w->q8) ok = launch_epi<false, false>(g, a);
+        else if (a.group == k) ok = launch_epi<true, true>(g, a);
+        else ok = launch_epi<true, false>(g, a);
+    }
     else {
         size_t total = (size_t)m * n;
         hipLaunchKernelGGL(gemm_small, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, a, w->q8 ? 1 : 0);
