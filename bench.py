@@ -159,12 +159,50 @@ def gemm_leg(steps, warmup, m=32400, seed=4):
     return out
 
 
+def step_leg(steps, warmup):
+    """one full 40-block synthetic DiT denoise step (M = 32400
+    video + 1024 audio rows, hidden 5120, 40 heads, MLP 13824, W8A16 weights,
+    Sage attention over a 25%-density 128x128 block mask plus audio<->audio and
+    the diagonal, blocks 20-39 streamed from pinned host memory)."""
+    from h3cli_amd.runtime import DitSynth
+    t0 = time.perf_counter()
+    with DitSynth() as m:
+        setup = time.perf_counter() - t0
+        kept, total = m.kept_blocks()
+        rows = m.rows
+        cfg = m.config
+        for i in range(warmup):
+            m.step(step=i, dt=-0.02)
+        times = []
+        for i in range(steps):
+            t1 = time.perf_counter()
+            m.step(step=warmup + i, dt=-0.02)
+            times.append(time.perf_counter() - t1)
+        lat = m.read("latent")
+        finite = bool(np.all(np.isfinite(lat)))
+    sec = float(np.mean(times))
+    H = cfg.hidden
+    gemm = 2.0 * rows * (H * 3 * H + H * H + 2 * H * cfg.mlp) * cfg.blocks
+    head = 2.0 * rows * cfg.latent * H * 2
+    density = kept / total
+    attn = attention_flops(rows, cfg.heads) * density * cfg.blocks
+    log(f"[bench] full step: {sec:.3f} s/step (setup {setup:.1f} s), mask density {density:.4f}, finite={finite}")
+    return {"workload": "full synthetic 40-block DiT denoise step (BASELINE config 5)",
+            "s_per_step": round(sec, 4), "steps": steps, "warmup": warmup, "rows": rows,
+            "blocks": cfg.blocks, "streamed_blocks": cfg.blocks - cfg.streamed_first,
+            "mask_kept_blocks": kept, "mask_total_blocks": total, "mask_density": round(density, 5),
+            "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop_effective": round(attn / 1e12, 3),
+            "achieved_tflops": round((gemm + head + attn) / sec / 1e12, 2), "latent_finite": finite,
+            "setup_s": round(setup, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,gemm")
+    ap.add_argument("--legs", default="attention,sage,gemm,step")
+    ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "192")))
     args = ap.parse_args()
@@ -200,7 +238,7 @@ def main():
                        "heads": HEADS, "head_dim": DIM, "batch": 1, "flop_convention": "4*S^2*H*D"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16, "unit": "TFLOP/s",
                          "frac": round(tflops / PEAK_BF16, 4), "traffic": None,
-                         "kernel": "attn_bf16_kernel<4,false>"},
+                         "kernel": "attn_bf16_kernel<8,1,2,false,true>"},
         })
         if not args.no_cpu:
             log(f"[bench] CPU baseline on {args.cpu_rows} rows")
@@ -224,6 +262,8 @@ def main():
                               "frac_of_fp8_peak": round(eff / PEAK_FP8, 4)}
     if "gemm" in legs:
         result["gemm"] = gemm_leg(args.steps, args.warmup)
+    if "step" in legs:
+        result["step"] = step_leg(args.step_count, 1)
     print(json.dumps(result), flush=True)
 
 

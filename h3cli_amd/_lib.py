@@ -94,6 +94,31 @@ _SIGNATURES = {
     "h3_hip_synthetic_block_mask": (C.c_uint, [_p, C.c_uint, C.c_uint, C.c_uint, C.c_double, C.c_uint64]),
 }
 
+class DitSynthConfig(C.Structure):
+    """include/h3_dit_synth.h h3_hip_dit_synth_config."""
+    _fields_ = [("blocks", _u32), ("hidden", _u32), ("heads", _u32), ("mlp", _u32),
+                ("frames", _u32), ("height", _u32), ("width", _u32), ("audio_rows", _u32),
+                ("latent", _u32), ("streamed_first", _u32), ("mask_density", _f),
+                ("attention_mode", _i), ("eps", _f), ("time", _f), ("seed", C.c_uint64)]
+
+
+_SIGNATURES.update({
+    "h3_hip_dit_synth_default": (DitSynthConfig, []),
+    "h3_hip_dit_synth_create": (_p, [_p, C.POINTER(DitSynthConfig), C.c_char_p, _sz]),
+    "h3_hip_dit_synth_free": (None, [_p]),
+    "h3_hip_dit_synth_step": (_i, [_p, _i, _f]),
+    "h3_hip_dit_synth_tensor": (_p, [_p, C.c_char_p]),
+    "h3_hip_dit_synth_rows": (_u32, [_p]),
+    "h3_hip_dit_synth_kept_blocks": (C.c_uint64, [_p, C.POINTER(C.c_uint64)]),
+    "h3_gpu_add_bf16": (_i, [_p, _p, _p, _p, _u32]),
+    "h3_gpu_silu_bf16": (_i, [_p, _p, _p, _u32]),
+    "h3_gpu_cast_f32_to_bf16": (_i, [_p, _p, _p, _u32]),
+    "h3_gpu_cast_bf16_to_f32": (_i, [_p, _p, _p, _u32]),
+    "h3_hip_q8_new": (_p, [_p, _u32, _u32, _u32]),
+    "h3_hip_fill_q8_random": (_i, [_p, _p, C.c_uint64, _f, _f]),
+    "h3_hip_tensor_copy_to_host": (_i, [_p, _p, _sz]),
+})
+
 # Declared in include/*.h but optional for this module's loader (added as the
 # backend grows); listed so the export test can check them when present.
 _OPTIONAL = set()

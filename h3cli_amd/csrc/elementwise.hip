@@ -340,3 +340,67 @@ extern "C" int h3_gpu_euler_bf16(h3_gpu *g, h3_gpu_tensor *sample, size_t offset
                        (const uint16_t *)last->data, (const uint16_t *)previous->data, n, delta, ratio);
     return h3_launch_status(g, "Euler");
 }
+
+namespace {
+__global__ __launch_bounds__(256) void add_kernel(uint16_t *out, const uint16_t *l, const uint16_t *r, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(bf16_to_f32(l[i]) + bf16_to_f32(r[i]));
+}
+__global__ __launch_bounds__(256) void silu_kernel(uint16_t *out, const uint16_t *in, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = bf16_to_f32(in[i]);
+    out[i] = f32_to_bf16(v / (1.0f + expf(-v)));
+}
+}  // namespace
+
+// gpu.h:750 (src/cuda/cuda_kernels.cuh:1170-1177).
+extern "C" int h3_gpu_add_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *l, const h3_gpu_tensor *r, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, l, H3_GPU_BF16, n, "add left") || !h3_require(g, r, H3_GPU_BF16, n, "add right") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "add output"))
+        return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)l->data, (const uint16_t *)r->data, (size_t)n);
+    return h3_launch_status(g, "add");
+}
+
+// gpu.h:564 (src/cuda/cuda_kernels.cuh:796-803).
+extern "C" int h3_gpu_silu_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, in, H3_GPU_BF16, n, "SiLU input") || !h3_require(g, out, H3_GPU_BF16, n, "SiLU output")) return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)in->data, (size_t)n);
+    return h3_launch_status(g, "SiLU");
+}
+
+namespace {
+__global__ __launch_bounds__(256) void cast_f32_bf16_kernel(uint16_t *out, const float *in, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(in[i]);
+}
+__global__ __launch_bounds__(256) void cast_bf16_f32_kernel(float *out, const uint16_t *in, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = bf16_to_f32(in[i]);
+}
+}  // namespace
+
+// gpu.h:329 and gpu.h:331.
+extern "C" int h3_gpu_cast_f32_to_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, in, H3_GPU_F32, n, "cast input") || !h3_require(g, out, H3_GPU_BF16, n, "cast output")) return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute,
+                       (uint16_t *)out->data, (const float *)in->data, (size_t)n);
+    return h3_launch_status(g, "cast f32->bf16");
+}
+extern "C" int h3_gpu_cast_bf16_to_f32(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, in, H3_GPU_BF16, n, "cast input") || !h3_require(g, out, H3_GPU_F32, n, "cast output")) return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute,
+                       (float *)out->data, (const uint16_t *)in->data, (size_t)n);
+    return h3_launch_status(g, "cast bf16->f32");
+}

@@ -34,3 +34,38 @@ extern "C" int h3_hip_fill_normal_bf16(h3_gpu *g, h3_gpu_tensor *t, uint64_t see
                        (uint16_t *)t->data, count, seed, scale);
     return h3_launch_status(g, "normal fill");
 }
+
+// Seeded random W8A16 weights: code = (u % 255) - 127 with u = splitmix64((seed << 40) + i)
+// over the codes, and scale = lo + (hi - lo) * ((v >> 11) * 2^-53) with
+// v = splitmix64((seed << 40) + (1 << 39) + j) over the scales.
+__global__ __launch_bounds__(256) void fill_q8(int8_t *codes, size_t n, float *scales, size_t ns, uint64_t seed,
+                                              float lo, float hi) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    uint64_t base = seed << 40;
+    if (i < n) codes[i] = (int8_t)((int)(splitmix64(base + i) % 255u) - 127);
+    if (i < ns) {
+        double u = (double)(splitmix64(base + (1ull << 39) + i) >> 11) * 0x1.0p-53;
+        scales[i] = lo + (hi - lo) * (float)u;
+    }
+}
+
+extern "C" int h3_hip_fill_q8_random(h3_gpu *g, h3_gpu_tensor *t, uint64_t seed, float lo, float hi) {
+    if (!h3_launch_ready(g) || !t || !t->q8) return h3_set_error(g, "q8 fill: needs a q8 weight and an active command");
+    size_t n = t->elements, ns = (size_t)t->q8_rows * ((t->q8_cols + t->q8_group - 1) / t->q8_group);
+    size_t total = n > ns ? n : ns;
+    hipLaunchKernelGGL(fill_q8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, (int8_t *)t->data, n,
+                       t->q8_scales, ns, seed, lo, hi);
+    return h3_launch_status(g, "q8 fill");
+}
+
+// Device -> host copy of a tensor (q8: codes then scales, the stream_host layout).
+extern "C" int h3_hip_tensor_copy_to_host(h3_gpu_tensor *t, void *dst, size_t bytes) {
+    if (!t || !dst) return 0;
+    h3_gpu *g = t->owner;
+    size_t code_bytes = t->bytes, scale_bytes = 0;
+    if (t->q8) scale_bytes = (size_t)t->q8_rows * ((t->q8_cols + t->q8_group - 1) / t->q8_group) * 4;
+    if (bytes != code_bytes + scale_bytes) return h3_set_error(g, "copy to host: %zu bytes, tensor holds %zu", bytes, code_bytes + scale_bytes);
+    return h3_hip_check(g, hipStreamSynchronize(g->compute), "copy fence") &&
+           h3_hip_check(g, hipMemcpy(dst, t->data, code_bytes, hipMemcpyDeviceToHost), "copy codes") &&
+           (!scale_bytes || h3_hip_check(g, hipMemcpy((char *)dst + code_bytes, t->q8_scales, scale_bytes, hipMemcpyDeviceToHost), "copy scales"));
+}

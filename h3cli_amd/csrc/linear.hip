@@ -78,6 +78,10 @@ static h3_gpu_tensor *q8_tensor(h3_gpu *g, uint32_t rows, uint32_t cols, uint32_
     return t;
 }
 
+extern "C" h3_gpu_tensor *h3_hip_q8_new(h3_gpu *g, uint32_t rows, uint32_t cols, uint32_t group) {
+    return g ? q8_tensor(g, rows, cols, group) : nullptr;
+}
+
 extern "C" h3_gpu_tensor *h3_hip_q8_from_packed(h3_gpu *g, const int8_t *codes, const float *scales, uint32_t rows,
                                                 uint32_t cols, uint32_t group) {
     if (!g || !codes || !scales) return nullptr;

@@ -1,0 +1,373 @@
+/* Synthetic DiT denoise step on the operator ABI (include/h3_dit_synth.h).
+ *
+ * The block body follows the reference's run_block op sequence
+ * (src/denoise/dit.c:2286-2539): AdaLN (modulation slots 0/1) -> QKV projection
+ * -> Q/K RoPE split -> DiT attention -> output projection -> gate (slot 2) fused
+ * with the second AdaLN (slots 3/4) -> MLP -> gate (slot 5). The block loop and
+ * weight streaming follow encode_forward (dit.c:2577-3038): resident blocks run
+ * from device memory; the rest are copied from pinned host memory into two
+ * alternating device slots on the copy stream, the copy for block b+1 overlapping
+ * the compute of block b. The modulation comes from the 256-d sinusoidal
+ * timestep features of dit_schedule.c:152-162 (cos for the first half, sin for
+ * the second) through a small time MLP, computed once at creation as the
+ * reference precomputes its per-step modulation. */
+#include "h3_dit_synth.h"
+#include "h3_hip_ext.h"
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define SLOTS 6u
+#define TIME_FEATURES 256u
+#define PROJ 4 /* qkv, out, up, down */
+
+struct h3_hip_dit_synth {
+    h3_gpu *gpu;
+    h3_hip_dit_synth_config c;
+    uint32_t video_rows, rows;
+    /* weights */
+    h3_gpu_tensor **proj;          /* [blocks][PROJ], NULL for streamed blocks */
+    h3_gpu_tensor *slot[2][PROJ];  /* streaming slots */
+    void **host;                   /* [blocks] pinned copies of streamed blocks */
+    size_t host_bytes[PROJ];
+    h3_gpu_tensor **norm1, **norm2, **mod; /* per block */
+    h3_gpu_tensor *patch, *head, *head_norm, *head_mod;
+    /* activations and tables */
+    h3_gpu_tensor *latent, *latent_bf16, *x, *xn, *qkv, *q, *k, *v, *attn, *o, *h, *f, *vel;
+    h3_gpu_tensor *cos_t, *sin_t, *row_map;
+    uint64_t kept, total;
+};
+
+static int fail(char *error, size_t size, const char *fmt, ...) {
+    if (error && size) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(error, size, fmt, ap);
+        va_end(ap);
+    }
+    return 0;
+}
+
+h3_hip_dit_synth_config h3_hip_dit_synth_default(void) {
+    h3_hip_dit_synth_config c;
+    memset(&c, 0, sizeof(c));
+    c.blocks = 40; c.hidden = 5120; c.heads = 40; c.mlp = 13824;
+    c.frames = 27; c.height = 30; c.width = 40; c.audio_rows = 1024;
+    c.latent = 256; c.streamed_first = 20; c.mask_density = 0.25f;
+    c.attention_mode = 1; c.eps = 1e-6f; c.time = 0.5f; c.seed = 5;
+    return c;
+}
+
+static uint16_t to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* BF16 tensor of `n` values offset + spread * N(0,1) from the device generator. */
+static h3_gpu_tensor *normal_tensor(h3_gpu *g, size_t n, uint64_t seed, float spread, float offset) {
+    h3_gpu_tensor *t = h3_gpu_tensor_new_bf16(g, n);
+    if (!t) return NULL;
+    if (!h3_hip_fill_normal_bf16(g, t, seed, spread, n)) { h3_gpu_tensor_free(t); return NULL; }
+    if (offset != 0.f) {
+        uint16_t *host = malloc(n * 2);
+        if (!host) { h3_gpu_tensor_free(t); return NULL; }
+        if (!h3_gpu_synchronize(g) || !h3_gpu_tensor_read_bf16(t, host, n)) { free(host); h3_gpu_tensor_free(t); return NULL; }
+        for (size_t i = 0; i < n; i++) {
+            uint32_t u = (uint32_t)host[i] << 16;
+            float v;
+            memcpy(&v, &u, 4);
+            host[i] = to_bf16(v + offset);
+        }
+        int ok = h3_gpu_tensor_write_bf16(t, host, n);
+        free(host);
+        if (!ok) { h3_gpu_tensor_free(t); return NULL; }
+    }
+    return t;
+}
+
+/* 3D RoPE tables over the video grid (rotate-half pairs d <-> d+64, frame / row /
+ * column split 44/42/42 channels, theta 1e4); audio rows get angle 0. */
+static int rope_tables(h3_hip_dit_synth *m) {
+    const uint32_t half = 64, split[3] = {22, 21, 21};
+    size_t n = (size_t)m->rows * half;
+    uint16_t *c = malloc(n * 2), *s = malloc(n * 2);
+    if (!c || !s) { free(c); free(s); return 0; }
+    for (uint32_t r = 0; r < m->rows; r++) {
+        uint32_t pos[3] = {0, 0, 0};
+        if (r < m->video_rows) {
+            pos[0] = r / (m->c.height * m->c.width);
+            pos[1] = (r / m->c.width) % m->c.height;
+            pos[2] = r % m->c.width;
+        }
+        uint32_t j = 0;
+        for (int axis = 0; axis < 3; axis++)
+            for (uint32_t i = 0; i < split[axis]; i++, j++) {
+                double inv = pow(10000.0, -2.0 * i / (2.0 * split[axis]));
+                double angle = pos[axis] * inv;
+                c[(size_t)r * half + j] = to_bf16((float)cos(angle));
+                s[(size_t)r * half + j] = to_bf16((float)sin(angle));
+            }
+    }
+    m->cos_t = h3_gpu_tensor_from_bf16(m->gpu, c, n);
+    m->sin_t = h3_gpu_tensor_from_bf16(m->gpu, s, n);
+    free(c); free(s);
+    return m->cos_t && m->sin_t;
+}
+
+/* Modulation [2 rows (video, audio), 6 slots, hidden] per block = a shared time
+ * projection of the timestep features plus a per-block table; the head uses 2
+ * slots (shift, scale). */
+static int modulation(h3_hip_dit_synth *m, char *error, size_t size) {
+    h3_gpu *g = m->gpu;
+    const uint32_t H = m->c.hidden;
+    float feat[2 * TIME_FEATURES];
+    uint16_t featb[2 * TIME_FEATURES];
+    for (int row = 0; row < 2; row++)
+        for (uint32_t i = 0; i < TIME_FEATURES / 2; i++) {
+            float freq = expf(-logf(10000.0f) * (float)i / (float)(TIME_FEATURES / 2));
+            float angle = m->c.time * freq;
+            feat[row * TIME_FEATURES + i] = cosf(angle);
+            feat[row * TIME_FEATURES + TIME_FEATURES / 2 + i] = sinf(angle);
+        }
+    for (uint32_t i = 0; i < 2 * TIME_FEATURES; i++) featb[i] = to_bf16(feat[i]);
+    uint64_t sd = m->c.seed * 1000003ull;
+    h3_gpu_tensor *tf = h3_gpu_tensor_from_bf16(g, featb, 2 * TIME_FEATURES);
+    h3_gpu_tensor *w1 = normal_tensor(g, (size_t)H * TIME_FEATURES, sd + 1, 1.0f / 16.0f, 0.f);
+    h3_gpu_tensor *w2 = normal_tensor(g, (size_t)SLOTS * H * H, sd + 2, 0.1f / sqrtf((float)H), 0.f);
+    h3_gpu_tensor *t1 = h3_gpu_tensor_new_bf16(g, 2 * (size_t)H), *t2 = h3_gpu_tensor_new_bf16(g, 2 * (size_t)H);
+    h3_gpu_tensor *shared = h3_gpu_tensor_new_bf16(g, 2 * (size_t)SLOTS * H);
+    int ok = tf && w1 && w2 && t1 && t2 && shared &&
+             h3_gpu_linear_bf16(g, t1, tf, w1, NULL, 2, TIME_FEATURES, H) &&
+             h3_gpu_silu_bf16(g, t2, t1, 2 * H) &&
+             h3_gpu_linear_bf16(g, shared, t2, w2, NULL, 2, H, SLOTS * H);
+    for (uint32_t b = 0; ok && b < m->c.blocks; b++) {
+        h3_gpu_tensor *table = normal_tensor(g, 2 * (size_t)SLOTS * H, sd + 100 + b, 0.05f, 0.f);
+        m->mod[b] = h3_gpu_tensor_new_bf16(g, 2 * (size_t)SLOTS * H);
+        ok = table && m->mod[b] && h3_gpu_add_bf16(g, m->mod[b], shared, table, 2 * SLOTS * H) && h3_gpu_synchronize(g);
+        h3_gpu_tensor_free(table);
+    }
+    m->head_mod = ok ? normal_tensor(g, 2 * 2 * (size_t)H, sd + 3, 0.05f, 0.f) : NULL;
+    ok = ok && m->head_mod && h3_gpu_synchronize(g);
+    h3_gpu_tensor_free(tf); h3_gpu_tensor_free(w1); h3_gpu_tensor_free(w2);
+    h3_gpu_tensor_free(t1); h3_gpu_tensor_free(t2); h3_gpu_tensor_free(shared);
+    return ok ? 1 : fail(error, size, "modulation: %s", h3_gpu_error(g));
+}
+
+static void proj_shape(const h3_hip_dit_synth_config *c, int j, uint32_t *n, uint32_t *k) {
+    switch (j) {
+    case 0: *n = 3 * c->hidden; *k = c->hidden; break;
+    case 1: *n = c->hidden; *k = c->hidden; break;
+    case 2: *n = c->mlp; *k = c->hidden; break;
+    default: *n = c->hidden; *k = c->mlp; break;
+    }
+}
+
+static h3_gpu_tensor *q8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed) {
+    h3_gpu_tensor *t = h3_hip_q8_new(g, n, k, k);
+    if (t && !h3_hip_fill_q8_random(g, t, seed, 1e-3f, 1e-2f)) { h3_gpu_tensor_free(t); t = NULL; }
+    return t;
+}
+
+static int weights(h3_hip_dit_synth *m, char *error, size_t size) {
+    h3_gpu *g = m->gpu;
+    const h3_hip_dit_synth_config *c = &m->c;
+    uint32_t streamed = c->blocks - (c->streamed_first < c->blocks ? c->streamed_first : c->blocks);
+    for (int j = 0; j < PROJ; j++) {
+        uint32_t n, k;
+        proj_shape(c, j, &n, &k);
+        m->host_bytes[j] = (size_t)n * k + (size_t)n * 4;
+        if (streamed)
+            for (int s = 0; s < 2; s++)
+                if (!(m->slot[s][j] = h3_hip_q8_new(g, n, k, k))) return fail(error, size, "slot: %s", h3_gpu_error(g));
+    }
+    size_t block_bytes = 0;
+    for (int j = 0; j < PROJ; j++) block_bytes += m->host_bytes[j];
+    for (uint32_t b = 0; b < c->blocks; b++) {
+        int resident = b < c->streamed_first;
+        if (!resident && !(m->host[b] = h3_hip_host_alloc(g, block_bytes)))
+            return fail(error, size, "pinned block %u: %s", b, h3_gpu_error(g));
+        size_t at = 0;
+        for (int j = 0; j < PROJ; j++) {
+            uint32_t n, k;
+            proj_shape(c, j, &n, &k);
+            h3_gpu_tensor *t = q8_random(g, n, k, c->seed * 7919ull + b * 8 + j);
+            if (!t) return fail(error, size, "block %u weight %d: %s", b, j, h3_gpu_error(g));
+            if (resident) m->proj[(size_t)b * PROJ + j] = t;
+            else {
+                int ok = h3_gpu_synchronize(g) && h3_hip_tensor_copy_to_host(t, (char *)m->host[b] + at, m->host_bytes[j]);
+                h3_gpu_tensor_free(t);
+                if (!ok) return fail(error, size, "block %u host copy: %s", b, h3_gpu_error(g));
+            }
+            at += m->host_bytes[j];
+        }
+        m->norm1[b] = normal_tensor(g, c->hidden, c->seed * 31 + 2 * b, 0.1f, 1.0f);
+        m->norm2[b] = normal_tensor(g, c->hidden, c->seed * 31 + 2 * b + 1, 0.1f, 1.0f);
+        if (!m->norm1[b] || !m->norm2[b] || !h3_gpu_synchronize(g)) return fail(error, size, "norms: %s", h3_gpu_error(g));
+    }
+    m->patch = normal_tensor(g, (size_t)c->hidden * c->latent, c->seed * 37 + 1, 1.0f / sqrtf((float)c->latent), 0.f);
+    m->head = normal_tensor(g, (size_t)c->latent * c->hidden, c->seed * 37 + 2, 1.0f / sqrtf((float)c->hidden), 0.f);
+    m->head_norm = normal_tensor(g, c->hidden, c->seed * 37 + 3, 0.1f, 1.0f);
+    if (!m->patch || !m->head || !m->head_norm || !h3_gpu_synchronize(g)) return fail(error, size, "head: %s", h3_gpu_error(g));
+    return 1;
+}
+
+static h3_gpu_tensor *bf16_buffer(h3_gpu *g, size_t n) { return h3_gpu_tensor_new_bf16(g, n); }
+
+h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_config *config, char *error, size_t size) {
+    if (!g || !config) { fail(error, size, "missing context or config"); return NULL; }
+    const h3_hip_dit_synth_config *c = config;
+    if (!c->blocks || !c->heads || c->hidden != c->heads * 128 || !c->mlp || c->mlp % 256 || c->hidden % 256 ||
+        !c->latent || c->latent % 256 || !c->frames || !c->height || !c->width) {
+        fail(error, size, "synthetic DiT: hidden must be heads*128, hidden/mlp/latent multiples of 256");
+        return NULL;
+    }
+    h3_hip_dit_synth *m = calloc(1, sizeof(*m));
+    if (!m) { fail(error, size, "out of host memory"); return NULL; }
+    m->gpu = g;
+    m->c = *c;
+    m->video_rows = c->frames * c->height * c->width;
+    m->rows = m->video_rows + c->audio_rows;
+    m->proj = calloc((size_t)c->blocks * PROJ, sizeof(*m->proj));
+    m->host = calloc(c->blocks, sizeof(*m->host));
+    m->norm1 = calloc(c->blocks, sizeof(*m->norm1));
+    m->norm2 = calloc(c->blocks, sizeof(*m->norm2));
+    m->mod = calloc(c->blocks, sizeof(*m->mod));
+    if (!m->proj || !m->host || !m->norm1 || !m->norm2 || !m->mod) { fail(error, size, "out of host memory"); goto bad; }
+    if (!h3_gpu_dit_attention_configure(g, c->attention_mode == 1 ? 1 : 0)) {
+        fail(error, size, "attention configure: %s", h3_gpu_error(g));
+        goto bad;
+    }
+    if (!h3_gpu_begin(g)) { fail(error, size, "begin: %s", h3_gpu_error(g)); goto bad; }
+    if (!weights(m, error, size) || !modulation(m, error, size) || !rope_tables(m)) { h3_gpu_cancel(g); goto bad; }
+    {
+        const size_t R = m->rows, H = c->hidden;
+        uint32_t *map = malloc(R * 4);
+        if (!map) { h3_gpu_cancel(g); goto bad; }
+        for (size_t r = 0; r < R; r++) map[r] = r < m->video_rows ? 0u : 1u;
+        m->row_map = h3_gpu_tensor_from_u32(g, map, R);
+        free(map);
+        m->latent = h3_gpu_tensor_new_f32(g, R * c->latent);
+        m->latent_bf16 = bf16_buffer(g, R * c->latent);
+        m->x = bf16_buffer(g, R * H); m->xn = bf16_buffer(g, R * H);
+        m->qkv = bf16_buffer(g, R * H * 3);
+        m->q = bf16_buffer(g, R * H); m->k = bf16_buffer(g, R * H); m->v = bf16_buffer(g, R * H);
+        m->attn = bf16_buffer(g, R * H); m->o = bf16_buffer(g, R * H);
+        m->h = bf16_buffer(g, R * c->mlp); m->f = bf16_buffer(g, R * H);
+        m->vel = bf16_buffer(g, R * c->latent);
+        if (!m->row_map || !m->latent || !m->latent_bf16 || !m->x || !m->xn || !m->qkv || !m->q || !m->k || !m->v ||
+            !m->attn || !m->o || !m->h || !m->f || !m->vel) {
+            fail(error, size, "activations: %s", h3_gpu_error(g));
+            h3_gpu_cancel(g);
+            goto bad;
+        }
+        /* Seeded N(0,1) latent. */
+        h3_gpu_tensor *init = normal_tensor(g, R * c->latent, c->seed * 41 + 1, 1.0f, 0.f);
+        int ok = init && h3_gpu_cast_bf16_to_f32(g, m->latent, init, (uint32_t)(R * c->latent)) && h3_gpu_synchronize(g);
+        h3_gpu_tensor_free(init);
+        if (!ok) { fail(error, size, "latent: %s", h3_gpu_error(g)); h3_gpu_cancel(g); goto bad; }
+    }
+    if (!h3_gpu_submit(g)) { fail(error, size, "setup: %s", h3_gpu_error(g)); goto bad; }
+    if (c->mask_density >= 0.f) {
+        uint32_t blocks = (m->rows + 127) / 128;
+        uint8_t *mask = malloc((size_t)blocks * blocks);
+        if (!mask) goto bad;
+        m->kept = h3_hip_synthetic_block_mask(mask, m->rows, m->video_rows, 128, c->mask_density, c->seed);
+        m->total = (uint64_t)blocks * blocks;
+        int ok = m->kept && h3_hip_dit_block_mask(g, mask, blocks, blocks, 128);
+        free(mask);
+        if (!ok) { fail(error, size, "mask: %s", h3_gpu_error(g)); goto bad; }
+    } else {
+        uint32_t blocks = (m->rows + 127) / 128;
+        m->kept = m->total = (uint64_t)blocks * blocks;
+    }
+    return m;
+bad:
+    h3_hip_dit_synth_free(m);
+    return NULL;
+}
+
+void h3_hip_dit_synth_free(h3_hip_dit_synth *m) {
+    if (!m) return;
+    h3_gpu *g = m->gpu;
+    if (m->proj) for (size_t i = 0; i < (size_t)m->c.blocks * PROJ; i++) h3_gpu_tensor_free(m->proj[i]);
+    for (int s = 0; s < 2; s++) for (int j = 0; j < PROJ; j++) h3_gpu_tensor_free(m->slot[s][j]);
+    size_t block_bytes = 0;
+    for (int j = 0; j < PROJ; j++) block_bytes += m->host_bytes[j];
+    if (m->host) for (uint32_t b = 0; b < m->c.blocks; b++) h3_hip_host_free(g, m->host[b], block_bytes);
+    for (uint32_t b = 0; b < m->c.blocks; b++) {
+        if (m->norm1) h3_gpu_tensor_free(m->norm1[b]);
+        if (m->norm2) h3_gpu_tensor_free(m->norm2[b]);
+        if (m->mod) h3_gpu_tensor_free(m->mod[b]);
+    }
+    h3_gpu_tensor *all[] = {m->patch, m->head, m->head_norm, m->head_mod, m->latent, m->latent_bf16, m->x, m->xn,
+                            m->qkv, m->q, m->k, m->v, m->attn, m->o, m->h, m->f, m->vel, m->cos_t, m->sin_t, m->row_map};
+    for (size_t i = 0; i < sizeof(all) / sizeof(*all); i++) h3_gpu_tensor_free(all[i]);
+    free(m->proj); free(m->host); free(m->norm1); free(m->norm2); free(m->mod);
+    free(m);
+}
+
+/* Queue the copy of streamed block b into its slot (b % 2) on the copy stream. */
+static int prefetch(h3_hip_dit_synth *m, uint32_t b) {
+    if (b >= m->c.blocks || b < m->c.streamed_first) return 1;
+    size_t at = 0;
+    for (int j = 0; j < PROJ; j++) {
+        if (!h3_hip_tensor_stream_host(m->slot[b % 2][j], (const char *)m->host[b] + at, m->host_bytes[j])) return 0;
+        at += m->host_bytes[j];
+    }
+    return 1;
+}
+
+int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
+    if (!m) return 0;
+    h3_gpu *g = m->gpu;
+    const h3_hip_dit_synth_config *c = &m->c;
+    const uint32_t R = m->rows, H = c->hidden, L = c->latent;
+    const float scale = 1.0f / sqrtf(128.0f);
+    if (!h3_gpu_begin(g)) return 0;
+    int ok = h3_gpu_dit_attention_noise(g, step, 0.5f, 0.5f) && prefetch(m, c->streamed_first) &&
+             h3_gpu_cast_f32_to_bf16(g, m->latent_bf16, m->latent, R * L) &&
+             h3_gpu_linear_bf16(g, m->x, m->latent_bf16, m->patch, NULL, R, L, H);
+    for (uint32_t b = 0; ok && b < c->blocks; b++) {
+        h3_gpu_tensor **w = b < c->streamed_first ? &m->proj[(size_t)b * PROJ] : m->slot[b % 2];
+        /* The next streamed block's copy overlaps this block's compute. */
+        if (b + 1 > c->streamed_first && !prefetch(m, b + 1)) { ok = 0; break; }
+        ok = h3_gpu_adaln_bf16(g, m->xn, m->x, m->norm1[b], m->mod[b], m->row_map, R, H, SLOTS, 0, 1, c->eps) &&
+             h3_gpu_linear_bf16(g, m->qkv, m->xn, w[0], NULL, R, H, 3 * H) &&
+             h3_gpu_qkv_rope_bf16(g, m->q, m->k, m->v, m->qkv, NULL, NULL, m->cos_t, m->sin_t, R, c->heads, 128, 64,
+                                  c->eps) &&
+             h3_gpu_dit_sdpa_bf16(g, m->attn, m->q, m->k, m->v, R, c->heads, 128, scale, 0, b, step) &&
+             h3_gpu_linear_bf16(g, m->o, m->attn, w[1], NULL, R, H, H) &&
+             h3_gpu_gate_adaln_bf16(g, m->x, m->xn, m->x, m->o, m->norm2[b], m->mod[b], m->mod[b], m->row_map, R, H,
+                                    SLOTS, 2, 3, 4, c->eps) &&
+             h3_hip_linear_gelu_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
+             h3_gpu_linear_bf16(g, m->f, m->h, w[3], NULL, R, c->mlp, H) &&
+             h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5);
+    }
+    ok = ok && h3_gpu_adaln_bf16(g, m->xn, m->x, m->head_norm, m->head_mod, m->row_map, R, H, 2, 0, 1, c->eps) &&
+         h3_gpu_linear_bf16(g, m->vel, m->xn, m->head, NULL, R, H, L) &&
+         h3_gpu_euler_bf16(g, m->latent, 0, m->vel, m->vel, R * L, dt, 0.0f);
+    if (!ok) {
+        h3_gpu_cancel(g);
+        return 0;
+    }
+    return h3_gpu_submit(g);
+}
+
+h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *m, const char *name) {
+    if (!m || !name) return NULL;
+    if (!strcmp(name, "latent")) return m->latent;
+    if (!strcmp(name, "hidden")) return m->x;
+    if (!strcmp(name, "velocity")) return m->vel;
+    return NULL;
+}
+
+uint32_t h3_hip_dit_synth_rows(const h3_hip_dit_synth *m) { return m ? m->rows : 0; }
+
+uint64_t h3_hip_dit_synth_kept_blocks(const h3_hip_dit_synth *m, uint64_t *total) {
+    if (total) *total = m ? m->total : 0;
+    return m ? m->kept : 0;
+}

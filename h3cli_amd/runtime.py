@@ -130,3 +130,58 @@ class Gpu:
         ms = C.c_float()
         self.check(self.lib.h3_hip_event_elapsed_ms(self.handle, a, b, C.byref(ms)), "elapsed")
         return ms.value
+
+
+class DitSynth:
+    """The synthetic DiT denoise step of include/h3_dit_synth.h on its own context."""
+
+    def __init__(self, **overrides):
+        self.lib = _lib.load()
+        cfg = self.lib.h3_hip_dit_synth_default()
+        for k, v in overrides.items():
+            setattr(cfg, k, v)
+        self.config = cfg
+        self.gpu = Gpu()
+        err = C.create_string_buffer(1024)
+        self.handle = self.lib.h3_hip_dit_synth_create(self.gpu.handle, C.byref(cfg), err, 1024)
+        if not self.handle:
+            msg = err.value.decode()
+            self.gpu.close()
+            raise H3Error(f"h3_hip_dit_synth_create: {msg}")
+
+    @property
+    def rows(self):
+        return self.lib.h3_hip_dit_synth_rows(self.handle)
+
+    def kept_blocks(self):
+        total = C.c_uint64()
+        kept = self.lib.h3_hip_dit_synth_kept_blocks(self.handle, C.byref(total))
+        return kept, total.value
+
+    def step(self, step=0, dt=-0.05):
+        if not self.lib.h3_hip_dit_synth_step(self.handle, step, dt):
+            raise H3Error(f"step: {self.gpu.error()}")
+
+    def read(self, name):
+        h = self.lib.h3_hip_dit_synth_tensor(self.handle, name.encode())
+        if not h:
+            raise H3Error(f"no tensor {name}")
+        n = self.lib.h3_gpu_tensor_elements(h)
+        dtype = self.lib.h3_gpu_tensor_dtype(h)
+        out = np.empty(n, dtype=_DTYPE_NP[dtype])
+        fn = {F32: self.lib.h3_gpu_tensor_read_f32, BF16: self.lib.h3_gpu_tensor_read_bf16}[dtype]
+        if not fn(h, out.ctypes.data, n):
+            raise H3Error(self.gpu.error())
+        return out
+
+    def close(self):
+        if self.handle:
+            self.lib.h3_hip_dit_synth_free(self.handle)
+            self.handle = None
+        self.gpu.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

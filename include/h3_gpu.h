@@ -233,6 +233,14 @@ int h3_gpu_grouped_qkv_linear_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *query, h3_gp
                                         const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
                                         uint32_t rows, uint32_t input_dim, uint32_t heads,
                                         uint32_t head_dim, uint32_t rope_half, float epsilon);
+/* gpu.h:329 and gpu.h:331. Element casts (round-to-nearest-even to BF16). */
+int h3_gpu_cast_f32_to_bf16(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *input, uint32_t elements);
+int h3_gpu_cast_bf16_to_f32(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *input, uint32_t elements);
+/* gpu.h:750. out = bf16(left + right). */
+int h3_gpu_add_bf16(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *left,
+                    const h3_gpu_tensor *right, uint32_t elements);
+/* gpu.h:564. out = bf16(x / (1 + exp(-x))). */
+int h3_gpu_silu_bf16(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *input, uint32_t elements);
 /* gpu.h:815-818. sample[offset+i] += delta*(last + ratio*(last - previous)). */
 int h3_gpu_euler_bf16(h3_gpu *gpu, h3_gpu_tensor *sample, size_t sample_offset,
                       const h3_gpu_tensor *last, const h3_gpu_tensor *previous,

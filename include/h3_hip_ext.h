@@ -31,6 +31,17 @@ int h3_hip_linear_gelu_bf16(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_ten
                             const h3_gpu_tensor *weight, const h3_gpu_tensor *bias,
                             uint32_t rows, uint32_t input_dim, uint32_t output_dim);
 
+/* An empty W8A16 weight (codes [rows, columns] and fp32 scales [rows,
+ * ceil(columns/group)] allocated on the device, contents undefined). */
+h3_gpu_tensor *h3_hip_q8_new(h3_gpu *gpu, uint32_t rows, uint32_t columns, uint32_t group);
+/* Seeded random W8A16 contents (requires an active command): code i =
+ * (splitmix64((seed << 40) + i) mod 255) - 127, scale j = lo + (hi - lo) *
+ * ((splitmix64((seed << 40) + 2^39 + j) >> 11) * 2^-53). */
+int h3_hip_fill_q8_random(h3_gpu *gpu, h3_gpu_tensor *weight, uint64_t seed, float lo, float hi);
+/* Synchronous device -> host copy of a tensor; for a q8 weight, dst receives the
+ * codes followed by the scales (the h3_hip_tensor_stream_host layout). */
+int h3_hip_tensor_copy_to_host(h3_gpu_tensor *tensor, void *dst, size_t bytes);
+
 /* Fixed block-sparse mask for main-DiT attention. mask is u8 [q_blocks, k_blocks]
  * (nonzero = keep) over block x block tiles; block must be 128 (or 64). While a
  * mask is bound, h3_gpu_dit_sdpa_bf16 computes softmax over the kept key tiles
