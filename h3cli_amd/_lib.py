@@ -117,6 +117,14 @@ _SIGNATURES.update({
     "h3_hip_q8_new": (_p, [_p, _u32, _u32, _u32]),
     "h3_hip_fill_q8_random": (_i, [_p, _p, C.c_uint64, _f, _f]),
     "h3_hip_tensor_copy_to_host": (_i, [_p, _p, _sz]),
+    "h3_hip_dit_subblock_policy": (_i, [_p, _f, _i]),
+    "h3_subblock_budget": (C.c_uint, [C.c_uint, _f]),
+    "h3_subblock_warmup": (_i, [_i]),
+    "h3_subblock_dense_reason": (C.c_char_p, [C.c_uint, C.c_uint, _i, _f, _i]),
+    "h3_attention_name": (C.c_char_p, [_i]),
+    "h3_attention_parse": (_i, [C.c_char_p, C.POINTER(_i)]),
+    "h3_attention_options": (_i, [_i, C.c_char_p, _sz]),
+    "h3_attention_preflight": (_i, [_i, C.c_char_p, _sz]),
 })
 
 # Declared in include/*.h but optional for this module's loader (added as the

@@ -6,6 +6,7 @@
 #include "common.h"
 #include "internal.h"
 #include "sage.h"
+#include "../../include/h3_policy.h"
 #include <cmath>
 #include <new>
 #include <vector>
@@ -16,6 +17,10 @@ struct h3_attention_state {
     bool configured = false;
     int mode = MODE_DEFAULT;
     int step = -1;
+    // SubBlock bypass policy (reference src/denoise/subblock.c:44-51): the
+    // request's sparsity and warmup; dense attention when a reason applies.
+    float subblock_sparsity = 0.75f;
+    int subblock_warmup = 0;
     // Bound block-sparse mask (128 x 128 tiles), compacted to kept 64-key tiles.
     bool masked = false;
     uint32_t mask_q_blocks = 0, mask_k_blocks = 0, mask_block = 0;
@@ -172,16 +177,23 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
     if ((head_major != 0 && head_major != 1) || step < 0)
         return h3_set_error(g, "DiT attention: head_major must be 0/1 and step >= 0");
     auto *s = g->attention;
+    bool masked = s->masked;
     if (s->mode == MODE_SUBBLOCK) {
         if (step != s->step) return h3_set_error(g, "SubBlock absolute step was not bound");
-        if (!s->masked) return h3_set_error(g, "SubBlock attention on HIP needs a bound block mask (h3_hip_dit_block_mask)");
+        const char *reason = h3_subblock_dense_reason(seq, block, step, s->subblock_sparsity, s->subblock_warmup);
+        if (reason) {
+            g->stats.subblock_bypass++;
+            masked = false;
+        } else if (!s->masked) {
+            return h3_set_error(g, "SubBlock attention on HIP needs a bound block mask (h3_hip_dit_block_mask)");
+        }
     }
     // A kept last 128-key block may list a 64-key tile wholly past the sequence
     // end; the kernels load zeros there and mask keys >= seq to -inf.
-    if (s->masked && (s->mask_q_blocks != (seq + 127) / 128 || s->mask_k_blocks != (seq + 127) / 128))
+    if (masked && (s->mask_q_blocks != (seq + 127) / 128 || s->mask_k_blocks != (seq + 127) / 128))
         return h3_set_error(g, "bound block mask does not match sequence %u", seq);
     return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), head_major != 0,
-                    s->mode == MODE_SAGE2 ? MODE_SAGE2 : MODE_DEFAULT, s->masked);
+                    s->mode == MODE_SAGE2 ? MODE_SAGE2 : MODE_DEFAULT, masked);
 }
 
 extern "C" int h3_gpu_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
@@ -195,4 +207,12 @@ extern "C" int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *g, h3_gpu_tensor *out,
                                                   uint32_t heads, uint32_t dim, float scale) {
     if (!g || !validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
     return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), true, MODE_DEFAULT, false);
+}
+
+extern "C" int h3_hip_dit_subblock_policy(h3_gpu *g, float sparsity, int warmup) {
+    if (!g) return 0;
+    if (!(sparsity >= 0.f) || sparsity >= 1.f) return h3_set_error(g, "SubBlock sparsity must be in [0, 1)");
+    g->attention->subblock_sparsity = sparsity;
+    g->attention->subblock_warmup = warmup;
+    return 1;
 }

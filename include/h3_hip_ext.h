@@ -58,6 +58,12 @@ int h3_hip_dit_block_mask(h3_gpu *gpu, const uint8_t *mask, uint32_t q_blocks,
 unsigned h3_hip_synthetic_block_mask(uint8_t *mask, unsigned seq, unsigned video_rows,
                                      unsigned block, double density, uint64_t seed);
 
+/* SubBlock (mode 4) bypass policy: the request's sparsity and warmup as passed
+ * to h3_subblock_dense_reason (reference src/denoise/subblock.c:44-51); a call
+ * for which a reason applies runs dense. Defaults: sparsity 0.75, warmup 0
+ * (= 10 steps); warmup < 0 disables the warmup rule. */
+int h3_hip_dit_subblock_policy(h3_gpu *gpu, float sparsity, int warmup);
+
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded
  * to a multiple of 64, padded rows zero):

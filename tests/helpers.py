@@ -32,7 +32,7 @@ def scale_bf16(scale):
     return float(bf16(synth.f32_to_bf16(np.float32(scale))))
 
 
-def sdpa(gpu, q, k, v, seq, heads, scale=None, head_major=False, dit=True, step=0):
+def sdpa(gpu, q, k, v, seq, heads, scale=None, head_major=False, dit=True, step=0, block=1):
     """Run the DiT attention entry point on bf16 arrays; returns bf16 bits
     shaped [seq, heads, 128] (head-major outputs are transposed back)."""
     lib = gpu.lib
@@ -43,7 +43,7 @@ def sdpa(gpu, q, k, v, seq, heads, scale=None, head_major=False, dit=True, step=
     gpu.begin()
     if dit:
         ok = lib.h3_gpu_dit_sdpa_bf16(gpu.handle, out.handle, tq.handle, tk.handle, tv.handle, seq, heads, 128,
-                                      scale, int(head_major), 0, step)
+                                      scale, int(head_major), block, step)
     elif head_major:
         ok = lib.h3_gpu_sdpa_bf16_head_major_output(gpu.handle, out.handle, tq.handle, tk.handle, tv.handle,
                                                     seq, heads, 128, scale)

@@ -1,0 +1,129 @@
+"""Host-side restatements in libh3hip.so checked bit for bit against the
+reference's own C sources, compiled where they lie by oracle/ref/Makefile into
+oracle/_ref/libh3ref.so (src/weights/q8.c, src/denoise/subblock.c,
+src/denoise/attention.c). Skipped when that library was not built (the GPU box
+has no /root/reference; the prebuilt file travels with the tree when present)."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+from h3cli_amd import _lib, synth
+
+REF = os.path.join(os.path.dirname(__file__), "..", "oracle", "_ref", "libh3ref.so")
+
+pytestmark = pytest.mark.skipif(not os.path.exists(REF), reason="oracle/_ref/libh3ref.so not built")
+
+
+def _bind(lib):
+    lib.h3_q8_layout.restype = C.c_int
+    lib.h3_q8_layout.argtypes = [C.c_uint32, C.c_uint32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    lib.h3_q8_pack_rows.restype = C.c_int
+    lib.h3_q8_pack_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32]
+    lib.h3_subblock_budget.restype = C.c_uint
+    lib.h3_subblock_budget.argtypes = [C.c_uint, C.c_float]
+    lib.h3_subblock_warmup.restype = C.c_int
+    lib.h3_subblock_warmup.argtypes = [C.c_int]
+    lib.h3_subblock_dense_reason.restype = C.c_char_p
+    lib.h3_subblock_dense_reason.argtypes = [C.c_uint, C.c_uint, C.c_int, C.c_float, C.c_int]
+    lib.h3_attention_name.restype = C.c_char_p
+    lib.h3_attention_name.argtypes = [C.c_int]
+    lib.h3_attention_parse.restype = C.c_int
+    lib.h3_attention_parse.argtypes = [C.c_char_p, C.POINTER(C.c_int)]
+    lib.h3_attention_options.restype = C.c_int
+    lib.h3_attention_options.argtypes = [C.c_int, C.c_char_p, C.c_size_t]
+    return lib
+
+
+@pytest.fixture(scope="module")
+def libs():
+    # RTLD_LOCAL keeps the two libraries' same-named symbols apart.
+    ref = _bind(C.CDLL(os.path.abspath(REF), mode=os.RTLD_LOCAL))
+    ours = _bind(C.CDLL(str(_lib.LIB_PATH), mode=os.RTLD_LOCAL))
+    return ours, ref
+
+
+def _layout(lib, rows, cols):
+    so, nb = C.c_size_t(), C.c_size_t()
+    ok = lib.h3_q8_layout(rows, cols, C.byref(so), C.byref(nb))
+    return ok, so.value, nb.value
+
+
+def test_q8_layout_matches_reference(libs):
+    ours, ref = libs
+    cases = [(0, 0), (1, 1), (1, 63), (3, 64), (5, 65), (7, 129), (5120, 5120), (13824, 5120),
+             (1, 2**31), (2**31, 2**31), (2**32 - 1, 2**32 - 1), (65536, 65536 * 4 + 3)]
+    for rows, cols in cases:
+        assert _layout(ours, rows, cols) == _layout(ref, rows, cols), (rows, cols)
+
+
+def _pack(lib, src, rows, cols):
+    codes = np.zeros(rows * cols, np.int8)
+    groups = -(-cols // 64)
+    scales = np.zeros(rows * groups, np.float32)
+    ok = lib.h3_q8_pack_rows(src.ctypes.data, codes.ctypes.data, scales.ctypes.data, rows, cols)
+    return ok, codes, scales
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(1, 1, 0), (3, 63, 1), (4, 64, 2), (5, 65, 3), (17, 300, 4),
+                                            (64, 5120, 5)])
+def test_q8_pack_matches_reference(libs, rows, cols, seed):
+    ours, ref = libs
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(rows * cols) * rng.choice([1e-3, 1.0, 30.0], rows * cols)).astype(np.float32)
+    x[rng.integers(0, x.size, max(1, x.size // 50))] = 0.0
+    src = synth.f32_to_bf16(x)
+    okr, cr, sr = _pack(ref, src, rows, cols)
+    oko, co, so = _pack(ours, src, rows, cols)
+    assert okr == oko == 1
+    assert np.array_equal(cr, co)
+    assert np.array_equal(sr.view(np.uint32), so.view(np.uint32))
+
+
+def test_q8_pack_edge_values_match_reference(libs):
+    ours, ref = libs
+    bits = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x7F7F, 0xFF7F, 0x3F80, 0xBF80, 0x0080, 0x4000] * 13,
+                    np.uint16)[:128]
+    for rows, cols in ((1, 128), (2, 64), (128, 1)):
+        okr, cr, sr = _pack(ref, bits, rows, cols)
+        oko, co, so = _pack(ours, bits, rows, cols)
+        assert okr == oko
+        assert np.array_equal(cr, co) and np.array_equal(sr.view(np.uint32), so.view(np.uint32))
+    for bad in (0x7F80, 0xFF80, 0x7FC0):  # +inf, -inf, NaN are rejected by both
+        b = bits.copy()
+        b[37] = bad
+        assert _pack(ref, b, 2, 64)[0] == _pack(ours, b, 2, 64)[0] == 0
+
+
+def test_subblock_budget_matches_reference(libs):
+    ours, ref = libs
+    sparsities = [0.0, 0.1, 0.5, 0.75, 0.875, 0.9, 0.99, 0.999999, 1.0, -0.1, float("nan"), float("inf")]
+    for blocks in list(range(0, 80)) + [506, 507, 1000, 2**20, 2**32 - 1]:
+        for s in sparsities:
+            assert ours.h3_subblock_budget(blocks, s) == ref.h3_subblock_budget(blocks, s), (blocks, s)
+
+
+def test_subblock_dense_reason_matches_reference(libs):
+    ours, ref = libs
+    for warmup in (-1, 0, 1, 10, 25):
+        assert ours.h3_subblock_warmup(warmup) == ref.h3_subblock_warmup(warmup)
+        for step in (-5, 0, 9, 10, 11, 30):
+            for block in (0, 1, 39):
+                for seq in (0, 64, 4095, 4096, 4097, 32400, 100000):
+                    for s in (0.0, 0.5, 0.75, 0.99):
+                        args = (seq, block, step, s, warmup)
+                        assert ours.h3_subblock_dense_reason(*args) == ref.h3_subblock_dense_reason(*args), args
+
+
+def test_attention_names_match_reference(libs):
+    ours, ref = libs
+    for mode in range(-2, 7):
+        assert ours.h3_attention_name(mode) == ref.h3_attention_name(mode)
+        eo, er = C.create_string_buffer(256), C.create_string_buffer(256)
+        assert ours.h3_attention_options(mode, eo, 256) == ref.h3_attention_options(mode, er, 256)
+        assert eo.value == er.value
+    for text in (b"default", b"sage2++", b"sage3", b"sol", b"subblock", b"Sage2++", b"", b"dense"):
+        mo, mr = C.c_int(-7), C.c_int(-7)
+        assert ours.h3_attention_parse(text, C.byref(mo)) == ref.h3_attention_parse(text, C.byref(mr))
+        assert mo.value == mr.value

@@ -26,14 +26,16 @@ def make_gpu(mode):
     return g
 
 
-@pytest.mark.parametrize("mode", [0, 4])
-@pytest.mark.parametrize("seq,video", [(1000, 900), (2100, 1700)])
+@pytest.mark.parametrize("mode,seq,video", [(0, 1000, 900), (0, 2100, 1700), (4, 4200, 3800)])
 def test_masked_bf16(mode, seq, video):
     print(f"[sparse bf16] mode={mode} seq={seq}", flush=True)
     g = make_gpu(mode)
     try:
         if mode == 4:
             g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.5, 0.5), "noise")
+            # Warmup off; block 1 of a sequence above the 4096-row "short"
+            # threshold is not bypassed, so the bound mask applies.
+            g.check(g.lib.h3_hip_dit_subblock_policy(g.handle, 0.75, -1), "policy")
         mask = oracle.block_mask(seq, video, 128, 0.25, seed=seq)
         bind_mask(g, mask)
         q, k, v = synth.attention_inputs(seq, 2, seed=seq, scale=1.0)
@@ -69,12 +71,30 @@ def test_masked_sage():
 def test_subblock_requires_mask_and_step():
     g = make_gpu(4)
     try:
-        seq = 256
+        seq = 4200
         q, k, v = synth.attention_inputs(seq, 1, seed=1)
         with pytest.raises(RuntimeError):
             sdpa(g, q, k, v, seq, 1, step=0)  # step not bound
-        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.5, 0.5), "noise")
+        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 12, 0.5, 0.5), "noise")
         with pytest.raises(RuntimeError):
-            sdpa(g, q, k, v, seq, 1, step=0)  # no mask bound
+            sdpa(g, q, k, v, seq, 1, step=12, block=3)  # sparse call without a bound mask
     finally:
         g.close()
+
+
+def test_subblock_dense_bypass_matches_dense():
+    """Calls for which the reference's bypass rules apply (warmup steps, probe
+    block 0, short sequences) run dense even with a mask bound."""
+    seq, video = 1000, 900
+    g = make_gpu(4)
+    d = Gpu()
+    try:
+        bind_mask(g, oracle.block_mask(seq, video, 128, 0.25, seed=1))
+        q, k, v = synth.attention_inputs(seq, 2, seed=5)
+        dense = sdpa(d, q, k, v, seq, 2)
+        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 3, 0.5, 0.5), "noise")
+        for block in (0, 5):  # warmup (step 3 < 10) and probe / short
+            assert np.array_equal(sdpa(g, q, k, v, seq, 2, step=3, block=block), dense)
+    finally:
+        g.close()
+        d.close()
