@@ -118,6 +118,25 @@ _SIGNATURES.update({
     "h3_hip_fill_q8_random": (_i, [_p, _p, C.c_uint64, _f, _f]),
     "h3_hip_tensor_copy_to_host": (_i, [_p, _p, _sz]),
     "h3_hip_dit_subblock_policy": (_i, [_p, _f, _i]),
+    # the rest of the reference surface implemented here (include/h3_gpu_surface.h)
+    "h3_gpu_adaln_bf16_offset": (_i, [_p, _p, _p, _sz, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _f]),
+    "h3_gpu_rms_norm_bf16": (_i, [_p, _p, _p, _p, _u32, _u32, _f]),
+    "h3_gpu_head_rms_norm_bf16": (_i, [_p, _p, _p, _u32, _u32, _u32, _f]),
+    "h3_gpu_sub_bf16": (_i, [_p, _p, _p, _p, _u32]),
+    "h3_gpu_silu_mul_bf16": (_i, [_p, _p, _p, _p, _u32]),
+    "h3_gpu_patch_linear_bf16": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32]),
+    "h3_gpu_patch_linear_bf16_offset": (_i, [_p, _p, _sz, _p, _sz, _p, _p, _u32, _u32, _u32]),
+    "h3_gpu_patch_linear_bf16_map": (_i, [_p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32]),
+    "h3_gpu_copy_bf16": (_i, [_p, _p, _sz, _p, _sz, _sz]),
+    "h3_gpu_copy_f32": (_i, [_p, _p, _sz, _p, _sz, _sz]),
+    "h3_gpu_tensor_load_bf16": (_p, [_p, C.c_char_p, C.c_uint64, _sz]),
+    "h3_gpu_tensor_load_f32": (_p, [_p, C.c_char_p, C.c_uint64, _sz]),
+    "h3_gpu_plan_weights": (_i, [_p, C.c_uint64, C.c_uint64]),
+    "h3_gpu_plan_bf16_weights": (_i, [_p, C.c_uint64, C.c_uint64, C.c_uint64, _i, _i, _p]),
+    "h3_gpu_weight_plan_compatible": (_i, [_p, _i]),
+    "h3_gpu_dit_sol_layout": (_i, [_p, _p]),
+    "h3_gpu_profile_set_label": (None, [_p, C.c_char_p]),
+    "h3_gpu_profile_mark": (None, [_p, C.c_char_p]),
     "h3_subblock_budget": (C.c_uint, [C.c_uint, _f]),
     "h3_subblock_warmup": (_i, [_i]),
     "h3_subblock_dense_reason": (C.c_char_p, [C.c_uint, C.c_uint, _i, _f, _i]),

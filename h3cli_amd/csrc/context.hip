@@ -96,6 +96,7 @@ extern "C" h3_gpu *h3_gpu_create(const char *shader_source_path, char *error, si
     h3_gpu *g = new (std::nothrow) h3_gpu();
     if (!g) { if (error && error_size) snprintf(error, error_size, "out of host memory"); return nullptr; }
     g->device = device;
+    g->created = now_seconds();
     g->profiling = getenv("H3_PROFILE") != nullptr;
     if (const char *v = getenv("H3_HIP_ATTENTION_VARIANT")) g->attention_variant = atoi(v);
     // Both streams keep the default priority.
@@ -198,6 +199,7 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_alloc(h3_gpu *g, size_t elements, h3_gpu
     if (e != hipSuccess) {
         size_t free_b = 0, total_b = 0; hipMemGetInfo(&free_b, &total_b);
         h3_set_error(g, "tensor allocation of %zu bytes failed: %s (free %.2f GiB)", alloc, hipGetErrorString(e), free_b / 1073741824.0);
+        if (e == hipErrorOutOfMemory) g->allocation_failed = true;
         delete t; hipGetLastError(); return nullptr;
     }
     if (storage != H3_GPU_DEVICE_ONLY) { g->stats.pinned_bytes += alloc; g->stats.peak_pinned_bytes = std::max(g->stats.peak_pinned_bytes, g->stats.pinned_bytes); }
@@ -396,16 +398,16 @@ static int fill_end(h3_gpu *g, h3_gpu_tensor *t) {
     return 1;
 }
 
-static int file_into(h3_gpu_tensor *t, const char *path, uint64_t offset, size_t n, bool streaming,
-                     char *error, size_t error_size) {
-    if (!t || !path || t->dtype != H3_GPU_BF16 || t->q8 || n > t->elements) return 0;
+static int file_into(h3_gpu_tensor *t, const char *path, uint64_t offset, size_t n, h3_gpu_dtype dtype,
+                     bool streaming, char *error, size_t error_size) {
+    if (!t || !path || t->dtype != dtype || t->q8 || n > t->elements) return 0;
     h3_gpu *g = t->owner;
     int ok = 1;
     int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) { if (error && error_size) snprintf(error, error_size, "%s: %s", path, strerror(errno)); return 0; }
     std::lock_guard<std::mutex> lock(g->copy_mutex);
     double started = now_seconds();
-    size_t bytes = n * 2;
+    size_t bytes = n * item_size(dtype);
     ok = streaming_init(g) && fill_begin(g, t);
     auto *s = g->streaming;
     unsigned slot = 0;
@@ -436,10 +438,49 @@ static int file_into(h3_gpu_tensor *t, const char *path, uint64_t offset, size_t
 }
 
 extern "C" int h3_gpu_tensor_read_file_bf16(h3_gpu_tensor *t, const char *p, uint64_t off, size_t n, char *e, size_t s) {
-    return file_into(t, p, off, n, false, e, s);
+    return file_into(t, p, off, n, H3_GPU_BF16, false, e, s);
 }
 extern "C" int h3_gpu_tensor_stream_file_bf16(h3_gpu_tensor *t, const char *p, uint64_t off, size_t n, char *e, size_t s) {
-    return file_into(t, p, off, n, true, e, s);
+    return file_into(t, p, off, n, H3_GPU_BF16, true, e, s);
+}
+
+// gpu.h:220-224 (src/cuda/gpu_cuda.cu:843-846): a new device tensor filled from a file.
+static h3_gpu_tensor *load_file(h3_gpu *g, const char *path, uint64_t offset, size_t n, h3_gpu_dtype dtype) {
+    h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, n, dtype, H3_GPU_DEVICE_ONLY);
+    if (t && !file_into(t, path, offset, n, dtype, false, g->error, sizeof(g->error))) {
+        h3_gpu_tensor_free(t);
+        t = nullptr;
+    }
+    return t;
+}
+extern "C" h3_gpu_tensor *h3_gpu_tensor_load_bf16(h3_gpu *g, const char *p, uint64_t off, size_t n) {
+    return load_file(g, p, off, n, H3_GPU_BF16);
+}
+extern "C" h3_gpu_tensor *h3_gpu_tensor_load_f32(h3_gpu *g, const char *p, uint64_t off, size_t n) {
+    return load_file(g, p, off, n, H3_GPU_F32);
+}
+// Tensors here are always device (or pinned) allocations, never file mappings.
+extern "C" int h3_gpu_tensor_is_file_mapped(const h3_gpu_tensor *t) { (void)t; return 0; }
+
+// gpu.h:333-338 (src/cuda/gpu_cuda.cu:847-856): ordered device-to-device copy on the compute stream.
+static int copy_tensor(h3_gpu *g, h3_gpu_tensor *d, size_t dst, const h3_gpu_tensor *s, size_t src, size_t n,
+                       h3_gpu_dtype dtype) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!d || !s || d->dtype != dtype || s->dtype != dtype || d->q8 || s->q8 || dst > d->elements ||
+        n > d->elements - dst || src > s->elements || n > s->elements - src)
+        return h3_set_error(g, "tensor copy: dtype or range mismatch");
+    if (!n) return 1;
+    size_t z = item_size(dtype);
+    g->stats.d2d_bytes += n * z;
+    return h3_hip_check(g, hipMemcpyAsync((char *)d->data + dst * z, (const char *)s->data + src * z, n * z,
+                                          hipMemcpyDeviceToDevice, g->compute), "tensor D2D") &&
+           h3_launch_status(g, "tensor D2D");
+}
+extern "C" int h3_gpu_copy_bf16(h3_gpu *g, h3_gpu_tensor *d, size_t dst, const h3_gpu_tensor *s, size_t src, size_t n) {
+    return copy_tensor(g, d, dst, s, src, n, H3_GPU_BF16);
+}
+extern "C" int h3_gpu_copy_f32(h3_gpu *g, h3_gpu_tensor *d, size_t dst, const h3_gpu_tensor *s, size_t src, size_t n) {
+    return copy_tensor(g, d, dst, s, src, n, H3_GPU_F32);
 }
 
 extern "C" void *h3_hip_host_alloc(h3_gpu *g, size_t bytes) {

@@ -33,17 +33,21 @@ struct AdaLNArgs {
     float eps;
 };
 
-// One wave per row. With GATE, the row is first gated (residual + branch * gate,
+// One wave per row. MODE 0: AdaLN. MODE 1 (gate_adaln): the row is first gated (residual + branch * gate,
 // rounded to BF16 and stored) and the AdaLN then normalizes that BF16 row, as the
 // reference's two-kernel composition does (src/cuda/gpu_cuda.cu:1118-1120).
-template <bool GATE>
+// MODE 2: plain RMSNorm y = bf16(x * rsqrt(mean x^2 + eps) * w), no modulation
+// (src/cuda/cuda_kernels.cuh:805-833).
+enum { ADALN = 0, GATE_ADALN = 1, RMS_NORM = 2 };
+template <int MODE>
 __global__ __launch_bounds__(256) void adaln_kernel(AdaLNArgs a) {
+    constexpr bool GATE = MODE == GATE_ADALN;
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned row = blockIdx.x * 4 + wave;
     if (row >= a.rows) return;
     const unsigned chunks = a.width / 8;
     const size_t base = (size_t)row * a.width;
-    const size_t mbase = (size_t)a.row_map[row] * a.slots * a.width;
+    const size_t mbase = MODE == RMS_NORM ? 0 : (size_t)a.row_map[row] * a.slots * a.width;
     float v[MAX_CHUNKS][8];
     float sumsq = 0.f;
 #pragma unroll
@@ -72,13 +76,18 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdaLNArgs a) {
         unsigned c = lane + 64 * i;
         if (c >= chunks) break;
         u16x8 wr = *reinterpret_cast<const u16x8 *>(a.weight + c * 8);
-        u16x8 sh = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.shift_slot * a.width + c * 8);
-        u16x8 sc = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.scale_slot * a.width + c * 8);
         u16x8 o;
+        if constexpr (MODE == RMS_NORM) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float normalized = v[i][e] * inv * bf16_to_f32(wr[e]);
-            o[e] = f32_to_bf16(fmaf(normalized, 1.0f + bf16_to_f32(sc[e]), bf16_to_f32(sh[e])));
+            for (int e = 0; e < 8; e++) o[e] = f32_to_bf16(v[i][e] * inv * bf16_to_f32(wr[e]));
+        } else {
+            u16x8 sh = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.shift_slot * a.width + c * 8);
+            u16x8 sc = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.scale_slot * a.width + c * 8);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float normalized = v[i][e] * inv * bf16_to_f32(wr[e]);
+                o[e] = f32_to_bf16(fmaf(normalized, 1.0f + bf16_to_f32(sc[e]), bf16_to_f32(sh[e])));
+            }
         }
         *reinterpret_cast<u16x8 *>(a.out + base + c * 8) = o;
     }
@@ -215,21 +224,47 @@ int check_map(h3_gpu *g, const h3_gpu_tensor *map, uint32_t rows, const char *wh
 
 }  // namespace
 
-extern "C" int h3_gpu_adaln_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w,
-                                 const h3_gpu_tensor *mod, const h3_gpu_tensor *map, uint32_t rows, uint32_t width,
-                                 uint32_t slots, uint32_t shift, uint32_t scale, float eps) {
+// gpu.h:593 (src/cuda/cuda_reference_wrappers.cuh:604): AdaLN of rows starting at
+// element `offset` of the input (a multiple of 8 here, for 16-byte rows).
+extern "C" int h3_gpu_adaln_bf16_offset(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, size_t offset,
+                                        const h3_gpu_tensor *w, const h3_gpu_tensor *mod, const h3_gpu_tensor *map,
+                                        uint32_t rows, uint32_t width, uint32_t slots, uint32_t shift, uint32_t scale,
+                                        float eps) {
     size_t n = (size_t)rows * width;
     if (!h3_launch_ready(g)) return 0;
-    if (!rows || !width || width % 8 || width > 64 * MAX_CHUNKS * 8 || shift >= slots || scale >= slots)
-        return h3_set_error(g, "AdaLN: width must be a multiple of 8 up to 8192 and slots valid");
-    if (!h3_require(g, in, H3_GPU_BF16, n, "AdaLN input") || !h3_require(g, w, H3_GPU_BF16, width, "AdaLN norm") ||
+    if (!rows || !width || width % 8 || width > 64 * MAX_CHUNKS * 8 || shift >= slots || scale >= slots || offset % 8)
+        return h3_set_error(g, "AdaLN: width and input offset must be multiples of 8, width up to 8192, slots valid");
+    if (!in || offset > in->elements) return h3_set_error(g, "AdaLN input offset out of range");
+    if (!h3_require(g, in, H3_GPU_BF16, offset + n, "AdaLN input") || !h3_require(g, w, H3_GPU_BF16, width, "AdaLN norm") ||
         !h3_require(g, mod, H3_GPU_BF16, (size_t)slots * width, "AdaLN modulation") || !check_map(g, map, rows, "AdaLN") ||
         !h3_require(g, out, H3_GPU_BF16, n, "AdaLN output"))
         return 0;
-    AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data, nullptr, (const uint16_t *)w->data,
+    AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data + offset, nullptr, (const uint16_t *)w->data,
                 (const uint16_t *)mod->data, nullptr, (const uint32_t *)map->data, rows, width, slots, shift, scale, 0, eps};
-    hipLaunchKernelGGL(adaln_kernel<false>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    hipLaunchKernelGGL(adaln_kernel<ADALN>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
     return h3_launch_status(g, "AdaLN");
+}
+
+extern "C" int h3_gpu_adaln_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w,
+                                 const h3_gpu_tensor *mod, const h3_gpu_tensor *map, uint32_t rows, uint32_t width,
+                                 uint32_t slots, uint32_t shift, uint32_t scale, float eps) {
+    return h3_gpu_adaln_bf16_offset(g, out, in, 0, w, mod, map, rows, width, slots, shift, scale, eps);
+}
+
+// gpu.h:566 (src/cuda/cuda_reference_wrappers.cuh:498, kernel cuda_kernels.cuh:805-833).
+extern "C" int h3_gpu_rms_norm_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w,
+                                    uint32_t rows, uint32_t width, float eps) {
+    size_t n = (size_t)rows * width;
+    if (!h3_launch_ready(g)) return 0;
+    if (!rows || !width || width % 8 || width > 64 * MAX_CHUNKS * 8)
+        return h3_set_error(g, "RMSNorm: width must be a multiple of 8 up to 8192");
+    if (!h3_require(g, in, H3_GPU_BF16, n, "RMSNorm input") || !h3_require(g, w, H3_GPU_BF16, width, "RMSNorm weight") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "RMSNorm output"))
+        return 0;
+    AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data, nullptr, (const uint16_t *)w->data,
+                nullptr, nullptr, nullptr, rows, width, 0, 0, 0, 0, eps};
+    hipLaunchKernelGGL(adaln_kernel<RMS_NORM>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    return h3_launch_status(g, "RMSNorm");
 }
 
 extern "C" int h3_gpu_gate_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *res, const h3_gpu_tensor *branch,
@@ -269,7 +304,7 @@ extern "C" int h3_gpu_gate_adaln_bf16(h3_gpu *g, h3_gpu_tensor *gated, h3_gpu_te
     AdaLNArgs a{(uint16_t *)out->data, (uint16_t *)gated->data, (const uint16_t *)res->data, (const uint16_t *)branch->data,
                 (const uint16_t *)w->data, (const uint16_t *)norm_mod->data, (const uint16_t *)gate_mod->data,
                 (const uint32_t *)map->data, rows, width, slots, shift, scale, gate_slot, eps};
-    hipLaunchKernelGGL(adaln_kernel<true>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    hipLaunchKernelGGL(adaln_kernel<GATE_ADALN>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
     return h3_launch_status(g, "gate AdaLN");
 }
 
@@ -403,4 +438,162 @@ extern "C" int h3_gpu_cast_bf16_to_f32(h3_gpu *g, h3_gpu_tensor *out, const h3_g
     hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute,
                        (float *)out->data, (const uint16_t *)in->data, (size_t)n);
     return h3_launch_status(g, "cast bf16->f32");
+}
+
+namespace {
+__global__ __launch_bounds__(256) void sub_kernel(uint16_t *out, const uint16_t *l, const uint16_t *r, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(bf16_to_f32(l[i]) - bf16_to_f32(r[i]));
+}
+__global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t *out, const uint16_t *gate, const uint16_t *up, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = bf16_to_f32(gate[i]);
+    out[i] = f32_to_bf16(v / (1.0f + expf(-v)) * bf16_to_f32(up[i]));
+}
+
+// In-place per-head RMSNorm, one wave per (row, head), head_dim <= 256.
+__global__ __launch_bounds__(256) void head_rms_norm_kernel(uint16_t *t, const uint16_t *w, unsigned seq, unsigned heads,
+                                                            unsigned dim, float eps) {
+    const size_t items = (size_t)seq * heads, item = (size_t)blockIdx.x * 4 + threadIdx.x / 64;
+    const unsigned lane = threadIdx.x % 64;
+    if (item >= items) return;
+    uint16_t *p = t + item * dim;
+    float v[4], ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned d = lane + 64 * i;
+        v[i] = d < dim ? bf16_to_f32(p[d]) : 0.f;
+        ss = fmaf(v[i], v[i], ss);
+    }
+    const float inv = rsqrtf(wave_sum(ss) / (float)dim + eps);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned d = lane + 64 * i;
+        if (d < dim) p[d] = f32_to_bf16(v[i] * inv * bf16_to_f32(w[d]));
+    }
+}
+
+// FP32 patch projection with BF16 output: y[map(r), n] = bf16(bias[n] + sum_k x[r,k] W[n,k]),
+// k ascending from the bias (the accumulation order of src/cuda/cuda_kernels.cuh:237-265).
+// 64x64 output tile per 256 threads, 4x4 outputs per thread, K staged through LDS.
+__global__ __launch_bounds__(256) void patch_linear_kernel(uint16_t *out, const float *x, const float *w, const float *bias,
+                                                           const uint32_t *map, unsigned out_rows, unsigned m,
+                                                           unsigned k, unsigned n) {
+    __shared__ float xs[16][65], ws[16][65];
+    const unsigned tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const unsigned row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
+    float acc[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        unsigned c = col0 + tx + 16 * j;
+        float b = bias && c < n ? bias[c] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i][j] = b;
+    }
+    for (unsigned k0 = 0; k0 < k; k0 += 16) {
+        // 64 rows x 16 k of X and 64 cols x 16 k of W; thread loads 4 of each.
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            unsigned r = ty + 16 * i, kk = k0 + tx;
+            xs[tx][r] = row0 + r < m && kk < k ? x[(size_t)(row0 + r) * k + kk] : 0.f;
+            ws[tx][r] = col0 + r < n && kk < k ? w[(size_t)(col0 + r) * k + kk] : 0.f;
+        }
+        __syncthreads();
+        const unsigned kn = min(16u, k - k0);
+        for (unsigned kk = 0; kk < kn; kk++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xs[kk][ty + 16 * i], ws[kk][tx + 16 * j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned r = row0 + ty + 16 * i;
+        if (r >= m) continue;
+        unsigned orow = map ? map[r] : r;
+        if (orow >= out_rows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            unsigned c = col0 + tx + 16 * j;
+            if (c < n) out[(size_t)orow * n + c] = f32_to_bf16(acc[i][j]);
+        }
+    }
+}
+
+int patch_linear(h3_gpu *g, h3_gpu_tensor *o, size_t oo, const h3_gpu_tensor *x, size_t xo, const h3_gpu_tensor *w,
+                 const h3_gpu_tensor *b, const h3_gpu_tensor *map, uint32_t out_rows, uint32_t m, uint32_t k, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!o || !x || !w || o->dtype != H3_GPU_BF16 || x->dtype != H3_GPU_F32 || w->dtype != H3_GPU_F32 ||
+        xo > x->elements || (size_t)m * k > x->elements - xo || oo > o->elements ||
+        (size_t)out_rows * n > o->elements - oo || w->elements < (size_t)k * n ||
+        (b && (b->dtype != H3_GPU_F32 || b->elements < n)))
+        return h3_set_error(g, "patch linear: F32 input/weight/bias and BF16 output of the stated sizes required");
+    if (map && (map->dtype != H3_GPU_U32 || map->elements < m)) return h3_set_error(g, "patch linear row map");
+    if (!m || !n) return 1;
+    dim3 grid((n + 63) / 64, (m + 63) / 64);
+    hipLaunchKernelGGL(patch_linear_kernel, grid, dim3(256), 0, g->compute, (uint16_t *)o->data + oo,
+                       (const float *)x->data + xo, (const float *)w->data, b ? (const float *)b->data : nullptr,
+                       map ? (const uint32_t *)map->data : nullptr, out_rows, m, k, n);
+    g->stats.linear_dispatches++;
+    return h3_launch_status(g, "patch linear");
+}
+}  // namespace
+
+// gpu.h:753 (src/cuda/cuda_kernels.cuh:1179-1185).
+extern "C" int h3_gpu_sub_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *l, const h3_gpu_tensor *r, uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, l, H3_GPU_BF16, n, "sub left") || !h3_require(g, r, H3_GPU_BF16, n, "sub right") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "sub output"))
+        return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(sub_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)l->data, (const uint16_t *)r->data, (size_t)n);
+    return h3_launch_status(g, "sub");
+}
+
+// gpu.h:845 (src/cuda/cuda_kernels.cuh:1321-1329).
+extern "C" int h3_gpu_silu_mul_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *gate, const h3_gpu_tensor *up,
+                                    uint32_t n) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!h3_require(g, gate, H3_GPU_BF16, n, "SiLU-mul gate") || !h3_require(g, up, H3_GPU_BF16, n, "SiLU-mul up") ||
+        !h3_require(g, out, H3_GPU_BF16, n, "SiLU-mul output"))
+        return 0;
+    if (!n) return 1;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, g->compute, (uint16_t *)out->data,
+                       (const uint16_t *)gate->data, (const uint16_t *)up->data, (size_t)n);
+    return h3_launch_status(g, "SiLU-mul");
+}
+
+// gpu.h:733 (src/cuda/cuda_reference_wrappers.cuh:732, kernel cuda_kernels.cuh:1117-1133).
+extern "C" int h3_gpu_head_rms_norm_bf16(h3_gpu *g, h3_gpu_tensor *t, const h3_gpu_tensor *w, uint32_t seq,
+                                         uint32_t heads, uint32_t dim, float eps) {
+    if (!h3_launch_ready(g)) return 0;
+    if (!dim || dim > 256) return h3_set_error(g, "head RMSNorm: head_dim must be 1..256");
+    if (!h3_require(g, t, H3_GPU_BF16, (size_t)seq * heads * dim, "head RMSNorm tensor") ||
+        !h3_require(g, w, H3_GPU_BF16, dim, "head RMSNorm weight"))
+        return 0;
+    if (!seq || !heads) return 1;
+    hipLaunchKernelGGL(head_rms_norm_kernel, dim3(blocks_for((size_t)seq * heads, 4)), dim3(256), 0, g->compute,
+                       (uint16_t *)t->data, (const uint16_t *)w->data, seq, heads, dim, eps);
+    return h3_launch_status(g, "head RMSNorm");
+}
+
+// gpu.h:307-325 (src/cuda/gpu_cuda.cu:1090-1108): the DiT patch-embedding projection.
+extern "C" int h3_gpu_patch_linear_bf16_offset(h3_gpu *g, h3_gpu_tensor *o, size_t oo, const h3_gpu_tensor *x, size_t xo,
+                                               const h3_gpu_tensor *w, const h3_gpu_tensor *b, uint32_t m, uint32_t k,
+                                               uint32_t n) {
+    return patch_linear(g, o, oo, x, xo, w, b, nullptr, m, m, k, n);
+}
+extern "C" int h3_gpu_patch_linear_bf16(h3_gpu *g, h3_gpu_tensor *o, const h3_gpu_tensor *x, const h3_gpu_tensor *w,
+                                        const h3_gpu_tensor *b, uint32_t m, uint32_t k, uint32_t n) {
+    return patch_linear(g, o, 0, x, 0, w, b, nullptr, m, m, k, n);
+}
+extern "C" int h3_gpu_patch_linear_bf16_map(h3_gpu *g, h3_gpu_tensor *o, const h3_gpu_tensor *x, const h3_gpu_tensor *w,
+                                            const h3_gpu_tensor *b, const h3_gpu_tensor *map, uint32_t out_rows, uint32_t m,
+                                            uint32_t k, uint32_t n) {
+    if (!map) return h3_set_error(g, "patch linear: row map required");
+    return patch_linear(g, o, 0, x, 0, w, b, map, out_rows, m, k, n);
 }

@@ -194,3 +194,43 @@ void oracle_euler(float *sample, const uint16_t *last, const uint16_t *previous,
         sample[i] = fmaf(delta, velocity, sample[i]);
     }
 }
+
+/* src/cuda/cuda_kernels.cuh:805-833: y = bf16(x * 1/sqrt(mean x^2 + eps) * w);
+ * the sum of squares by fmaf in column order. */
+void oracle_rms_norm(uint16_t *y, const uint16_t *x, const uint16_t *w, unsigned rows, unsigned width, float eps) {
+#pragma omp parallel for
+    for (unsigned r = 0; r < rows; r++) {
+        const uint16_t *xr = x + (size_t)r * width;
+        float sum = 0.f;
+        for (unsigned c = 0; c < width; c++) {
+            float v = oracle_bf16_to_f32(xr[c]);
+            sum = fmaf(v, v, sum);
+        }
+        float inv = 1.0f / sqrtf(sum / (float)width + eps);
+        for (unsigned c = 0; c < width; c++)
+            y[(size_t)r * width + c] = oracle_f32_to_bf16(oracle_bf16_to_f32(xr[c]) * inv * oracle_bf16_to_f32(w[c]));
+    }
+}
+
+/* src/cuda/cuda_kernels.cuh:1117-1133: the same RMSNorm per (row, head) of
+ * [seq, heads, dim], in place. */
+void oracle_head_rms_norm(uint16_t *t, const uint16_t *w, unsigned seq, unsigned heads, unsigned dim, float eps) {
+    oracle_rms_norm(t, t, w, seq * heads, dim, eps);
+}
+
+/* src/cuda/cuda_kernels.cuh:237-265 (and the row-mapped variant :267-300):
+ * y[map(r), n] = bf16(bias[n] + sum_k x[r,k] * W[n,k]) with FP32 fmaf in
+ * ascending k from the bias; rows whose map entry is >= out_rows are skipped. */
+void oracle_patch_linear(uint16_t *y, const float *x, const float *w, const float *bias, const uint32_t *map,
+                         unsigned out_rows, unsigned m, unsigned k, unsigned n) {
+#pragma omp parallel for
+    for (unsigned r = 0; r < m; r++) {
+        unsigned o = map ? map[r] : r;
+        if (o >= out_rows) continue;
+        for (unsigned c = 0; c < n; c++) {
+            float acc = bias ? bias[c] : 0.f;
+            for (unsigned i = 0; i < k; i++) acc = fmaf(x[(size_t)r * k + i], w[(size_t)c * k + i], acc);
+            y[(size_t)o * n + c] = oracle_f32_to_bf16(acc);
+        }
+    }
+}

@@ -54,6 +54,9 @@ def load():
         lib.oracle_gelu_tanh.restype = _f
         lib.oracle_swiglu.argtypes = [_p, _p, _u, _u]
         lib.oracle_euler.argtypes = [_p, _p, _p, C.c_size_t, _f, _f]
+        lib.oracle_rms_norm.argtypes = [_p, _p, _p, _u, _u, _f]
+        lib.oracle_head_rms_norm.argtypes = [_p, _p, _u, _u, _u, _f]
+        lib.oracle_patch_linear.argtypes = [_p, _p, _p, _p, _p, _u, _u, _u, _u]
         _lib = lib
     return _lib
 
@@ -256,3 +259,26 @@ def euler(sample, last, previous, delta, ratio):
     s = np.array(sample, np.float32, copy=True)
     load().oracle_euler(_ptr(s), _ptr(_u16(last)), _ptr(_u16(previous)), s.size, delta, ratio)
     return s
+
+
+def rms_norm(x, w, rows, width, eps):
+    y = np.zeros(rows * width, np.uint16)
+    load().oracle_rms_norm(_ptr(y), _ptr(_u16(x)), _ptr(_u16(w)), rows, width, eps)
+    return y
+
+
+def head_rms_norm(t, w, seq, heads, dim, eps):
+    y = np.array(_u16(t), copy=True)
+    load().oracle_head_rms_norm(_ptr(y), _ptr(_u16(w)), seq, heads, dim, eps)
+    return y
+
+
+def patch_linear(x, w, bias, m, k, n, row_map=None, out_rows=None):
+    out_rows = m if out_rows is None else out_rows
+    y = np.zeros(out_rows * n, np.uint16)
+    xf = np.ascontiguousarray(x, np.float32)
+    wf = np.ascontiguousarray(w, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    mp = None if row_map is None else np.ascontiguousarray(row_map, np.uint32)
+    load().oracle_patch_linear(_ptr(y), _ptr(xf), _ptr(wf), _ptr(b), _ptr(mp), out_rows, m, k, n)
+    return y

@@ -231,3 +231,88 @@ def test_activations_and_euler(gpu):
     want = sample.copy()
     want[7:7 + n] = oracle.euler(sample[7:7 + n], last, prev, -0.05, 0.25)
     assert np.array_equal(ts.read(), want)
+
+
+def test_adaln_offset_and_rms_norms(gpu):
+    rows, width, off = 45, 1024, 3 * 1024 + 8
+    x = synth.normal_bf16(21, off + rows * width, scale=2.0)
+    w = synth.normal_bf16(22, width, scale=0.5)
+    mod = modulation(23, 2, 6, width)
+    rmap = (np.arange(rows) % 2).astype(np.uint32)
+    tx, tw, tm, tr, ty = gpu.from_bf16(x), gpu.from_bf16(w), gpu.from_bf16(mod), gpu.from_u32(rmap), gpu.empty(rows * width)
+    run(gpu, gpu.lib.h3_gpu_adaln_bf16_offset, ty.handle, tx.handle, off, tw.handle, tm.handle, tr.handle, rows, width,
+        6, 3, 4, C.c_float(1e-6))
+    ref = oracle.adaln(x[off:], w, mod, rmap, rows, width, 6, 3, 4, 1e-6)
+    assert ulp_diff(ty.read(), ref).max() <= 1
+    with pytest.raises(RuntimeError):  # offset not a multiple of 8
+        run(gpu, gpu.lib.h3_gpu_adaln_bf16_offset, ty.handle, tx.handle, 3, tw.handle, tm.handle, tr.handle, rows,
+            width, 6, 3, 4, C.c_float(1e-6))
+    run(gpu, gpu.lib.h3_gpu_rms_norm_bf16, ty.handle, tx.handle, tw.handle, rows, width, C.c_float(1e-5))
+    assert ulp_diff(ty.read(), oracle.rms_norm(x[:rows * width], w, rows, width, 1e-5)).max() <= 1
+    seq, heads, dim = 131, 6, 128
+    t = synth.normal_bf16(24, seq * heads * dim, scale=3.0)
+    hw = synth.normal_bf16(25, dim, scale=0.5)
+    tt, thw = gpu.from_bf16(t), gpu.from_bf16(hw)
+    run(gpu, gpu.lib.h3_gpu_head_rms_norm_bf16, tt.handle, thw.handle, seq, heads, dim, C.c_float(1e-6))
+    assert ulp_diff(tt.read(), oracle.head_rms_norm(t, hw, seq, heads, dim, 1e-6)).max() <= 1
+
+
+def test_sub_silu_mul_copy(gpu):
+    n = 70001
+    a, b = synth.normal_bf16(31, n, scale=3.0), synth.normal_bf16(32, n, scale=3.0)
+    ta, tb, to = gpu.from_bf16(a), gpu.from_bf16(b), gpu.empty(n)
+    run(gpu, gpu.lib.h3_gpu_sub_bf16, to.handle, ta.handle, tb.handle, n)
+    want = synth.f32_to_bf16(bf16(a) - bf16(b))  # one rounding of an exact FP32 difference
+    assert np.array_equal(to.read(), want)
+    run(gpu, gpu.lib.h3_gpu_silu_mul_bf16, to.handle, ta.handle, tb.handle, n)
+    fa = bf16(a).astype(np.float64)
+    ref = synth.f32_to_bf16((fa / (1 + np.exp(-fa)) * bf16(b)).astype(np.float32))
+    assert ulp_diff(to.read(), ref).max() <= 1
+    dst = gpu.empty(n + 100)
+    run(gpu, gpu.lib.h3_gpu_copy_bf16, dst.handle, 100, ta.handle, 5, n - 5)
+    assert np.array_equal(dst.read()[100:100 + n - 5], a[5:])
+    with pytest.raises(RuntimeError):
+        run(gpu, gpu.lib.h3_gpu_copy_bf16, dst.handle, 101, ta.handle, 0, n)  # destination range overflows
+
+
+@pytest.mark.parametrize("m,k,n,mapped", [(33, 128, 320, False), (200, 48, 5120, False), (70, 100, 130, True)])
+def test_patch_linear_bit_exact(gpu, m, k, n, mapped):
+    """FP32 patch projection: bit-exact against the ordered-fma restatement."""
+    rng = np.random.default_rng(m + k + n)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(n * k) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    tx, tw, tb = gpu.from_f32(x), gpu.from_f32(w), gpu.from_f32(bias)
+    if mapped:
+        out_rows = m + 9
+        rmap = rng.permutation(out_rows)[:m].astype(np.uint32)
+        rmap[3] = out_rows + 4  # out-of-range entries are skipped
+        tr = gpu.from_u32(rmap)
+        zero = gpu.from_bf16(np.zeros(out_rows * n, np.uint16))
+        run(gpu, gpu.lib.h3_gpu_patch_linear_bf16_map, zero.handle, tx.handle, tw.handle, tb.handle, tr.handle,
+            out_rows, m, k, n)
+        got = zero.read()
+        want = oracle.patch_linear(x, w, bias, m, k, n, row_map=rmap, out_rows=out_rows)
+    else:
+        ty = gpu.empty(m * n)
+        run(gpu, gpu.lib.h3_gpu_patch_linear_bf16, ty.handle, tx.handle, tw.handle, tb.handle, m, k, n)
+        got = ty.read()
+        want = oracle.patch_linear(x, w, bias, m, k, n)
+    assert np.array_equal(got, want)
+
+
+def test_tensor_load_files(gpu):
+    vals = synth.normal(41, 1000).astype(np.float32)
+    with tempfile.NamedTemporaryFile(delete=False) as f:
+        f.write(b"\0" * 12 + vals.tobytes())
+        path = f.name
+    try:
+        h = gpu.lib.h3_gpu_tensor_load_f32(gpu.handle, path.encode(), 12, 1000)
+        assert h, gpu.error()
+        from h3cli_amd.runtime import Tensor
+        t = Tensor(gpu, h, 1000, 0)
+        gpu.tensors.append(t)
+        assert np.array_equal(t.read(), vals)
+        assert not gpu.lib.h3_gpu_tensor_load_f32(gpu.handle, path.encode(), 12, 2000)  # short file
+    finally:
+        os.unlink(path)

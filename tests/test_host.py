@@ -60,3 +60,34 @@ def test_v_position_is_a_permutation():
     pos = [lib.h3_hip_sage_v_position(j) for j in range(64)]
     assert sorted(pos) == list(range(64))
     assert pos == [oracle.sage_v_position(j) for j in range(64)]
+
+
+def test_exports_reference_link_contract():
+    """Every symbol the reference's tests/test_gpu_contract.c links (non-Apple
+    branch) is exported, so h3cli links against this library unchanged."""
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    names = (ROOT / "tests" / "golden" / "gpu_contract_symbols.txt").read_text().split()
+    assert len(names) == 166
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_context_free_surface_calls():
+    """Calls that need no device: NULL contexts are rejected, host parses work."""
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    lib.h3_qwen_gqa_scale_name.restype = C.c_char_p
+    mode = C.c_int(-1)
+    err = C.create_string_buffer(128)
+    for text, want in ((None, 0), (b"", 0), (b"reference", 0), (b"scaled-q", 1), (b"legacy", 2)):
+        assert lib.h3_qwen_gqa_scale_parse(text, C.byref(mode), err, 128) == 1 and mode.value == want
+        assert lib.h3_qwen_gqa_scale_name(want) == (text or b"reference")
+    assert lib.h3_qwen_gqa_scale_parse(b"bogus", C.byref(mode), err, 128) == 0
+    assert err.value == b"invalid H3_QWEN_GQA_SCALE_MODE: bogus"
+    assert lib.h3_gpu_prefers_device_sampler(None, 0) == 0
+    assert lib.h3_gpu_should_retry_streaming(None) == 0
+    assert lib.h3_gpu_is_m5(None) == 0 and lib.h3_gpu_has_int8_mlp(None) == 0
+    # Out-of-path ops fail without a context rather than crash.
+    assert lib.h3_gpu_conv3d_f32(None, None, None, None, None, *([1] * 13)) == 0
+    assert lib.h3_gpu_video_graph_begin(None) == 0
+    lib.h3_gpu_sglang_vae_weight.restype = C.c_void_p
+    assert lib.h3_gpu_sglang_vae_weight(None, None) is None

@@ -163,3 +163,39 @@ def test_reference_input_generator_known_values():
         vals.append(((s % 4097) - 2048) / 1024.0)
     assert np.array_equal(out, synth.f32_to_bf16(np.float32(vals)))
     assert st[0] == s
+
+
+def test_rms_norm_oracle_closed_form():
+    rows, width = 9, 640
+    x = synth.normal_bf16(1, rows * width, scale=2.0)
+    w = synth.normal_bf16(2, width, scale=0.5)
+    xf = synth.bf16_to_f32(x).astype(np.float64).reshape(rows, width)
+    inv = 1 / np.sqrt((xf * xf).mean(axis=1, keepdims=True) + 1e-5)
+    want = xf * inv * synth.bf16_to_f32(w).astype(np.float64)
+    got = synth.bf16_to_f32(oracle.rms_norm(x, w, rows, width, 1e-5)).reshape(rows, width)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
+    # head RMSNorm is the same per (row, head) slice
+    h = oracle.head_rms_norm(x, w[:128], rows * 5, 1, 128, 1e-5)
+    assert np.array_equal(h, oracle.rms_norm(x, w[:128], rows * 5, 128, 1e-5))
+
+
+def test_patch_linear_oracle_exact_and_mapped():
+    m, k, n = 13, 40, 24
+    rng = np.random.default_rng(0)
+    # Small integers times powers of two: every partial sum is exact in FP32, so
+    # the result is bf16 of the exact dot product in any order.
+    x = (rng.integers(-8, 9, m * k) * 0.25).astype(np.float32)
+    w = (rng.integers(-8, 9, n * k) * 0.5).astype(np.float32)
+    b = (rng.integers(-8, 9, n) * 1.0).astype(np.float32)
+    exact = x.reshape(m, k).astype(np.float64) @ w.reshape(n, k).T.astype(np.float64) + b
+    assert np.array_equal(oracle.patch_linear(x, w, b, m, k, n), synth.f32_to_bf16(exact.astype(np.float32)).reshape(-1))
+    rmap = np.array([5, 0, 99] + list(range(6, 16)), np.uint32)
+    got = oracle.patch_linear(x, w, b, m, k, n, row_map=rmap, out_rows=16).reshape(16, n)
+    full = synth.f32_to_bf16(exact.astype(np.float32))
+    assert np.array_equal(got[5], full[0]) and np.array_equal(got[0], full[1])
+    assert not got[1:5].any()  # row 2 maps out of range and is skipped; rows 1-4 untouched
+    xr = rng.standard_normal(m * k).astype(np.float32)
+    wr = rng.standard_normal(n * k).astype(np.float32)
+    ref = xr.reshape(m, k).astype(np.float64) @ wr.reshape(n, k).T.astype(np.float64)
+    got = synth.bf16_to_f32(oracle.patch_linear(xr, wr, None, m, k, n)).reshape(m, n)
+    assert np.max(np.abs(got - ref)) <= 2.0 ** -7 * np.abs(ref).max()

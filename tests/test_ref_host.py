@@ -127,3 +127,70 @@ def test_attention_names_match_reference(libs):
         mo, mr = C.c_int(-7), C.c_int(-7)
         assert ours.h3_attention_parse(text, C.byref(mo)) == ref.h3_attention_parse(text, C.byref(mr))
         assert mo.value == mr.value
+
+
+class WeightOptions(C.Structure):
+    _fields_ = [("mode", C.c_int), ("max_resident", C.c_int), ("capacity_limit", C.c_uint64),
+                ("allocation_limit", C.c_uint64)]
+
+
+class WeightPlan(C.Structure):
+    _fields_ = [("options", WeightOptions), ("active_mask", C.c_uint64), ("resident_mask", C.c_uint64),
+                ("free_bytes", C.c_uint64), ("live_bytes", C.c_uint64), ("reserve_bytes", C.c_uint64),
+                ("future_bytes", C.c_uint64), ("block_bytes", C.c_uint64), ("resident_bytes", C.c_uint64),
+                ("slot_bytes", C.c_uint64), ("active_count", C.c_uint), ("resident_count", C.c_uint),
+                ("effective_mode", C.c_int)]
+
+
+def _plan(lib, opts, *args):
+    fn = lib.h3_weight_plan_build
+    fn.restype = C.c_int
+    fn.argtypes = [C.POINTER(WeightPlan), WeightOptions] + [C.c_uint64] * 6 + [C.c_char_p, C.c_size_t]
+    p = WeightPlan()
+    err = C.create_string_buffer(256)
+    ok = fn(C.byref(p), opts, *args, err, 256)
+    return ok, bytes(memoryview(p)), err.value
+
+
+def test_weight_plan_matches_reference(libs):
+    ours, ref = libs
+    GiB = 1 << 30
+    block = 246_400_000
+    masks = [0, 1, (1 << 40) - 1, (1 << 50) - 1, 1 << 50, 0b1011 << 20]
+    for mode in (0, 1, 2, 3):
+        for max_res in (-2, -1, 0, 3, 50, 51):
+            for cap in (0, 30 * GiB):
+                opts = WeightOptions(mode, max_res, cap, 0)
+                for mask in masks:
+                    for avail in (0, 2 * GiB, 20 * GiB, 280 * GiB):
+                        for blk in (0, block):
+                            args = (mask, blk, avail, 5 * GiB, 8 * GiB, 28 * GiB)
+                            assert _plan(ours, opts, *args) == _plan(ref, opts, *args), (mode, max_res, cap, mask, avail)
+
+
+def test_weight_options_and_names_match_reference(libs, monkeypatch):
+    ours, ref = libs
+    for lib in (ours, ref):
+        lib.h3_weight_mode_name.restype = C.c_char_p
+        lib.h3_weight_options_read.argtypes = [C.POINTER(WeightOptions), C.c_int, C.c_char_p, C.c_size_t]
+    for m in range(-1, 4):
+        assert ours.h3_weight_mode_name(m) == ref.h3_weight_mode_name(m)
+    for n in (0, 1, 2, 7, 100):
+        assert ours.h3_weight_retry_cap(n) == ref.h3_weight_retry_cap(n)
+    envs = [{}, {"H3_CUDA_WEIGHT_MODE": "stream"}, {"H3_CUDA_WEIGHT_MODE": "resident"},
+            {"H3_CUDA_WEIGHT_MODE": "bogus"}, {"H3_TEST_CUDA_RESIDENT_BLOCKS": "7"},
+            {"H3_TEST_CUDA_RESIDENT_BLOCKS": "51"}, {"H3_TEST_CUDA_CAPACITY_BYTES": "12x"},
+            {"H3_TEST_CUDA_CAPACITY_BYTES": "123456", "H3_CUDA_TEST_MEMORY_BUDGET": "99"}]
+    for env in envs:
+        for k in ("H3_CUDA_WEIGHT_MODE", "H3_TEST_CUDA_RESIDENT_BLOCKS", "H3_TEST_CUDA_CAPACITY_BYTES",
+                  "H3_CUDA_TEST_MEMORY_BUDGET"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        for force in (0, 1):
+            out = []
+            for lib in (ours, ref):
+                o, e = WeightOptions(9, 9, 9, 9), C.create_string_buffer(256)
+                ok = lib.h3_weight_options_read(C.byref(o), force, e, 256)
+                out.append((ok, bytes(memoryview(o)) if ok else None, e.value))
+            assert out[0] == out[1], (env, force)
