@@ -91,3 +91,20 @@ def test_context_free_surface_calls():
     assert lib.h3_gpu_video_graph_begin(None) == 0
     lib.h3_gpu_sglang_vae_weight.restype = C.c_void_p
     assert lib.h3_gpu_sglang_vae_weight(None, None) is None
+
+
+def test_device_configure_validation(monkeypatch):
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    err = C.create_string_buffer(128)
+    monkeypatch.delenv("H3_CUDA_DEVICE", raising=False)
+    monkeypatch.delenv("H3_CUDA_WEIGHT_MODE", raising=False)
+    assert lib.h3_device_configure(b"x1", None, err, 128) == 0 and b"invalid HIP device index" in err.value
+    assert lib.h3_device_configure(None, b"bogus", err, 128) == 0
+    libc = C.CDLL(None)
+    libc.getenv.restype = C.c_char_p
+    try:
+        assert lib.h3_device_configure(b"0", b"stream", err, 128) == 1
+        assert libc.getenv(b"H3_CUDA_DEVICE") == b"0" and libc.getenv(b"H3_CUDA_WEIGHT_MODE") == b"stream"
+    finally:  # the C-level environment is not restored by monkeypatch
+        libc.unsetenv(b"H3_CUDA_DEVICE")
+        libc.unsetenv(b"H3_CUDA_WEIGHT_MODE")
