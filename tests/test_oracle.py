@@ -114,8 +114,11 @@ def test_sage_pack_closed_forms():
         for b in range(1, blocks):
             x = q3[b * 64:min(seq, b * 64 + 64), h]
             amax = np.float32(np.abs(x).max())
-            assert p["q_scale"][h * blocks + b] == np.float32(np.fma(amax, np.float32(1 / 127), np.float32(1e-7))) \
-                if hasattr(np, "fma") else True
+            # fmaf(amax, 1/127, 1e-7): the FP64 evaluation of the two FP32 terms is
+            # exact here (48-bit product plus a term inside its 53-bit span), so one
+            # rounding to FP32 gives the fused result.
+            fused = np.float32(np.float64(amax) * np.float64(np.float32(1 / 127)) + np.float64(np.float32(1e-7)))
+            assert p["q_scale"][h * blocks + b] == fused
             s = p["q_scale"][h * blocks + b]
             codes = p["q8"].reshape(heads, padded, 128)[h, b * 64:b * 64 + x.shape[0]]
             assert np.all(np.abs(codes - x / s) <= 0.5 + 1e-6)
@@ -199,3 +202,69 @@ def test_patch_linear_oracle_exact_and_mapped():
     ref = xr.reshape(m, k).astype(np.float64) @ wr.reshape(n, k).T.astype(np.float64)
     got = synth.bf16_to_f32(oracle.patch_linear(xr, wr, None, m, k, n)).reshape(m, n)
     assert np.max(np.abs(got - ref)) <= 2.0 ** -7 * np.abs(ref).max()
+
+
+def _ulps(got_bits, want):
+    g = synth.bf16_to_f32(got_bits).astype(np.float64)
+    w = np.asarray(want, np.float64)
+    mag = np.maximum(np.maximum(np.abs(g), np.abs(w)), 2.0 ** -126)
+    return np.abs(g - w) / np.maximum(2.0 ** (np.floor(np.log2(mag)) - 7), 2.0 ** -17)
+
+
+def test_elementwise_oracles_closed_forms():
+    """AdaLN, gate, GELU, SwiGLU and Euler against FP64 numpy closed forms."""
+    rows, width, slots = 7, 256, 6
+    x = synth.normal_bf16(1, rows * width, scale=2.0)
+    w = synth.normal_bf16(2, width, scale=0.5)
+    mod = synth.normal_bf16(3, 2 * slots * width, scale=0.3)
+    rmap = (np.arange(rows) % 2).astype(np.uint32)
+    xf = bf16(x).astype(np.float64).reshape(rows, width)
+    mf = bf16(mod).astype(np.float64).reshape(2, slots, width)[rmap]
+    inv = 1 / np.sqrt((xf * xf).mean(1, keepdims=True) + 1e-6)
+    want = xf * inv * bf16(w) * (1 + mf[:, 4]) + mf[:, 3]
+    assert _ulps(oracle.adaln(x, w, mod, rmap, rows, width, slots, 3, 4, 1e-6), want.reshape(-1)).max() <= 1
+    br = synth.normal_bf16(4, rows * width)
+    want = xf + bf16(br).astype(np.float64).reshape(rows, width) * mf[:, 2]
+    assert _ulps(oracle.gate(x, br, mod, rmap, rows, width, slots, 2), want.reshape(-1)).max() <= 0.5 + 1e-9
+    g = np.linspace(-12, 12, 4001)
+    gb = synth.f32_to_bf16(g.astype(np.float32))
+    gf = bf16(gb).astype(np.float64)
+    tanh_form = 0.5 * gf * (1 + np.tanh(0.7978845608028654 * (gf + 0.044715 * gf ** 3)))
+    erf_form = 0.5 * gf * (1 + np.array([math.erf(t / math.sqrt(2)) for t in gf]))
+    assert _ulps(oracle.gelu(gb, True), tanh_form).max() <= 1
+    assert _ulps(oracle.gelu(gb, False), erf_form).max() <= 1
+    fused = synth.normal_bf16(5, 2 * rows * width, scale=2.0)
+    ff = bf16(fused).astype(np.float64).reshape(rows, 2, width)
+    want = ff[:, 0] / (1 + np.exp(-ff[:, 0])) * ff[:, 1]
+    assert _ulps(oracle.swiglu(fused, rows, width), want.reshape(-1)).max() <= 1
+    sample = synth.normal(6, 1000).astype(np.float32)
+    last, prev = synth.normal_bf16(7, 1000), synth.normal_bf16(8, 1000)
+    lf, pf = bf16(last).astype(np.float64), bf16(prev).astype(np.float64)
+    want = sample + (-0.05) * (lf + 0.25 * (lf - pf))
+    assert np.max(np.abs(oracle.euler(sample, last, prev, -0.05, 0.25) - want)) <= 4e-7 * np.abs(want).max()
+
+
+def test_qkv_rope_oracle_identities():
+    """RoPE restatement: zero angle is the identity on Q/K, a rotation preserves
+    each pair's norm and matches the FP64 rotate-half formula, V is copied, and
+    the optional per-head RMSNorm matches its closed form."""
+    seq, heads, dim, half = 5, 3, 128, 64
+    qkv = synth.normal_bf16(9, seq * heads * dim * 3)
+    ones = synth.f32_to_bf16(np.ones(seq * half, np.float32))
+    zeros = np.zeros(seq * half, np.uint16)
+    q, k, v = oracle.qkv_rope(qkv, None, None, ones, zeros, seq, heads, dim, half, 1e-6, 0)
+    src = qkv.reshape(seq, 3, heads, dim)
+    assert np.array_equal(q, src[:, 0].reshape(-1)) and np.array_equal(k, src[:, 1].reshape(-1))
+    assert np.array_equal(v, src[:, 2].reshape(-1))
+    ang = np.random.default_rng(1).uniform(-3, 3, (seq, half))
+    cb, sb = synth.f32_to_bf16(np.cos(ang).astype(np.float32)), synth.f32_to_bf16(np.sin(ang).astype(np.float32))
+    c, s = bf16(cb).astype(np.float64), bf16(sb).astype(np.float64)
+    q, _, _ = oracle.qkv_rope(qkv, None, None, cb.reshape(-1), sb.reshape(-1), seq, heads, dim, half, 1e-6, 0)
+    x = bf16(src[:, 0]).astype(np.float64)  # [seq, heads, dim]
+    lo, hi = x[..., :half], x[..., half:]
+    want = np.concatenate([lo * c[:, None] - hi * s[:, None], hi * c[:, None] + lo * s[:, None]], -1)
+    assert _ulps(q, want.reshape(-1)).max() <= 1
+    qw = synth.normal_bf16(10, dim, scale=0.5)
+    q, _, _ = oracle.qkv_rope(qkv, qw, qw, ones, zeros, seq, heads, dim, half, 1e-6, 0)
+    normed = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * bf16(qw)
+    assert _ulps(q, normed.reshape(-1)).max() <= 1
