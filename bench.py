@@ -30,6 +30,14 @@ SEQ, HEADS, DIM = 32400, 40, 128
 ROPE_SHAPE = (27, 30, 40)
 PEAK_BF16 = 2500.0      # MI355X dense BF16 MFMA, TFLOP/s
 PEAK_FP8 = 5000.0       # MI355X dense FP8 / INT8 MFMA, TFLOP/s (TOP/s)
+PEAK_HBM = 8000.0       # MI355X HBM3E, GB/s
+# HBM bytes per launch of the attention kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes over `python3 bench.py --probe`, each scaled by the same
+# counter's reading for a device copy of known size (probe's calibration copy);
+# the summary with the commands and raw readings is
+# profiles/attn_bf16_wide_s32400_h40_traffic.md: fetched 2.0 x 1718490 KiB +
+# written 1.0 x 325613 KiB per launch.
+TRAFFIC = 3.853e9
 
 
 def attention_flops(seq, heads, dim=DIM, density=1.0):
@@ -81,12 +89,18 @@ class Workload:
         return [synth.bf16_to_f32(t.read()) for t in (self.q, self.k, self.v)]
 
 
-def time_calls(gpu, call, steps, warmup):
+def time_calls(gpu, call, steps, warmup, kernel_times=None):
+    """Average ms per call between HIP events on the compute stream around the
+    timed calls. With kernel_times (a list), the library also times the dominant
+    kernel of every call on that stream and (avg ms, launches) is appended."""
+    import ctypes as C
     gpu.begin()
     for _ in range(warmup):
         gpu.check(call(), "warmup")
     gpu.submit()
     e0, e1 = gpu.timing_event(), gpu.timing_event()
+    if kernel_times is not None:
+        gpu.check(gpu.lib.h3_hip_kernel_timing(gpu.handle, 1), "kernel timing")
     gpu.begin()
     gpu.record(e0)
     for _ in range(steps):
@@ -98,6 +112,11 @@ def time_calls(gpu, call, steps, warmup):
     ms = gpu.elapsed_ms(e0, e1)
     gpu.lib.h3_gpu_event_free(e0)
     gpu.lib.h3_gpu_event_free(e1)
+    if kernel_times is not None:
+        total, n = C.c_double(), C.c_uint64()
+        gpu.check(gpu.lib.h3_hip_kernel_timing_read(gpu.handle, C.byref(total), C.byref(n)), "kernel timing read")
+        gpu.check(gpu.lib.h3_hip_kernel_timing(gpu.handle, 0), "kernel timing")
+        kernel_times.append((total.value / max(n.value, 1), n.value))
     return ms / steps, wall
 
 
@@ -196,6 +215,29 @@ def step_leg(steps, warmup):
             "setup_s": round(setup, 1)}
 
 
+def probe():
+    """Launches for HBM-traffic counters: attention twice (config 2 inputs),
+    then a plain device-to-device copy of exactly 2^30 bytes, whose FETCH_SIZE
+    and WRITE_SIZE readings calibrate the counters (2^30 bytes each way)."""
+    from h3cli_amd.runtime import Gpu
+    with Gpu() as gpu:
+        w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=False)
+        gpu.begin()
+        for _ in range(2):
+            gpu.check(w.call(), "attention")
+        gpu.submit()
+        n = (1 << 30) // 2
+        src, dst = gpu.empty(n), gpu.empty(n)
+        gpu.begin()
+        gpu.check(gpu.lib.h3_hip_fill_normal_bf16(gpu.handle, src.handle, 7, 1.0, n), "fill copy source")
+        gpu.check(gpu.lib.h3_hip_fill_normal_bf16(gpu.handle, dst.handle, 8, 1.0, n), "fill copy target")
+        gpu.submit()
+        gpu.begin()
+        gpu.check(gpu.lib.h3_gpu_copy_bf16(gpu.handle, dst.handle, 0, src.handle, 0, n), "copy")
+        gpu.submit()
+    log("[probe] 2 attention launches (S=32400, H=40) + 1 GiB device copy done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +247,9 @@ def main():
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "192")))
+    ap.add_argument("--probe", action="store_true",
+                    help="counter probe for rocprofv3 --pmc: two attention launches and one 1 GiB device copy "
+                         "(the calibration kernel), nothing timed")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the DiT hot path here runs on a single MI355X "
@@ -212,15 +257,22 @@ def main():
         sys.exit(2)
 
     from h3cli_amd.runtime import Gpu
+    if args.probe:
+        probe()
+        return
     legs = [x for x in args.legs.split(",") if x]
     result = {}
     with Gpu() as gpu:
         log(f"[bench] bf16 attention S={SEQ} H={HEADS}: preparing inputs")
         w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=True)
-        ms, wall = time_calls(gpu, w.call, args.steps, args.warmup)
+        kt = []
+        ms, wall = time_calls(gpu, w.call, args.steps, args.warmup, kt)
         flops = attention_flops(SEQ, HEADS)
         tflops = flops / (ms * 1e-3) / 1e12
-        log(f"[bench] bf16 attention: {ms:.3f} ms/call, {tflops:.1f} TFLOP/s")
+        kernel_ms, kernel_n = kt[0]
+        kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
+        log(f"[bench] bf16 attention: {ms:.3f} ms/call, {tflops:.1f} TFLOP/s; "
+            f"attention kernel {kernel_ms:.3f} ms avg over {kernel_n} launches ({kernel_tflops:.1f} TFLOP/s)")
         result.update({
             "metric": "attention TFLOP/s + %MFMA peak; s/denoise-step (40-block DiT, S=32400) 1 GPU",
             "value": round(tflops, 3),
@@ -236,9 +288,11 @@ def main():
             "data": "synthetic: seeded 0.5*N(0,1) bf16 Q/K/V with 3D RoPE (44/42/42, theta 1e4) on Q,K",
             "config": {"workload": "bf16 DiT video self-attention (BASELINE config 2)", "seq": SEQ,
                        "heads": HEADS, "head_dim": DIM, "batch": 1, "flop_convention": "4*S^2*H*D"},
-            "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16, "unit": "TFLOP/s",
-                         "frac": round(tflops / PEAK_BF16, 4), "traffic": None,
-                         "kernel": "attn_bf16_kernel<8,1,2,false,true>"},
+            "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3), "peak": PEAK_BF16,
+                         "unit": "TFLOP/s", "frac": round(kernel_tflops / PEAK_BF16, 4), "traffic": TRAFFIC,
+                         "kernel": "attn_bf16_wide<2, false, false>", "kernel_ms": round(kernel_ms, 4),
+                         "kernel_launches": kernel_n, "traffic_unit": "HBM bytes per launch (rocprofv3, calibrated)",
+                         "algorithmic": "4*S^2*H*D = 21.499 TFLOP per launch (one launch covers all 40 heads)"},
         })
         if not args.no_cpu:
             log(f"[bench] CPU baseline on {args.cpu_rows} rows")

@@ -137,6 +137,11 @@ _SIGNATURES.update({
     "h3_gpu_dit_sol_layout": (_i, [_p, _p]),
     "h3_gpu_profile_set_label": (None, [_p, C.c_char_p]),
     "h3_gpu_profile_mark": (None, [_p, C.c_char_p]),
+    "h3_device_query": (_i, [_p, C.c_char_p, _sz]),
+    "h3_hip_kernel_timing": (_i, [_p, _i]),
+    "h3_hip_kernel_timing_read": (_i, [_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    "h3_device_configure": (_i, [C.c_char_p, C.c_char_p, C.c_char_p, _sz]),
+    "h3_device_memory_fits": (_i, [C.c_uint64]),
     "h3_subblock_budget": (C.c_uint, [C.c_uint, _f]),
     "h3_subblock_warmup": (_i, [_i]),
     "h3_subblock_dense_reason": (C.c_char_p, [C.c_uint, C.c_uint, _i, _f, _i]),

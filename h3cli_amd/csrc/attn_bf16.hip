@@ -7,20 +7,26 @@
 // BF16 matrix cores, as the reference's tensor-core path and FlashAttention do.
 //
 // Work decomposition (MI355X-first, not a translation of the CUDA kernels):
-//  * one workgroup = WAVES wavefronts x 64 queries of one head; the query
-//    fragments of a wave stay in VGPRs for the whole key sweep;
+//  * one workgroup = WAVES wavefronts x 32 queries of one head; the query
+//    fragments of a wave stay in VGPRs for the whole key sweep, and two waves
+//    share each SIMD so one wave's softmax overlaps the other's MFMAs;
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
 //    each lane then owns one query column, so the row max is a register max
 //    plus one v_permlane32_swap between the two 32-lane halves, and the FP32
-//    score accumulator is already laid out as the B operand of O^T += V^T P^T;
+//    score accumulator, rounded to BF16, is already laid out as the B operand
+//    of O^T += V^T P^T;
 //  * V is transposed once per call by a bandwidth-bound pre-pass into
-//    [head, channel, key] with the key order the score accumulator produces, so
-//    the main loop stages both K and V^T tiles with plain 16-byte copies;
-//  * K / V^T tiles (64 keys) are double buffered in LDS with one barrier per
-//    tile; global loads of tile t+1 are issued before the MFMAs of tile t;
+//    [head, channel, key] with the key order the score accumulator produces;
+//  * K and V^T tiles go from global memory straight into LDS
+//    (global_load_lds, 16 bytes per lane) in XOR-swizzled 16-byte chunks, so
+//    both operand reads are free of bank conflicts; the next interval's tiles
+//    load while the current one is processed (two LDS stages);
+//  * the dense kernel covers 128 keys per barrier interval (two 64-key
+//    sub-tiles) and requests all fragments of a sub-tile before its first
+//    MFMA, so LDS latency is paid once per sub-tile;
 //  * the running max is only raised when a tile's max exceeds it by more than
-//    2^8 (P then stays below 256, exact in BF16/FP32 range), so the FP32
-//    accumulator rescale runs a handful of times per row instead of per tile;
+//    8 (log2 units; P then stays below 256), so the accumulator rescale runs a
+//    handful of times per row instead of per tile;
 //  * workgroup ids are remapped so that the workgroups of one head share an XCD
 //    (and its L2), which is where their K/V tiles are re-read.
 #include "common.h"
@@ -232,7 +238,7 @@ void attn_bf16_kernel(Args a) {
                 mx0 = fmaxf(fmaxf(mx0, s[0][nb][r]), s[0][nb][r + 1]);
                 mx1 = fmaxf(fmaxf(mx1, s[1][nb][r]), s[1][nb][r + 1]);
             }
-            const float mx = half_max(fmaxf(mx0, mx1)) * c;
+            const float mx = half_max_swap(fmaxf(mx0, mx1)) * c;
             // Raise the running max only when this tile exceeds it by the slack.
             if (__builtin_amdgcn_ballot_w64(mx > m[nb] + RESCALE_SLACK)) {
                 const float mnew = fmaxf(m[nb], mx);
@@ -296,7 +302,7 @@ void attn_bf16_kernel(Args a) {
     bool bad = false;
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        const float total = MSUM ? lsum[nb][0] : half_sum(l[nb]);
+        const float total = MSUM ? lsum[nb][0] : half_sum_swap(l[nb]);
         const float inv = total > 0.f ? 1.f / total : 0.f;
         const unsigned q = q0 + wave * WQ + nb * 32 + n;
         if (q >= a.seq) continue;
@@ -329,7 +335,224 @@ int launch(h3_gpu *g, const Args &a, unsigned groups) {
             return 0;
         configured = true;
     }
+    hipEvent_t timing = h3_kernel_timing_begin(g);
     hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "BF16 attention");
+}
+
+// Wide tiles: each barrier interval covers KT consecutive 64-key sub-tiles, so
+// the per-interval fixed costs (the barrier, the load wait and the serial
+// max / ballot chain) are paid once per KT * 64 keys.
+template <int KT, bool SPARSE, bool MSUM>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+void attn_bf16_wide(Args a) {
+    constexpr int WAVES = 8;
+    constexpr int BM = 32 * WAVES;
+    constexpr int BLOCKS = K_BYTES / 1024;
+    constexpr int STAGE = KT * (K_BYTES + V_BYTES);
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const unsigned n = lane % 32, hf = lane / 32;
+    const unsigned nqb = (a.seq + BM - 1) / BM;
+    const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned head = id / nqb, qb = id % nqb;
+    const unsigned q0 = qb * BM;
+    const size_t stride = (size_t)a.heads * D;
+    const uint16_t *qh = a.q + (size_t)head * D;
+    const uint16_t *kh = a.k + (size_t)head * D;
+    const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
+    const float c = a.scale_log2;
+
+    unsigned count;  // 64-key sub-tiles
+    const uint32_t *list = nullptr;
+    if constexpr (SPARSE) {
+        count = a.kv_count[qb];
+        list = a.kv_list + (size_t)qb * a.list_stride;
+    } else {
+        count = (a.seq + BN - 1) / BN;
+    }
+    const unsigned groups = (count + KT - 1) / KT;
+    auto sub_at = [&](unsigned i) { i = min(i, count - 1); return SPARSE ? list[i] : i; };
+
+    bf16x8 qf[8];
+    {
+        unsigned row = q0 + wave * 32 + n;
+        row = row < a.seq ? row : a.seq - 1;
+        const uint16_t *p = qh + (size_t)row * stride + hf * 8;
+        bool bad = false;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            qf[ks] = *reinterpret_cast<const bf16x8 *>(p + ks * 16);
+            bad |= bf16_vec_nonfinite(qf[ks]);
+        }
+        if (bad) a.fault[0] = 1u;
+    }
+
+    auto load_group = [&](unsigned g, int stage) {
+        uint8_t *base = smem + stage * STAGE;
+#pragma unroll
+        for (int j = 0; j < KT; j++) {
+            const unsigned tile = sub_at(g * KT + j);
+            const unsigned key0 = tile * BN;
+            uint8_t *ks = base + j * K_BYTES;
+            uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
+#pragma unroll
+            for (unsigned b = wave; b < BLOCKS; b += WAVES) {
+                unsigned key = 4 * b + lane / 16, phys = lane % 16;
+                unsigned row = min(key0 + key, a.seq - 1);
+                const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                                 (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
+                unsigned d = 8 * b + lane / 8, vph = lane % 8;
+                unsigned col = min(key0, a.padded - BN);
+                const uint16_t *vsrc = vth + (size_t)d * a.padded + col + v_chunk(d, vph) * 8;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vsrc,
+                                                 (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
+            }
+        }
+    };
+
+    f32x16 o[4];
+#pragma unroll
+    for (int md = 0; md < 4; md++) o[md] = f32x16{};
+    float m = -1e30f, l = 0.f;
+    f32x16 lsum = f32x16{};
+    bf16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
+
+    if (groups) load_group(0, 0);
+    wait_vm_loads();
+    __syncthreads();
+    for (unsigned g = 0; g < groups; g++) {
+        const int cur = g & 1;
+        if (g + 1 < groups) load_group(g + 1, cur ^ 1);
+        const uint8_t *base = smem + cur * STAGE;
+        f32x16 s[KT][2];
+#pragma unroll
+        for (int j = 0; j < KT; j++) {
+            const uint8_t *ks = base + j * K_BYTES;
+            bf16x8 kfr[16];
+#pragma unroll
+            for (int x = 0; x < 16; x++) {
+                const unsigned key = (x % 2) * 32 + n;
+                kfr[x] = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, (x / 2) * 2 + hf) * 16);
+            }
+            s[j][0] = f32x16{};
+            s[j][1] = f32x16{};
+#pragma unroll
+            for (int kstep = 0; kstep < 8; kstep++)
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+                    s[j][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[kstep * 2 + mb], qf[kstep], s[j][mb], 0, 0, 0);
+        }
+        // Mask keys past the sequence end and sub-tiles past the list end.
+#pragma unroll
+        for (int j = 0; j < KT; j++) {
+            const unsigned idx = g * KT + j;
+            const unsigned tile = sub_at(idx);
+            if (idx >= count || tile * BN + BN > a.seq) {
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
+                        if (idx >= count || key >= a.seq) s[j][mb][r] = -INFINITY;
+                    }
+            }
+        }
+        float mx0 = -INFINITY, mx1 = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < KT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                mx0 = fmaxf(fmaxf(mx0, s[j][0][r]), s[j][0][r + 1]);
+                mx1 = fmaxf(fmaxf(mx1, s[j][1][r]), s[j][1][r + 1]);
+            }
+        const float mx = half_max_swap(fmaxf(mx0, mx1)) * c;
+        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_SLACK)) {
+            const float mnew = fmaxf(m, mx);
+            const float alpha = exp2f_fast(m - mnew);
+            m = mnew;
+            if constexpr (MSUM) lsum *= alpha;
+            else l *= alpha;
+#pragma unroll
+            for (int md = 0; md < 4; md++) o[md] *= alpha;
+        }
+        const float neg = -m;
+#pragma unroll
+        for (int j = 0; j < KT; j++) {
+            const uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
+            bf16x8 vfr[16];
+#pragma unroll
+            for (int x = 0; x < 16; x++) {
+                const unsigned d = (x % 4) * 32 + n;
+                vfr[x] = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, (x / 4) * 2 + hf) * 16);
+            }
+            bf16x8 pb[4];
+            float psum = 0.f;
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    float p0 = exp2f_fast(fmaf(s[j][mb][r], c, neg));
+                    float p1 = exp2f_fast(fmaf(s[j][mb][r + 1], c, neg));
+                    if constexpr (!MSUM) psum += p0 + p1;
+                    pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
+                    pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
+                }
+            if constexpr (!MSUM) l += psum;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+                for (int md = 0; md < 4; md++)
+                    o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[kk * 4 + md], pb[kk], o[md], 0, 0, 0);
+                if constexpr (MSUM) lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[kk], lsum, 0, 0, 0);
+            }
+        }
+        wait_vm_loads();
+        __syncthreads();
+    }
+
+    const float total = MSUM ? lsum[0] : half_sum_swap(l);
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const unsigned q = q0 + wave * 32 + n;
+    bool bad = false;
+    if (q < a.seq) {
+        uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
+#pragma unroll
+        for (int md = 0; md < 4; md++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                u16x4 w;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float x = o[md][g4 * 4 + i] * inv;
+                    bad |= !finite_f32(x);
+                    w[i] = f32_to_bf16(x);
+                }
+                *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
+            }
+    }
+    if (bad) a.fault[0] = 1u;
+}
+
+template <int KT, bool SPARSE, bool MSUM>
+int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
+    constexpr size_t shared = 2 * KT * STAGE_BYTES;
+    static bool configured = false;
+    auto kernel = attn_bf16_wide<KT, SPARSE, MSUM>;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
+                          "attention shared memory"))
+            return 0;
+        configured = true;
+    }
+    hipEvent_t timing = h3_kernel_timing_begin(g);
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(512), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "BF16 attention");
 }
 
@@ -353,8 +576,10 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     // Sparse lists are per 128-query block: 4 waves per workgroup, two
-    // workgroups per CU. Dense: 8 waves x 32 queries, two waves per SIMD.
+    // workgroups per CU. Dense: 8 waves x 32 queries, two waves per SIMD, 128
+    // keys per barrier interval (measured fastest of the shapes kept here).
     if (kv_list) return launch<4, 1, 2, true, true>(g, a, (seq + 127) / 128 * heads);
+    if (g->attention_variant == 1) return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
     if (g->attention_variant == 2) return launch<12, 1, 3, false, false>(g, a, (seq + 383) / 384 * heads);
-    return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
+    return launch_wide<2, false, false>(g, a, (seq + 255) / 256 * heads);
 }

@@ -7,6 +7,8 @@
 #include <cstdarg>
 #include <cstring>
 #include <mutex>
+#include <utility>
+#include <vector>
 #include "../../include/h3_gpu.h"
 #include "../../include/h3_hip_ext.h"
 
@@ -109,6 +111,10 @@ struct h3_gpu {
     char label[64];         // h3_gpu_profile_set_label
     double created;         // wall clock at creation (profile marks)
     bool allocation_failed; // a device allocation ran out of memory
+    // Opt-in timing of the dominant kernel of each dispatch (h3_hip_kernel_timing):
+    // event pairs on the compute stream, summed when read.
+    bool kernel_timing;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> *kernel_events;
 };
 
 // ---------------------------------------------------------------- helpers

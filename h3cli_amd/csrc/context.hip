@@ -113,12 +113,16 @@ extern "C" h3_gpu *h3_gpu_create(const char *shader_source_path, char *error, si
     return g;
 }
 
+static void kernel_events_clear(h3_gpu *g);
+
 extern "C" void h3_gpu_free(h3_gpu *g) {
     if (!g) return;
     if (g->compute) hipStreamSynchronize(g->compute);
     if (g->copy) hipStreamSynchronize(g->copy);
     h3_attention_destroy(g);
     h3_streaming_destroy(g);
+    kernel_events_clear(g);
+    delete g->kernel_events;
     if (g->fault) hipFree(g->fault);
     if (g->compute) hipStreamDestroy(g->compute);
     if (g->copy) hipStreamDestroy(g->copy);
@@ -535,4 +539,57 @@ int h3_buffer_reserve(h3_gpu *g, h3_device_buffer *b, size_t bytes, const char *
 void h3_buffer_free(h3_device_buffer *b) {
     if (b->ptr) hipFree(b->ptr);
     b->ptr = nullptr; b->bytes = 0;
+}
+
+// ------------------------------------------------------------ kernel timing
+hipEvent_t h3_kernel_timing_begin(h3_gpu *g) {
+    if (!g->kernel_timing) return nullptr;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    hipEventRecord(e, g->compute);
+    return e;
+}
+
+void h3_kernel_timing_end(h3_gpu *g, hipEvent_t start) {
+    if (!start) return;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) { hipEventDestroy(start); return; }
+    hipEventRecord(e, g->compute);
+    if (!g->kernel_events) g->kernel_events = new std::vector<std::pair<hipEvent_t, hipEvent_t>>();
+    g->kernel_events->emplace_back(start, e);
+}
+
+static void kernel_events_clear(h3_gpu *g) {
+    if (!g->kernel_events) return;
+    for (auto &p : *g->kernel_events) { hipEventDestroy(p.first); hipEventDestroy(p.second); }
+    g->kernel_events->clear();
+}
+
+extern "C" int h3_hip_kernel_timing(h3_gpu *g, int enable) {
+    if (!g) return 0;
+    if (g->active) return h3_set_error(g, "kernel timing: cannot change inside begin/submit");
+    kernel_events_clear(g);
+    g->kernel_timing = enable != 0;
+    return 1;
+}
+
+extern "C" int h3_hip_kernel_timing_read(h3_gpu *g, double *ms_total, uint64_t *launches) {
+    if (!g || !ms_total || !launches) return 0;
+    if (g->active) return h3_set_error(g, "kernel timing: read after submit");
+    double total = 0;
+    uint64_t n = 0;
+    if (g->kernel_events) {
+        for (auto &p : *g->kernel_events) {
+            float ms = 0;
+            if (!h3_hip_check(g, hipEventSynchronize(p.second), "kernel timing") ||
+                !h3_hip_check(g, hipEventElapsedTime(&ms, p.first, p.second), "kernel timing"))
+                return 0;
+            total += ms;
+            n++;
+        }
+        kernel_events_clear(g);
+    }
+    *ms_total = total;
+    *launches = n;
+    return 1;
 }

@@ -245,7 +245,9 @@ int launch_tiled(h3_gpu *g, const GemmArgs &a) {
         configured = true;
     }
     unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
+    hipEvent_t timing = h3_kernel_timing_begin(g);
     hipLaunchKernelGGL(kernel, dim3(tiles), dim3(512), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, Q8 ? "W8A16 GEMM" : "BF16 GEMM");
 }
 

@@ -24,3 +24,9 @@ struct h3_device_buffer {
 };
 int h3_buffer_reserve(h3_gpu *g, h3_device_buffer *b, size_t bytes, const char *what);
 void h3_buffer_free(h3_device_buffer *b);
+
+// Dominant-kernel timing: h3_kernel_timing_begin records a start event on the
+// compute stream when timing is enabled (else returns nullptr); _end records the
+// stop event and queues the pair for h3_hip_kernel_timing_read.
+hipEvent_t h3_kernel_timing_begin(h3_gpu *g);
+void h3_kernel_timing_end(h3_gpu *g, hipEvent_t start);

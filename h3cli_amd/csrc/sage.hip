@@ -326,7 +326,7 @@ void sage_attn_kernel(SArgs a) {
             mi0 = max(max(mi0, si[0][r]), si[0][r + 1]);
             mi1 = max(max(mi1, si[1][r]), si[1][r + 1]);
         }
-        const float mx = half_max((float)max(mi0, mi1)) * c;
+        const float mx = half_max_swap((float)max(mi0, mi1)) * c;
         if (__builtin_amdgcn_ballot_w64(mx > m + P_SLACK)) {
             const float mnew = fmaxf(m, mx);
             const float alpha = exp2f_fast(m - mnew);
@@ -403,7 +403,9 @@ void sage_attn_kernel(SArgs a) {
 template <int WAVES, int OCC, bool SPARSE>
 int launch_sage(h3_gpu *g, const SArgs &a, unsigned groups) {
     constexpr size_t shared = 2 * SAGE_TILE;
+    hipEvent_t timing = h3_kernel_timing_begin(g);
     hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE>), dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "Sage attention");
 }
 }  // namespace

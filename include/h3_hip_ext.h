@@ -104,6 +104,13 @@ int h3_hip_fill_normal_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor, uint64_t seed, f
  * h3_gpu_submit/synchronize. */
 h3_gpu_event *h3_hip_timing_event_new(h3_gpu *gpu);
 int h3_hip_event_elapsed_ms(h3_gpu *gpu, h3_gpu_event *start, h3_gpu_event *end, float *ms);
+/* Dominant-kernel timing: while enabled, each BF16 / Sage attention dispatch and
+ * each tiled GEMM records HIP events on the compute stream around its main
+ * kernel only (not the V transpose, the quantizers or small fallbacks).
+ * h3_hip_kernel_timing_read (after submit) returns the summed milliseconds and
+ * the number of timed launches, and clears them. Enabling or disabling also clears. */
+int h3_hip_kernel_timing(h3_gpu *gpu, int enable);
+int h3_hip_kernel_timing_read(h3_gpu *gpu, double *ms_total, uint64_t *launches);
 
 #ifdef __cplusplus
 }
