@@ -17,6 +17,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -29,11 +30,18 @@ __host__ __device__ inline float bf16_to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 // Round-to-nearest-even; NaN stays a quiet NaN.
+// Round-to-nearest-even FP32 -> BF16. On the device this is one
+// v_cvt_pk_bf16_f32 (same result for every non-NaN input; NaN becomes a quiet
+// NaN); the host keeps the bit-level rounding.
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
     uint32_t u = __builtin_bit_cast(uint32_t, f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
+#endif
 }
 
 // Finite test on the bit pattern. The library is built with relaxed NaN

@@ -39,7 +39,10 @@ struct AdaLNArgs {
 // MODE 2: plain RMSNorm y = bf16(x * rsqrt(mean x^2 + eps) * w), no modulation
 // (src/cuda/cuda_kernels.cuh:805-833).
 enum { ADALN = 0, GATE_ADALN = 1, RMS_NORM = 2 };
-template <int MODE>
+// CH: 16-byte chunks per lane (width <= 512 * CH); the row stays in registers
+// as packed BF16 between the reduction and the output pass (exact: the value
+// normalized is the BF16 input, or the BF16-rounded gated row).
+template <int MODE, int CH>
 __global__ __launch_bounds__(256) void adaln_kernel(AdaLNArgs a) {
     constexpr bool GATE = MODE == GATE_ADALN;
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -48,49 +51,67 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdaLNArgs a) {
     const unsigned chunks = a.width / 8;
     const size_t base = (size_t)row * a.width;
     const size_t mbase = MODE == RMS_NORM ? 0 : (size_t)a.row_map[row] * a.slots * a.width;
-    float v[MAX_CHUNKS][8];
+    u16x8 raw[CH];
     float sumsq = 0.f;
 #pragma unroll
-    for (int i = 0; i < MAX_CHUNKS; i++) {
-        unsigned c = lane + 64 * i;
+    for (int i = 0; i < CH; i++) {
+        const unsigned c = lane + 64 * i;
         if (c >= chunks) break;
-        u16x8 xr = *reinterpret_cast<const u16x8 *>(a.x + base + c * 8);
-        unpack8(xr, v[i]);
+        raw[i] = *reinterpret_cast<const u16x8 *>(a.x + base + c * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const unsigned c = lane + 64 * i;
+        if (c >= chunks) break;
         if constexpr (GATE) {
             u16x8 br = *reinterpret_cast<const u16x8 *>(a.branch + base + c * 8);
             u16x8 gr = *reinterpret_cast<const u16x8 *>(a.gate_mod + mbase + (size_t)a.gate_slot * a.width + c * 8);
-            u16x8 outr;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                outr[e] = f32_to_bf16(fmaf(bf16_to_f32(br[e]), bf16_to_f32(gr[e]), v[i][e]));
-                v[i][e] = bf16_to_f32(outr[e]);
-            }
-            *reinterpret_cast<u16x8 *>(a.gated + base + c * 8) = outr;
+            for (int e = 0; e < 8; e++)
+                raw[i][e] = f32_to_bf16(fmaf(bf16_to_f32(br[e]), bf16_to_f32(gr[e]), bf16_to_f32(raw[i][e])));
+            *reinterpret_cast<u16x8 *>(a.gated + base + c * 8) = raw[i];
         }
 #pragma unroll
-        for (int e = 0; e < 8; e++) sumsq = fmaf(v[i][e], v[i][e], sumsq);
+        for (int e = 0; e < 8; e++) {
+            const float v = bf16_to_f32(raw[i][e]);
+            sumsq = fmaf(v, v, sumsq);
+        }
     }
     const float inv = rsqrtf(wave_sum(sumsq) / (float)a.width + a.eps);
 #pragma unroll
-    for (int i = 0; i < MAX_CHUNKS; i++) {
-        unsigned c = lane + 64 * i;
+    for (int i = 0; i < CH; i++) {
+        const unsigned c = lane + 64 * i;
         if (c >= chunks) break;
         u16x8 wr = *reinterpret_cast<const u16x8 *>(a.weight + c * 8);
         u16x8 o;
         if constexpr (MODE == RMS_NORM) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) o[e] = f32_to_bf16(v[i][e] * inv * bf16_to_f32(wr[e]));
+            for (int e = 0; e < 8; e++) o[e] = f32_to_bf16(bf16_to_f32(raw[i][e]) * inv * bf16_to_f32(wr[e]));
         } else {
             u16x8 sh = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.shift_slot * a.width + c * 8);
             u16x8 sc = *reinterpret_cast<const u16x8 *>(a.mod + mbase + (size_t)a.scale_slot * a.width + c * 8);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                float normalized = v[i][e] * inv * bf16_to_f32(wr[e]);
+                float normalized = bf16_to_f32(raw[i][e]) * inv * bf16_to_f32(wr[e]);
                 o[e] = f32_to_bf16(fmaf(normalized, 1.0f + bf16_to_f32(sc[e]), bf16_to_f32(sh[e])));
             }
         }
         *reinterpret_cast<u16x8 *>(a.out + base + c * 8) = o;
     }
+}
+
+// Launch with the smallest chunk count that covers the row.
+template <int MODE>
+void launch_adaln(h3_gpu *g, const AdaLNArgs &a) {
+    const unsigned per_lane = (a.width / 8 + 63) / 64;
+    const dim3 grid((a.rows + 3) / 4), block(256);
+#define H3_ADALN_CASE(n) case n: hipLaunchKernelGGL((adaln_kernel<MODE, n>), grid, block, 0, g->compute, a); break;
+    switch (per_lane) {
+        H3_ADALN_CASE(1) H3_ADALN_CASE(2) H3_ADALN_CASE(3) H3_ADALN_CASE(4) H3_ADALN_CASE(5) H3_ADALN_CASE(6)
+        H3_ADALN_CASE(7) H3_ADALN_CASE(8) H3_ADALN_CASE(9) H3_ADALN_CASE(10) H3_ADALN_CASE(11) H3_ADALN_CASE(12)
+        H3_ADALN_CASE(13) H3_ADALN_CASE(14) H3_ADALN_CASE(15) default: H3_ADALN_CASE(16)
+    }
+#undef H3_ADALN_CASE
 }
 
 // out = bf16(residual + branch * gate), 8 elements per thread.
@@ -185,6 +206,83 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(QkvArgs a) {
     }
 }
 
+// D = 128 with 2 * half <= 128 and half % 8 == 0 (the DiT shapes): 16 lanes per
+// (row, head), each owning one 16-byte chunk of Q, K and V. A lane rotating
+// chunk c < half/8 pairs it with chunk c + half/8 (and vice versa), loading the
+// partner chunk itself (the partner lane loads it at the same time, so the
+// second read hits L1); chunks past 2*half pass through. The per-head RMSNorm
+// reduces over the 16 lanes with xor shuffles.
+__device__ inline float sum16(float v) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void qkv_rope_vec(QkvArgs a) {
+    const size_t items = (size_t)a.seq * a.heads;
+    const size_t item = (size_t)blockIdx.x * 16 + threadIdx.x / 16;
+    if (item >= items) return;   // whole 16-lane groups exit together (no barriers here)
+    const unsigned c = threadIdx.x % 16;              // chunk: channels 8c .. 8c+7
+    const unsigned row = item / a.heads, head = item % a.heads;
+    const unsigned hc = a.half / 8;
+    const size_t inner = (size_t)a.heads * 128, row_base = (size_t)row * inner * 3;
+    size_t qb = row_base + (size_t)head * 128, kb = qb + inner, vb = qb + 2 * inner;
+    if (a.grouped) { qb = row_base + (size_t)head * 384; kb = qb + 128; vb = kb + 128; }
+    const size_t out = ((size_t)row * a.heads + head) * 128 + c * 8;
+
+    const bool rot = c < 2 * hc;
+    const unsigned pc = c < hc ? c + hc : c - hc;     // partner chunk (rotating lanes)
+    u16x8 qr = *reinterpret_cast<const u16x8 *>(a.qkv + qb + c * 8);
+    u16x8 kr = *reinterpret_cast<const u16x8 *>(a.qkv + kb + c * 8);
+    u16x8 vr = *reinterpret_cast<const u16x8 *>(a.qkv + vb + c * 8);
+    u16x8 qp = {}, kp = {}, cs = {}, sn = {};
+    if (rot) {
+        qp = *reinterpret_cast<const u16x8 *>(a.qkv + qb + pc * 8);
+        kp = *reinterpret_cast<const u16x8 *>(a.qkv + kb + pc * 8);
+        const unsigned pos = (c < hc ? c : pc) * 8;   // pair index of this chunk
+        cs = *reinterpret_cast<const u16x8 *>(a.cos_t + (size_t)row * a.half + pos);
+        sn = *reinterpret_cast<const u16x8 *>(a.sin_t + (size_t)row * a.half + pos);
+    }
+    *reinterpret_cast<u16x8 *>(a.v + out) = vr;
+
+    float q[8], k[8], q2[8], k2[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        q[e] = bf16_to_f32(qr[e]); k[e] = bf16_to_f32(kr[e]);
+        q2[e] = bf16_to_f32(qp[e]); k2[e] = bf16_to_f32(kp[e]);
+    }
+    if (a.qw) {
+        float qs = 0.f, ks = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) { qs = fmaf(q[e], q[e], qs); ks = fmaf(k[e], k[e], ks); }
+        const float qi = rsqrtf(sum16(qs) / 128.0f + a.eps), ki = rsqrtf(sum16(ks) / 128.0f + a.eps);
+        u16x8 wq = *reinterpret_cast<const u16x8 *>(a.qw + c * 8), wk = *reinterpret_cast<const u16x8 *>(a.kw + c * 8);
+        u16x8 wq2 = {}, wk2 = {};
+        if (rot) { wq2 = *reinterpret_cast<const u16x8 *>(a.qw + pc * 8); wk2 = *reinterpret_cast<const u16x8 *>(a.kw + pc * 8); }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            q[e] = q[e] * qi * bf16_to_f32(wq[e]);
+            k[e] = k[e] * ki * bf16_to_f32(wk[e]);
+            q2[e] = q2[e] * qi * bf16_to_f32(wq2[e]);
+            k2[e] = k2[e] * ki * bf16_to_f32(wk2[e]);
+        }
+    }
+    u16x8 qo, ko;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        float qv = q[e], kv = k[e];
+        if (rot) {
+            const float cv = bf16_to_f32(cs[e]), sv = bf16_to_f32(sn[e]);
+            if (c < hc) { qv = q[e] * cv - q2[e] * sv; kv = k[e] * cv - k2[e] * sv; }
+            else { qv = q[e] * cv + q2[e] * sv; kv = k[e] * cv + k2[e] * sv; }
+        }
+        qo[e] = f32_to_bf16(qv);
+        ko[e] = f32_to_bf16(kv);
+    }
+    *reinterpret_cast<u16x8 *>(a.q + out) = qo;
+    *reinterpret_cast<u16x8 *>(a.k + out) = ko;
+}
+
 __device__ inline float gelu_value(float v, int approximate) {
     if (approximate) {
         float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
@@ -241,7 +339,7 @@ extern "C" int h3_gpu_adaln_bf16_offset(h3_gpu *g, h3_gpu_tensor *out, const h3_
         return 0;
     AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data + offset, nullptr, (const uint16_t *)w->data,
                 (const uint16_t *)mod->data, nullptr, (const uint32_t *)map->data, rows, width, slots, shift, scale, 0, eps};
-    hipLaunchKernelGGL(adaln_kernel<ADALN>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    launch_adaln<ADALN>(g, a);
     return h3_launch_status(g, "AdaLN");
 }
 
@@ -263,7 +361,7 @@ extern "C" int h3_gpu_rms_norm_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
         return 0;
     AdaLNArgs a{(uint16_t *)out->data, nullptr, (const uint16_t *)in->data, nullptr, (const uint16_t *)w->data,
                 nullptr, nullptr, nullptr, rows, width, 0, 0, 0, 0, eps};
-    hipLaunchKernelGGL(adaln_kernel<RMS_NORM>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    launch_adaln<RMS_NORM>(g, a);
     return h3_launch_status(g, "RMSNorm");
 }
 
@@ -304,7 +402,7 @@ extern "C" int h3_gpu_gate_adaln_bf16(h3_gpu *g, h3_gpu_tensor *gated, h3_gpu_te
     AdaLNArgs a{(uint16_t *)out->data, (uint16_t *)gated->data, (const uint16_t *)res->data, (const uint16_t *)branch->data,
                 (const uint16_t *)w->data, (const uint16_t *)norm_mod->data, (const uint16_t *)gate_mod->data,
                 (const uint32_t *)map->data, rows, width, slots, shift, scale, gate_slot, eps};
-    hipLaunchKernelGGL(adaln_kernel<GATE_ADALN>, dim3(blocks_for(rows, 4)), dim3(256), 0, g->compute, a);
+    launch_adaln<GATE_ADALN>(g, a);
     return h3_launch_status(g, "gate AdaLN");
 }
 
@@ -325,7 +423,10 @@ static int qkv_rope(h3_gpu *g, h3_gpu_tensor *q, h3_gpu_tensor *k, h3_gpu_tensor
               qw ? (const uint16_t *)qw->data : nullptr, kw ? (const uint16_t *)kw->data : nullptr,
               half ? (const uint16_t *)c->data : nullptr, half ? (const uint16_t *)s->data : nullptr,
               seq, heads, dim, half, eps, grouped};
-    hipLaunchKernelGGL(qkv_rope_kernel, dim3(blocks_for((size_t)seq * heads, 4)), dim3(256), 0, g->compute, a);
+    if (dim == 128 && half % 8 == 0 && half <= 64)
+        hipLaunchKernelGGL(qkv_rope_vec, dim3(blocks_for((size_t)seq * heads, 16)), dim3(256), 0, g->compute, a);
+    else
+        hipLaunchKernelGGL(qkv_rope_kernel, dim3(blocks_for((size_t)seq * heads, 4)), dim3(256), 0, g->compute, a);
     return h3_launch_status(g, "QKV norm/RoPE");
 }
 

@@ -55,7 +55,6 @@ __device__ inline float gelu_tanh(float v) {
 }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // 8 waves as 2 (M) x 4 (N); each wave owns a 128 x 64 output tile (8 MFMA
 // blocks), two waves per SIMD. CHANNEL: one scale per output row (group == K),

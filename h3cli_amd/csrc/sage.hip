@@ -57,36 +57,33 @@ void h3_sage_workspace_free(h3_sage_workspace *w) {
 }
 
 // ---------------------------------------------------------------- quantizers
-// Partial K sums and V maxima: thread = (partial, head, 8-channel chunk), rows
-// of the partial summed in row order in fp32.
+// Partial K sums and V maxima: thread = (partial, head, channel pair), rows of
+// the partial summed in row order in fp32. A wave covers one head's 128
+// channels, so every row read is one contiguous 256-byte segment.
 __global__ __launch_bounds__(256) void sage_reduce_partials(const uint16_t *k, const uint16_t *v, float *sums,
                                                            float *maxima, unsigned seq, unsigned heads,
                                                            unsigned partials, unsigned *fault) {
-    unsigned idx = blockIdx.x * 256 + threadIdx.x;
-    unsigned chunk = idx % 16, rest = idx / 16, head = rest % heads, p = rest / heads;
+    const unsigned idx = blockIdx.x * 256 + threadIdx.x;
+    const unsigned pair = idx % 64, rest = idx / 64, head = rest % heads, p = rest / heads;
     if (p >= partials) return;
-    float sum[8], vmax[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) { sum[e] = 0.f; vmax[e] = 0.f; }
-    bool bad = false;
-    unsigned end = min(seq, (p + 1) * PARTIAL_ROWS);
+    float s0 = 0.f, s1 = 0.f, m0 = 0.f, m1 = 0.f;
+    uint32_t bad = 0;
+    const unsigned end = min(seq, (p + 1) * PARTIAL_ROWS);
     const size_t stride = (size_t)heads * D;
-    const size_t col = (size_t)head * D + chunk * 8;
-#pragma unroll 4
+    const size_t col = (size_t)head * D + pair * 2;
+#pragma unroll 8
     for (unsigned row = p * PARTIAL_ROWS; row < end; row++) {
-        u16x8 kx = *reinterpret_cast<const u16x8 *>(k + row * stride + col);
-        u16x8 vx = *reinterpret_cast<const u16x8 *>(v + row * stride + col);
-        bad |= bf16_vec_nonfinite(kx) | bf16_vec_nonfinite(vx);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float x = bf16_to_f32(kx[e]), y = bf16_to_f32(vx[e]);
-            sum[e] = __fadd_rn(sum[e], x);
-            vmax[e] = fmaxf(vmax[e], fabsf(y));
-        }
+        const uint32_t kx = *reinterpret_cast<const uint32_t *>(k + row * stride + col);
+        const uint32_t vx = *reinterpret_cast<const uint32_t *>(v + row * stride + col);
+        bad |= bf16x2_nonfinite(kx) | bf16x2_nonfinite(vx);
+        s0 = __fadd_rn(s0, bf16_to_f32((uint16_t)kx));
+        s1 = __fadd_rn(s1, bf16_to_f32((uint16_t)(kx >> 16)));
+        m0 = fmaxf(m0, fabsf(bf16_to_f32((uint16_t)vx)));
+        m1 = fmaxf(m1, fabsf(bf16_to_f32((uint16_t)(vx >> 16))));
     }
-    size_t at = ((size_t)head * partials + p) * D + chunk * 8;
-#pragma unroll
-    for (int e = 0; e < 8; e++) { sums[at + e] = sum[e]; maxima[at + e] = vmax[e]; }
+    const size_t at = ((size_t)head * partials + p) * D + pair * 2;
+    *reinterpret_cast<f32x2 *>(sums + at) = f32x2{s0, s1};
+    *reinterpret_cast<f32x2 *>(maxima + at) = f32x2{m0, m1};
     if (bad) fault[1] = 1u;
 }
 
@@ -97,6 +94,7 @@ __global__ __launch_bounds__(128) void sage_reduce_finish(const float *sums, con
                                                          unsigned partials) {
     unsigned head = blockIdx.x, d = threadIdx.x;
     float sum = 0.f, vmax = 0.f;
+#pragma unroll 8
     for (unsigned p = 0; p < partials; p++) {
         size_t at = ((size_t)head * partials + p) * D + d;
         sum = __fadd_rn(sum, sums[at]);
@@ -178,25 +176,31 @@ __global__ __launch_bounds__(256) void sage_pack_v(const uint16_t *v, const floa
     __syncthreads();
     const unsigned d = t / 2, half = t % 2;
     const float rcp = v_recip[head * D + d];
-    uint32_t w[8];
+    // Hardware RNE encode (v_cvt_pk_fp8_f32, OCP e4m3): |v| * 448 / max|v| stays
+    // below 464, the first value that would overflow, so it matches the
+    // saturating software encoder f32_to_e4m3 bit for bit.
+    int w[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) w[j] = 0;
+    for (int j = 0; j < 8; j++) {
+        float f[4];
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-        // Position p = half*32 + i holds key mb*32 + (r/4)*8 + half*4 + r%4 with mb = i/16, r = i%16.
-        unsigned mb = i / 16, r = i % 16;
-        unsigned key = mb * 32 + (r / 4) * 8 + half * 4 + (r % 4);
-        uint8_t code = f32_to_e4m3(__fmul_rn(bf16_to_f32(tile[key][d]), rcp));
-        w[i / 4] |= (uint32_t)code << (8 * (i % 4));
+        for (int u = 0; u < 4; u++) {
+            // Position p = half*32 + i holds key mb*32 + (r/4)*8 + half*4 + r%4 with mb = i/16, r = i%16.
+            const unsigned i = 4 * j + u, mb = i / 16, r = i % 16;
+            const unsigned key = mb * 32 + (r / 4) * 8 + half * 4 + (r % 4);
+            f[u] = __fmul_rn(bf16_to_f32(tile[key][d]), rcp);
+        }
+        w[j] = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+        w[j] = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], w[j], true);
     }
     uint8_t *dst = codes + ((size_t)head * D + d) * padded + blk * BN + half * 32;
-    *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    *reinterpret_cast<i32x4 *>(dst + 16) = i32x4{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+    *reinterpret_cast<i32x4 *>(dst) = i32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<i32x4 *>(dst + 16) = i32x4{w[4], w[5], w[6], w[7]};
 }
 
 int h3_sage_quantize(h3_gpu *g, const h3_sage_layout &L, char *ws, const uint16_t *q, const uint16_t *k,
                      const uint16_t *v) {
-    unsigned threads = L.partials * L.heads * 16;
+    unsigned threads = L.partials * L.heads * 64;
     hipLaunchKernelGGL(sage_reduce_partials, dim3((threads + 255) / 256), dim3(256), 0, g->compute, k, v,
                        (float *)(ws + L.sums), (float *)(ws + L.maxima), L.seq, L.heads, L.partials, g->fault);
     hipLaunchKernelGGL(sage_reduce_finish, dim3(L.heads), dim3(128), 0, g->compute, (const float *)(ws + L.sums),
