@@ -435,7 +435,8 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride; a.fault = g->fault;
-    if (kv_list) return launch_sage<4, 2, true>(g, a, (seq + 127) / 128 * heads);
+    // Block-sparse lists are per 128-query block: 4 waves, three workgroups per CU.
+    if (kv_list) return launch_sage<4, 3, true>(g, a, (seq + 127) / 128 * heads);
     // 12 waves x 32 queries: three waves per SIMD (166 VGPRs each).
     if (g->attention_variant == 1) return launch_sage<8, 2, false>(g, a, (seq + 255) / 256 * heads);
     return launch_sage<12, 3, false>(g, a, (seq + 383) / 384 * heads);
