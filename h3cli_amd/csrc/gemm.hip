@@ -32,7 +32,19 @@ constexpr int TILE_BYTES = 256 * ROW_BYTES;     // 32 KB per operand tile
 constexpr int STAGE = 2 * TILE_BYTES;           // X tile + W tile
 constexpr int GROUP_M = 8;                      // tile rows per grouped band
 
+// 16-byte chunk swizzle of a 128-byte LDS row. A ds_read_b128 serves sixteen
+// lanes (sixteen consecutive rows) per cycle across 256 bytes of banks: rows
+// 2i and 2i+1 sit in different halves, and (row >> 1) & 7 spreads the eight
+// pairs over eight chunks. Writes are served eight lanes per cycle across 128
+// bytes; the weight store therefore gives eight consecutive lanes eight rows
+// of the same parity (see w_row).
 __device__ inline unsigned swz(unsigned row, unsigned ch) { return ch ^ ((row >> 1) & 7); }
+
+// Weight staging map: chunk c (0..1023) of a 256 x 64 int8 tile -> (row, part).
+// A wave covers 16 rows x 4 parts; lanes 8i..8i+7 of a part take rows of one
+// parity, so their LDS stores hit eight different chunks.
+__device__ inline unsigned w_row(unsigned c) { const unsigned l = c % 16; return (c / 64) * 16 + 2 * (l % 8) + l / 8; }
+__device__ inline unsigned w_part(unsigned c) { return (c / 16) % 4; }
 
 struct GemmArgs {
     uint16_t *y;
@@ -86,14 +98,14 @@ void gemm_kernel(GemmArgs a) {
     float wscale[2];
     if constexpr (Q8 && CHANNEL) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) wscale[j] = a.scales[n0 + (tid + 512 * j) / 4];
+        for (int j = 0; j < 2; j++) wscale[j] = a.scales[n0 + w_row(tid + 512 * j)];
     }
     auto load_w = [&](unsigned kt) {
         if constexpr (Q8) {
             const int8_t *w8 = reinterpret_cast<const int8_t *>(a.w);
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                unsigned c = tid + 512 * j, row = c / 4, part = c % 4;
+                unsigned c = tid + 512 * j, row = w_row(c), part = w_part(c);
                 wq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
                 if constexpr (!CHANNEL)
                     wscale[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
@@ -105,7 +117,7 @@ void gemm_kernel(GemmArgs a) {
             uint8_t *ws = lds + stage * STAGE + TILE_BYTES;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                unsigned c = tid + 512 * j, row = c / 4, part = c % 4;
+                unsigned c = tid + 512 * j, row = w_row(c), part = w_part(c);
                 bf16x8 half[2];
 #pragma unroll
                 for (int e = 0; e < 16; e += 2) {
