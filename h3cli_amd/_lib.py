@@ -94,6 +94,22 @@ _SIGNATURES = {
     "h3_hip_synthetic_block_mask": (C.c_uint, [_p, C.c_uint, C.c_uint, C.c_uint, C.c_double, C.c_uint64]),
 }
 
+
+
+class SolBlock(C.Structure):
+    """h3_sol_block (include/h3_gpu_surface.h; reference src/denoise/sol.h:7)."""
+    _fields_ = [("protect", C.c_uint32), ("first_frame", C.c_int32), ("last_frame", C.c_int32), ("rows", C.c_uint32)]
+
+
+class SolLayout(C.Structure):
+    """h3_sol_layout (include/h3_gpu_surface.h; reference src/denoise/sol.h:8-11)."""
+    _fields_ = [("sequence", C.c_uint32), ("query_blocks", C.c_uint32), ("key_blocks", C.c_uint32),
+                ("protected_rows", C.c_uint32), ("query", C.POINTER(SolBlock)), ("key", C.POINTER(SolBlock))]
+
+class GpuStats(C.Structure):
+    """h3_gpu_stats (include/h3_gpu.h), field for field."""
+    _fields_ = [("q8_weights", C.c_uint64), ("q8_source_bytes", C.c_uint64), ("q8_storage_bytes", C.c_uint64), ("q8_dispatches", C.c_uint64), ("q8_load_seconds", C.c_double), ("layout_prepares", C.c_uint64), ("layout_inplace_packs", C.c_uint64), ("layout_scan_replaced_bytes", C.c_uint64), ("layout_partial_bytes", C.c_uint64), ("allocated_bytes", C.c_uint64), ("live_bytes", C.c_uint64), ("peak_live_bytes", C.c_uint64), ("tensor_allocations", C.c_uint64), ("direct_dispatches", C.c_uint64), ("mps_linear_dispatches", C.c_uint64), ("mps_conv_dispatches", C.c_uint64), ("mps_sdpa_dispatches", C.c_uint64), ("native_attention_dispatches", C.c_uint64), ("metal_current_allocated_bytes", C.c_uint64), ("blit_copies", C.c_uint64), ("submissions", C.c_uint64), ("command_encode_seconds", C.c_double), ("command_wait_seconds", C.c_double), ("gpu_seconds", C.c_double), ("linear_dispatches", C.c_uint64), ("conv_dispatches", C.c_uint64), ("attention_dispatches", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2h_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64), ("streamed_bytes", C.c_uint64), ("resident_weight_bytes", C.c_uint64), ("stream_slot_bytes", C.c_uint64), ("resident_block_mask", C.c_uint64), ("resident_blocks", C.c_uint32), ("active_weight_blocks", C.c_uint32), ("device_bytes", C.c_uint64), ("managed_bytes", C.c_uint64), ("pinned_bytes", C.c_uint64), ("peak_pinned_bytes", C.c_uint64), ("stream_stalls", C.c_uint64), ("transfer_seconds", C.c_double), ("stream_wait_seconds", C.c_double), ("linear_seconds", C.c_double), ("attention_seconds", C.c_double), ("conv_seconds", C.c_double), ("h2d_seconds", C.c_double), ("d2h_seconds", C.c_double), ("slot_wait_seconds", C.c_double), ("normalization_seconds", C.c_double), ("weight_cache_bytes", C.c_uint64), ("weight_cache_hits", C.c_uint64), ("weight_cache_hit_bytes", C.c_uint64), ("weight_cache_misses", C.c_uint64), ("weight_cache_evictions", C.c_uint64), ("quant_conversion_seconds", C.c_double), ("quant_clipped_values", C.c_uint64), ("quant_zeroed_values", C.c_uint64), ("quant_projection_dispatches", C.c_uint64), ("quant_cache_hits", C.c_uint64), ("quant_cache_misses", C.c_uint64), ("sage2_attention_dispatches", C.c_uint64), ("sage3_attention_dispatches", C.c_uint64), ("attention_workspace_bytes", C.c_uint64), ("inflight_peak", C.c_uint64), ("command_retirements", C.c_uint64), ("bounded_waits", C.c_uint64), ("pressure_drains", C.c_uint64), ("native_scratch_bytes", C.c_uint64), ("native_scratch_allocations", C.c_uint64), ("native_scratch_reuses", C.c_uint64), ("native_pipeline_count", C.c_uint64), ("main_dense_calls", C.c_uint64), ("subblock_calls", C.c_uint64), ("subblock_bypass", C.c_uint64), ("subblock_protected_calls", C.c_uint64), ("subblock_selected", C.c_uint64), ("subblock_possible", C.c_uint64), ("subblock_router_calls", C.c_uint64), ("attention_timing_samples", C.c_uint64), ("attention_timing_missed", C.c_uint64), ("main_attention_seconds", C.c_double), ("subblock_router_seconds", C.c_double), ("subblock_kernel_seconds", C.c_double)]
+
 class DitSynthConfig(C.Structure):
     """include/h3_dit_synth.h h3_hip_dit_synth_config."""
     _fields_ = [("blocks", _u32), ("hidden", _u32), ("heads", _u32), ("mlp", _u32),
@@ -118,6 +134,7 @@ _SIGNATURES.update({
     "h3_hip_fill_q8_random": (_i, [_p, _p, C.c_uint64, _f, _f]),
     "h3_hip_tensor_copy_to_host": (_i, [_p, _p, _sz]),
     "h3_hip_dit_subblock_policy": (_i, [_p, _f, _i]),
+    "h3_hip_subblock_routes": (_i, [_p, _p, _p, C.c_size_t, _p, _p, C.c_size_t]),
     # the rest of the reference surface implemented here (include/h3_gpu_surface.h)
     "h3_gpu_adaln_bf16_offset": (_i, [_p, _p, _p, _sz, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _f]),
     "h3_gpu_rms_norm_bf16": (_i, [_p, _p, _p, _p, _u32, _u32, _f]),

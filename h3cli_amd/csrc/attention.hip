@@ -6,6 +6,7 @@
 #include "common.h"
 #include "internal.h"
 #include "sage.h"
+#include "subblock.h"
 #include "../../include/h3_policy.h"
 #include <cmath>
 #include <new>
@@ -27,6 +28,8 @@ struct h3_attention_state {
     uint32_t *kv_list = nullptr, *kv_count = nullptr;
     uint32_t list_stride = 0;
     uint64_t kept_tiles = 0, total_tiles = 0;  // over 128-query blocks x 64-key tiles
+    // SubBlock router over the bound layout (used when no host mask is bound).
+    h3_subblock_router router;
     h3_sage_workspace sage;
     h3_device_buffer bf16_ws;              // transposed V of the BF16 kernel
     // Per-dispatch timing (H3_PROFILE): pairs of events collected at synchronize.
@@ -44,14 +47,19 @@ void h3_attention_destroy(h3_gpu *g) {
     if (s->kv_list) hipFree(s->kv_list);
     if (s->kv_count) hipFree(s->kv_count);
     h3_sage_workspace_free(&s->sage);
+    h3_subblock_free(&s->router);
     h3_buffer_free(&s->bf16_ws);
     for (auto &p : s->pending) { hipEventDestroy(p.first); hipEventDestroy(p.second); }
     delete s; g->attention = nullptr;
 }
 
+int h3_attention_mode(h3_gpu *g) { return g && g->attention && g->attention->configured ? g->attention->mode : 0; }
+h3_subblock_router *h3_attention_router(h3_gpu *g) { return g && g->attention ? &g->attention->router : nullptr; }
+
 void h3_attention_collect_timing(h3_gpu *g) {
     auto *s = g->attention;
     if (!s) return;
+    h3_subblock_collect(g, &s->router);
     for (auto &p : s->pending) {
         float ms = 0;
         if (hipEventElapsedTime(&ms, p.first, p.second) == hipSuccess) {
@@ -101,7 +109,7 @@ extern "C" int h3_hip_dit_block_mask(h3_gpu *g, const uint8_t *mask, uint32_t qb
     for (uint32_t r = 0; r < q_rows; r++) {
         uint32_t c = 0;
         for (uint32_t t = 0; t < tiles; t++)
-            if (mask[(size_t)r * kb + t / 2]) list[(size_t)r * tiles + c++] = t;
+            if (mask[(size_t)r * kb + t / 2]) list[(size_t)r * tiles + c++] = t | (3u << 30);  // both query halves
         count[r] = c;
         s->kept_tiles += c;
     }
@@ -125,7 +133,7 @@ static float round_scale_bf16(float scale) {
 
 static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
                     const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                    int mode, bool masked) {
+                    int mode, bool masked, bool routed = false) {
     auto *s = g->attention;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     if (g->profiling) {
@@ -134,15 +142,18 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
     }
     const uint32_t *list = masked ? s->kv_list : nullptr;
     const uint32_t *cnt = masked ? s->kv_count : nullptr;
+    uint32_t stride = s->list_stride;
+    if (routed) { list = h3_subblock_lists(&s->router); cnt = h3_subblock_counts(&s->router); stride = s->router.blocks; }
     int ok;
     if (mode == MODE_SAGE2) {
         ok = h3_sage_attention(g, &s->sage, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
-                               (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
+                               (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride);
         if (ok) g->stats.sage2_attention_dispatches++;
     } else {
         ok = h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") &&
              h3_launch_attention_bf16(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
-                                      (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, s->list_stride);
+                                      (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride,
+                                      routed);
     }
     g->stats.attention_workspace_bytes = s->sage.bytes + s->bf16_ws.bytes;
     if (g->profiling) {
@@ -151,7 +162,8 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
     }
     if (ok) {
         g->stats.attention_dispatches++;
-        if (masked) { g->stats.subblock_calls++; g->stats.subblock_selected += s->kept_tiles; g->stats.subblock_possible += s->total_tiles; }
+        if (routed) { g->stats.subblock_calls++; g->stats.subblock_protected_calls += s->router.protected_ranges; }
+        else if (masked) { g->stats.subblock_calls++; g->stats.subblock_selected += s->kept_tiles; g->stats.subblock_possible += s->total_tiles; }
         else if (mode == MODE_DEFAULT) g->stats.main_dense_calls++;
     }
     return ok;
@@ -185,7 +197,15 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
             g->stats.subblock_bypass++;
             masked = false;
         } else if (!s->masked) {
-            return h3_set_error(g, "SubBlock attention on HIP needs a bound block mask (h3_hip_dit_block_mask)");
+            // Router path (reference gpu_cuda.cu:1620-1639): the scale is used
+            // as given; protected query blocks route every key block, which
+            // is the dense result the reference computes for them separately.
+            const unsigned blocks = (seq + 63) / 64;
+            const unsigned keep = h3_subblock_budget(blocks, s->subblock_sparsity);
+            if (!h3_subblock_route(g, &s->router, (const uint16_t *)q->data, (const uint16_t *)k->data, seq, heads,
+                                   scale, keep, false))
+                return 0;
+            return dispatch(g, out, q, k, v, seq, heads, scale, head_major != 0, MODE_DEFAULT, false, true);
         }
     }
     // A kept last 128-key block may list a 64-key tile wholly past the sequence

@@ -54,9 +54,14 @@ struct Args {
     unsigned seq, heads, padded;
     float scale_log2;                      // softmax scale * log2(e)
     int head_major;
-    const uint32_t *kv_list;               // sparse: per 128-query block, kept 64-key tile ids (all heads)
-    const uint32_t *kv_count;              // sparse: number of kept tiles per 128-query block
+    // Sparse: per 128-query block (and per head when list_head_blocks != 0),
+    // the kept 64-key tiles in ascending order. An entry is the tile id in
+    // bits 0-29; bit 30 + h says whether query half h (rows 64h .. 64h+63 of
+    // the block) attends to it.
+    const uint32_t *kv_list;
+    const uint32_t *kv_count;              // sparse: number of entries per list
     unsigned list_stride;
+    unsigned list_head_blocks;             // 0: one list set for all heads; else 128-query blocks per head
     unsigned *fault;
 };
 
@@ -131,11 +136,15 @@ void attn_bf16_kernel(Args a) {
     unsigned count;
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        count = a.kv_count[qb];
-        list = a.kv_list + (size_t)qb * a.list_stride;
+        static_assert(BM == 128, "sparse lists describe 128-query blocks");
+        const size_t lq = (size_t)head * a.list_head_blocks + qb;
+        count = a.kv_count[lq];
+        list = a.kv_list + lq * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
     }
+    // Route bit of this wave's 64-query half in a sparse list entry.
+    const unsigned route_bit = 1u << (30 + wave * WQ / 64);
 
     // Query fragments: B operand of S^T = K Q^T, 8 k-steps of 16 channels.
     bf16x8 qf[NB][8];
@@ -284,16 +293,19 @@ void attn_bf16_kernel(Args a) {
         }
     };
 
-    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    constexpr uint32_t TILE_BITS = 0x3fffffffu;
+    if (count) load_tile(SPARSE ? list[0] & TILE_BITS : 0, 0);
     wait_vm_loads();
     __syncthreads();
 
     for (unsigned it = 0; it < count; it++) {
         const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        const uint32_t entry = SPARSE ? list[it] : it;
+        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] & TILE_BITS : it + 1, cur ^ 1);
         const uint8_t *ks = smem + cur * STAGE_BYTES;
-        process(ks, ks + K_BYTES, tile);
+        // A wave whose query half does not route this tile only joins the
+        // shared load and the barrier.
+        if (!SPARSE || (entry & route_bit)) process(ks, ks + K_BYTES, entry & TILE_BITS);
         wait_vm_loads();
         __syncthreads();
     }
@@ -368,13 +380,14 @@ void attn_bf16_wide(Args a) {
     unsigned count;  // 64-key sub-tiles
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        count = a.kv_count[qb];
-        list = a.kv_list + (size_t)qb * a.list_stride;
+        const size_t lq = (size_t)head * a.list_head_blocks + qb;
+        count = a.kv_count[lq];
+        list = a.kv_list + lq * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
     }
     const unsigned groups = (count + KT - 1) / KT;
-    auto sub_at = [&](unsigned i) { i = min(i, count - 1); return SPARSE ? list[i] : i; };
+    auto sub_at = [&](unsigned i) { i = min(i, count - 1); return SPARSE ? list[i] & 0x3fffffffu : i; };
 
     bf16x8 qf[8];
     {
@@ -564,13 +577,15 @@ size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads) {
 
 int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                             const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride) {
+                             const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride,
+                             bool per_head_lists) {
     Args a;
     a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
     a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride;
+    a.list_head_blocks = per_head_lists ? (seq + 127) / 128 : 0;
     a.fault = g->fault;
     hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);

@@ -5,6 +5,8 @@
 int h3_attention_init(h3_gpu *g);
 void h3_attention_destroy(h3_gpu *g);
 void h3_attention_collect_timing(h3_gpu *g);
+struct h3_subblock_router *h3_attention_router(h3_gpu *g);
+int h3_attention_mode(h3_gpu *g);          // configured DiT attention mode (0 when unconfigured)
 void h3_streaming_destroy(h3_gpu *g);
 int h3_tensor_events(h3_gpu *g, h3_gpu_tensor *t);
 int h3_tensor_acquire(h3_gpu *g, const h3_gpu_tensor *t);
@@ -15,7 +17,7 @@ size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads);
 int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale,
                              bool head_major, const uint32_t *kv_list, const uint32_t *kv_count,
-                             uint32_t list_stride);
+                             uint32_t list_stride, bool per_head_lists);
 
 // Grow-only device buffer; growing waits for queued work that may read the old one.
 struct h3_device_buffer {

@@ -262,8 +262,14 @@ void sage_attn_kernel(SArgs a) {
 
     unsigned count;
     const uint32_t *list = nullptr;
-    if constexpr (SPARSE) { count = a.kv_count[qb]; list = a.kv_list + (size_t)qb * a.list_stride; }
-    else count = ntiles;
+    if constexpr (SPARSE) {
+        static_assert(BM == 128, "sparse lists describe 128-query blocks");
+        count = a.kv_count[qb];
+        list = a.kv_list + (size_t)qb * a.list_stride;
+    } else count = ntiles;
+    // Entry layout of the BF16 kernel's lists: tile id in bits 0-29, bit
+    // 30 + h routes query half h.
+    const unsigned route_bit = 1u << (30 + wave / 2);
 
     // Query fragments (B operand of S^T = K Q^T): 4 k-steps of 32 channels.
     i32x4 qf[4];
@@ -366,15 +372,16 @@ void sage_attn_kernel(SArgs a) {
         lsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, lsum, 0, 0, 0, 0, 0, 0);
     };
 
-    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    constexpr uint32_t TILE_BITS = 0x3fffffffu;
+    if (count) load_tile(SPARSE ? list[0] & TILE_BITS : 0, 0);
     wait_vm_loads();
     __syncthreads();
     for (unsigned it = 0; it < count; it++) {
         const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        const uint32_t entry = SPARSE ? list[it] : it;
+        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] & TILE_BITS : it + 1, cur ^ 1);
         const uint8_t *ks = lds + cur * SAGE_TILE;
-        process(ks, ks + Q8_TILE, tile);
+        if (!SPARSE || (entry & route_bit)) process(ks, ks + Q8_TILE, entry & TILE_BITS);
         wait_vm_loads();
         __syncthreads();
     }

@@ -64,6 +64,16 @@ unsigned h3_hip_synthetic_block_mask(uint8_t *mask, unsigned seq, unsigned video
  * (= 10 steps); warmup < 0 disables the warmup rule. */
 int h3_hip_dit_subblock_policy(h3_gpu *gpu, float sparsity, int warmup);
 
+/* SubBlock router capture, the counterpart of the reference's
+ * h3_cuda_subblock_routes (src/cuda/cuda_subblock.cu): after a routed mode-4
+ * call (a layout bound with h3_gpu_dit_sol_layout, no host mask), copies that
+ * call's routes u8 [heads][B][B] and block scores f32 [heads][B][B]
+ * (B = ceil(seq / 64), route_count = heads * B * B) and its pooled BF16 cells
+ * [heads][4B][128] of Q (scaled by scale * log2 e) and K (pool_count =
+ * heads * 4B * 128). Any output may be NULL. Waits for the compute stream. */
+int h3_hip_subblock_routes(h3_gpu *gpu, uint8_t *routes, float *scores, size_t route_count,
+                           uint16_t *q_pool, uint16_t *k_pool, size_t pool_count);
+
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded
  * to a multiple of 64, padded rows zero):

@@ -234,3 +234,113 @@ void oracle_patch_linear(uint16_t *y, const float *x, const float *w, const floa
         }
     }
 }
+
+/* ---- SubBlock router (reference src/cuda/cuda_subblock.cu:256-324) ---- */
+
+/* Pooled 16-row cells: for cell c (rows 16c..16c+15, missing rows 0), the fp32
+ * pairwise tree v[i] += v[i+s] for s = 8, 4, 2, 1 (cuda_subblock.cu:262-263),
+ * mean = v[0] / count * scale, rounded to BF16. out: [heads][cells][128],
+ * cells = ceil(seq/64) * 4 (cells past the sequence are 0). */
+void oracle_sb_pool(uint16_t *out, const uint16_t *x, unsigned seq, unsigned heads, float scale) {
+    const unsigned cells = (seq + 63) / 64 * 4;
+#pragma omp parallel for
+    for (unsigned h = 0; h < heads; h++)
+        for (unsigned cell = 0; cell < cells; cell++)
+            for (unsigned d = 0; d < 128; d++) {
+                unsigned start = cell * 16, count = start < seq ? (seq - start < 16 ? seq - start : 16) : 0;
+                float v[16];
+                for (unsigned i = 0; i < 16; i++)
+                    v[i] = i < count ? oracle_bf16_to_f32(x[((size_t)(start + i) * heads + h) * 128 + d]) : 0.f;
+                for (unsigned s = 8; s; s >>= 1)
+                    for (unsigned i = 0; i < s; i++) v[i] += v[i + s];
+                float mean = count ? v[0] / (float)count * scale : 0.f;
+                out[((size_t)h * cells + cell) * 128 + d] = oracle_f32_to_bf16(mean);
+            }
+}
+
+/* Block scores (cuda_subblock.cu:272-297): for query block i and key block j,
+ * dots of the (up to 4 x 4) valid pooled cells, each an fp32 fmaf chain over d;
+ * per query cell a: lse_a = max_b + log2(sum_b exp2(dot - max_b)); score =
+ * (max_a + log2(sum_a exp2(lse_a - max_a))) * ln 2. scores: [heads][B][B]. */
+void oracle_sb_score(float *scores, const uint16_t *qp, const uint16_t *kp, unsigned seq, unsigned heads) {
+    const unsigned blocks = (seq + 63) / 64, cells = blocks * 4;
+#pragma omp parallel for collapse(2)
+    for (unsigned h = 0; h < heads; h++)
+        for (unsigned qb = 0; qb < blocks; qb++)
+            for (unsigned kb = 0; kb < blocks; kb++) {
+                unsigned nq = (seq - qb * 64 + 15) / 16, nk = (seq - kb * 64 + 15) / 16;
+                if (nq > 4) nq = 4;
+                if (nk > 4) nk = 4;
+                float qlse[4] = {0};
+                for (unsigned a = 0; a < nq; a++) {
+                    float dots[4] = {0};
+                    for (unsigned b = 0; b < nk; b++) {
+                        const uint16_t *qr = qp + ((size_t)h * cells + qb * 4 + a) * 128;
+                        const uint16_t *kr = kp + ((size_t)h * cells + kb * 4 + b) * 128;
+                        float sum = 0.f;
+                        for (unsigned d = 0; d < 128; d++) sum = fmaf(oracle_bf16_to_f32(qr[d]), oracle_bf16_to_f32(kr[d]), sum);
+                        dots[b] = sum;
+                    }
+                    float largest = dots[0], sum = 0.f;
+                    for (unsigned b = 1; b < nk; b++) largest = fmaxf(largest, dots[b]);
+                    for (unsigned b = 0; b < nk; b++) sum += exp2f(dots[b] - largest);
+                    qlse[a] = largest + log2f(sum);
+                }
+                float largest = qlse[0], sum = 0.f;
+                for (unsigned a = 1; a < nq; a++) largest = fmaxf(largest, qlse[a]);
+                for (unsigned a = 0; a < nq; a++) sum += exp2f(qlse[a] - largest);
+                scores[((size_t)h * blocks + qb) * blocks + kb] = (largest + log2f(sum)) * 0.6931471805599453f;
+            }
+}
+
+/* Routes (cuda_subblock.cu:300-324): key block k of query row i is kept when
+ * its rank (scores greater, or equal with a lower index) is below `keep`, when
+ * k is protected, or when the query block is protected. routes: [heads][B][B]. */
+void oracle_sb_select(uint8_t *routes, const float *scores, unsigned heads, unsigned blocks, unsigned keep,
+                      const uint8_t *q_protect, const uint8_t *k_protect) {
+#pragma omp parallel for collapse(2)
+    for (unsigned h = 0; h < heads; h++)
+        for (unsigned qb = 0; qb < blocks; qb++) {
+            const float *row = scores + ((size_t)h * blocks + qb) * blocks;
+            for (unsigned k = 0; k < blocks; k++) {
+                unsigned rank = 0;
+                for (unsigned j = 0; j < blocks; j++) rank += row[j] > row[k] || (row[j] == row[k] && j < k);
+                routes[((size_t)h * blocks + qb) * blocks + k] =
+                    (uint8_t)(rank < keep || (k_protect && k_protect[k]) || (q_protect && q_protect[qb]));
+            }
+        }
+}
+
+/* Attention with a per-head 64 x 64 route mask (routes [heads][B][B]), rows
+ * [row0, row1): the masked online softmax of oracle_attention_masked with the
+ * head's own mask. out: FP32 [row1-row0, heads, 128]. */
+void oracle_attention_routed(float *out, const float *q, const float *k, const float *v, unsigned seq,
+                             unsigned heads, float scale, const uint8_t *routes, unsigned row0, unsigned row1) {
+    const unsigned blocks = (seq + 63) / 64;
+#pragma omp parallel for collapse(2)
+    for (unsigned h = 0; h < heads; h++)
+        for (unsigned r = row0; r < row1; r++) {
+            const uint8_t *mrow = routes + ((size_t)h * blocks + r / 64) * blocks;
+            const float *qr = q + ((size_t)r * heads + h) * 128;
+            double m = -1e300, l = 0, acc[128] = {0};
+            for (unsigned j = 0; j < seq; j++) {
+                if (!mrow[j / 64]) continue;
+                const float *kr = k + ((size_t)j * heads + h) * 128;
+                double s = 0;
+                for (unsigned d = 0; d < 128; d++) s += (double)qr[d] * kr[d];
+                s *= scale;
+                if (s > m) {
+                    double a = exp(m - s);
+                    for (unsigned d = 0; d < 128; d++) acc[d] *= a;
+                    l *= a;
+                    m = s;
+                }
+                double p = exp(s - m);
+                l += p;
+                const float *vr = v + ((size_t)j * heads + h) * 128;
+                for (unsigned d = 0; d < 128; d++) acc[d] += p * vr[d];
+            }
+            float *o = out + ((size_t)(r - row0) * heads + h) * 128;
+            for (unsigned d = 0; d < 128; d++) o[d] = l > 0 ? (float)(acc[d] / l) : 0.f;
+        }
+}

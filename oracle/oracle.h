@@ -97,6 +97,14 @@ void oracle_euler(float *sample, const uint16_t *last, const uint16_t *previous,
 
 
 
+/* ---- SubBlock router (src/cuda/cuda_subblock.cu:256-324); see block.c ---- */
+void oracle_sb_pool(uint16_t *out, const uint16_t *x, unsigned seq, unsigned heads, float scale);
+void oracle_sb_score(float *scores, const uint16_t *qp, const uint16_t *kp, unsigned seq, unsigned heads);
+void oracle_sb_select(uint8_t *routes, const float *scores, unsigned heads, unsigned blocks, unsigned keep,
+                      const uint8_t *q_protect, const uint8_t *k_protect);
+void oracle_attention_routed(float *out, const float *q, const float *k, const float *v, unsigned seq,
+                             unsigned heads, float scale, const uint8_t *routes, unsigned row0, unsigned row1);
+
 /* ---- reference test-input generators (tests/cuda_attention.c:14-18,
  * tests/attention_native.c:20) ---- */
 void oracle_xorshift_bf16(uint16_t *out, size_t count, uint32_t *seed);

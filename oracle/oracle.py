@@ -55,6 +55,10 @@ def load():
         lib.oracle_swiglu.argtypes = [_p, _p, _u, _u]
         lib.oracle_euler.argtypes = [_p, _p, _p, C.c_size_t, _f, _f]
         lib.oracle_rms_norm.argtypes = [_p, _p, _p, _u, _u, _f]
+        lib.oracle_sb_pool.argtypes = [_p, _p, _u, _u, _f]
+        lib.oracle_sb_score.argtypes = [_p, _p, _p, _u, _u]
+        lib.oracle_sb_select.argtypes = [_p, _p, _u, _u, _u, _p, _p]
+        lib.oracle_attention_routed.argtypes = [_p, _p, _p, _p, _u, _u, _f, _p, _u, _u]
         lib.oracle_head_rms_norm.argtypes = [_p, _p, _u, _u, _u, _f]
         lib.oracle_patch_linear.argtypes = [_p, _p, _p, _p, _p, _u, _u, _u, _u]
         _lib = lib
@@ -282,3 +286,34 @@ def patch_linear(x, w, bias, m, k, n, row_map=None, out_rows=None):
     mp = None if row_map is None else np.ascontiguousarray(row_map, np.uint32)
     load().oracle_patch_linear(_ptr(y), _ptr(xf), _ptr(wf), _ptr(b), _ptr(mp), out_rows, m, k, n)
     return y
+
+
+def sb_pool(x, seq, heads, scale):
+    cells = (seq + 63) // 64 * 4
+    out = np.zeros(heads * cells * 128, np.uint16)
+    load().oracle_sb_pool(_ptr(out), _ptr(_u16(x)), seq, heads, scale)
+    return out
+
+
+def sb_score(qp, kp, seq, heads):
+    blocks = (seq + 63) // 64
+    out = np.zeros(heads * blocks * blocks, np.float32)
+    load().oracle_sb_score(_ptr(out), _ptr(_u16(qp)), _ptr(_u16(kp)), seq, heads)
+    return out
+
+
+def sb_select(scores, heads, blocks, keep, q_protect=None, k_protect=None):
+    routes = np.zeros(heads * blocks * blocks, np.uint8)
+    qp = None if q_protect is None else np.ascontiguousarray(q_protect, np.uint8)
+    kp = None if k_protect is None else np.ascontiguousarray(k_protect, np.uint8)
+    load().oracle_sb_select(_ptr(routes), _ptr(np.ascontiguousarray(scores, np.float32)), heads, blocks, keep,
+                            _ptr(qp), _ptr(kp))
+    return routes
+
+
+def attention_routed(q, k, v, seq, heads, scale, routes, rows=None):
+    r0, r1 = rows or (0, seq)
+    out = np.zeros((r1 - r0) * heads * 128, np.float32)
+    load().oracle_attention_routed(_ptr(out), _ptr(_f32(q)), _ptr(_f32(k)), _ptr(_f32(v)), seq, heads, scale,
+                                   _ptr(np.ascontiguousarray(routes, np.uint8)), r0, r1)
+    return out
