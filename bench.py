@@ -136,6 +136,50 @@ def cpu_baseline(q, k, v, seq, heads, rows):
                        f"{dt:.2f} s; TFLOP/s of that slice (same FLOP convention)")
 
 
+def subblock_leg(steps, warmup, sparsity=0.75):
+    """Attention mode 4 with the router: a 64-row-block layout bound for S,
+    sparsity 0.75 (keep = 8 * ceil(0.25 * B / 8) key blocks per query block),
+    a step past the warmup and a non-probe block, so every call routes. Per
+    call: pooling, block scores, selection and list build, V transpose and the
+    routed attention kernel (timed on its own)."""
+    import ctypes as C
+    from h3cli_amd._lib import GpuStats, SolBlock, SolLayout
+    from h3cli_amd.runtime import Gpu
+    with Gpu() as gpu:
+        lib = gpu.lib
+        gpu.check(lib.h3_gpu_dit_attention_configure(gpu.handle, 4), "configure subblock")
+        gpu.check(lib.h3_hip_dit_subblock_policy(gpu.handle, sparsity, 0), "policy")
+        blocks = (SEQ + 63) // 64
+        meta = (SolBlock * blocks)()
+        for b in range(blocks):
+            meta[b].rows = min(64, SEQ - b * 64)
+        layout = SolLayout(SEQ, blocks, blocks, 0, C.cast(meta, C.POINTER(SolBlock)), C.cast(meta, C.POINTER(SolBlock)))
+        gpu.check(lib.h3_gpu_dit_sol_layout(gpu.handle, C.byref(layout)), "layout")
+        gpu.check(lib.h3_gpu_dit_attention_noise(gpu.handle, 12, 0.5, 0.5), "noise")
+        log("[bench] subblock attention: preparing inputs")
+        w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=True)
+
+        def call():
+            return lib.h3_gpu_dit_sdpa_bf16(gpu.handle, w.out.handle, w.q.handle, w.k.handle, w.v.handle, SEQ, HEADS,
+                                            DIM, 1.0 / math.sqrt(DIM), 0, 1, 12)
+        kt = []
+        ms, _ = time_calls(gpu, call, steps, warmup, kt)
+        st = GpuStats()
+        gpu.check(lib.h3_gpu_get_stats(gpu.handle, C.byref(st)), "stats")
+        density = st.subblock_selected / max(st.subblock_possible, 1)
+        kernel_ms = kt[0][0]
+        dense_eq = attention_flops(SEQ, HEADS) / (ms * 1e-3) / 1e12
+        routed = attention_flops(SEQ, HEADS, density=density) / (kernel_ms * 1e-3) / 1e12
+        log(f"[bench] subblock: {ms:.3f} ms/call, density {density:.4f}, routed kernel {kernel_ms:.3f} ms "
+            f"({routed:.1f} TFLOP/s on kept tiles), router + transpose {ms - kernel_ms:.3f} ms")
+        return {"workload": "SubBlock routed attention, S=32400 H=40, sparsity 0.75, no protected blocks",
+                "ms_per_call": round(ms, 4), "density": round(density, 5),
+                "dense_equivalent_tflops": round(dense_eq, 3), "kernel_ms": round(kernel_ms, 4),
+                "kernel_tflops_on_kept_tiles": round(routed, 3),
+                "kernel_frac_of_bf16_peak": round(routed / PEAK_BF16, 4),
+                "router_and_transpose_ms": round(ms - kernel_ms, 4)}
+
+
 GEMM_SHAPES = [("qkv", 5120, 15360, False), ("out", 5120, 5120, False), ("up_gelu", 5120, 13824, True),
                ("down", 13824, 5120, False)]
 
@@ -245,7 +289,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,gemm,step")
+    ap.add_argument("--legs", default="attention,sage,subblock,gemm,step")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -319,6 +363,8 @@ def main():
                               "speedup_vs_bf16": round(ms / ms_s, 3),
                               "kernel_ms": round(kt[0][0], 4),
                               "frac_of_fp8_peak": round(eff / PEAK_FP8, 4)}
+    if "subblock" in legs:
+        result["subblock"] = subblock_leg(args.steps, args.warmup)
     if "gemm" in legs:
         result["gemm"] = gemm_leg(args.steps, args.warmup)
     if "step" in legs:

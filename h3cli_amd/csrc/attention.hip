@@ -109,7 +109,7 @@ extern "C" int h3_hip_dit_block_mask(h3_gpu *g, const uint8_t *mask, uint32_t qb
     for (uint32_t r = 0; r < q_rows; r++) {
         uint32_t c = 0;
         for (uint32_t t = 0; t < tiles; t++)
-            if (mask[(size_t)r * kb + t / 2]) list[(size_t)r * tiles + c++] = t | (3u << 30);  // both query halves
+            if (mask[(size_t)r * kb + t / 2]) list[(size_t)r * tiles + c++] = t;
         count[r] = c;
         s->kept_tiles += c;
     }
@@ -142,18 +142,22 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
     }
     const uint32_t *list = masked ? s->kv_list : nullptr;
     const uint32_t *cnt = masked ? s->kv_count : nullptr;
-    uint32_t stride = s->list_stride;
-    if (routed) { list = h3_subblock_lists(&s->router); cnt = h3_subblock_counts(&s->router); stride = s->router.blocks; }
+    const uint32_t stride = s->list_stride;
     int ok;
-    if (mode == MODE_SAGE2) {
+    if (routed) {
+        ok = h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") &&
+             h3_launch_attention_routed(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data,
+                                        (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads, scale,
+                                        head_major, h3_subblock_lists(&s->router), h3_subblock_counts(&s->router),
+                                        s->router.blocks);
+    } else if (mode == MODE_SAGE2) {
         ok = h3_sage_attention(g, &s->sage, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
                                (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride);
         if (ok) g->stats.sage2_attention_dispatches++;
     } else {
         ok = h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") &&
              h3_launch_attention_bf16(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
-                                      (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride,
-                                      routed);
+                                      (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride);
     }
     g->stats.attention_workspace_bytes = s->sage.bytes + s->bf16_ws.bytes;
     if (g->profiling) {

@@ -54,14 +54,11 @@ struct Args {
     unsigned seq, heads, padded;
     float scale_log2;                      // softmax scale * log2(e)
     int head_major;
-    // Sparse: per 128-query block (and per head when list_head_blocks != 0),
-    // the kept 64-key tiles in ascending order. An entry is the tile id in
-    // bits 0-29; bit 30 + h says whether query half h (rows 64h .. 64h+63 of
-    // the block) attends to it.
+    // Sparse: kept 64-key tile ids in ascending order, per 128-query block
+    // (host masks, all heads) or per (head, 64-query block) (routed kernel).
     const uint32_t *kv_list;
     const uint32_t *kv_count;              // sparse: number of entries per list
     unsigned list_stride;
-    unsigned list_head_blocks;             // 0: one list set for all heads; else 128-query blocks per head
     unsigned *fault;
 };
 
@@ -73,12 +70,13 @@ __host__ __device__ inline unsigned v_position(unsigned j) {
     return (j & ~15u) + ((k16 >> 2) & 1) * 8 + (k16 >> 3) * 4 + (k16 & 3);
 }
 
-// V [seq, heads, 128] -> Vt [heads, 128, padded]; one workgroup per (64-key tile,
-// head). The pass also screens this tile's K and V rows for Inf/NaN.
+// V [seq, heads, 128] -> Vt [heads, 128, padded]; one workgroup per (head,
+// 64-key tile), heads fastest so that concurrent workgroups read whole
+// sequence rows. The pass also screens this tile's K and V rows for Inf/NaN.
 __global__ __launch_bounds__(256) void transpose_v(const uint16_t *v, const uint16_t *k, uint16_t *vt, unsigned seq,
                                                   unsigned heads, unsigned padded, unsigned *fault) {
     __shared__ uint16_t tile[BN][D + 8];
-    const unsigned blk = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+    const unsigned blk = blockIdx.y, head = blockIdx.x, t = threadIdx.x;
     const size_t stride = (size_t)heads * D;
     bool bad = false;
 #pragma unroll
@@ -136,15 +134,11 @@ void attn_bf16_kernel(Args a) {
     unsigned count;
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        static_assert(BM == 128, "sparse lists describe 128-query blocks");
-        const size_t lq = (size_t)head * a.list_head_blocks + qb;
-        count = a.kv_count[lq];
-        list = a.kv_list + lq * a.list_stride;
+        count = a.kv_count[qb];
+        list = a.kv_list + (size_t)qb * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
     }
-    // Route bit of this wave's 64-query half in a sparse list entry.
-    const unsigned route_bit = 1u << (30 + wave * WQ / 64);
 
     // Query fragments: B operand of S^T = K Q^T, 8 k-steps of 16 channels.
     bf16x8 qf[NB][8];
@@ -293,19 +287,16 @@ void attn_bf16_kernel(Args a) {
         }
     };
 
-    constexpr uint32_t TILE_BITS = 0x3fffffffu;
-    if (count) load_tile(SPARSE ? list[0] & TILE_BITS : 0, 0);
+    if (count) load_tile(SPARSE ? list[0] : 0, 0);
     wait_vm_loads();
     __syncthreads();
 
     for (unsigned it = 0; it < count; it++) {
         const int cur = it & 1;
-        const uint32_t entry = SPARSE ? list[it] : it;
-        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] & TILE_BITS : it + 1, cur ^ 1);
+        const unsigned tile = SPARSE ? list[it] : it;
+        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
         const uint8_t *ks = smem + cur * STAGE_BYTES;
-        // A wave whose query half does not route this tile only joins the
-        // shared load and the barrier.
-        if (!SPARSE || (entry & route_bit)) process(ks, ks + K_BYTES, entry & TILE_BITS);
+        process(ks, ks + K_BYTES, tile);
         wait_vm_loads();
         __syncthreads();
     }
@@ -380,14 +371,13 @@ void attn_bf16_wide(Args a) {
     unsigned count;  // 64-key sub-tiles
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        const size_t lq = (size_t)head * a.list_head_blocks + qb;
-        count = a.kv_count[lq];
-        list = a.kv_list + lq * a.list_stride;
+        count = a.kv_count[qb];
+        list = a.kv_list + (size_t)qb * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
     }
     const unsigned groups = (count + KT - 1) / KT;
-    auto sub_at = [&](unsigned i) { i = min(i, count - 1); return SPARSE ? list[i] & 0x3fffffffu : i; };
+    auto sub_at = [&](unsigned i) { i = min(i, count - 1); return SPARSE ? list[i] : i; };
 
     bf16x8 qf[8];
     {
@@ -569,6 +559,222 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
     return h3_launch_status(g, "BF16 attention");
 }
 
+
+// Routed sparse attention: one workgroup of two waves per (64-query block,
+// head) walks that block's own list of kept 64-key tiles (ascending tile ids,
+// a list per head and query block).
+//  * SPLIT: 32 KB of LDS hold one K tile and one V^T tile; the phases are
+//    offset so that the next K tile loads during this tile's softmax and P.V,
+//    and the next V^T tile during the next scores. Barriers: one after the
+//    scores (K free, V^T ready), one after P.V (V^T free, next K ready).
+//  * otherwise two full stages (64 KB): the next tile loads during this one.
+// MSUM: row sums of P on the matrix core instead of VALU adds.
+template <bool SPLIT, bool MSUM, int OCC>
+__global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(OCC, OCC)))
+void attn_bf16_routed(Args a) {
+    constexpr int BLOCKS = K_BYTES / 1024;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const unsigned n = lane % 32, hf = lane / 32;
+    const unsigned nqb = (a.seq + 63) / 64;
+    const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned head = id / nqb, qb = id % nqb;
+    const unsigned q0 = qb * 64;
+    const size_t stride = (size_t)a.heads * D;
+    const uint16_t *qh = a.q + (size_t)head * D;
+    const uint16_t *kh = a.k + (size_t)head * D;
+    const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
+    const float c = a.scale_log2;
+    const size_t lq = (size_t)head * nqb + qb;
+    const unsigned count = a.kv_count[lq];
+    const uint32_t *list = a.kv_list + lq * a.list_stride;
+
+    bf16x8 qf[8];
+    {
+        unsigned row = min(q0 + wave * 32 + n, a.seq - 1);
+        const uint16_t *p = qh + (size_t)row * stride + hf * 8;
+        bool bad = false;
+#pragma unroll
+        for (int k8 = 0; k8 < 8; k8++) {
+            qf[k8] = *reinterpret_cast<const bf16x8 *>(p + k8 * 16);
+            bad |= bf16_vec_nonfinite(qf[k8]);
+        }
+        if (bad) a.fault[0] = 1u;
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int md = 0; md < 4; md++) o[md] = f32x16{};
+    f32x16 lsum = f32x16{};
+    float m = -1e30f, l = 0.f;
+    bf16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
+
+    auto load_k = [&](unsigned tile, uint8_t *ks) {
+        const unsigned key0 = tile * BN;
+#pragma unroll
+        for (unsigned b = wave; b < BLOCKS; b += 2) {
+            unsigned key = 4 * b + lane / 16, phys = lane % 16;
+            unsigned row = min(key0 + key, a.seq - 1);
+            const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
+        }
+    };
+    auto load_v = [&](unsigned tile, uint8_t *vs) {
+        const unsigned col = min(tile * BN, a.padded - BN);
+#pragma unroll
+        for (unsigned b = wave; b < BLOCKS; b += 2) {
+            unsigned d = 8 * b + lane / 8, vph = lane % 8;
+            const uint16_t *src = vth + (size_t)d * a.padded + col + v_chunk(d, vph) * 8;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
+        }
+    };
+    // Scores S^T = K Q^T for a tile's 64 keys.
+    auto scores = [&](const uint8_t *ks, f32x16 (&s)[2]) {
+        s[0] = f32x16{}; s[1] = f32x16{};
+#pragma unroll
+        for (int kstep = 0; kstep < 8; kstep++)
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++) {
+                const unsigned key = mb * 32 + n;
+                bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, kstep * 2 + hf) * 16);
+                s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kstep], s[mb], 0, 0, 0);
+            }
+    };
+    // Online softmax of the tile and O^T += V^T P^T.
+    auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, unsigned tile) {
+        if (tile * BN + BN > a.seq) {
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
+                    if (key >= a.seq) s[mb][r] = -INFINITY;
+                }
+        }
+        float mx0 = fmaxf(s[0][0], s[0][1]), mx1 = fmaxf(s[1][0], s[1][1]);
+#pragma unroll
+        for (int r = 2; r < 16; r += 2) {
+            mx0 = fmaxf(fmaxf(mx0, s[0][r]), s[0][r + 1]);
+            mx1 = fmaxf(fmaxf(mx1, s[1][r]), s[1][r + 1]);
+        }
+        const float mx = half_max_swap(fmaxf(mx0, mx1)) * c;
+        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_SLACK)) {
+            const float mnew = fmaxf(m, mx);
+            const float alpha = exp2f_fast(m - mnew);
+            m = mnew;
+            if constexpr (MSUM) lsum *= alpha;
+            else l *= alpha;
+#pragma unroll
+            for (int md = 0; md < 4; md++) o[md] *= alpha;
+        }
+        const float neg = -m;
+        bf16x8 pb[4];
+        float psum = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float p0 = exp2f_fast(fmaf(s[mb][r], c, neg));
+                float p1 = exp2f_fast(fmaf(s[mb][r + 1], c, neg));
+                if constexpr (!MSUM) psum += p0 + p1;
+                pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
+                pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
+            }
+        if constexpr (!MSUM) l += psum;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+            for (int md = 0; md < 4; md++) {
+                const unsigned d = md * 32 + n;
+                bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, kk * 2 + hf) * 16);
+                o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kk], o[md], 0, 0, 0);
+            }
+            if constexpr (MSUM) lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[kk], lsum, 0, 0, 0);
+        }
+    };
+
+    if constexpr (SPLIT) {
+        uint8_t *ks = smem, *vs = smem + K_BYTES;
+        if (count) { load_k(list[0], ks); load_v(list[0], vs); }
+        wait_vm_loads();
+        __syncthreads();
+        for (unsigned it = 0; it < count; it++) {
+            const unsigned tile = list[it];
+            const bool has_next = it + 1 < count;
+            const unsigned next = has_next ? list[it + 1] : 0;
+            f32x16 s[2];
+            scores(ks, s);
+            wait_vm_loads();               // this tile's V^T (own share)
+            __syncthreads();               // K free; every share of V^T landed
+            if (has_next) load_k(next, ks);
+            softmax_pv(s, vs, tile);
+            wait_vm_loads();               // next K (own share)
+            __syncthreads();               // V^T free; every share of the next K landed
+            if (has_next) load_v(next, vs);
+        }
+    } else {
+        if (count) { load_k(list[0], smem); load_v(list[0], smem + K_BYTES); }
+        wait_vm_loads();
+        __syncthreads();
+        for (unsigned it = 0; it < count; it++) {
+            const int cur = it & 1;
+            uint8_t *ks = smem + cur * STAGE_BYTES;
+            if (it + 1 < count) {
+                uint8_t *nk = smem + (cur ^ 1) * STAGE_BYTES;
+                load_k(list[it + 1], nk);
+                load_v(list[it + 1], nk + K_BYTES);
+            }
+            f32x16 s[2];
+            scores(ks, s);
+            softmax_pv(s, ks + K_BYTES, list[it]);
+            wait_vm_loads();
+            __syncthreads();
+        }
+    }
+
+    const float total = MSUM ? lsum[0] : half_sum_swap(l);
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const unsigned q = q0 + wave * 32 + n;
+    bool bad = false;
+    if (q < a.seq) {
+        uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
+#pragma unroll
+        for (int md = 0; md < 4; md++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                u16x4 w;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float x = o[md][g4 * 4 + i] * inv;
+                    bad |= !finite_f32(x);
+                    w[i] = f32_to_bf16(x);
+                }
+                *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
+            }
+    }
+    if (bad) a.fault[0] = 1u;
+}
+
+template <bool SPLIT, bool MSUM, int OCC>
+int launch_routed(h3_gpu *g, const Args &a, unsigned groups) {
+    constexpr size_t shared = SPLIT ? STAGE_BYTES : 2 * STAGE_BYTES;
+    static bool configured = false;
+    auto kernel = attn_bf16_routed<SPLIT, MSUM, OCC>;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
+                          "attention shared memory"))
+            return 0;
+        configured = true;
+    }
+    hipEvent_t timing = h3_kernel_timing_begin(g);
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(128), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "routed BF16 attention");
+}
+
 }  // namespace
 
 size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads) {
@@ -577,17 +783,15 @@ size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads) {
 
 int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                             const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride,
-                             bool per_head_lists) {
+                             const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride) {
     Args a;
     a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
     a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride;
-    a.list_head_blocks = per_head_lists ? (seq + 127) / 128 : 0;
     a.fault = g->fault;
-    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+    hipLaunchKernelGGL(transpose_v, dim3(heads, a.padded / BN), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     // Sparse lists are per 128-query block: 4 waves per workgroup, two
@@ -597,4 +801,26 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     if (g->attention_variant == 1) return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
     if (g->attention_variant == 2) return launch<12, 1, 3, false, false>(g, a, (seq + 383) / 384 * heads);
     return launch_wide<2, false, false>(g, a, (seq + 255) / 256 * heads);
+}
+
+int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                               const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
+                               const uint32_t *lists, const uint32_t *counts, uint32_t list_stride) {
+    Args a;
+    a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
+    a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.head_major = head_major ? 1 : 0;
+    a.kv_list = lists; a.kv_count = counts; a.list_stride = list_stride;
+    a.fault = g->fault;
+    hipLaunchKernelGGL(transpose_v, dim3(heads, a.padded / BN), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+                       seq, heads, a.padded, g->fault);
+    if (!h3_launch_status(g, "V transpose")) return 0;
+    const unsigned groups = (seq + 63) / 64 * heads;
+    switch (g->attention_variant) {
+    case 11: return launch_routed<true, true, 2>(g, a, groups);
+    case 12: return launch_routed<false, false, 1>(g, a, groups);
+    case 13: return launch_routed<false, false, 2>(g, a, groups);
+    default: return launch_routed<true, false, 2>(g, a, groups);
+    }
 }

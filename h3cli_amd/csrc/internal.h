@@ -17,7 +17,12 @@ size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads);
 int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale,
                              bool head_major, const uint32_t *kv_list, const uint32_t *kv_count,
-                             uint32_t list_stride, bool per_head_lists);
+                             uint32_t list_stride);
+// Routed attention over per-(head, 64-query block) lists of kept 64-key tiles:
+// lists [heads][ceil(seq/64)][list_stride], counts [heads][ceil(seq/64)].
+int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                               const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
+                               const uint32_t *lists, const uint32_t *counts, uint32_t list_stride);
 
 // Grow-only device buffer; growing waits for queued work that may read the old one.
 struct h3_device_buffer {

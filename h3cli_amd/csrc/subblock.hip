@@ -23,38 +23,41 @@ constexpr unsigned D = 128;
 constexpr unsigned CELL_TILE = 128;        // query cells per score workgroup (4 waves x 32)
 constexpr unsigned KEY_SPLIT = 16;         // 32-cell key tiles per score workgroup
 
-// One thread per (cell, head, channel pair): fp32 tree sum over the cell's 16
-// rows (missing rows are zero), mean * scale, rounded to BF16.
+// One thread per (cell, head, 8 channels): fp32 tree sum over the cell's 16
+// rows (missing rows are zero), mean * scale, rounded to BF16. 16-byte loads;
+// a workgroup covers 16 cells of one head, and the heads of one row range are
+// consecutive workgroups, so concurrent loads cover whole sequence rows.
 __global__ __launch_bounds__(256) void sb_pool(const uint16_t *q, const uint16_t *k, uint16_t *qpool,
                                                uint16_t *kpool, unsigned seq, unsigned heads, unsigned cells,
                                                float qscale, unsigned *fault) {
-    const unsigned cell = blockIdx.x * 4 + threadIdx.x / 64, pair = threadIdx.x % 64, head = blockIdx.y;
+    const unsigned cell = blockIdx.y * 16 + threadIdx.x / 16, part = threadIdx.x % 16, head = blockIdx.x;
     const bool is_k = blockIdx.z != 0;
     const uint16_t *src = is_k ? k : q;
-    uint16_t *dst = (is_k ? kpool : qpool) + ((size_t)head * cells + cell) * D + pair * 2;
+    uint16_t *dst = (is_k ? kpool : qpool) + ((size_t)head * cells + cell) * D + part * 8;
     const float scale = is_k ? 1.f : qscale;
     const unsigned start = cell * 16, count = start < seq ? min(16u, seq - start) : 0u;
-    float a[16], b[16];
+    u16x8 raw[16];
 #pragma unroll
-    for (unsigned i = 0; i < 16; i++) {
-        uint32_t w = 0;
-        if (i < count) w = *reinterpret_cast<const uint32_t *>(src + ((size_t)(start + i) * heads + head) * D + pair * 2);
-        a[i] = bf16_to_f32((uint16_t)(w & 0xffffu));
-        b[i] = bf16_to_f32((uint16_t)(w >> 16));
+    for (unsigned i = 0; i < 16; i++)
+        raw[i] = i < count ? *reinterpret_cast<const u16x8 *>(src + ((size_t)(start + i) * heads + head) * D + part * 8)
+                           : u16x8{};
+    u16x8 result;
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        float v[16];
+#pragma unroll
+        for (unsigned i = 0; i < 16; i++) v[i] = bf16_to_f32(raw[i][c]);
+#pragma unroll
+        for (unsigned s = 8; s; s >>= 1)
+#pragma unroll
+            for (unsigned i = 0; i < s; i++) v[i] += v[i + s];
+        const float mean = count ? __fdiv_rn(v[0], (float)count) * scale : 0.f;
+        result[c] = f32_to_bf16(mean);
+        bad |= !finite_f32(mean) || !finite_f32(bf16_to_f32(result[c]));
     }
-#pragma unroll
-    for (unsigned s = 8; s; s >>= 1)
-#pragma unroll
-        for (unsigned i = 0; i < s; i++) { a[i] += a[i + s]; b[i] += b[i + s]; }
-    float ma = 0.f, mb = 0.f;
-    if (count) {
-        ma = __fdiv_rn(a[0], (float)count) * scale;
-        mb = __fdiv_rn(b[0], (float)count) * scale;
-    }
-    const uint16_t ra = f32_to_bf16(ma), rb = f32_to_bf16(mb);
-    if (!finite_f32(ma) || !finite_f32(mb) || !finite_f32(bf16_to_f32(ra)) || !finite_f32(bf16_to_f32(rb)))
-        fault[0] = 1u;
-    *reinterpret_cast<uint32_t *>(dst) = (uint32_t)ra | ((uint32_t)rb << 16);
+    if (bad) fault[0] = 1u;
+    *reinterpret_cast<u16x8 *>(dst) = result;
 }
 
 __device__ inline float quad_max(float x) {
@@ -88,13 +91,19 @@ __global__ __launch_bounds__(256) void sb_score(const uint16_t *qpool, const uin
     const unsigned ktiles = cells / 32;
     const unsigned kt0 = blockIdx.y * KEY_SPLIT, kt1 = min(ktiles, kt0 + KEY_SPLIT);
     bool bad = false;
-    for (unsigned kt = kt0; kt < kt1 && kt * 8 < blocks; kt++) {
+    const unsigned kend = min(kt1, (blocks + 7) / 8);
+    bf16x8 kf[8];
+    auto load_k = [&](unsigned kt) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            kf[ks] = *reinterpret_cast<const bf16x8 *>(kh + (size_t)(kt * 32 + n) * D + ks * 16 + hf * 8);
+    };
+    if (kt0 < kend) load_k(kt0);
+    for (unsigned kt = kt0; kt < kend; kt++) {
         f32x16 s = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kh + (size_t)(kt * 32 + n) * D + ks * 16 + hf * 8);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s, 0, 0, 0);
-        }
+        for (int ks = 0; ks < 8; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+        if (kt + 1 < kend) load_k(kt + 1);     // next tile's fragments load during the reductions
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const unsigned kblock = kt * 8 + 2 * g + hf;
@@ -108,13 +117,13 @@ __global__ __launch_bounds__(256) void sb_score(const uint16_t *qpool, const uin
             float sum = 0.f;
 #pragma unroll
             for (unsigned b = 0; b < 4; b++)
-                if (b < nk) sum += exp2f(s[4 * g + b] - largest);
-            float lse = (q_valid && nk) ? largest + log2f(sum) : -INFINITY;
+                if (b < nk) sum += __builtin_amdgcn_exp2f(s[4 * g + b] - largest);
+            float lse = (q_valid && nk) ? largest + __builtin_amdgcn_logf(sum) : -INFINITY;
             // Query-cell log-sum-exp over the block's four lanes.
             const float top = quad_max(lse);
-            const float total = quad_sum(q_valid && nk ? exp2f(lse - top) : 0.f);
+            const float total = quad_sum(q_valid && nk ? __builtin_amdgcn_exp2f(lse - top) : 0.f);
             if (a == 0 && qblock < blocks && kblock < blocks) {
-                const float score = (top + log2f(total)) * 0.6931471805599453f;
+                const float score = (top + __builtin_amdgcn_logf(total)) * 0.6931471805599453f;
                 bad |= !finite_f32(score);
                 scores[((size_t)head * blocks + qblock) * blocks + kblock] = score;
             }
@@ -123,78 +132,104 @@ __global__ __launch_bounds__(256) void sb_score(const uint16_t *qpool, const uin
     if (bad) fault[0] = 1u;
 }
 
-// One workgroup per (128-query block p, head): query blocks 2p and 2p + 1.
-// Route rule and counters of the reference's selection
-// (cuda_subblock.cu:300-324): rank = #{j : s_j > s_k or (s_j == s_k and j < k)},
-// kept when rank < keep, the key block is protected, the query block is
-// protected or force_all is set. counters: [0] kept, [1] possible,
-// [2] protected query blocks, [3] protected key blocks added beyond the top.
+// Order-preserving key of a score: larger float, larger key; -0 and +0 map to
+// the same key, so keys tie exactly when the scores compare equal.
+__device__ inline uint32_t score_key(float f) {
+    uint32_t u = __float_as_uint(f == 0.f ? 0.f : f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One workgroup per (query block, head). Route rule and counters of the
+// reference's selection (cuda_subblock.cu:300-324): with
+// rank(k) = #{j : s_j > s_k} + #{j < k : s_j == s_k}, key block k is kept
+// when rank < keep, when it is protected, when the query block is protected
+// or with force_all. rank(k) is k's position when the row is sorted by
+// descending score and ascending index, so a bitonic sort of
+// (key << 32 | ~index) in LDS gives every rank at once (P = next power of two
+// of B; padding sorts last). The kept blocks are then compacted in ascending
+// order into the row's tile list; counts[row] is its length and
+// added_blocks[row] the protected key blocks kept beyond the top.
 __global__ __launch_bounds__(256) void sb_select(const float *scores, uint8_t *routes, const uint8_t *q_protect,
-                                                 const uint8_t *k_protect, unsigned blocks, unsigned keep,
-                                                 int force_all, uint32_t *lists, uint32_t *counts, unsigned nqb,
-                                                 unsigned long long *counters) {
-    extern __shared__ float row[];         // [2][blocks]
+                                                 const uint8_t *k_protect, unsigned blocks, unsigned padded,
+                                                 unsigned keep, int force_all, uint32_t *lists, uint32_t *counts,
+                                                 uint32_t *added_blocks) {
+    extern __shared__ unsigned long long sortbuf[];   // [padded], then top flags [blocks]
+    uint8_t *top_flag = reinterpret_cast<uint8_t *>(sortbuf + padded);
     __shared__ unsigned wave_total[4];
-    __shared__ unsigned long long red[4][4];
+    __shared__ unsigned red[4];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned p = blockIdx.x, head = blockIdx.y;
-    const unsigned qa = 2 * p, rows = min(2u, blocks - qa);
-    const float *src = scores + ((size_t)head * blocks + qa) * blocks;
-    for (unsigned i = tid; i < rows * blocks; i += 256) row[i] = src[i];
+    const unsigned qb = blockIdx.x, head = blockIdx.y;
+    const size_t row = (size_t)head * blocks + qb;
+    const float *src = scores + row * blocks;
+    for (unsigned i = tid; i < padded; i += 256)
+        sortbuf[i] = i < blocks ? ((unsigned long long)score_key(src[i]) << 32) | (0xffffffffu - i) : 0ull;
     __syncthreads();
-    bool pq[2];
-    for (unsigned r = 0; r < 2; r++) pq[r] = r < rows && q_protect[qa + r];
-    uint32_t *list = lists + ((size_t)head * nqb + p) * blocks;
+    // Descending bitonic sort.
+    for (unsigned size = 2; size <= padded; size <<= 1)
+        for (unsigned step = size >> 1; step; step >>= 1) {
+            for (unsigned t = tid; t < padded / 2; t += 256) {
+                const unsigned i = 2 * step * (t / step) + (t % step), j = i + step;
+                const unsigned long long x = sortbuf[i], y = sortbuf[j];
+                const bool descending = (i & size) == 0;
+                if (descending ? x < y : x > y) { sortbuf[i] = y; sortbuf[j] = x; }
+            }
+            __syncthreads();
+        }
+    for (unsigned i = tid; i < blocks; i += 256) top_flag[i] = 0;
+    __syncthreads();
+    for (unsigned p = tid; p < keep; p += 256) top_flag[0xffffffffu - (uint32_t)sortbuf[p]] = 1;
+    __syncthreads();
+
+    const bool pq = q_protect[qb] != 0;
+    uint32_t *list = lists + row * blocks;
+    uint8_t *route_row = routes + row * blocks;
     unsigned offset = 0;
-    unsigned long long kept = 0, added = 0;
+    unsigned added = 0;
     for (unsigned base = 0; base < blocks; base += 256) {
         const unsigned k = base + tid;
-        unsigned route[2] = {0, 0};
+        bool retain = false;
         if (k < blocks) {
+            const bool top = top_flag[k] != 0;
             const bool protect = k_protect[k] != 0;
-            for (unsigned r = 0; r < rows; r++) {
-                const float *sr = row + r * blocks;
-                const float score = sr[k];
-                unsigned rank = 0;
-                for (unsigned j = 0; j < blocks; j++) {
-                    const float x = sr[j];
-                    rank += (x > score) | ((x == score) & (j < k));
-                }
-                const bool top = rank < keep;
-                const bool retain = force_all || pq[r] || top || protect;
-                route[r] = retain;
-                routes[((size_t)head * blocks + qa + r) * blocks + k] = (uint8_t)retain;
-                kept += retain;
-                added += protect && !top && !pq[r] && !force_all;
-            }
+            retain = force_all || pq || top || protect;
+            route_row[k] = (uint8_t)retain;
+            added += protect && !top && !pq && !force_all;
         }
-        // Ordered compaction of the tiles either half routes.
-        const bool any = route[0] | route[1];
-        const unsigned long long mask = __ballot(any);
+        const unsigned long long mask = __ballot(retain);
         const unsigned before = __popcll(mask & ((1ull << lane) - 1ull));
         if (lane == 0) wave_total[wave] = __popcll(mask);
         __syncthreads();
-        unsigned wave_base = offset;
-        for (unsigned w = 0; w < wave; w++) wave_base += wave_total[w];
-        if (any) list[wave_base + before] = k | (route[0] << 30) | (route[1] << 31);
+        unsigned pos = offset + before;
+        for (unsigned w = 0; w < wave; w++) pos += wave_total[w];
+        if (retain) list[pos] = k;
         offset += wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
         __syncthreads();
     }
-    // Workgroup totals of the counters.
-    for (int off = 32; off; off >>= 1) {
-        kept += __shfl_xor(kept, off, 64);
-        added += __shfl_xor(added, off, 64);
-    }
-    if (lane == 0) { red[wave][0] = kept; red[wave][1] = added; }
+    for (int off = 32; off; off >>= 1) added += __shfl_xor(added, off, 64);
+    if (lane == 0) red[wave] = added;
     __syncthreads();
     if (tid == 0) {
-        unsigned long long k_sum = red[0][0] + red[1][0] + red[2][0] + red[3][0];
-        unsigned long long a_sum = red[0][1] + red[1][1] + red[2][1] + red[3][1];
-        counts[(size_t)head * nqb + p] = offset;
-        atomicAdd(counters + 0, k_sum);
-        atomicAdd(counters + 1, (unsigned long long)rows * blocks);
-        atomicAdd(counters + 2, (unsigned long long)(pq[0] + pq[1]));
-        atomicAdd(counters + 3, a_sum);
+        counts[row] = offset;
+        added_blocks[row] = red[0] + red[1] + red[2] + red[3];
+    }
+}
+
+// One workgroup: folds a call's per-row list lengths and added protected
+// blocks into the running counters ([0] kept, [1] protected key blocks added
+// beyond the top).
+__global__ __launch_bounds__(1024) void sb_count(const uint32_t *counts, const uint32_t *added, size_t rows,
+                                                 unsigned long long *counters) {
+    __shared__ unsigned long long red[16][2];
+    unsigned long long k = 0, a = 0;
+    for (size_t i = threadIdx.x; i < rows; i += 1024) { k += counts[i]; a += added[i]; }
+    for (int off = 32; off; off >>= 1) { k += __shfl_xor(k, off, 64); a += __shfl_xor(a, off, 64); }
+    if (threadIdx.x % 64 == 0) { red[threadIdx.x / 64][0] = k; red[threadIdx.x / 64][1] = a; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long kept = 0, extra = 0;
+        for (int w = 0; w < 16; w++) { kept += red[w][0]; extra += red[w][1]; }
+        counters[0] += kept;
+        counters[1] += extra;
     }
 }
 
@@ -207,7 +242,7 @@ int h3_subblock_bind(h3_gpu *g, h3_subblock_router *r, const h3_sol_layout *layo
         return h3_set_error(g, "SubBlock: missing layout");
     if (r->bound) return h3_set_error(g, "SubBlock: layout is already configured");
     const uint32_t seq = layout->sequence, blocks = (seq + 63) / 64;
-    // Selection holds two score rows in 64 KB of LDS: at most 8192 blocks.
+    // Selection sorts a row of 8-byte keys in LDS: at most 8192 blocks.
     if (blocks > 8192) return h3_set_error(g, "SubBlock: sequence %u exceeds the router's limit", seq);
     if (layout->query_blocks != blocks || layout->key_blocks != blocks)
         return h3_set_error(g, "SubBlock: layout geometry differs from Q64/K64");
@@ -238,45 +273,50 @@ int h3_subblock_route(h3_gpu *g, h3_subblock_router *r, const uint16_t *q, const
     const uint32_t blocks = r->blocks;
     // Cells padded to whole score workgroups (128 cells); pad cells pool to 0.
     const uint32_t cells = (blocks * 4 + CELL_TILE - 1) / CELL_TILE * CELL_TILE;
-    const uint32_t nqb = (seq + 127) / 128;
     size_t off = 0;
     r->off_qpool = off; off = align256(off + (size_t)heads * cells * D * 2);
     r->off_kpool = off; off = align256(off + (size_t)heads * cells * D * 2);
     r->off_scores = off; off = align256(off + (size_t)heads * blocks * blocks * 4);
     r->off_routes = off; off = align256(off + (size_t)heads * blocks * blocks);
-    r->off_list = off; off = align256(off + (size_t)heads * nqb * blocks * 4);
-    r->off_count = off; off = align256(off + (size_t)heads * nqb * 4);
+    r->off_list = off; off = align256(off + (size_t)heads * blocks * blocks * 4);
+    r->off_count = off; off = align256(off + (size_t)heads * blocks * 4);
+    r->off_added = off; off = align256(off + (size_t)heads * blocks * 4);
     r->off_counters = off; off = align256(off + 4 * 8);
     const bool fresh = r->ws.bytes < off;
     if (!h3_buffer_reserve(g, &r->ws, off, "SubBlock workspace")) return 0;
     auto *base = (uint8_t *)r->ws.ptr;
     auto *counters = (unsigned long long *)(base + r->off_counters);
     if (fresh && !h3_hip_check(g, hipMemsetAsync(counters, 0, 4 * 8, g->compute), "SubBlock counters")) return 0;
-    r->heads = heads; r->cells = cells; r->nqb = nqb;
+    r->heads = heads; r->cells = cells;
     auto *qpool = (uint16_t *)(base + r->off_qpool), *kpool = (uint16_t *)(base + r->off_kpool);
     auto *scores = (float *)(base + r->off_scores);
     const auto *meta = (const uint8_t *)r->meta.ptr;
 
-    hipLaunchKernelGGL(sb_pool, dim3(cells / 4, heads, 2), dim3(256), 0, g->compute, q, k, qpool, kpool, seq, heads,
+    hipLaunchKernelGGL(sb_pool, dim3(heads, cells / 16, 2), dim3(256), 0, g->compute, q, k, qpool, kpool, seq, heads,
                        cells, scale * 1.4426950408889634f, g->fault);
     if (!h3_launch_status(g, "SubBlock pool")) return 0;
     const unsigned ktiles = cells / 32;
     hipLaunchKernelGGL(sb_score, dim3(cells / CELL_TILE, (ktiles + KEY_SPLIT - 1) / KEY_SPLIT, heads), dim3(256), 0,
                        g->compute, qpool, kpool, scores, seq, cells, blocks, g->fault);
     if (!h3_launch_status(g, "SubBlock score")) return 0;
-    const size_t shared = 2 * (size_t)blocks * sizeof(float);
-    if (shared > 64 * 1024) return h3_set_error(g, "SubBlock: %u blocks exceed the selection workgroup", blocks);
+    unsigned padded = 1;
+    while (padded < blocks) padded <<= 1;
+    const size_t shared = (size_t)padded * 8 + blocks;
     static bool configured = false;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)sb_select, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 64 * 1024), "SubBlock select shared memory"))
+                                                 (int)(8192 * 8 + 8192)), "SubBlock select shared memory"))
             return 0;
         configured = true;
     }
-    hipLaunchKernelGGL(sb_select, dim3(nqb, heads), dim3(256), shared, g->compute, scores, base + r->off_routes, meta,
-                       meta + blocks, blocks, keep, force_all ? 1 : 0, (uint32_t *)(base + r->off_list),
-                       (uint32_t *)(base + r->off_count), nqb, counters);
+    hipLaunchKernelGGL(sb_select, dim3(blocks, heads), dim3(256), shared, g->compute, scores, base + r->off_routes,
+                       meta, meta + blocks, blocks, padded, keep, force_all ? 1 : 0, (uint32_t *)(base + r->off_list),
+                       (uint32_t *)(base + r->off_count), (uint32_t *)(base + r->off_added));
     if (!h3_launch_status(g, "SubBlock select")) return 0;
+    hipLaunchKernelGGL(sb_count, dim3(1), dim3(1024), 0, g->compute, (const uint32_t *)(base + r->off_count),
+                       (const uint32_t *)(base + r->off_added), (size_t)heads * blocks, counters);
+    if (!h3_launch_status(g, "SubBlock counters")) return 0;
+    r->possible += (uint64_t)heads * blocks * blocks;
     r->counters_pending = true;
     g->stats.subblock_router_calls++;
     return 1;
@@ -296,7 +336,8 @@ void h3_subblock_collect(h3_gpu *g, h3_subblock_router *r) {
     if (hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost) != hipSuccess) return;
     if (hipMemset(counters, 0, sizeof(c)) != hipSuccess) return;
     g->stats.subblock_selected += c[0];
-    g->stats.subblock_possible += c[1];
+    g->stats.subblock_possible += r->possible;
+    r->possible = 0;
     r->counters_pending = false;
 }
 
