@@ -70,13 +70,12 @@ __host__ __device__ inline unsigned v_position(unsigned j) {
     return (j & ~15u) + ((k16 >> 2) & 1) * 8 + (k16 >> 3) * 4 + (k16 & 3);
 }
 
-// V [seq, heads, 128] -> Vt [heads, 128, padded]; one workgroup per (head,
-// 64-key tile), heads fastest so that concurrent workgroups read whole
-// sequence rows. The pass also screens this tile's K and V rows for Inf/NaN.
+// V [seq, heads, 128] -> Vt [heads, 128, padded]; one workgroup per (64-key tile,
+// head). The pass also screens this tile's K and V rows for Inf/NaN.
 __global__ __launch_bounds__(256) void transpose_v(const uint16_t *v, const uint16_t *k, uint16_t *vt, unsigned seq,
                                                   unsigned heads, unsigned padded, unsigned *fault) {
     __shared__ uint16_t tile[BN][D + 8];
-    const unsigned blk = blockIdx.y, head = blockIdx.x, t = threadIdx.x;
+    const unsigned blk = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
     const size_t stride = (size_t)heads * D;
     bool bad = false;
 #pragma unroll
@@ -791,7 +790,7 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride;
     a.fault = g->fault;
-    hipLaunchKernelGGL(transpose_v, dim3(heads, a.padded / BN), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     // Sparse lists are per 128-query block: 4 waves per workgroup, two
@@ -813,7 +812,7 @@ int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const 
     a.head_major = head_major ? 1 : 0;
     a.kv_list = lists; a.kv_count = counts; a.list_stride = list_stride;
     a.fault = g->fault;
-    hipLaunchKernelGGL(transpose_v, dim3(heads, a.padded / BN), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     const unsigned groups = (seq + 63) / 64 * heads;

@@ -111,7 +111,7 @@ template <bool KEY>
 __global__ __launch_bounds__(256) void sage_quant_int8(const uint16_t *x, const uint16_t *mean, int8_t *codes,
                                                       float *scales, unsigned seq, unsigned heads,
                                                       unsigned padded, unsigned *fault) {
-    const unsigned blk = blockIdx.y, head = blockIdx.x, t = threadIdx.x;  // heads fastest: whole rows per wave of workgroups
+    const unsigned blk = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
     const unsigned chunk = t % 16, r0 = t / 16;
     const size_t stride = (size_t)heads * D;
     float val[4][8];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void sage_quant_int8(const uint16_t *x, const 
 __global__ __launch_bounds__(256) void sage_pack_v(const uint16_t *v, const float *v_recip, uint8_t *codes,
                                                   unsigned seq, unsigned heads, unsigned padded) {
     __shared__ uint16_t tile[BN][D + 8];
-    const unsigned blk = blockIdx.y, head = blockIdx.x, t = threadIdx.x;  // heads fastest: whole rows per wave of workgroups
+    const unsigned blk = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
     const size_t stride = (size_t)heads * D;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -206,13 +206,13 @@ int h3_sage_quantize(h3_gpu *g, const h3_sage_layout &L, char *ws, const uint16_
     hipLaunchKernelGGL(sage_reduce_finish, dim3(L.heads), dim3(128), 0, g->compute, (const float *)(ws + L.sums),
                        (const float *)(ws + L.maxima), (uint16_t *)(ws + L.k_mean), (float *)(ws + L.v_scale),
                        (float *)(ws + L.v_recip), L.seq, L.partials);
-    hipLaunchKernelGGL(sage_quant_int8<false>, dim3(L.heads, L.blocks), dim3(256), 0, g->compute, q,
+    hipLaunchKernelGGL(sage_quant_int8<false>, dim3(L.blocks, L.heads), dim3(256), 0, g->compute, q,
                        (const uint16_t *)nullptr, (int8_t *)(ws + L.q8), (float *)(ws + L.q_scale), L.seq, L.heads,
                        L.padded, g->fault);
-    hipLaunchKernelGGL(sage_quant_int8<true>, dim3(L.heads, L.blocks), dim3(256), 0, g->compute, k,
+    hipLaunchKernelGGL(sage_quant_int8<true>, dim3(L.blocks, L.heads), dim3(256), 0, g->compute, k,
                        (const uint16_t *)(ws + L.k_mean), (int8_t *)(ws + L.k8), (float *)(ws + L.k_scale), L.seq,
                        L.heads, L.padded, g->fault);
-    hipLaunchKernelGGL(sage_pack_v, dim3(L.heads, L.blocks), dim3(256), 0, g->compute, v,
+    hipLaunchKernelGGL(sage_pack_v, dim3(L.blocks, L.heads), dim3(256), 0, g->compute, v,
                        (const float *)(ws + L.v_recip), (uint8_t *)(ws + L.v8), L.seq, L.heads, L.padded);
     return h3_launch_status(g, "Sage quantization");
 }

@@ -25,12 +25,11 @@ constexpr unsigned KEY_SPLIT = 16;         // 32-cell key tiles per score workgr
 
 // One thread per (cell, head, 8 channels): fp32 tree sum over the cell's 16
 // rows (missing rows are zero), mean * scale, rounded to BF16. 16-byte loads;
-// a workgroup covers 16 cells of one head, and the heads of one row range are
-// consecutive workgroups, so concurrent loads cover whole sequence rows.
+// a workgroup covers 16 cells of one head.
 __global__ __launch_bounds__(256) void sb_pool(const uint16_t *q, const uint16_t *k, uint16_t *qpool,
                                                uint16_t *kpool, unsigned seq, unsigned heads, unsigned cells,
                                                float qscale, unsigned *fault) {
-    const unsigned cell = blockIdx.y * 16 + threadIdx.x / 16, part = threadIdx.x % 16, head = blockIdx.x;
+    const unsigned cell = blockIdx.x * 16 + threadIdx.x / 16, part = threadIdx.x % 16, head = blockIdx.y;
     const bool is_k = blockIdx.z != 0;
     const uint16_t *src = is_k ? k : q;
     uint16_t *dst = (is_k ? kpool : qpool) + ((size_t)head * cells + cell) * D + part * 8;
@@ -292,7 +291,7 @@ int h3_subblock_route(h3_gpu *g, h3_subblock_router *r, const uint16_t *q, const
     auto *scores = (float *)(base + r->off_scores);
     const auto *meta = (const uint8_t *)r->meta.ptr;
 
-    hipLaunchKernelGGL(sb_pool, dim3(heads, cells / 16, 2), dim3(256), 0, g->compute, q, k, qpool, kpool, seq, heads,
+    hipLaunchKernelGGL(sb_pool, dim3(cells / 16, heads, 2), dim3(256), 0, g->compute, q, k, qpool, kpool, seq, heads,
                        cells, scale * 1.4426950408889634f, g->fault);
     if (!h3_launch_status(g, "SubBlock pool")) return 0;
     const unsigned ktiles = cells / 32;
