@@ -133,7 +133,7 @@ void attn_bf16_kernel(Args a) {
     unsigned count;
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        count = a.kv_count[qb];
+        count = __builtin_amdgcn_readfirstlane(a.kv_count[qb]);
         list = a.kv_list + (size_t)qb * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
@@ -286,18 +286,29 @@ void attn_bf16_kernel(Args a) {
         }
     };
 
-    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    // Sparse tile ids are wave-uniform and read one iteration ahead, so the
+    // id load completes under the tile-load wait instead of stalling the
+    // next iteration's loads.
+    unsigned tile = 0, next = 1;
+    if constexpr (SPARSE) {
+        if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
+        if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
+    }
+    if (count) load_tile(tile, 0);
     wait_vm_loads();
     __syncthreads();
 
     for (unsigned it = 0; it < count; it++) {
         const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        if (it + 1 < count) load_tile(next, cur ^ 1);
+        uint32_t later = it + 2;
+        if constexpr (SPARSE) later = it + 2 < count ? list[it + 2] : 0u;
         const uint8_t *ks = smem + cur * STAGE_BYTES;
         process(ks, ks + K_BYTES, tile);
         wait_vm_loads();
         __syncthreads();
+        tile = next;
+        next = SPARSE ? __builtin_amdgcn_readfirstlane(later) : later;
     }
 
     // Normalize and store. Lane holds query column n, channels (r/4)*8 + hf*4 + r%4.
@@ -567,8 +578,12 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 //    and the next V^T tile during the next scores. Barriers: one after the
 //    scores (K free, V^T ready), one after P.V (V^T free, next K ready).
 //  * otherwise two full stages (64 KB): the next tile loads during this one.
-// MSUM: row sums of P on the matrix core instead of VALU adds.
-template <bool SPLIT, bool MSUM, int OCC>
+// The list length and tile ids are read as wave-uniform values one iteration
+// ahead: a vector load used at once would make the compiler wait for every
+// outstanding load, the tile loads included. Fragments are read from LDS as
+// they are consumed (requesting all 16 ahead, as the dense kernel does, costs
+// 42 more VGPRs and spills here).
+template <bool SPLIT, int OCC>
 __global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(OCC, OCC)))
 void attn_bf16_routed(Args a) {
     constexpr int BLOCKS = K_BYTES / 1024;
@@ -585,7 +600,10 @@ void attn_bf16_routed(Args a) {
     const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
     const float c = a.scale_log2;
     const size_t lq = (size_t)head * nqb + qb;
-    const unsigned count = a.kv_count[lq];
+    // The list length and tile ids are wave-uniform (readfirstlane keeps the
+    // loop scalar); each id is loaded one iteration before its use so that
+    // the load completes under the tile-load waits already in the loop.
+    const unsigned count = __builtin_amdgcn_readfirstlane(a.kv_count[lq]);
     const uint32_t *list = a.kv_list + lq * a.list_stride;
 
     bf16x8 qf[8];
@@ -603,11 +621,7 @@ void attn_bf16_routed(Args a) {
     f32x16 o[4];
 #pragma unroll
     for (int md = 0; md < 4; md++) o[md] = f32x16{};
-    f32x16 lsum = f32x16{};
     float m = -1e30f, l = 0.f;
-    bf16x8 ones;
-#pragma unroll
-    for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
 
     auto load_k = [&](unsigned tile, uint8_t *ks) {
         const unsigned key0 = tile * BN;
@@ -638,7 +652,7 @@ void attn_bf16_routed(Args a) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
                 const unsigned key = mb * 32 + n;
-                bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, kstep * 2 + hf) * 16);
+                const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, kstep * 2 + hf) * 16);
                 s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kstep], s[mb], 0, 0, 0);
             }
     };
@@ -664,8 +678,7 @@ void attn_bf16_routed(Args a) {
             const float mnew = fmaxf(m, mx);
             const float alpha = exp2f_fast(m - mnew);
             m = mnew;
-            if constexpr (MSUM) lsum *= alpha;
-            else l *= alpha;
+            l *= alpha;
 #pragma unroll
             for (int md = 0; md < 4; md++) o[md] *= alpha;
         }
@@ -678,44 +691,46 @@ void attn_bf16_routed(Args a) {
             for (int r = 0; r < 16; r += 2) {
                 float p0 = exp2f_fast(fmaf(s[mb][r], c, neg));
                 float p1 = exp2f_fast(fmaf(s[mb][r + 1], c, neg));
-                if constexpr (!MSUM) psum += p0 + p1;
+                psum += p0 + p1;
                 pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
                 pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
             }
-        if constexpr (!MSUM) l += psum;
+        l += psum;
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
+        for (int kk = 0; kk < 4; kk++)
 #pragma unroll
             for (int md = 0; md < 4; md++) {
                 const unsigned d = md * 32 + n;
-                bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, kk * 2 + hf) * 16);
+                const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, kk * 2 + hf) * 16);
                 o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kk], o[md], 0, 0, 0);
             }
-            if constexpr (MSUM) lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[kk], lsum, 0, 0, 0);
-        }
     };
 
+    unsigned tile = 0, next = 0;
+    if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
+    if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
     if constexpr (SPLIT) {
         uint8_t *ks = smem, *vs = smem + K_BYTES;
-        if (count) { load_k(list[0], ks); load_v(list[0], vs); }
+        if (count) { load_k(tile, ks); load_v(tile, vs); }
         wait_vm_loads();
         __syncthreads();
         for (unsigned it = 0; it < count; it++) {
-            const unsigned tile = list[it];
             const bool has_next = it + 1 < count;
-            const unsigned next = has_next ? list[it + 1] : 0;
             f32x16 s[2];
             scores(ks, s);
             wait_vm_loads();               // this tile's V^T (own share)
             __syncthreads();               // K free; every share of V^T landed
             if (has_next) load_k(next, ks);
+            const uint32_t later = it + 2 < count ? list[it + 2] : 0u;
             softmax_pv(s, vs, tile);
-            wait_vm_loads();               // next K (own share)
+            wait_vm_loads();               // next K and the id after it (own share)
             __syncthreads();               // V^T free; every share of the next K landed
             if (has_next) load_v(next, vs);
+            tile = next;
+            next = __builtin_amdgcn_readfirstlane(later);
         }
     } else {
-        if (count) { load_k(list[0], smem); load_v(list[0], smem + K_BYTES); }
+        if (count) { load_k(tile, smem); load_v(tile, smem + K_BYTES); }
         wait_vm_loads();
         __syncthreads();
         for (unsigned it = 0; it < count; it++) {
@@ -723,18 +738,21 @@ void attn_bf16_routed(Args a) {
             uint8_t *ks = smem + cur * STAGE_BYTES;
             if (it + 1 < count) {
                 uint8_t *nk = smem + (cur ^ 1) * STAGE_BYTES;
-                load_k(list[it + 1], nk);
-                load_v(list[it + 1], nk + K_BYTES);
+                load_k(next, nk);
+                load_v(next, nk + K_BYTES);
             }
+            const uint32_t later = it + 2 < count ? list[it + 2] : 0u;
             f32x16 s[2];
             scores(ks, s);
-            softmax_pv(s, ks + K_BYTES, list[it]);
+            softmax_pv(s, ks + K_BYTES, tile);
             wait_vm_loads();
             __syncthreads();
+            tile = next;
+            next = __builtin_amdgcn_readfirstlane(later);
         }
     }
 
-    const float total = MSUM ? lsum[0] : half_sum_swap(l);
+    const float total = half_sum_swap(l);
     const float inv = total > 0.f ? 1.f / total : 0.f;
     const unsigned q = q0 + wave * 32 + n;
     bool bad = false;
@@ -757,11 +775,11 @@ void attn_bf16_routed(Args a) {
     if (bad) a.fault[0] = 1u;
 }
 
-template <bool SPLIT, bool MSUM, int OCC>
+template <bool SPLIT, int OCC>
 int launch_routed(h3_gpu *g, const Args &a, unsigned groups) {
     constexpr size_t shared = SPLIT ? STAGE_BYTES : 2 * STAGE_BYTES;
     static bool configured = false;
-    auto kernel = attn_bf16_routed<SPLIT, MSUM, OCC>;
+    auto kernel = attn_bf16_routed<SPLIT, OCC>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
                           "attention shared memory"))
@@ -816,10 +834,8 @@ int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const 
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     const unsigned groups = (seq + 63) / 64 * heads;
-    switch (g->attention_variant) {
-    case 11: return launch_routed<true, true, 2>(g, a, groups);
-    case 12: return launch_routed<false, false, 1>(g, a, groups);
-    case 13: return launch_routed<false, false, 2>(g, a, groups);
-    default: return launch_routed<true, false, 2>(g, a, groups);
-    }
+    // Split K/V phases, two waves per SIMD (measured fastest); variant 12:
+    // two full 64 KB stages at one wave per SIMD.
+    if (g->attention_variant == 12) return launch_routed<false, 1>(g, a, groups);
+    return launch_routed<true, 2>(g, a, groups);
 }

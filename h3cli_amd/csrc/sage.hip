@@ -262,8 +262,10 @@ void sage_attn_kernel(SArgs a) {
 
     unsigned count;
     const uint32_t *list = nullptr;
-    if constexpr (SPARSE) { count = a.kv_count[qb]; list = a.kv_list + (size_t)qb * a.list_stride; }
-    else count = ntiles;
+    if constexpr (SPARSE) {
+        count = __builtin_amdgcn_readfirstlane(a.kv_count[qb]);
+        list = a.kv_list + (size_t)qb * a.list_stride;
+    } else count = ntiles;
 
     // Query fragments (B operand of S^T = K Q^T): 4 k-steps of 32 channels.
     i32x4 qf[4];
@@ -366,17 +368,27 @@ void sage_attn_kernel(SArgs a) {
         lsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, lsum, 0, 0, 0, 0, 0, 0);
     };
 
-    if (count) load_tile(SPARSE ? list[0] : 0, 0);
+    // Sparse tile ids are wave-uniform and read one iteration ahead (see the
+    // BF16 kernel): the id load completes under the tile-load wait.
+    unsigned tile = 0, next = 1;
+    if constexpr (SPARSE) {
+        if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
+        if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
+    }
+    if (count) load_tile(tile, 0);
     wait_vm_loads();
     __syncthreads();
     for (unsigned it = 0; it < count; it++) {
         const int cur = it & 1;
-        const unsigned tile = SPARSE ? list[it] : it;
-        if (it + 1 < count) load_tile(SPARSE ? list[it + 1] : it + 1, cur ^ 1);
+        if (it + 1 < count) load_tile(next, cur ^ 1);
+        uint32_t later = it + 2;
+        if constexpr (SPARSE) later = it + 2 < count ? list[it + 2] : 0u;
         const uint8_t *ks = lds + cur * SAGE_TILE;
         process(ks, ks + Q8_TILE, tile);
         wait_vm_loads();
         __syncthreads();
+        tile = next;
+        next = SPARSE ? __builtin_amdgcn_readfirstlane(later) : later;
     }
 
     bool bad = false;
