@@ -115,11 +115,14 @@ class DitSynthConfig(C.Structure):
     _fields_ = [("blocks", _u32), ("hidden", _u32), ("heads", _u32), ("mlp", _u32),
                 ("frames", _u32), ("height", _u32), ("width", _u32), ("audio_rows", _u32),
                 ("latent", _u32), ("streamed_first", _u32), ("mask_density", _f),
-                ("attention_mode", _i), ("eps", _f), ("time", _f), ("seed", C.c_uint64)]
+                ("attention_mode", _i), ("eps", _f), ("time", _f), ("seed", C.c_uint64),
+                ("rope_half", _u32), ("swiglu", _i), ("qk_norm", _i), ("grouped_qkv", _i),
+                ("subblock_sparsity", _f)]
 
 
 _SIGNATURES.update({
     "h3_hip_dit_synth_default": (DitSynthConfig, []),
+    "h3_hip_dit_synth_h3": (DitSynthConfig, []),
     "h3_hip_dit_synth_create": (_p, [_p, C.POINTER(DitSynthConfig), C.c_char_p, _sz]),
     "h3_hip_dit_synth_free": (None, [_p]),
     "h3_hip_dit_synth_step": (_i, [_p, _i, _f]),

@@ -2,8 +2,9 @@
  *
  * The block body follows the reference's run_block op sequence
  * (src/denoise/dit.c:2286-2539): AdaLN (modulation slots 0/1) -> QKV projection
- * -> Q/K RoPE split -> DiT attention -> output projection -> gate (slot 2) fused
- * with the second AdaLN (slots 3/4) -> MLP -> gate (slot 5). The block loop and
+ * -> Q/K (RMSNorm and) RoPE split -> DiT attention -> output projection -> gate
+ * (slot 2) fused with the second AdaLN (slots 3/4) -> MLP (GELU-tanh, or fc1 ->
+ * SwiGLU -> fc2 as dit.c:2479-2485) -> gate (slot 5). The block loop and
  * weight streaming follow encode_forward (dit.c:2577-3038): resident blocks run
  * from device memory; the rest are copied from pinned host memory into two
  * alternating device slots on the copy stream, the copy for block b+1 overlapping
@@ -12,6 +13,7 @@
  * the second) through a small time MLP, computed once at creation as the
  * reference precomputes its per-step modulation. */
 #include "h3_dit_synth.h"
+#include "h3_gpu_surface.h"
 #include "h3_hip_ext.h"
 #include <math.h>
 #include <stdarg.h>
@@ -35,7 +37,9 @@ struct h3_hip_dit_synth {
     h3_gpu_tensor **norm1, **norm2, **mod; /* per block */
     h3_gpu_tensor *patch, *head, *head_norm, *head_mod;
     /* activations and tables */
-    h3_gpu_tensor *latent, *latent_bf16, *x, *xn, *qkv, *q, *k, *v, *attn, *o, *h, *f, *vel;
+    h3_gpu_tensor **qn, **kn;      /* per block Q/K RMSNorm weights [128] (qk_norm) */
+    h3_gpu_tensor *latent, *latent_bf16, *x, *xn, *qkv, *q, *k, *v, *attn, *o, *h, *act, *f, *vel;
+    h3_sol_block *layout_blocks;   /* attention_mode 4: the bound 64-row layout */
     h3_gpu_tensor *cos_t, *sin_t, *row_map;
     uint64_t kept, total;
 };
@@ -57,6 +61,16 @@ h3_hip_dit_synth_config h3_hip_dit_synth_default(void) {
     c.frames = 27; c.height = 30; c.width = 40; c.audio_rows = 1024;
     c.latent = 256; c.streamed_first = 20; c.mask_density = 0.25f;
     c.attention_mode = 1; c.eps = 1e-6f; c.time = 0.5f; c.seed = 5;
+    c.rope_half = 64; c.subblock_sparsity = 0.75f;
+    return c;
+}
+
+h3_hip_dit_synth_config h3_hip_dit_synth_h3(void) {
+    h3_hip_dit_synth_config c = h3_hip_dit_synth_default();
+    c.blocks = 50; c.hidden = 5376; c.heads = 56; c.mlp = 14336;
+    c.frames = 25; c.height = 27; c.width = 27; c.audio_rows = 0;
+    c.streamed_first = 50; c.mask_density = -1.f; c.attention_mode = 0; c.eps = 1e-5f;
+    c.rope_half = 48; c.swiglu = 1; c.qk_norm = 1; c.grouped_qkv = 1;
     return c;
 }
 
@@ -89,10 +103,13 @@ static h3_gpu_tensor *normal_tensor(h3_gpu *g, size_t n, uint64_t seed, float sp
     return t;
 }
 
-/* 3D RoPE tables over the video grid (rotate-half pairs d <-> d+64, frame / row /
- * column split 44/42/42 channels, theta 1e4); audio rows get angle 0. */
+/* 3D RoPE tables over the video grid (rotate-half pairs d <-> d + half; half 64:
+ * frame / row / column split 44/42/42 channels, half 48: 16 frequencies per axis
+ * as dit.c ROPE_FREQS; theta 1e4); audio rows get angle 0. */
 static int rope_tables(h3_hip_dit_synth *m) {
-    const uint32_t half = 64, split[3] = {22, 21, 21};
+    const uint32_t half = m->c.rope_half;
+    uint32_t split[3] = {22, 21, 21};
+    if (half != 64) split[0] = split[1] = split[2] = half / 3;
     size_t n = (size_t)m->rows * half;
     uint16_t *c = malloc(n * 2), *s = malloc(n * 2);
     if (!c || !s) { free(c); free(s); return 0; }
@@ -158,10 +175,11 @@ static int modulation(h3_hip_dit_synth *m, char *error, size_t size) {
 }
 
 static void proj_shape(const h3_hip_dit_synth_config *c, int j, uint32_t *n, uint32_t *k) {
+    const uint32_t inner = c->heads * 128;
     switch (j) {
-    case 0: *n = 3 * c->hidden; *k = c->hidden; break;
-    case 1: *n = c->hidden; *k = c->hidden; break;
-    case 2: *n = c->mlp; *k = c->hidden; break;
+    case 0: *n = 3 * inner; *k = c->hidden; break;
+    case 1: *n = c->hidden; *k = inner; break;
+    case 2: *n = c->swiglu ? 2 * c->mlp : c->mlp; *k = c->hidden; break;
     default: *n = c->hidden; *k = c->mlp; break;
     }
 }
@@ -206,6 +224,11 @@ static int weights(h3_hip_dit_synth *m, char *error, size_t size) {
         }
         m->norm1[b] = normal_tensor(g, c->hidden, c->seed * 31 + 2 * b, 0.1f, 1.0f);
         m->norm2[b] = normal_tensor(g, c->hidden, c->seed * 31 + 2 * b + 1, 0.1f, 1.0f);
+        if (c->qk_norm) {
+            m->qn[b] = normal_tensor(g, 128, c->seed * 43 + 2 * b, 0.1f, 1.0f);
+            m->kn[b] = normal_tensor(g, 128, c->seed * 43 + 2 * b + 1, 0.1f, 1.0f);
+            if (!m->qn[b] || !m->kn[b]) return fail(error, size, "qk norms: %s", h3_gpu_error(g));
+        }
         if (!m->norm1[b] || !m->norm2[b] || !h3_gpu_synchronize(g)) return fail(error, size, "norms: %s", h3_gpu_error(g));
     }
     m->patch = normal_tensor(g, (size_t)c->hidden * c->latent, c->seed * 37 + 1, 1.0f / sqrtf((float)c->latent), 0.f);
@@ -220,9 +243,12 @@ static h3_gpu_tensor *bf16_buffer(h3_gpu *g, size_t n) { return h3_gpu_tensor_ne
 h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_config *config, char *error, size_t size) {
     if (!g || !config) { fail(error, size, "missing context or config"); return NULL; }
     const h3_hip_dit_synth_config *c = config;
-    if (!c->blocks || !c->heads || c->hidden != c->heads * 128 || !c->mlp || c->mlp % 256 || c->hidden % 256 ||
-        !c->latent || c->latent % 256 || !c->frames || !c->height || !c->width) {
-        fail(error, size, "synthetic DiT: hidden must be heads*128, hidden/mlp/latent multiples of 256");
+    if (!c->blocks || !c->heads || !c->mlp || c->mlp % 256 || !c->hidden || c->hidden % 256 || !c->latent ||
+        c->latent % 256 || !c->frames || !c->height || !c->width ||
+        (c->rope_half != 64 && (!c->rope_half || c->rope_half > 64 || c->rope_half % 3)) ||
+        (c->attention_mode != 0 && c->attention_mode != 1 && c->attention_mode != 4)) {
+        fail(error, size, "synthetic DiT: hidden/mlp/latent multiples of 256, rope_half 64 or a multiple of 3 "
+                          "below it, attention mode 0/1/4");
         return NULL;
     }
     h3_hip_dit_synth *m = calloc(1, sizeof(*m));
@@ -236,15 +262,20 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
     m->norm1 = calloc(c->blocks, sizeof(*m->norm1));
     m->norm2 = calloc(c->blocks, sizeof(*m->norm2));
     m->mod = calloc(c->blocks, sizeof(*m->mod));
-    if (!m->proj || !m->host || !m->norm1 || !m->norm2 || !m->mod) { fail(error, size, "out of host memory"); goto bad; }
-    if (!h3_gpu_dit_attention_configure(g, c->attention_mode == 1 ? 1 : 0)) {
+    m->qn = calloc(c->blocks, sizeof(*m->qn));
+    m->kn = calloc(c->blocks, sizeof(*m->kn));
+    if (!m->proj || !m->host || !m->norm1 || !m->norm2 || !m->mod || !m->qn || !m->kn) {
+        fail(error, size, "out of host memory");
+        goto bad;
+    }
+    if (!h3_gpu_dit_attention_configure(g, c->attention_mode)) {
         fail(error, size, "attention configure: %s", h3_gpu_error(g));
         goto bad;
     }
     if (!h3_gpu_begin(g)) { fail(error, size, "begin: %s", h3_gpu_error(g)); goto bad; }
     if (!weights(m, error, size) || !modulation(m, error, size) || !rope_tables(m)) { h3_gpu_cancel(g); goto bad; }
     {
-        const size_t R = m->rows, H = c->hidden;
+        const size_t R = m->rows, H = c->hidden, I = (size_t)c->heads * 128;
         uint32_t *map = malloc(R * 4);
         if (!map) { h3_gpu_cancel(g); goto bad; }
         for (size_t r = 0; r < R; r++) map[r] = r < m->video_rows ? 0u : 1u;
@@ -253,13 +284,14 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         m->latent = h3_gpu_tensor_new_f32(g, R * c->latent);
         m->latent_bf16 = bf16_buffer(g, R * c->latent);
         m->x = bf16_buffer(g, R * H); m->xn = bf16_buffer(g, R * H);
-        m->qkv = bf16_buffer(g, R * H * 3);
-        m->q = bf16_buffer(g, R * H); m->k = bf16_buffer(g, R * H); m->v = bf16_buffer(g, R * H);
-        m->attn = bf16_buffer(g, R * H); m->o = bf16_buffer(g, R * H);
-        m->h = bf16_buffer(g, R * c->mlp); m->f = bf16_buffer(g, R * H);
+        m->qkv = bf16_buffer(g, R * I * 3);
+        m->q = bf16_buffer(g, R * I); m->k = bf16_buffer(g, R * I); m->v = bf16_buffer(g, R * I);
+        m->attn = bf16_buffer(g, R * I); m->o = bf16_buffer(g, R * H);
+        m->h = bf16_buffer(g, R * c->mlp * (c->swiglu ? 2 : 1)); m->f = bf16_buffer(g, R * H);
+        m->act = c->swiglu ? bf16_buffer(g, R * c->mlp) : NULL;
         m->vel = bf16_buffer(g, R * c->latent);
         if (!m->row_map || !m->latent || !m->latent_bf16 || !m->x || !m->xn || !m->qkv || !m->q || !m->k || !m->v ||
-            !m->attn || !m->o || !m->h || !m->f || !m->vel) {
+            !m->attn || !m->o || !m->h || !m->f || !m->vel || (c->swiglu && !m->act)) {
             fail(error, size, "activations: %s", h3_gpu_error(g));
             h3_gpu_cancel(g);
             goto bad;
@@ -271,7 +303,20 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         if (!ok) { fail(error, size, "latent: %s", h3_gpu_error(g)); h3_gpu_cancel(g); goto bad; }
     }
     if (!h3_gpu_submit(g)) { fail(error, size, "setup: %s", h3_gpu_error(g)); goto bad; }
-    if (c->mask_density >= 0.f) {
+    if (c->attention_mode == 4) {
+        /* SubBlock: the router runs over a 64-row layout with no protected
+         * blocks, at the request's sparsity, from the first step (warmup off). */
+        uint32_t nb = (m->rows + 63) / 64;
+        m->layout_blocks = calloc(nb, sizeof(*m->layout_blocks));
+        if (!m->layout_blocks) goto bad;
+        for (uint32_t b = 0; b < nb; b++) m->layout_blocks[b].rows = m->rows - b * 64 < 64 ? m->rows - b * 64 : 64;
+        h3_sol_layout layout = {m->rows, nb, nb, 0, m->layout_blocks, m->layout_blocks};
+        if (!h3_hip_dit_subblock_policy(g, c->subblock_sparsity, -1) || !h3_gpu_dit_sol_layout(g, &layout)) {
+            fail(error, size, "subblock layout: %s", h3_gpu_error(g));
+            goto bad;
+        }
+        m->kept = m->total = (uint64_t)nb * nb;
+    } else if (c->mask_density >= 0.f) {
         uint32_t blocks = (m->rows + 127) / 128;
         uint8_t *mask = malloc((size_t)blocks * blocks);
         if (!mask) goto bad;
@@ -302,11 +347,15 @@ void h3_hip_dit_synth_free(h3_hip_dit_synth *m) {
         if (m->norm1) h3_gpu_tensor_free(m->norm1[b]);
         if (m->norm2) h3_gpu_tensor_free(m->norm2[b]);
         if (m->mod) h3_gpu_tensor_free(m->mod[b]);
+        if (m->qn) h3_gpu_tensor_free(m->qn[b]);
+        if (m->kn) h3_gpu_tensor_free(m->kn[b]);
     }
     h3_gpu_tensor *all[] = {m->patch, m->head, m->head_norm, m->head_mod, m->latent, m->latent_bf16, m->x, m->xn,
-                            m->qkv, m->q, m->k, m->v, m->attn, m->o, m->h, m->f, m->vel, m->cos_t, m->sin_t, m->row_map};
+                            m->qkv, m->q, m->k, m->v, m->attn, m->o, m->h, m->act, m->f, m->vel, m->cos_t, m->sin_t,
+                            m->row_map};
     for (size_t i = 0; i < sizeof(all) / sizeof(*all); i++) h3_gpu_tensor_free(all[i]);
-    free(m->proj); free(m->host); free(m->norm1); free(m->norm2); free(m->mod);
+    free(m->proj); free(m->host); free(m->norm1); free(m->norm2); free(m->mod); free(m->qn); free(m->kn);
+    free(m->layout_blocks);
     free(m);
 }
 
@@ -325,7 +374,7 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
     if (!m) return 0;
     h3_gpu *g = m->gpu;
     const h3_hip_dit_synth_config *c = &m->c;
-    const uint32_t R = m->rows, H = c->hidden, L = c->latent;
+    const uint32_t R = m->rows, H = c->hidden, L = c->latent, I = c->heads * 128;
     const float scale = 1.0f / sqrtf(128.0f);
     if (!h3_gpu_begin(g)) return 0;
     int ok = h3_gpu_dit_attention_noise(g, step, 0.5f, 0.5f) && prefetch(m, c->streamed_first) &&
@@ -335,17 +384,27 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
         h3_gpu_tensor **w = b < c->streamed_first ? &m->proj[(size_t)b * PROJ] : m->slot[b % 2];
         /* The next streamed block's copy overlaps this block's compute. */
         if (b + 1 > c->streamed_first && !prefetch(m, b + 1)) { ok = 0; break; }
-        ok = h3_gpu_adaln_bf16(g, m->xn, m->x, m->norm1[b], m->mod[b], m->row_map, R, H, SLOTS, 0, 1, c->eps) &&
-             h3_gpu_linear_bf16(g, m->qkv, m->xn, w[0], NULL, R, H, 3 * H) &&
-             h3_gpu_qkv_rope_bf16(g, m->q, m->k, m->v, m->qkv, NULL, NULL, m->cos_t, m->sin_t, R, c->heads, 128, 64,
-                                  c->eps) &&
-             h3_gpu_dit_sdpa_bf16(g, m->attn, m->q, m->k, m->v, R, c->heads, 128, scale, 0, b, step) &&
-             h3_gpu_linear_bf16(g, m->o, m->attn, w[1], NULL, R, H, H) &&
+        const h3_gpu_tensor *qn = c->qk_norm ? m->qn[b] : NULL, *kn = c->qk_norm ? m->kn[b] : NULL;
+        ok = h3_gpu_adaln_bf16(g, m->xn, m->x, m->norm1[b], m->mod[b], m->row_map, R, H, SLOTS, 0, 1, c->eps);
+        if (c->grouped_qkv)
+            ok = ok && h3_gpu_grouped_qkv_linear_rope_bf16(g, m->q, m->k, m->v, m->qkv, m->xn, w[0], qn, kn, m->cos_t,
+                                                           m->sin_t, R, H, c->heads, 128, c->rope_half, c->eps);
+        else
+            ok = ok && h3_gpu_linear_bf16(g, m->qkv, m->xn, w[0], NULL, R, H, 3 * I) &&
+                 h3_gpu_qkv_rope_bf16(g, m->q, m->k, m->v, m->qkv, qn, kn, m->cos_t, m->sin_t, R, c->heads, 128,
+                                      c->rope_half, c->eps);
+        ok = ok && h3_gpu_dit_sdpa_bf16(g, m->attn, m->q, m->k, m->v, R, c->heads, 128, scale, 0, b, step) &&
+             h3_gpu_linear_bf16(g, m->o, m->attn, w[1], NULL, R, I, H) &&
              h3_gpu_gate_adaln_bf16(g, m->x, m->xn, m->x, m->o, m->norm2[b], m->mod[b], m->mod[b], m->row_map, R, H,
-                                    SLOTS, 2, 3, 4, c->eps) &&
-             h3_hip_linear_gelu_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
-             h3_gpu_linear_bf16(g, m->f, m->h, w[3], NULL, R, c->mlp, H) &&
-             h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5);
+                                    SLOTS, 2, 3, 4, c->eps);
+        if (c->swiglu)
+            ok = ok && h3_gpu_linear_bf16(g, m->h, m->xn, w[2], NULL, R, H, 2 * c->mlp) &&
+                 h3_gpu_swiglu_bf16(g, m->act, m->h, R, c->mlp) &&
+                 h3_gpu_linear_bf16(g, m->f, m->act, w[3], NULL, R, c->mlp, H);
+        else
+            ok = ok && h3_hip_linear_gelu_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
+                 h3_gpu_linear_bf16(g, m->f, m->h, w[3], NULL, R, c->mlp, H);
+        ok = ok && h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5);
     }
     ok = ok && h3_gpu_adaln_bf16(g, m->xn, m->x, m->head_norm, m->head_mod, m->row_map, R, H, 2, 0, 1, c->eps) &&
          h3_gpu_linear_bf16(g, m->vel, m->xn, m->head, NULL, R, H, L) &&

@@ -135,9 +135,10 @@ class Gpu:
 class DitSynth:
     """The synthetic DiT denoise step of include/h3_dit_synth.h on its own context."""
 
-    def __init__(self, **overrides):
+    def __init__(self, geometry="synthetic", **overrides):
+        """geometry: "synthetic" or "h3" (the real H3 block)."""
         self.lib = _lib.load()
-        cfg = self.lib.h3_hip_dit_synth_default()
+        cfg = self.lib.h3_hip_dit_synth_h3() if geometry == "h3" else self.lib.h3_hip_dit_synth_default()
         for k, v in overrides.items():
             setattr(cfg, k, v)
         self.config = cfg

@@ -1,8 +1,11 @@
-/* h3_dit_synth.h — the synthetic 40-block DiT denoise step that exercises the
- * whole hot path through the operator ABI (no reference counterpart: it stands
- * in for the reference's src/denoise/dit.c encode_forward / run_block loop,
- * dit.c:2286-2539 and 2577-3038, on random-init weights of the benchmark's
- * synthetic geometry). Host C; every device operation goes through h3_gpu.h. */
+/* h3_dit_synth.h — a DiT denoise step that exercises the whole hot path through
+ * the operator ABI (no reference counterpart: it stands in for the reference's
+ * src/denoise/dit.c encode_forward / run_block loop, dit.c:2286-2539 and
+ * 2577-3038, on random-init weights). Two geometries: the benchmark's synthetic
+ * 40-block model (h3_hip_dit_synth_default) and the real H3 block
+ * (h3_hip_dit_synth_h3: dit.c:31-46, 50 blocks, hidden 5376, 56 heads x 128,
+ * grouped QKV with per-head Q/K RMSNorm, 48 RoPE pairs, SwiGLU 14336).
+ * Host C; every device operation goes through h3_gpu.h. */
 #ifndef H3_DIT_SYNTH_H
 #define H3_DIT_SYNTH_H
 #include <stddef.h>
@@ -14,22 +17,32 @@ extern "C" {
 
 typedef struct {
     uint32_t blocks;            /* 40 */
-    uint32_t hidden;            /* 5120 (heads * 128) */
-    uint32_t heads;             /* 40 */
-    uint32_t mlp;               /* 13824, GELU-tanh MLP */
+    uint32_t hidden;            /* residual width: 5120 (H3: 5376); attention width is heads * 128 */
+    uint32_t heads;             /* 40 (H3: 56) */
+    uint32_t mlp;               /* 13824 GELU-tanh MLP (H3: 14336 SwiGLU) */
     uint32_t frames, height, width; /* video latent grid: 27 x 30 x 40 = 32400 rows */
     uint32_t audio_rows;        /* 1024 audio rows after the video rows */
     uint32_t latent;            /* latent width per row (patch embed in, head out) */
     uint32_t streamed_first;    /* blocks >= this stream from pinned host memory */
     float mask_density;         /* block-sparse density of 128x128 blocks; < 0 = dense */
-    int attention_mode;         /* 1 sage2++ (int8 QK / fp8 PV), 0 BF16 */
+    int attention_mode;         /* 1 sage2++ (int8 QK / fp8 PV), 0 BF16, 4 SubBlock router */
     float eps;                  /* AdaLN RMSNorm epsilon (1e-6) */
     float time;                 /* timestep of the modulation embedding (0.5) */
     uint64_t seed;
+    uint32_t rope_half;         /* rotate-half pairs d <-> d + rope_half: 64 (H3: 48) */
+    int swiglu;                 /* 1: fc1 -> 2 * mlp (gate rows, then up rows), SwiGLU, fc2 */
+    int qk_norm;                /* 1: per-head RMSNorm of Q and K with learned [128] weights */
+    int grouped_qkv;            /* 1: QKV rows grouped per head [heads, 3, 128] (H3 checkpoint layout) */
+    float subblock_sparsity;    /* attention_mode 4: the request's sparsity (0.75) */
 } h3_hip_dit_synth_config;
 
 /* The benchmark geometry. */
 h3_hip_dit_synth_config h3_hip_dit_synth_default(void);
+/* The real H3 block geometry (reference dit.c:31-46): 50 blocks, hidden 5376,
+ * 56 heads, SwiGLU 14336, grouped QKV, Q/K RMSNorm, 48 RoPE pairs (16 per
+ * axis), eps 1e-5, BF16 attention; video grid 25 x 27 x 27 = 18225 rows (the
+ * reference's 18,225-token attention case), no audio rows, all blocks resident. */
+h3_hip_dit_synth_config h3_hip_dit_synth_h3(void);
 
 typedef struct h3_hip_dit_synth h3_hip_dit_synth;
 
