@@ -22,6 +22,7 @@ import time
 from pathlib import Path
 
 import numpy as np
+from ctypes import c_float as C_float
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -261,6 +262,109 @@ def step_leg(steps, warmup):
             "setup_s": round(setup, 1)}
 
 
+# The reference's published real-H3 figures (other hardware), for the legs below.
+H3_PUBLISHED = {
+    "attention_18225": {"cudnn_bf16_ms": {"RTX 5090": 40.419, "RTX PRO 6000": 24.291, "H100": 14.347, "B200": 6.270},
+                        "sage2pp_ms": {"RTX 5090": 19.056},
+                        "source": "docs/cuda/attention-validation.md:54, cuda-fast-validation.md:13,120, "
+                                  "cuda-h100-qualification.md:90, cuda-b200-qualification.md:122"},
+    "attention_109078": {"cudnn_bf16_ms": {"RTX 5090": 1485.910}, "sage2pp_ms": {"RTX 5090": 609.853},
+                         "source": "docs/cuda/attention-validation.md:56"},
+    "proj_8193": {"bf16_ms": {"RTX 5090": 26.415}, "fp8_ms": {"RTX 5090": 15.767}, "nvfp4_ms": {"RTX 5090": 7.281},
+                  "source": "docs/cuda/denoiser-quantization-validation.md:174-177"},
+}
+
+
+def h3_attention_leg(seqs=(18225, 109078), heads=56):
+    """Real-H3 attention (H = 56, D = 128) at the reference's published token
+    counts: dense BF16 and Sage2++ (int8 QK / fp8 PV, quantization included)
+    per call, on seeded 0.5 N(0,1) Q/K/V resident in HBM."""
+    from h3cli_amd.runtime import Gpu
+    out = {"workload": "real-H3 attention, H=56 D=128, per call", "published": {}}
+    for seq in seqs:
+        steps, warmup = (5, 1) if seq < 50000 else (2, 1)
+        row = {}
+        for name, mode in (("bf16", 0), ("sage2pp", 1)):
+            with Gpu() as gpu:
+                gpu.check(gpu.lib.h3_gpu_dit_attention_configure(gpu.handle, mode), "configure")
+                w = Workload(gpu, seq, heads, seed=7, scale=0.5, rope=False)
+                ms, _ = time_calls(gpu, w.call, steps, warmup)
+            tf = attention_flops(seq, heads) / (ms * 1e-3) / 1e12
+            row[name] = {"ms": round(ms, 3), "tflops": round(tf, 1)}
+            log(f"[bench] h3 attention S={seq} H={heads} {name}: {ms:.3f} ms ({tf:.1f} TFLOP/s)")
+        out[f"s{seq}"] = row
+        out["published"][f"s{seq}"] = H3_PUBLISHED[f"attention_{seq}"]
+    return out
+
+
+def h3_proj_leg(steps, warmup, m=8193, seed=9):
+    """The four real-H3 block projections at 8,193 rows (reference
+    quant_prepare.c:20 shapes): qkv 5376 -> 21504, out 7168 -> 5376, fc1 5376 ->
+    28672, fc2 14336 -> 5376, as W8A16 in the reference q8 recipe (int8 codes,
+    fp32 scale per 64 columns) with BF16 activations."""
+    from h3cli_amd.runtime import Gpu, Tensor
+    shapes = [("qkv", 5376, 21504), ("out", 7168, 5376), ("fc1", 5376, 28672), ("fc2", 14336, 5376)]
+    res = {"workload": "real-H3 block-0 projections, 8193 rows, W8A16 (q8 group 64)", "rows": m, "shapes": {},
+           "published": H3_PUBLISHED["proj_8193"]}
+    total_flops, total_ms = 0.0, 0.0
+    with Gpu() as gpu:
+        lib = gpu.lib
+        x = gpu.empty(m * 14336)
+        gpu.begin()
+        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, seed * 16, 1.0, m * 14336), "fill")
+        gpu.submit()
+        for i, (name, k, n) in enumerate(shapes):
+            w = Tensor(gpu, lib.h3_hip_q8_new(gpu.handle, n, k, 64), n * k, 2)
+            gpu.tensors.append(w)
+            gpu.begin()
+            gpu.check(lib.h3_hip_fill_q8_random(gpu.handle, w.handle, seed * 8 + i, C_float(1e-3), C_float(1e-2)),
+                      "fill q8")
+            gpu.submit()
+            y = gpu.empty(m * n)
+            call = lambda: lib.h3_gpu_linear_bf16(gpu.handle, y.handle, x.handle, w.handle, None, m, k, n)
+            ms, _ = time_calls(gpu, call, steps, warmup)
+            flops = 2.0 * m * k * n
+            total_flops += flops
+            total_ms += ms
+            res["shapes"][name] = {"k": k, "n": n, "ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2)}
+            log(f"[bench] h3 proj {name} {m}x{k}x{n}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s")
+            gpu.free(y)
+            gpu.free(w)
+    res["ms_total"] = round(total_ms, 4)
+    res["tflops"] = round(total_flops / total_ms / 1e9, 2)
+    return res
+
+
+def h3_step_leg(steps, warmup):
+    """One real-H3-geometry denoise step (include/h3_dit_synth.h
+    h3_hip_dit_synth_h3): 50 blocks, 18225 video rows, hidden 5376, 56 heads,
+    grouped QKV with Q/K norm, 48 RoPE pairs, SwiGLU 14336, W8A16 weights all
+    resident, dense BF16 attention."""
+    from h3cli_amd.runtime import DitSynth
+    t0 = time.perf_counter()
+    with DitSynth(geometry="h3") as m:
+        setup = time.perf_counter() - t0
+        rows, cfg = m.rows, m.config
+        for i in range(warmup):
+            m.step(step=i, dt=-0.02)
+        times = []
+        for i in range(steps):
+            t1 = time.perf_counter()
+            m.step(step=warmup + i, dt=-0.02)
+            times.append(time.perf_counter() - t1)
+        finite = bool(np.all(np.isfinite(m.read("latent"))))
+    sec = float(np.mean(times))
+    H, I, F = cfg.hidden, cfg.heads * 128, cfg.mlp
+    gemm = 2.0 * rows * (H * 3 * I + I * H + H * 2 * F + F * H) * cfg.blocks
+    attn = attention_flops(rows, cfg.heads) * cfg.blocks
+    log(f"[bench] h3 step: {sec:.3f} s/step over {rows} rows (setup {setup:.1f} s), finite={finite}")
+    return {"workload": "real-H3-geometry 50-block denoise step, 18225 rows, dense BF16 attention",
+            "s_per_step": round(sec, 4), "steps": steps, "rows": rows, "blocks": cfg.blocks,
+            "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
+            "achieved_tflops": round((gemm + attn) / sec / 1e12, 2), "latent_finite": finite,
+            "setup_s": round(setup, 1)}
+
+
 def probe():
     """Launches for HBM-traffic counters: attention twice (config 2 inputs),
     then a plain device-to-device copy of exactly 2^30 bytes, whose FETCH_SIZE
@@ -289,7 +393,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,subblock,gemm,step")
+    ap.add_argument("--legs", default="attention,sage,subblock,gemm,step,h3_attention,h3_proj,h3_step")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -367,6 +471,12 @@ def main():
         result["subblock"] = subblock_leg(args.steps, args.warmup)
     if "gemm" in legs:
         result["gemm"] = gemm_leg(args.steps, args.warmup)
+    if "h3_attention" in legs:
+        result["h3_attention"] = h3_attention_leg()
+    if "h3_proj" in legs:
+        result["h3_proj"] = h3_proj_leg(args.steps, args.warmup)
+    if "h3_step" in legs:
+        result["h3_step"] = h3_step_leg(2, 1)
     if "step" in legs:
         result["step"] = step_leg(args.step_count, 1)
     print(json.dumps(result), flush=True)
