@@ -125,6 +125,7 @@ _SIGNATURES.update({
     "h3_hip_dit_synth_h3": (DitSynthConfig, []),
     "h3_hip_dit_synth_create": (_p, [_p, C.POINTER(DitSynthConfig), C.c_char_p, _sz]),
     "h3_hip_dit_synth_free": (None, [_p]),
+    "h3_hip_dit_synth_load": (_i, [_p, C.c_char_p, C.c_char_p, _sz]),
     "h3_hip_dit_synth_step": (_i, [_p, _i, _f]),
     "h3_hip_dit_synth_tensor": (_p, [_p, C.c_char_p]),
     "h3_hip_dit_synth_rows": (_u32, [_p]),

@@ -96,17 +96,47 @@ extern "C" h3_gpu_tensor *h3_hip_q8_from_packed(h3_gpu *g, const int8_t *codes, 
     return t;
 }
 
-// Reference q8 packing (src/weights/q8.c:26-56), restated: per 64-wide group of a
-// row, scale = max|w| / 127 (1 for an all-zero group, floored at FLT_MIN), codes
-// round half to even and clamp to +-127. Non-finite weights are rejected.
-extern "C" int h3_q8_pack_rows(const uint16_t *source, int8_t *weights, float *scales, uint32_t rows, uint32_t columns);
+// Reference q8 packing (src/weights/q8.c:26-56), restated on the device: one
+// thread per (row, 64-wide group): scale = max|w| / 127 (IEEE division; 1 for an
+// all-zero group, floored at FLT_MIN), code = round-half-to-even(w / scale)
+// clamped to +-127. Bit-identical to h3_q8_pack_rows. A non-finite weight sets
+// bad[0] (the whole tensor is then rejected, as the reference does).
+__global__ __launch_bounds__(256) void q8_pack_kernel(const uint16_t *src, int8_t *codes, float *scales, uint32_t rows,
+                                                      uint32_t cols, uint32_t groups, unsigned *bad) {
+    const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (size_t)rows * groups) return;
+    const uint32_t r = (uint32_t)(id / groups), gi = (uint32_t)(id % groups);
+    const uint32_t begin = gi * 64, end = min(begin + 64, cols);
+    const uint16_t *row = src + (size_t)r * cols;
+    float amax = 0.f;
+    bool finite = true;
+    for (uint32_t c = begin; c < end; c++) {
+        const float w = bf16_to_f32(row[c]);
+        finite &= finite_f32(w);
+        amax = fmaxf(amax, fabsf(w));
+    }
+    if (!finite) { bad[0] = 1u; return; }
+    const float scale = amax == 0.f ? 1.f : fmaxf(__fdiv_rn(amax, 127.f), 1.17549435e-38f);
+    scales[id] = scale;
+    int8_t *out = codes + (size_t)r * cols;
+    for (uint32_t c = begin; c < end; c++) {
+        const float q = rintf(__fdiv_rn(bf16_to_f32(row[c]), scale));
+        out[c] = (int8_t)fminf(fmaxf(q, -127.f), 127.f);
+    }
+}
 
+extern "C" int h3_q8_layout(uint32_t rows, uint32_t columns, size_t *offset, size_t *bytes);
+
+// Reads rows x columns BF16 at `offset` of `path` and packs it on the device.
 extern "C" h3_gpu_tensor *h3_gpu_q8_load(h3_gpu *g, const char *path, uint64_t offset, uint32_t rows, uint32_t columns) {
     if (!g || !path || !rows || !columns) return nullptr;
-    size_t n = (size_t)rows * columns, groups = (columns + 63) / 64;
+    size_t layout_offset, layout_bytes;
+    if (!h3_q8_layout(rows, columns, &layout_offset, &layout_bytes)) {
+        h3_set_error(g, "q8 load %s: invalid shape %ux%u", path, rows, columns);
+        return nullptr;
+    }
+    const size_t n = (size_t)rows * columns, groups = (columns + 63) / 64;
     std::vector<uint16_t> src(n);
-    std::vector<int8_t> codes(n);
-    std::vector<float> scales((size_t)rows * groups);
     int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) { h3_set_error(g, "q8 load %s: %s", path, strerror(errno)); return nullptr; }
     size_t got = 0;
@@ -117,12 +147,27 @@ extern "C" h3_gpu_tensor *h3_gpu_q8_load(h3_gpu *g, const char *path, uint64_t o
         got += (size_t)r;
     }
     close(fd);
-    if (!h3_q8_pack_rows(src.data(), codes.data(), scales.data(), rows, columns)) {
-        h3_set_error(g, "q8 load %s: non-finite weight or invalid shape", path);
-        return nullptr;
+    h3_gpu_tensor *t = q8_tensor(g, rows, columns, 64);
+    if (!t) return nullptr;
+    void *staging = nullptr;
+    const size_t flag_at = (n * 2 + 255) & ~(size_t)255;
+    unsigned bad = 0;
+    bool ok = h3_hip_check(g, hipMalloc(&staging, flag_at + 4), "q8 load staging") &&
+              h3_hip_check(g, hipMemcpy(staging, src.data(), n * 2, hipMemcpyHostToDevice), "q8 load upload") &&
+              h3_hip_check(g, hipMemset((char *)staging + flag_at, 0, 4), "q8 load flag");
+    if (ok) {
+        const size_t threads = (size_t)rows * groups;
+        hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, nullptr,
+                           (const uint16_t *)staging, (int8_t *)t->data, (float *)t->q8_scales, rows, columns,
+                           (uint32_t)groups, (unsigned *)((char *)staging + flag_at));
+        ok = h3_hip_check(g, hipGetLastError(), "q8 pack") &&
+             h3_hip_check(g, hipMemcpy(&bad, (char *)staging + flag_at, 4, hipMemcpyDeviceToHost), "q8 pack flag");
     }
+    if (staging) hipFree(staging);
+    if (ok && bad) { h3_set_error(g, "q8 load %s: non-finite weight or invalid shape", path); ok = false; }
+    if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
     g->stats.q8_source_bytes += n * 2;
-    return h3_hip_q8_from_packed(g, codes.data(), scales.data(), rows, columns, 64);
+    return t;
 }
 
 extern "C" int h3_gpu_quant_configure(h3_gpu *g, int mode, const char *cache, uint64_t bf16_weights,

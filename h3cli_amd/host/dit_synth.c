@@ -14,6 +14,7 @@
  * reference precomputes its per-step modulation. */
 #include "h3_dit_synth.h"
 #include "h3_gpu_surface.h"
+#include "h3_safetensors.h"
 #include "h3_hip_ext.h"
 #include <math.h>
 #include <stdarg.h>
@@ -416,11 +417,81 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
     return h3_gpu_submit(g);
 }
 
+/* Checkpoint names of a block's tensors (dit.c:604-611) in load order; the
+ * projections map to PROJ slots 0-3. */
+static const char *const BLOCK_NAMES[8] = {"attn.qkv_proj.weight", "attn.out_proj.weight", "mlp.fc1.weight",
+                                           "mlp.fc2.weight", "norm1.weight", "norm2.weight",
+                                           "attn.q_norm.weight", "attn.k_norm.weight"};
+
+static h3_gpu_tensor **block_slot(h3_hip_dit_synth *m, uint32_t b, int i) {
+    switch (i) {
+    case 4: return &m->norm1[b];
+    case 5: return &m->norm2[b];
+    case 6: return &m->qn[b];
+    case 7: return &m->kn[b];
+    default: return b < m->c.streamed_first ? &m->proj[(size_t)b * PROJ + i] : NULL;
+    }
+}
+
+/* Expected [rows, columns] of tensor i (columns 0 for a vector). */
+static void block_shape(const h3_hip_dit_synth_config *c, int i, uint32_t *rows, uint32_t *cols) {
+    if (i < PROJ) { proj_shape(c, i, rows, cols); return; }
+    *rows = i < 6 ? c->hidden : 128;
+    *cols = 0;
+}
+
+int h3_hip_dit_synth_load(h3_hip_dit_synth *m, const char *path, char *error, size_t size) {
+    if (!m || !path) return fail(error, size, "missing model or path");
+    const h3_hip_dit_synth_config *c = &m->c;
+    if (c->streamed_first < c->blocks) return fail(error, size, "checkpoint loading needs every block resident");
+    h3_st_header header;
+    if (!h3_st_read_header(path, &header, error, size)) return 0;
+    h3_gpu *g = m->gpu;
+    int ok = 1;
+    char name[160];
+    /* Validate everything before replacing anything. */
+    for (uint32_t b = 0; ok && b < c->blocks; b++)
+        for (int i = 0; ok && i < 8; i++) {
+            if (i >= 6 && !c->qk_norm) continue;
+            uint32_t rows, cols;
+            block_shape(c, i, &rows, &cols);
+            snprintf(name, sizeof(name), "blocks.%u.%s", b, BLOCK_NAMES[i]);
+            const h3_st_tensor *t = h3_st_find(&header, name);
+            int shape_ok = t && t->dtype == H3_DTYPE_BF16 &&
+                           (cols ? t->ndim == 2 && t->shape[0] == rows && t->shape[1] == cols
+                                 : t->ndim == 1 && t->shape[0] == rows);
+            if (!shape_ok) ok = fail(error, size, "missing/invalid %s", name);
+        }
+    for (uint32_t b = 0; ok && b < c->blocks; b++)
+        for (int i = 0; ok && i < 8; i++) {
+            if (i >= 6 && !c->qk_norm) continue;
+            uint32_t rows, cols;
+            block_shape(c, i, &rows, &cols);
+            snprintf(name, sizeof(name), "blocks.%u.%s", b, BLOCK_NAMES[i]);
+            const h3_st_tensor *t = h3_st_find(&header, name);
+            h3_gpu_tensor *loaded = cols ? h3_gpu_q8_load(g, path, t->file_offset, rows, cols)
+                                         : h3_gpu_tensor_load_bf16(g, path, t->file_offset, rows);
+            if (!loaded) { ok = fail(error, size, "%s: %s", name, h3_gpu_error(g)); break; }
+            h3_gpu_tensor **slot = block_slot(m, b, i);
+            h3_gpu_tensor_free(*slot);
+            *slot = loaded;
+        }
+    h3_st_free_header(&header);
+    return ok;
+}
+
 h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *m, const char *name) {
     if (!m || !name) return NULL;
     if (!strcmp(name, "latent")) return m->latent;
     if (!strcmp(name, "hidden")) return m->x;
     if (!strcmp(name, "velocity")) return m->vel;
+    unsigned b, used = 0;
+    if (sscanf(name, "blocks.%u.%n", &b, &used) == 1 && used && b < m->c.blocks)
+        for (int i = 0; i < 8; i++)
+            if (!strcmp(name + used, BLOCK_NAMES[i])) {
+                h3_gpu_tensor **slot = block_slot(m, b, i);
+                return slot ? *slot : NULL;
+            }
     return NULL;
 }
 

@@ -159,6 +159,12 @@ class DitSynth:
         kept = self.lib.h3_hip_dit_synth_kept_blocks(self.handle, C.byref(total))
         return kept, total.value
 
+    def load(self, path):
+        """Load block weights from a safetensors checkpoint (reference names)."""
+        err = C.create_string_buffer(1024)
+        if not self.lib.h3_hip_dit_synth_load(self.handle, str(path).encode(), err, 1024):
+            raise H3Error(err.value.decode())
+
     def step(self, step=0, dt=-0.05):
         if not self.lib.h3_hip_dit_synth_step(self.handle, step, dt):
             raise H3Error(f"step: {self.gpu.error()}")

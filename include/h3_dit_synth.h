@@ -61,9 +61,21 @@ void h3_hip_dit_synth_free(h3_hip_dit_synth *model);
  * absolute sampler step bound for sparse attention. */
 int h3_hip_dit_synth_step(h3_hip_dit_synth *model, int step, float dt);
 
+/* Replaces the block weights with those of a safetensors checkpoint that uses
+ * the reference's names (dit.c:592-611): "blocks.<b>." + "norm1.weight" and
+ * "norm2.weight" [hidden], "attn.qkv_proj.weight" [3 * heads * 128, hidden],
+ * "attn.q_norm.weight" and "attn.k_norm.weight" [128] (loaded when qk_norm),
+ * "attn.out_proj.weight" [hidden, heads * 128], "mlp.fc1.weight" [2 * mlp
+ * (SwiGLU) or mlp, hidden], "mlp.fc2.weight" [hidden, mlp]; all BF16. The four
+ * projections are packed to W8A16 on the device with the reference q8 recipe
+ * (group 64). Every block must be resident (streamed_first >= blocks); no
+ * command may be active. Errors name the first missing or mismatched tensor. */
+int h3_hip_dit_synth_load(h3_hip_dit_synth *model, const char *path, char *error, size_t error_size);
+
 /* Model tensors for inspection: "latent" (F32 [rows, latent]), "hidden" (BF16
- * [rows, hidden], the residual stream after the last block), "velocity",
- * "mask" (U32 kept-block count in element 0 is not provided; use the config). */
+ * [rows, hidden], the residual stream after the last block), "velocity", and a
+ * resident block's weights under the checkpoint names above
+ * ("blocks.0.attn.qkv_proj.weight": a W8A16 tensor; norms BF16). */
 h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *model, const char *name);
 uint32_t h3_hip_dit_synth_rows(const h3_hip_dit_synth *model);
 /* Kept 128x128 blocks of the bound mask and the total (for FLOP accounting). */

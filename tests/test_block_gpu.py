@@ -140,6 +140,52 @@ def test_q8_load_from_file(gpu):
         os.unlink(path)
 
 
+def test_q8_load_device_pack_bit_exact(gpu):
+    """The device packer of h3_gpu_q8_load gives the codes and scales of the
+    reference recipe bit for bit (vs the oracle and the host h3_q8_pack_rows):
+    exact half ties, an all-zero group, a ragged last group (200 columns =
+    64+64+64+8), large and tiny magnitudes. A NaN weight is rejected."""
+    import ctypes as C
+    n, k = 67, 200
+    rng = np.random.default_rng(8)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    w[0, :64] = 0.0                                    # all-zero group -> scale 1
+    w[1, :64] = np.arange(64) - 31.5                   # ties after scaling by 127/amax
+    w[2] *= 1e30
+    w[3] *= 1e-30
+    w[4, 192:] = [127, -127, 63.5, -63.5, 0.5, -0.5, 1.5, 2.5]
+    wb = synth.f32_to_bf16(w).reshape(-1)
+    with tempfile.NamedTemporaryFile(delete=False) as f:
+        f.write(b"\0" * 10 + wb.tobytes())
+        path = f.name
+    try:
+        h = gpu.lib.h3_gpu_q8_load(gpu.handle, path.encode(), 10, n, k)
+        assert h, gpu.error()
+        from h3cli_amd.runtime import Tensor
+        t = Tensor(gpu, h, n * k, 2)
+        gpu.tensors.append(t)
+        groups = (k + 63) // 64
+        raw = np.zeros(n * k + n * groups * 4, np.uint8)
+        assert gpu.lib.h3_hip_tensor_copy_to_host(h, raw.ctypes.data, raw.size), gpu.error()
+        codes, scales = raw[:n * k].view(np.int8), raw[n * k:].view(np.float32)
+        ref_codes, ref_scales = oracle.q8_pack(wb, n, k, 64)
+        assert np.array_equal(codes, ref_codes) and np.array_equal(scales.view(np.uint32), ref_scales.view(np.uint32))
+        host_codes, host_scales = np.zeros(n * k, np.int8), np.zeros(n * groups, np.float32)
+        gpu.lib.h3_q8_pack_rows.restype = C.c_int
+        assert gpu.lib.h3_q8_pack_rows(C.c_void_p(wb.ctypes.data), C.c_void_p(host_codes.ctypes.data),
+                                       C.c_void_p(host_scales.ctypes.data), C.c_uint32(n), C.c_uint32(k))
+        assert np.array_equal(codes, host_codes) and np.array_equal(scales, host_scales)
+        bad = wb.copy()
+        bad[5 * k + 7] = 0x7FC0
+        with open(path, "r+b") as f:
+            f.seek(10)
+            f.write(bad.tobytes())
+        assert not gpu.lib.h3_gpu_q8_load(gpu.handle, path.encode(), 10, n, k)
+        assert "non-finite" in gpu.error()
+    finally:
+        os.unlink(path)
+
+
 def test_linear_contract_errors(gpu):
     w = gpu.from_bf16(np.zeros(256 * 256, np.uint16))
     x = gpu.from_bf16(np.zeros(4 * 256, np.uint16))

@@ -1,0 +1,95 @@
+"""Checkpoint loading into the DiT step (h3_hip_dit_synth_load): a safetensors
+file with the reference's block tensor names (src/denoise/dit.c:592-611),
+written by the `safetensors` package. Loaded projections must equal the
+reference q8 recipe applied to the file's BF16 weights bit for bit, norms must
+equal the file, the loaded model must step deterministically, and missing or
+mismatched tensors must be named in the error."""
+import numpy as np
+import pytest
+
+from h3cli_amd import synth
+from h3cli_amd.runtime import DitSynth, H3Error
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(blocks=2, hidden=512, heads=3, mlp=768, frames=3, height=8, width=200, latent=256, seed=4,
+             streamed_first=2)
+
+
+def checkpoint(path, drop=None, reshape=None, f32=None):
+    torch = pytest.importorskip("torch")
+    from safetensors.torch import save_file
+    g = torch.Generator().manual_seed(21)
+    H, I, F = SMALL["hidden"], SMALL["heads"] * 128, SMALL["mlp"]
+    shapes = {"norm1.weight": (H,), "norm2.weight": (H,), "attn.qkv_proj.weight": (3 * I, H),
+              "attn.q_norm.weight": (128,), "attn.k_norm.weight": (128,), "attn.out_proj.weight": (H, I),
+              "mlp.fc1.weight": (2 * F, H), "mlp.fc2.weight": (H, F)}
+    tensors = {}
+    for b in range(SMALL["blocks"]):
+        for suffix, shape in shapes.items():
+            scale = 0.05 if len(shape) == 2 else 0.1
+            t = torch.randn(*shape, generator=g) * scale + (1.0 if len(shape) == 1 else 0.0)
+            tensors[f"blocks.{b}.{suffix}"] = t.to(torch.bfloat16)
+    tensors["unrelated.bias"] = torch.zeros(7, dtype=torch.bfloat16)
+    if drop:
+        del tensors[drop]
+    if reshape:
+        tensors[reshape] = tensors[reshape].reshape(-1)
+    if f32:
+        tensors[f32] = tensors[f32].float()
+    save_file(tensors, str(path), metadata={"format": "pt"})
+    return {k: v.view(torch.int16).numpy().view(np.uint16).copy() for k, v in tensors.items() if v.dtype == torch.bfloat16}
+
+
+def test_load_weights_bit_exact_and_step(tmp_path):
+    path = tmp_path / "h3.safetensors"
+    ref = checkpoint(path)
+    runs = []
+    for _ in range(2):
+        with DitSynth(geometry="h3", **SMALL) as m:
+            m.load(path)
+            for b in range(SMALL["blocks"]):
+                for suffix in ("attn.qkv_proj.weight", "attn.out_proj.weight", "mlp.fc1.weight", "mlp.fc2.weight"):
+                    name = f"blocks.{b}.{suffix}"
+                    h = m.lib.h3_hip_dit_synth_tensor(m.handle, name.encode())
+                    assert h, name
+                    w = ref[name]
+                    n, k = {"attn.qkv_proj.weight": (3 * 384, 512), "attn.out_proj.weight": (512, 384),
+                            "mlp.fc1.weight": (1536, 512), "mlp.fc2.weight": (512, 768)}[suffix]
+                    groups = (k + 63) // 64
+                    raw = np.zeros(n * k + n * groups * 4, np.uint8)
+                    assert m.lib.h3_hip_tensor_copy_to_host(h, raw.ctypes.data, raw.size), m.gpu.error()
+                    codes, scales = oracle.q8_pack(w, n, k, 64)
+                    assert np.array_equal(raw[:n * k].view(np.int8), codes), name
+                    assert np.array_equal(raw[n * k:].view(np.float32), scales), name
+                for suffix in ("norm1.weight", "norm2.weight", "attn.q_norm.weight", "attn.k_norm.weight"):
+                    name = f"blocks.{b}.{suffix}"
+                    assert np.array_equal(m.read(name), ref[name]), name
+            m.step(step=0, dt=-0.1)
+            runs.append((m.read("latent"), m.read("hidden")))
+    assert np.all(np.isfinite(runs[0][0])) and np.all(np.isfinite(runs[0][1]))
+    assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+    with DitSynth(geometry="h3", **SMALL) as m:
+        m.step(step=0, dt=-0.1)
+        assert not np.array_equal(m.read("hidden"), runs[0][1])      # the loaded weights were used
+
+
+@pytest.mark.parametrize("kind,name", [("drop", "blocks.1.mlp.fc2.weight"), ("reshape", "blocks.0.attn.out_proj.weight"),
+                                       ("f32", "blocks.0.norm2.weight")])
+def test_load_errors_name_the_tensor(tmp_path, kind, name):
+    path = tmp_path / "bad.safetensors"
+    checkpoint(path, **{kind: name})
+    with DitSynth(geometry="h3", **SMALL) as m:
+        with pytest.raises(H3Error) as e:
+            m.load(path)
+        assert f"missing/invalid {name}" in str(e.value)
+
+
+def test_load_needs_resident_blocks(tmp_path):
+    path = tmp_path / "h3.safetensors"
+    checkpoint(path)
+    with DitSynth(geometry="h3", **dict(SMALL, streamed_first=1)) as m:
+        with pytest.raises(H3Error) as e:
+            m.load(path)
+        assert "resident" in str(e.value)
