@@ -194,3 +194,73 @@ def test_weight_options_and_names_match_reference(libs, monkeypatch):
                 ok = lib.h3_weight_options_read(C.byref(o), force, e, 256)
                 out.append((ok, bytes(memoryview(o)) if ok else None, e.value))
             assert out[0] == out[1], (env, force)
+
+
+class SolOptions(C.Structure):
+    """h3_cuda_sol_options (cuda_sol_policy.h:12-15)."""
+    _fields_ = [("q_block", C.c_int), ("kv_block", C.c_int), ("dense_layers", C.c_int), ("dense_steps", C.c_int),
+                ("local_radius", C.c_int), ("tau", C.c_float), ("min_exact", C.c_float), ("dense_sigma", C.c_float)]
+
+
+def _bind_sol(lib):
+    lib.h3_cuda_sol_options_valid.restype = C.c_int
+    lib.h3_cuda_sol_options_valid.argtypes = [SolOptions, C.c_char_p, C.c_size_t]
+    lib.h3_cuda_sol_options_match.restype = C.c_int
+    lib.h3_cuda_sol_options_match.argtypes = [SolOptions, SolOptions, C.c_uint]
+    lib.h3_cuda_sol_dense_reason.restype = C.c_char_p
+    lib.h3_cuda_sol_dense_reason.argtypes = [SolOptions, C.c_uint, C.c_int, C.c_float, C.c_float]
+    lib.h3_cuda_sol_current.restype = SolOptions
+    lib.h3_cuda_sol_current.argtypes = []
+    lib.h3_cuda_sol_exchange.restype = SolOptions
+    lib.h3_cuda_sol_exchange.argtypes = [SolOptions]
+    return lib
+
+
+def _opts(**kw):
+    o = SolOptions(32, 64, 1, 1, 1, 1.0, 0.0, -1.0)
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+def test_sol_policy_matches_reference(libs):
+    """SOL options validity, field matching, dense reasons and the thread's
+    current options, against src/cuda/cuda_sol_policy.c, plus the reference's
+    own assertions (tests/test_cuda_sol_policy.c:10-26)."""
+    ours, ref = (_bind_sol(lib) for lib in libs)
+    nan, inf = float("nan"), float("inf")
+    grid = [dict()] + [{k: v} for k, vals in dict(
+        q_block=[16, 31, 32, 33, 64, 128], kv_block=[32, 63, 64, 128], dense_layers=[-1, 0, 50, 51],
+        dense_steps=[-1, 0, 1000, 1001], local_radius=[-1, 0, 10000, 10001], tau=[-0.1, 0, 16, 16.5, nan, inf],
+        min_exact=[-0.1, 0, 0.5, 1, 1.1, nan], dense_sigma=[-1, -0.5, 0, 0.8, 1, 1.1, nan, inf]).items() for v in vals]
+    for kw in grid:
+        o = _opts(**kw)
+        ea, eb = C.create_string_buffer(256), C.create_string_buffer(256)
+        assert ours.h3_cuda_sol_options_valid(o, ea, 256) == ref.h3_cuda_sol_options_valid(o, eb, 256), kw
+        assert ea.value == eb.value, kw
+        for block in (0, 1, 49):
+            for step in (-1, 0, 1, 5):
+                for video, audio in ((0.2, 0.2), (0.2, 0.9), (nan, 0.1), (1.2, 0.1), (0.8, 0.0)):
+                    args = (o, block, step, video, audio)
+                    assert ours.h3_cuda_sol_dense_reason(*args) == ref.h3_cuda_sol_dense_reason(*args), (kw, args)
+    base = _opts()
+    for kw in grid[1:]:
+        for mask in range(256):
+            assert (ours.h3_cuda_sol_options_match(_opts(**kw), base, mask) ==
+                    ref.h3_cuda_sol_options_match(_opts(**kw), base, mask))
+    # tests/test_cuda_sol_policy.c:10-26
+    d = ours.h3_cuda_sol_current()
+    assert (d.q_block, d.kv_block, d.min_exact, d.dense_steps) == (32, 64, 0.0, 1)
+    assert ours.h3_cuda_sol_dense_reason(d, 49, 0, 0.2, 0.2) == b"early-evaluation"
+    assert ours.h3_cuda_sol_dense_reason(d, 0, 1, 0.2, 0.2) == b"early-layer"
+    assert ours.h3_cuda_sol_dense_reason(d, 1, 1, 0.2, 0.2) is None
+    assert ours.h3_cuda_sol_dense_reason(_opts(dense_sigma=0.8), 1, 1, 0.2, 0.9) == b"high-noise"
+    assert ours.h3_cuda_sol_dense_reason(_opts(min_exact=1), 49, 1, 0.2, 0.2) == b"all-exact"
+    saved = ours.h3_cuda_sol_exchange(_opts(min_exact=0.5))
+    assert ours.h3_cuda_sol_current().min_exact == 0.5
+    nested = ours.h3_cuda_sol_exchange(_opts())
+    assert nested.min_exact == 0.5
+    ours.h3_cuda_sol_exchange(nested)
+    assert ours.h3_cuda_sol_current().min_exact == 0.5
+    ours.h3_cuda_sol_exchange(saved)
+    assert ours.h3_cuda_sol_current().min_exact == 0.0
