@@ -7,6 +7,7 @@
 #include "internal.h"
 #include "sage.h"
 #include "subblock.h"
+#include "sol.h"
 #include "../../include/h3_policy.h"
 #include <cmath>
 #include <new>
@@ -18,6 +19,7 @@ struct h3_attention_state {
     bool configured = false;
     int mode = MODE_DEFAULT;
     int step = -1;
+    float sigma_video = 0.f, sigma_audio = 0.f;
     // SubBlock bypass policy (reference src/denoise/subblock.c:44-51): the
     // request's sparsity and warmup; dense attention when a reason applies.
     float subblock_sparsity = 0.75f;
@@ -30,6 +32,8 @@ struct h3_attention_state {
     uint64_t kept_tiles = 0, total_tiles = 0;  // over 128-query blocks x 64-key tiles
     // SubBlock router over the bound layout (used when no host mask is bound).
     h3_subblock_router router;
+    // SOL router and the options read at configure (mode 3).
+    h3_sol_router sol;
     h3_sage_workspace sage;
     h3_device_buffer bf16_ws;              // transposed V of the BF16 kernel
     // Per-dispatch timing (H3_PROFILE): pairs of events collected at synchronize.
@@ -48,12 +52,14 @@ void h3_attention_destroy(h3_gpu *g) {
     if (s->kv_count) hipFree(s->kv_count);
     h3_sage_workspace_free(&s->sage);
     h3_subblock_free(&s->router);
+    h3_sol_free(&s->sol);
     h3_buffer_free(&s->bf16_ws);
     for (auto &p : s->pending) { hipEventDestroy(p.first); hipEventDestroy(p.second); }
     delete s; g->attention = nullptr;
 }
 
 int h3_attention_mode(h3_gpu *g) { return g && g->attention && g->attention->configured ? g->attention->mode : 0; }
+h3_sol_router *h3_attention_sol(h3_gpu *g) { return g && g->attention ? &g->attention->sol : nullptr; }
 h3_subblock_router *h3_attention_router(h3_gpu *g) { return g && g->attention ? &g->attention->router : nullptr; }
 
 void h3_attention_collect_timing(h3_gpu *g) {
@@ -77,7 +83,12 @@ extern "C" int h3_gpu_dit_attention_configure(h3_gpu *g, int mode) {
     if (s->configured) return h3_set_error(g, "attention context is already configured");
     if (mode < 0 || mode > 4) return h3_set_error(g, "cuda-attention must be default, sage2++, sage3, sol or subblock");
     if (mode == MODE_SAGE3) return h3_set_error(g, "sage3 (NVFP4) attention is unsupported on the HIP backend");
-    if (mode == MODE_SOL) return h3_set_error(g, "SOL attention is unsupported on the HIP backend");
+    if (mode == MODE_SOL) {
+        // The request's options, as the reference reads them (gpu_cuda.cu:1553-1555).
+        h3_cuda_sol_options o = h3_cuda_sol_current();
+        if (!h3_cuda_sol_options_valid(o, g->error, sizeof(g->error))) return 0;
+        s->sol.options = o;
+    }
     s->mode = mode; s->configured = true;
     return 1;
 }
@@ -85,10 +96,12 @@ extern "C" int h3_gpu_dit_attention_configure(h3_gpu *g, int mode) {
 extern "C" int h3_gpu_dit_attention_noise(h3_gpu *g, int step, float video, float audio) {
     if (!g) return 0;
     auto *s = g->attention;
-    if (s->mode != MODE_SUBBLOCK) return 1;
+    if (s->mode != MODE_SUBBLOCK && s->mode != MODE_SOL) return 1;
     if (step < 0 || !finite_f32(video) || !finite_f32(audio) || video < 0 || video > 1 || audio < 0 || audio > 1)
         return h3_set_error(g, "invalid HIP attention absolute step/noise");
     s->step = step;
+    s->sigma_video = video;
+    s->sigma_audio = audio;
     return 1;
 }
 
@@ -194,6 +207,25 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
         return h3_set_error(g, "DiT attention: head_major must be 0/1 and step >= 0");
     auto *s = g->attention;
     bool masked = s->masked;
+    if (s->mode == MODE_SOL) {
+        // reference gpu_cuda.cu:1643-1662: the bypass rules run dense; routed
+        // calls use the BF16-rounded scale.
+        if (step != s->step) return h3_set_error(g, "SOL absolute step was not bound");
+        if (h3_cuda_sol_dense_reason(s->sol.options, block, step, s->sigma_video, s->sigma_audio))
+            return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), head_major != 0, MODE_DEFAULT, false);
+        const float rounded = round_scale_bf16(scale);
+        if (!h3_sol_route(g, &s->sol, (const uint16_t *)q->data, (const uint16_t *)k->data, (const uint16_t *)v->data,
+                          seq, heads, rounded))
+            return 0;
+        const h3_sol_lists lists = h3_sol_lists_of(&s->sol);
+        if (!h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") ||
+            !h3_launch_attention_sol(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data,
+                                     (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads, rounded,
+                                     head_major != 0, (uint32_t)s->sol.options.q_block, &lists))
+            return 0;
+        g->stats.attention_dispatches++;
+        return 1;
+    }
     if (s->mode == MODE_SUBBLOCK) {
         if (step != s->step) return h3_set_error(g, "SubBlock absolute step was not bound");
         const char *reason = h3_subblock_dense_reason(seq, block, step, s->subblock_sparsity, s->subblock_warmup);
@@ -238,5 +270,11 @@ extern "C" int h3_hip_dit_subblock_policy(h3_gpu *g, float sparsity, int warmup)
     if (!(sparsity >= 0.f) || sparsity >= 1.f) return h3_set_error(g, "SubBlock sparsity must be in [0, 1)");
     g->attention->subblock_sparsity = sparsity;
     g->attention->subblock_warmup = warmup;
+    return 1;
+}
+
+extern "C" int h3_hip_dit_sol_force_exact(h3_gpu *g, int on) {
+    if (!g) return 0;
+    g->attention->sol.force_exact = on != 0;
     return 1;
 }

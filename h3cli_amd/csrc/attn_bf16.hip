@@ -60,6 +60,14 @@ struct Args {
     const uint32_t *kv_count;              // sparse: number of entries per list
     unsigned list_stride;
     unsigned *fault;
+    // SOL centroid phase (listed kernel with CENT): per (head, query block) the
+    // centroid tile list, its length and the approximate-block mask of each
+    // tile; centroid K rows [key_blocks][heads][128] and transposed V
+    // [heads][128][kc_padded] in the V^T key order.
+    const uint32_t *cent_list, *cent_count;
+    const uint64_t *cent_mask;
+    unsigned cent_stride, key_blocks, kc_padded;
+    const uint16_t *kc, *vct;
 };
 
 // Position of key j (0..63) inside a transposed V row: keys are grouped by 16
@@ -570,41 +578,53 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 }
 
 
-// Routed sparse attention: one workgroup of two waves per (64-query block,
+// Listed sparse attention: one workgroup of QW waves per (32 * QW-query block,
 // head) walks that block's own list of kept 64-key tiles (ascending tile ids,
-// a list per head and query block).
+// a list per head and query block): SubBlock routes (QW 2) and SOL exact tiles
+// (QW 1 or 2).
+//  * CENT (SOL): after the exact tiles, centroid tiles: tile t holds the
+//    centroids of key blocks 64t .. 64t+63 (K centroids in K's row layout, V
+//    centroids transposed like V^T); only the approximate blocks of the query
+//    block (a 64-bit mask per tile) take part, each with the bias ln 64 (6 in
+//    the kernel's log2 units), in the same online softmax.
 //  * SPLIT: 32 KB of LDS hold one K tile and one V^T tile; the phases are
 //    offset so that the next K tile loads during this tile's softmax and P.V,
 //    and the next V^T tile during the next scores. Barriers: one after the
 //    scores (K free, V^T ready), one after P.V (V^T free, next K ready).
 //  * otherwise two full stages (64 KB): the next tile loads during this one.
-// The list length and tile ids are read as wave-uniform values one iteration
+// The list lengths and tile ids are read as wave-uniform values one iteration
 // ahead: a vector load used at once would make the compiler wait for every
 // outstanding load, the tile loads included. Fragments are read from LDS as
 // they are consumed (requesting all 16 ahead, as the dense kernel does, costs
-// 42 more VGPRs and spills here).
-template <bool SPLIT, int OCC>
-__global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(OCC, OCC)))
-void attn_bf16_routed(Args a) {
+// 42 more VGPRs and spills here). Row sums of P are VALU adds.
+constexpr uint32_t CENT_BIT = 0x80000000u;
+
+template <bool SPLIT, int OCC, int QW, bool CENT>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * QW, 64 * QW), amdgpu_waves_per_eu(OCC, OCC)))
+void attn_bf16_listed(Args a) {
     constexpr int BLOCKS = K_BYTES / 1024;
+    constexpr unsigned QROWS = 32 * QW;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
-    const unsigned nqb = (a.seq + 63) / 64;
+    const unsigned nqb = (a.seq + QROWS - 1) / QROWS;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned head = id / nqb, qb = id % nqb;
-    const unsigned q0 = qb * 64;
+    const unsigned q0 = qb * QROWS;
     const size_t stride = (size_t)a.heads * D;
     const uint16_t *qh = a.q + (size_t)head * D;
     const uint16_t *kh = a.k + (size_t)head * D;
     const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
+    const uint16_t *kch = CENT ? a.kc + (size_t)head * D : nullptr;
+    const uint16_t *vcth = CENT ? a.vct + (size_t)head * D * a.kc_padded : nullptr;
     const float c = a.scale_log2;
     const size_t lq = (size_t)head * nqb + qb;
-    // The list length and tile ids are wave-uniform (readfirstlane keeps the
-    // loop scalar); each id is loaded one iteration before its use so that
-    // the load completes under the tile-load waits already in the loop.
     const unsigned count = __builtin_amdgcn_readfirstlane(a.kv_count[lq]);
+    const unsigned ccount = CENT ? __builtin_amdgcn_readfirstlane(a.cent_count[lq]) : 0u;
+    const unsigned total = count + ccount;
     const uint32_t *list = a.kv_list + lq * a.list_stride;
+    const uint32_t *clist = CENT ? a.cent_list + lq * a.cent_stride : nullptr;
+    const uint64_t *cmask = CENT ? a.cent_mask + lq * a.cent_stride : nullptr;
 
     bf16x8 qf[8];
     {
@@ -623,23 +643,33 @@ void attn_bf16_routed(Args a) {
     for (int md = 0; md < 4; md++) o[md] = f32x16{};
     float m = -1e30f, l = 0.f;
 
-    auto load_k = [&](unsigned tile, uint8_t *ks) {
-        const unsigned key0 = tile * BN;
+    // Entry i of the walk: an exact tile id, or a centroid tile (CENT_BIT | t).
+    auto entry_at = [&](unsigned i) -> uint32_t {
+        if (!CENT || i < count) return list[i];
+        return clist[i - count] | CENT_BIT;
+    };
+    auto load_k = [&](uint32_t e, uint8_t *ks) {
+        const bool cent = CENT && (e & CENT_BIT);
+        const unsigned key0 = (e & ~CENT_BIT) * BN, limit = cent ? a.key_blocks : a.seq;
+        const uint16_t *base = cent ? kch : kh;
 #pragma unroll
-        for (unsigned b = wave; b < BLOCKS; b += 2) {
+        for (unsigned b = wave; b < BLOCKS; b += QW) {
             unsigned key = 4 * b + lane / 16, phys = lane % 16;
-            unsigned row = min(key0 + key, a.seq - 1);
-            const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
+            unsigned row = min(key0 + key, limit - 1);
+            const uint16_t *src = base + (size_t)row * stride + k_chunk(key, phys) * 8;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                              (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
         }
     };
-    auto load_v = [&](unsigned tile, uint8_t *vs) {
-        const unsigned col = min(tile * BN, a.padded - BN);
+    auto load_v = [&](uint32_t e, uint8_t *vs) {
+        const bool cent = CENT && (e & CENT_BIT);
+        const unsigned padded = cent ? a.kc_padded : a.padded;
+        const unsigned col = min((e & ~CENT_BIT) * BN, padded - BN);
+        const uint16_t *base = cent ? vcth : vth;
 #pragma unroll
-        for (unsigned b = wave; b < BLOCKS; b += 2) {
+        for (unsigned b = wave; b < BLOCKS; b += QW) {
             unsigned d = 8 * b + lane / 8, vph = lane % 8;
-            const uint16_t *src = vth + (size_t)d * a.padded + col + v_chunk(d, vph) * 8;
+            const uint16_t *src = base + (size_t)d * padded + col + v_chunk(d, vph) * 8;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                              (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
         }
@@ -656,9 +686,20 @@ void attn_bf16_routed(Args a) {
                 s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kstep], s[mb], 0, 0, 0);
             }
     };
-    // Online softmax of the tile and O^T += V^T P^T.
-    auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, unsigned tile) {
-        if (tile * BN + BN > a.seq) {
+    // Online softmax of the tile and O^T += V^T P^T. bits: for a centroid
+    // tile, bit mb * 16 + r says whether the key of accumulator element
+    // s[mb][r] takes part; the bias is added in log2 units.
+    auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, uint32_t e, uint32_t bits) {
+        const bool cent = CENT && (e & CENT_BIT);
+        const unsigned tile = e & ~CENT_BIT;
+        const float bias = cent ? 6.0f : 0.0f;      // log2(64)
+        if (cent) {
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (!((bits >> (mb * 16 + r)) & 1u)) s[mb][r] = -INFINITY;
+        } else if (tile * BN + BN > a.seq) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
@@ -673,7 +714,7 @@ void attn_bf16_routed(Args a) {
             mx0 = fmaxf(fmaxf(mx0, s[0][r]), s[0][r + 1]);
             mx1 = fmaxf(fmaxf(mx1, s[1][r]), s[1][r + 1]);
         }
-        const float mx = half_max_swap(fmaxf(mx0, mx1)) * c;
+        const float mx = fmaf(half_max_swap(fmaxf(mx0, mx1)), c, bias);
         if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_SLACK)) {
             const float mnew = fmaxf(m, mx);
             const float alpha = exp2f_fast(m - mnew);
@@ -682,7 +723,7 @@ void attn_bf16_routed(Args a) {
 #pragma unroll
             for (int md = 0; md < 4; md++) o[md] *= alpha;
         }
-        const float neg = -m;
+        const float neg = bias - m;
         bf16x8 pb[4];
         float psum = 0.f;
 #pragma unroll
@@ -705,24 +746,38 @@ void attn_bf16_routed(Args a) {
                 o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kk], o[md], 0, 0, 0);
             }
     };
+    // This lane's 32 bits of the approximate-block mask of entry i (centroid
+    // entries only): keys mb * 32 + g * 8 + hf * 4 + (0..3) -> bits mb * 16 + g * 4.
+    auto bits_at = [&](unsigned i) -> uint32_t {
+        if (!CENT || i < count) return 0u;
+        const uint64_t w = cmask[i - count];
+        uint32_t bits = 0;
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                bits |= (uint32_t)((w >> (mb * 32 + g * 8 + hf * 4)) & 0xfu) << (mb * 16 + g * 4);
+        return bits;
+    };
 
-    unsigned tile = 0, next = 0;
-    if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
-    if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
+    uint32_t tile = 0, next = 0;
+    if (total) tile = __builtin_amdgcn_readfirstlane(entry_at(0));
+    if (total > 1) next = __builtin_amdgcn_readfirstlane(entry_at(1));
     if constexpr (SPLIT) {
         uint8_t *ks = smem, *vs = smem + K_BYTES;
-        if (count) { load_k(tile, ks); load_v(tile, vs); }
+        if (total) { load_k(tile, ks); load_v(tile, vs); }
         wait_vm_loads();
         __syncthreads();
-        for (unsigned it = 0; it < count; it++) {
-            const bool has_next = it + 1 < count;
+        for (unsigned it = 0; it < total; it++) {
+            const bool has_next = it + 1 < total;
             f32x16 s[2];
             scores(ks, s);
             wait_vm_loads();               // this tile's V^T (own share)
             __syncthreads();               // K free; every share of V^T landed
             if (has_next) load_k(next, ks);
-            const uint32_t later = it + 2 < count ? list[it + 2] : 0u;
-            softmax_pv(s, vs, tile);
+            const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
+            const uint32_t bits = bits_at(it);
+            softmax_pv(s, vs, tile, bits);
             wait_vm_loads();               // next K and the id after it (own share)
             __syncthreads();               // V^T free; every share of the next K landed
             if (has_next) load_v(next, vs);
@@ -730,21 +785,22 @@ void attn_bf16_routed(Args a) {
             next = __builtin_amdgcn_readfirstlane(later);
         }
     } else {
-        if (count) { load_k(tile, smem); load_v(tile, smem + K_BYTES); }
+        if (total) { load_k(tile, smem); load_v(tile, smem + K_BYTES); }
         wait_vm_loads();
         __syncthreads();
-        for (unsigned it = 0; it < count; it++) {
+        for (unsigned it = 0; it < total; it++) {
             const int cur = it & 1;
             uint8_t *ks = smem + cur * STAGE_BYTES;
-            if (it + 1 < count) {
+            if (it + 1 < total) {
                 uint8_t *nk = smem + (cur ^ 1) * STAGE_BYTES;
                 load_k(next, nk);
                 load_v(next, nk + K_BYTES);
             }
-            const uint32_t later = it + 2 < count ? list[it + 2] : 0u;
+            const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
+            const uint32_t bits = bits_at(it);
             f32x16 s[2];
             scores(ks, s);
-            softmax_pv(s, ks + K_BYTES, tile);
+            softmax_pv(s, ks + K_BYTES, tile, bits);
             wait_vm_loads();
             __syncthreads();
             tile = next;
@@ -752,8 +808,8 @@ void attn_bf16_routed(Args a) {
         }
     }
 
-    const float total = half_sum_swap(l);
-    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const float sum = half_sum_swap(l);
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
     const unsigned q = q0 + wave * 32 + n;
     bool bad = false;
     if (q < a.seq) {
@@ -775,11 +831,11 @@ void attn_bf16_routed(Args a) {
     if (bad) a.fault[0] = 1u;
 }
 
-template <bool SPLIT, int OCC>
-int launch_routed(h3_gpu *g, const Args &a, unsigned groups) {
+template <bool SPLIT, int OCC, int QW, bool CENT>
+int launch_listed(h3_gpu *g, const Args &a, unsigned groups) {
     constexpr size_t shared = SPLIT ? STAGE_BYTES : 2 * STAGE_BYTES;
     static bool configured = false;
-    auto kernel = attn_bf16_routed<SPLIT, OCC>;
+    auto kernel = attn_bf16_listed<SPLIT, OCC, QW, CENT>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
                           "attention shared memory"))
@@ -787,9 +843,9 @@ int launch_routed(h3_gpu *g, const Args &a, unsigned groups) {
         configured = true;
     }
     hipEvent_t timing = h3_kernel_timing_begin(g);
-    hipLaunchKernelGGL(kernel, dim3(groups), dim3(128), shared, g->compute, a);
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * QW), shared, g->compute, a);
     h3_kernel_timing_end(g, timing);
-    return h3_launch_status(g, "routed BF16 attention");
+    return h3_launch_status(g, CENT ? "SOL attention" : "routed BF16 attention");
 }
 
 }  // namespace
@@ -836,6 +892,26 @@ int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const 
     const unsigned groups = (seq + 63) / 64 * heads;
     // Split K/V phases, two waves per SIMD (measured fastest); variant 12:
     // two full 64 KB stages at one wave per SIMD.
-    if (g->attention_variant == 12) return launch_routed<false, 1>(g, a, groups);
-    return launch_routed<true, 2>(g, a, groups);
+    if (g->attention_variant == 12) return launch_listed<false, 1, 2, false>(g, a, groups);
+    return launch_listed<true, 2, 2, false>(g, a, groups);
+}
+
+int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                            const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
+                            uint32_t q_block, const h3_sol_lists *lists) {
+    Args a{};
+    a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
+    a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.head_major = head_major ? 1 : 0;
+    a.kv_list = lists->exact; a.kv_count = lists->exact_count; a.list_stride = lists->exact_stride;
+    a.cent_list = lists->cent; a.cent_count = lists->cent_count; a.cent_mask = lists->cent_mask;
+    a.cent_stride = lists->cent_stride; a.key_blocks = lists->key_blocks; a.kc_padded = lists->kc_padded;
+    a.kc = lists->kc; a.vct = lists->vct;
+    a.fault = g->fault;
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+                       seq, heads, a.padded, g->fault);
+    if (!h3_launch_status(g, "V transpose")) return 0;
+    if (q_block == 64) return launch_listed<true, 2, 2, true>(g, a, (seq + 63) / 64 * heads);
+    return launch_listed<true, 2, 1, true>(g, a, (seq + 31) / 32 * heads);
 }

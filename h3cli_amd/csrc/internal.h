@@ -6,7 +6,8 @@ int h3_attention_init(h3_gpu *g);
 void h3_attention_destroy(h3_gpu *g);
 void h3_attention_collect_timing(h3_gpu *g);
 struct h3_subblock_router *h3_attention_router(h3_gpu *g);
-int h3_attention_mode(h3_gpu *g);          // configured DiT attention mode (0 when unconfigured)
+int h3_attention_mode(h3_gpu *g);
+struct h3_sol_router *h3_attention_sol(h3_gpu *g);          // configured DiT attention mode (0 when unconfigured)
 void h3_streaming_destroy(h3_gpu *g);
 int h3_tensor_events(h3_gpu *g, h3_gpu_tensor *t);
 int h3_tensor_acquire(h3_gpu *g, const h3_gpu_tensor *t);
@@ -23,6 +24,20 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
 int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                                const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
                                const uint32_t *lists, const uint32_t *counts, uint32_t list_stride);
+
+// SOL attention lists (see csrc/sol.hip): exact tiles per (head, query block),
+// centroid tiles with their approximate-block masks, and the centroid arrays.
+struct h3_sol_lists {
+    const uint32_t *exact, *exact_count;
+    uint32_t exact_stride;
+    const uint32_t *cent, *cent_count;
+    const uint64_t *cent_mask;
+    uint32_t cent_stride, key_blocks, kc_padded;
+    const uint16_t *kc, *vct;
+};
+int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                            const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
+                            uint32_t q_block, const h3_sol_lists *lists);
 
 // Grow-only device buffer; growing waits for queued work that may read the old one.
 struct h3_device_buffer {

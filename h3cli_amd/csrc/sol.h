@@ -1,0 +1,33 @@
+// SOL routed attention (reference src/cuda/cuda_sol.cu:92-310): block centroids,
+// threshold routing of exact vs centroid-approximated key blocks, and the
+// per-(head, query block) lists the listed attention kernel walks.
+#pragma once
+#include "common.h"
+#include "internal.h"
+#include "../../include/h3_gpu_surface.h"
+#include "../../include/h3_sol_policy.h"
+#include <vector>
+
+struct h3_sol_router {
+    bool bound = false;
+    h3_cuda_sol_options options = H3_CUDA_SOL_DEFAULT;
+    bool force_exact = false;              // every key block exact (operator tests)
+    uint32_t seq = 0, qblocks = 0, kblocks = 0;
+    h3_device_buffer meta;                 // h3_sol_block query [qblocks], key [kblocks]
+    h3_device_buffer ws;
+    // Geometry of the workspace for the last routed call.
+    uint32_t heads = 0, kpad = 0, tiles = 0;
+    size_t off_qc = 0, off_kc = 0, off_vct = 0, off_moments = 0, off_routes = 0, off_exact = 0, off_exact_count = 0,
+           off_cent = 0, off_cent_count = 0, off_cent_mask = 0;
+};
+
+// Validates a layout as the reference's configure (cuda_sol.cu:356-364):
+// query_blocks = ceil(seq / q_block), key_blocks = ceil(seq / 64), true block
+// rows, frames -1 <= first <= last <= 1e7.
+int h3_sol_bind(h3_gpu *g, h3_sol_router *r, const h3_sol_layout *layout, const h3_cuda_sol_options &options);
+// Centroids, moments, routes and lists for one call (enqueued on g->compute);
+// scale is the call's (BF16-rounded) softmax scale.
+int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint32_t seq,
+                 uint32_t heads, float scale);
+h3_sol_lists h3_sol_lists_of(const h3_sol_router *r);
+void h3_sol_free(h3_sol_router *r);

@@ -1,0 +1,274 @@
+// SOL routed attention on HIP. The recipe is the reference's
+// (src/cuda/cuda_sol.cu:92-310): per head, BF16 centroids of Q blocks (32 or
+// 64 rows) and of K and V blocks (64 rows); per-channel mean and variance of
+// the K centroids; per query block a threshold mean + tau * sigma of the
+// centroid logit (log2 units); a key block is exact when it is protected,
+// local in frames, on the minimum-exact floor, non-finite, a short tail block,
+// or scores above the threshold, and is otherwise replaced by its centroid
+// with weight 64 (bias ln 64) in the same softmax.
+//
+// MI355X layout: the K centroids are written in K's own row layout and the V
+// centroids transposed and key-permuted exactly like the V^T workspace, so a
+// "centroid tile" (64 consecutive key blocks) loads and multiplies with the
+// same code as a key tile. Routing writes, per (head, query block), the
+// ascending exact tile list, the list of centroid tiles that hold at least one
+// approximate block, and each such tile's 64-bit approximate-block mask.
+#include "sol.h"
+#include <algorithm>
+#include <cmath>
+
+namespace {
+
+constexpr unsigned D = 128;
+
+__host__ __device__ inline unsigned vt_position(unsigned j) {   // key order of a V^T tile (attn_bf16.hip)
+    unsigned k16 = j & 15;
+    return (j & ~15u) + ((k16 >> 2) & 1) * 8 + (k16 >> 3) * 4 + (k16 & 3);
+}
+
+enum { SUM_Q = 0, SUM_K = 1, SUM_V = 2 };
+
+// Centroid of block b, head h, channel d: fp32 sum of the block's rows in
+// order, divided by the row count, rounded to BF16. Q -> qc [heads][qblocks][128];
+// K -> kc [kblocks][heads][128]; V -> vct [heads][128][kpad] at the V^T key
+// position (blocks kblocks .. kpad-1 write zeros).
+template <int WHICH>
+__global__ __launch_bounds__(128) void sol_summary(const uint16_t *x, uint16_t *out, unsigned seq, unsigned heads,
+                                                   unsigned block, unsigned blocks, unsigned kpad, unsigned *fault) {
+    const unsigned b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    uint16_t value = 0;
+    if (b < blocks) {
+        const unsigned start = b * block, len = min(block, seq - start);
+        float sum = 0.f;
+        for (unsigned i = 0; i < len; i++) sum += bf16_to_f32(x[((size_t)(start + i) * heads + h) * D + d]);
+        const float mean = __fdiv_rn(sum, (float)len);
+        value = f32_to_bf16(mean);
+        if (!finite_f32(mean) || !finite_f32(bf16_to_f32(value))) fault[0] = 1u;
+    }
+    if (WHICH == SUM_Q) out[((size_t)h * blocks + b) * D + d] = value;
+    else if (WHICH == SUM_K) out[((size_t)b * heads + h) * D + d] = value;
+    else out[((size_t)h * D + d) * kpad + (b & ~63u) + vt_position(b & 63u)] = value;
+}
+
+// Per head and channel: mean and variance of the K centroids over the key
+// blocks, each product and sum rounded separately. out: [heads][256].
+__global__ __launch_bounds__(128) void sol_moments(const uint16_t *kc, float *out, unsigned heads, unsigned blocks) {
+    const unsigned h = blockIdx.x, d = threadIdx.x;
+    float sum = 0.f, sq = 0.f;
+    for (unsigned b = 0; b < blocks; b++) {
+        const float x = bf16_to_f32(kc[((size_t)b * heads + h) * D + d]);
+        sum = __fadd_rn(sum, x);
+        sq = __fadd_rn(sq, __fmul_rn(x, x));
+    }
+    const float mean = __fdiv_rn(sum, (float)blocks);
+    const float var = __fsub_rn(__fdiv_rn(sq, (float)blocks), __fmul_rn(mean, mean));
+    out[h * 256 + d] = mean;
+    out[h * 256 + 128 + d] = var > 0.f ? var : 0.f;
+}
+
+// One workgroup per (query block, head). m, v and each dot are fmaf chains
+// over the 128 channels in order (the oracle's order); see oracle_sol_route.
+__global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint16_t *kc, const float *moments,
+                                                 const h3_sol_block *qmeta, const h3_sol_block *kmeta,
+                                                 uint8_t *routes, uint32_t *exact_list, uint32_t *exact_count,
+                                                 uint32_t *cent_list, uint32_t *cent_count, uint64_t *cent_mask,
+                                                 unsigned heads, unsigned qblocks, unsigned kblocks, unsigned tiles,
+                                                 unsigned radius, unsigned minimum, float scale, float tau,
+                                                 int force_exact) {
+    __shared__ float q[D];
+    __shared__ float limit;
+    __shared__ unsigned wave_total[4][2];
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const unsigned qb = blockIdx.x, h = blockIdx.y;
+    const float a = __fmul_rn(scale, 1.4426950408889634f);
+    if (tid < D) q[tid] = bf16_to_f32(qc[((size_t)h * qblocks + qb) * D + tid]);
+    __syncthreads();
+    if (tid == 0) {
+        float m = 0.f, v = 0.f;
+        for (unsigned d = 0; d < D; d++) {
+            m = fmaf(q[d], moments[h * 256 + d], m);
+            v = fmaf(__fmul_rn(q[d], q[d]), moments[h * 256 + 128 + d], v);
+        }
+        const float mean = __fmul_rn(m, a), var = __fmul_rn(__fmul_rn(v > 0.f ? v : 0.f, a), a);
+        limit = __fadd_rn(mean, __fmul_rn(tau, __fsqrt_rn(__fadd_rn(var, 1e-6f))));
+    }
+    __syncthreads();
+    const float threshold = limit;
+    const h3_sol_block qm = qmeta[qb];
+    const size_t row = (size_t)h * qblocks + qb;
+    uint32_t *exact_row = exact_list + row * kblocks;
+    uint32_t *cent_row = cent_list + row * tiles;
+    uint64_t *mask_row = cent_mask + row * tiles;
+    unsigned n_exact = 0, n_cent = 0;
+    for (unsigned base = 0; base < kblocks; base += 256) {
+        const unsigned b = base + tid;
+        const bool valid = b < kblocks;
+        bool exact = false;
+        if (valid) {
+            const uint16_t *kr = kc + ((size_t)b * heads + h) * D;
+            float dot = 0.f;
+            for (unsigned c8 = 0; c8 < D / 8; c8++) {
+                const u16x8 w = *reinterpret_cast<const u16x8 *>(kr + c8 * 8);
+#pragma unroll
+                for (int i = 0; i < 8; i++) dot = fmaf(q[c8 * 8 + i], bf16_to_f32(w[i]), dot);
+            }
+            dot = __fmul_rn(dot, a);
+            const h3_sol_block km = kmeta[b];
+            const bool protect = qm.protect || km.protect;
+            const bool local = qm.first_frame >= 0 && km.first_frame >= 0 &&
+                               qm.first_frame <= km.last_frame + (int)radius && km.first_frame <= qm.last_frame + (int)radius;
+            const bool floor_ = (uint64_t)(b + 1) * minimum / kblocks != (uint64_t)b * minimum / kblocks;
+            const bool recovery = !finite_f32(dot) || !finite_f32(threshold), tail = km.rows < 64;
+            exact = force_exact || protect || local || floor_ || recovery || tail || dot > threshold;
+            routes[row * kblocks + b] = (uint8_t)exact;
+        }
+        // Ordered compaction of the exact blocks; wave w's approximate blocks
+        // are the mask of centroid tile base / 64 + w.
+        const unsigned long long ex = __ballot(exact), approx = __ballot(valid && !exact);
+        if (lane == 0) { wave_total[wave][0] = __popcll(ex); wave_total[wave][1] = approx != 0; }
+        __syncthreads();
+        unsigned pos = n_exact + __popcll(ex & ((1ull << lane) - 1ull)), cpos = n_cent;
+        for (unsigned w = 0; w < wave; w++) { pos += wave_total[w][0]; cpos += wave_total[w][1]; }
+        if (exact) exact_row[pos] = b;
+        if (lane == 0 && approx) { cent_row[cpos] = base / 64 + wave; mask_row[cpos] = approx; }
+        for (unsigned w = 0; w < 4; w++) { n_exact += wave_total[w][0]; n_cent += wave_total[w][1]; }
+        __syncthreads();
+    }
+    if (tid == 0) { exact_count[row] = n_exact; cent_count[row] = n_cent; }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+int h3_sol_bind(h3_gpu *g, h3_sol_router *r, const h3_sol_layout *layout, const h3_cuda_sol_options &o) {
+    if (r->bound || !layout || !layout->query || !layout->key || !layout->sequence)
+        return h3_set_error(g, "SOL: missing or already configured layout");
+    const uint32_t seq = layout->sequence, qblock = (uint32_t)o.q_block;
+    const uint32_t qblocks = (seq + qblock - 1) / qblock, kblocks = (seq + 63) / 64;
+    if (layout->query_blocks != qblocks || layout->key_blocks != kblocks)
+        return h3_set_error(g, "SOL: layout block counts disagree with policy");
+    for (int which = 0; which < 2; which++) {
+        const uint32_t count = which ? kblocks : qblocks, block = which ? 64 : qblock;
+        const h3_sol_block *m = which ? layout->key : layout->query;
+        for (uint32_t i = 0; i < count; i++)
+            if (m[i].rows != std::min(block, seq - i * block) || m[i].first_frame < -1 ||
+                m[i].last_frame < m[i].first_frame || m[i].last_frame > 10000000)
+                return h3_set_error(g, "SOL: invalid protection metadata");
+    }
+    const size_t qbytes = (size_t)qblocks * sizeof(h3_sol_block), kbytes = (size_t)kblocks * sizeof(h3_sol_block);
+    if (!h3_buffer_reserve(g, &r->meta, qbytes + kbytes, "SOL layout") ||
+        !h3_hip_check(g, hipMemcpy(r->meta.ptr, layout->query, qbytes, hipMemcpyHostToDevice), "SOL layout") ||
+        !h3_hip_check(g, hipMemcpy((uint8_t *)r->meta.ptr + qbytes, layout->key, kbytes, hipMemcpyHostToDevice),
+                      "SOL layout"))
+        return 0;
+    r->options = o;
+    r->seq = seq; r->qblocks = qblocks; r->kblocks = kblocks;
+    r->bound = true;
+    return 1;
+}
+
+int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint32_t seq,
+                 uint32_t heads, float scale) {
+    if (!r->bound) return h3_set_error(g, "SOL attention needs a bound layout (h3_gpu_dit_sol_layout)");
+    if (seq != r->seq) return h3_set_error(g, "SOL layout was bound for sequence %u, not %u", r->seq, seq);
+    const uint32_t QB = r->qblocks, KB = r->kblocks, kpad = (KB + 63) / 64 * 64, tiles = kpad / 64;
+    size_t off = 0;
+    r->off_qc = off; off = align256(off + (size_t)heads * QB * D * 2);
+    r->off_kc = off; off = align256(off + (size_t)KB * heads * D * 2);
+    r->off_vct = off; off = align256(off + (size_t)heads * D * kpad * 2);
+    r->off_moments = off; off = align256(off + (size_t)heads * 256 * 4);
+    r->off_routes = off; off = align256(off + (size_t)heads * QB * KB);
+    r->off_exact = off; off = align256(off + (size_t)heads * QB * KB * 4);
+    r->off_exact_count = off; off = align256(off + (size_t)heads * QB * 4);
+    r->off_cent = off; off = align256(off + (size_t)heads * QB * tiles * 4);
+    r->off_cent_count = off; off = align256(off + (size_t)heads * QB * 4);
+    r->off_cent_mask = off; off = align256(off + (size_t)heads * QB * tiles * 8);
+    if (!h3_buffer_reserve(g, &r->ws, off, "SOL workspace")) return 0;
+    r->heads = heads; r->kpad = kpad; r->tiles = tiles;
+    auto *base = (uint8_t *)r->ws.ptr;
+    auto *qc = (uint16_t *)(base + r->off_qc), *kc = (uint16_t *)(base + r->off_kc);
+    auto *vct = (uint16_t *)(base + r->off_vct);
+    auto *moments = (float *)(base + r->off_moments);
+    const auto *qmeta = (const h3_sol_block *)r->meta.ptr;
+    const auto *kmeta = qmeta + QB;
+    const uint32_t qblock = (uint32_t)r->options.q_block;
+    hipLaunchKernelGGL(sol_summary<SUM_Q>, dim3(QB, heads), dim3(128), 0, g->compute, q, qc, seq, heads, qblock, QB,
+                       kpad, g->fault);
+    hipLaunchKernelGGL(sol_summary<SUM_K>, dim3(KB, heads), dim3(128), 0, g->compute, k, kc, seq, heads, 64u, KB,
+                       kpad, g->fault);
+    hipLaunchKernelGGL(sol_summary<SUM_V>, dim3(kpad, heads), dim3(128), 0, g->compute, v, vct, seq, heads, 64u, KB,
+                       kpad, g->fault);
+    hipLaunchKernelGGL(sol_moments, dim3(heads), dim3(128), 0, g->compute, kc, moments, heads, KB);
+    if (!h3_launch_status(g, "SOL summaries")) return 0;
+    const unsigned minimum = (unsigned)std::ceil((double)r->options.min_exact * KB);
+    hipLaunchKernelGGL(sol_route, dim3(QB, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta, kmeta,
+                       base + r->off_routes, (uint32_t *)(base + r->off_exact), (uint32_t *)(base + r->off_exact_count),
+                       (uint32_t *)(base + r->off_cent), (uint32_t *)(base + r->off_cent_count),
+                       (uint64_t *)(base + r->off_cent_mask), heads, QB, KB, tiles,
+                       (unsigned)r->options.local_radius, minimum, scale, r->options.tau, r->force_exact ? 1 : 0);
+    return h3_launch_status(g, "SOL route");
+}
+
+h3_sol_lists h3_sol_lists_of(const h3_sol_router *r) {
+    const auto *base = (const uint8_t *)r->ws.ptr;
+    h3_sol_lists l{};
+    l.exact = (const uint32_t *)(base + r->off_exact);
+    l.exact_count = (const uint32_t *)(base + r->off_exact_count);
+    l.exact_stride = r->kblocks;
+    l.cent = (const uint32_t *)(base + r->off_cent);
+    l.cent_count = (const uint32_t *)(base + r->off_cent_count);
+    l.cent_mask = (const uint64_t *)(base + r->off_cent_mask);
+    l.cent_stride = r->tiles;
+    l.key_blocks = r->kblocks;
+    l.kc_padded = r->kpad;
+    l.kc = (const uint16_t *)(base + r->off_kc);
+    l.vct = (const uint16_t *)(base + r->off_vct);
+    return l;
+}
+
+void h3_sol_free(h3_sol_router *r) {
+    h3_buffer_free(&r->ws);
+    h3_buffer_free(&r->meta);
+    r->bound = false;
+}
+
+// Route and centroid capture for tests, the counterpart of the reference's
+// h3_cuda_sol_routes (cuda_sol.cu:418-423): the last call's routes u8
+// [heads][qblocks][kblocks] and centroids BF16 qc [heads][qblocks][128], kc and
+// vc [heads][kblocks][128]. Any output may be null; counts must match.
+extern "C" int h3_hip_sol_routes(h3_gpu *g, uint8_t *routes, size_t route_count, uint16_t *qc, size_t qc_count,
+                                 uint16_t *kc, uint16_t *vc, size_t kv_count) {
+    if (!g) return 0;
+    auto *r = h3_attention_sol(g);
+    if (!r || !r->heads) return h3_set_error(g, "SOL routes: no routed call yet");
+    const size_t H = r->heads, QB = r->qblocks, KB = r->kblocks;
+    if (routes && route_count != H * QB * KB) return h3_set_error(g, "SOL routes: expected %zu routes", H * QB * KB);
+    if (qc && qc_count != H * QB * D) return h3_set_error(g, "SOL routes: expected %zu query centroids", H * QB * D);
+    if ((kc || vc) && kv_count != H * KB * D) return h3_set_error(g, "SOL routes: expected %zu key centroids", H * KB * D);
+    if (!h3_hip_check(g, hipStreamSynchronize(g->compute), "SOL routes")) return 0;
+    const auto *base = (const uint8_t *)r->ws.ptr;
+    if (routes && !h3_hip_check(g, hipMemcpy(routes, base + r->off_routes, H * QB * KB, hipMemcpyDeviceToHost), "routes"))
+        return 0;
+    if (qc && !h3_hip_check(g, hipMemcpy(qc, base + r->off_qc, H * QB * D * 2, hipMemcpyDeviceToHost), "centroids"))
+        return 0;
+    if (kc) {
+        std::vector<uint16_t> rows(KB * H * D);
+        if (!h3_hip_check(g, hipMemcpy(rows.data(), base + r->off_kc, rows.size() * 2, hipMemcpyDeviceToHost), "centroids"))
+            return 0;
+        for (size_t h = 0; h < H; h++)
+            for (size_t b = 0; b < KB; b++)
+                std::copy_n(&rows[(b * H + h) * D], D, kc + (h * KB + b) * D);
+    }
+    if (vc) {
+        const size_t kpad = r->kpad;
+        std::vector<uint16_t> t(H * D * kpad);
+        if (!h3_hip_check(g, hipMemcpy(t.data(), base + r->off_vct, t.size() * 2, hipMemcpyDeviceToHost), "centroids"))
+            return 0;
+        for (size_t h = 0; h < H; h++)
+            for (size_t b = 0; b < KB; b++)
+                for (size_t d = 0; d < D; d++)
+                    vc[(h * KB + b) * D + d] = t[(h * D + d) * kpad + (b & ~(size_t)63) + vt_position((unsigned)(b & 63))];
+    }
+    return 1;
+}

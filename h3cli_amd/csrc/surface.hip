@@ -6,6 +6,7 @@
 #include "common.h"
 #include "internal.h"
 #include "subblock.h"
+#include "sol.h"
 #include "../../include/h3_gpu_surface.h"
 #include <algorithm>
 #include <chrono>
@@ -108,9 +109,13 @@ extern "C" int h3_gpu_dit_sol_layout(h3_gpu *g, const h3_sol_layout *layout) {
     if (!g || !layout) return 0;
     if (!layout->sequence || !layout->query_blocks || !layout->key_blocks || !layout->query || !layout->key)
         return h3_set_error(g, "SOL layout: empty sequence or block tables");
-    // SubBlock mode binds the layout's protected blocks for its router
-    // (reference gpu_cuda.cu:1572-1591); other modes only validate it.
+    // SubBlock and SOL modes bind the layout for their routers (reference
+    // gpu_cuda.cu:1572-1591); other modes only validate it.
     if (h3_attention_mode(g) == 4) return h3_subblock_bind(g, h3_attention_router(g), layout);
+    if (h3_attention_mode(g) == 3) {
+        h3_sol_router *r = h3_attention_sol(g);
+        return h3_sol_bind(g, r, layout, r->options);
+    }
     return 1;
 }
 

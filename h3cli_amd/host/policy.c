@@ -31,10 +31,10 @@ WEAK int h3_attention_options(int mode, char *error, size_t size) {
     return 0;
 }
 
-/* Modes this backend runs: default (dense BF16), sage2++ and subblock. */
+/* Modes this backend runs: default (dense BF16), sage2++, sol and subblock. */
 WEAK int h3_attention_preflight(int mode, char *error, size_t size) {
     if (!h3_attention_options(mode, error, size)) return 0;
-    if (mode == 2 || mode == 3) {
+    if (mode == 2) {
         if (error && size) snprintf(error, size, "%s attention is unsupported on the HIP backend", h3_attention_name(mode));
         return 0;
     }

@@ -74,6 +74,18 @@ int h3_hip_dit_subblock_policy(h3_gpu *gpu, float sparsity, int warmup);
 int h3_hip_subblock_routes(h3_gpu *gpu, uint8_t *routes, float *scores, size_t route_count,
                            uint16_t *q_pool, uint16_t *k_pool, size_t pool_count);
 
+/* SOL (mode 3) route capture, the counterpart of the reference's
+ * h3_cuda_sol_routes (src/cuda/cuda_sol.cu:418-423): after a routed SOL call,
+ * copies its routes u8 [heads][QB][KB] (QB = ceil(seq / q_block), KB =
+ * ceil(seq / 64); route_count = heads * QB * KB) and its BF16 centroids: qc
+ * [heads][QB][128] (qc_count = heads * QB * 128), kc and vc [heads][KB][128]
+ * (kv_count = heads * KB * 128). Any output may be NULL. Waits for the stream. */
+int h3_hip_sol_routes(h3_gpu *gpu, uint8_t *routes, size_t route_count, uint16_t *qc, size_t qc_count,
+                      uint16_t *kc, uint16_t *vc, size_t kv_count);
+/* SOL operator tests: route every key block exact (the reference's run-time
+ * force_exact, h3_cuda_sol_run). */
+int h3_hip_dit_sol_force_exact(h3_gpu *gpu, int on);
+
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded
  * to a multiple of 64, padded rows zero):

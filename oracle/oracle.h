@@ -105,6 +105,17 @@ void oracle_sb_select(uint8_t *routes, const float *scores, unsigned heads, unsi
 void oracle_attention_routed(float *out, const float *q, const float *k, const float *v, unsigned seq,
                              unsigned heads, float scale, const uint8_t *routes, unsigned row0, unsigned row1);
 
+/* ---- SOL routed attention (src/cuda/cuda_sol.cu:92-310); see sol.c ---- */
+void oracle_sol_summary(uint16_t *out, const uint16_t *x, unsigned seq, unsigned heads, unsigned block);
+void oracle_sol_moments(float *out, const uint16_t *kc, unsigned heads, unsigned blocks);
+void oracle_sol_route(uint8_t *routes, uint64_t *counts, const uint16_t *qc, const uint16_t *kc,
+                      const float *moments, const int32_t *qmeta, const int32_t *kmeta, unsigned heads,
+                      unsigned qblocks, unsigned kblocks, unsigned radius, unsigned minimum, float scale,
+                      float tau, int force_exact);
+void oracle_sol_attention(float *out, const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *kc,
+                          const uint16_t *vc, const uint8_t *routes, unsigned seq, unsigned heads, unsigned qblock,
+                          float scale, unsigned row0, unsigned row1);
+
 /* ---- reference test-input generators (tests/cuda_attention.c:14-18,
  * tests/attention_native.c:20) ---- */
 void oracle_xorshift_bf16(uint16_t *out, size_t count, uint32_t *seed);

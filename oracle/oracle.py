@@ -56,6 +56,10 @@ def load():
         lib.oracle_euler.argtypes = [_p, _p, _p, C.c_size_t, _f, _f]
         lib.oracle_rms_norm.argtypes = [_p, _p, _p, _u, _u, _f]
         lib.oracle_sb_pool.argtypes = [_p, _p, _u, _u, _f]
+        lib.oracle_sol_summary.argtypes = [_p, _p, _u, _u, _u]
+        lib.oracle_sol_moments.argtypes = [_p, _p, _u, _u]
+        lib.oracle_sol_route.argtypes = [_p, _p, _p, _p, _p, _p, _p, _u, _u, _u, _u, _u, _f, _f, C.c_int]
+        lib.oracle_sol_attention.argtypes = [_p, _p, _p, _p, _p, _p, _p, _u, _u, _u, _f, _u, _u]
         lib.oracle_sb_score.argtypes = [_p, _p, _p, _u, _u]
         lib.oracle_sb_select.argtypes = [_p, _p, _u, _u, _u, _p, _p]
         lib.oracle_attention_routed.argtypes = [_p, _p, _p, _p, _u, _u, _f, _p, _u, _u]
@@ -316,4 +320,40 @@ def attention_routed(q, k, v, seq, heads, scale, routes, rows=None):
     out = np.zeros((r1 - r0) * heads * 128, np.float32)
     load().oracle_attention_routed(_ptr(out), _ptr(_f32(q)), _ptr(_f32(k)), _ptr(_f32(v)), seq, heads, scale,
                                    _ptr(np.ascontiguousarray(routes, np.uint8)), r0, r1)
+    return out
+
+
+def sol_summary(x, seq, heads, block):
+    blocks = (seq + block - 1) // block
+    out = np.zeros(heads * blocks * 128, np.uint16)
+    load().oracle_sol_summary(_ptr(out), _ptr(_u16(x)), seq, heads, block)
+    return out
+
+
+def sol_moments(kc, heads, blocks):
+    out = np.zeros(heads * 256, np.float32)
+    load().oracle_sol_moments(_ptr(out), _ptr(_u16(kc)), heads, blocks)
+    return out
+
+
+def sol_route(qc, kc, moments, qmeta, kmeta, heads, radius, minimum, scale, tau, force_exact=False):
+    """qmeta/kmeta: int32 [blocks, 4] (protect, first_frame, last_frame, rows).
+    Returns (routes u8 [heads, qblocks, kblocks], counts[7])."""
+    qm = np.ascontiguousarray(qmeta, np.int32)
+    km = np.ascontiguousarray(kmeta, np.int32)
+    qb, kb = len(qm), len(km)
+    routes = np.zeros(heads * qb * kb, np.uint8)
+    counts = np.zeros(7, np.uint64)
+    load().oracle_sol_route(_ptr(routes), _ptr(counts), _ptr(_u16(qc)), _ptr(_u16(kc)),
+                            _ptr(np.ascontiguousarray(moments, np.float32)), _ptr(qm), _ptr(km), heads, qb, kb,
+                            radius, minimum, scale, tau, int(force_exact))
+    return routes.reshape(heads, qb, kb), counts
+
+
+def sol_attention(q, k, v, kc, vc, routes, seq, heads, qblock, scale, rows=None):
+    r0, r1 = rows or (0, seq)
+    out = np.zeros((r1 - r0) * heads * 128, np.float32)
+    load().oracle_sol_attention(_ptr(out), _ptr(_u16(q)), _ptr(_u16(k)), _ptr(_u16(v)), _ptr(_u16(kc)),
+                                _ptr(_u16(vc)), _ptr(np.ascontiguousarray(routes, np.uint8)), seq, heads, qblock,
+                                scale, r0, r1)
     return out

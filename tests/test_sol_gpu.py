@@ -1,0 +1,194 @@
+"""SOL routed attention (mode 3) on the GPU against oracle/sol.c, over the
+reference's operator acceptance cases (tests/cuda_sol_acceptance.json,
+tests/cuda_sol_oracle.py:58-98): centroids bit-exact, routes equal to the
+oracle's on the same centroids (and to the float64 rule where separated),
+outputs within the reference's gates (rel-L2 <= 0.01, max relative <= 0.02)
+of the float64 SOL softmax, force-exact calls equal to dense attention, NaN
+inputs rejected, dense bypass for early steps and layers."""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from h3cli_amd import synth
+from h3cli_amd._lib import SolBlock, SolLayout
+from h3cli_amd.runtime import Gpu
+from oracle import oracle
+from tests.helpers import ATTN_COSINE, bf16, metrics, scale_bf16, sdpa
+from tests.sol_fixtures import inputs, metadata, routes64
+from tests.test_ref_host import SolOptions
+
+pytestmark = pytest.mark.gpu
+
+SCALE = scale_bf16(1 / math.sqrt(128))
+STEP, BLOCK = 5, 1
+
+
+class Layout:
+    def __init__(self, seq, meta):
+        self.blocks = []
+        arrays = []
+        for m in meta:
+            arr = (SolBlock * len(m))()
+            for i, (p, f0, f1, rows) in enumerate(m):
+                arr[i].protect, arr[i].first_frame, arr[i].last_frame, arr[i].rows = int(p), int(f0), int(f1), int(rows)
+            arrays.append(arr)
+        self.arrays = arrays
+        self.layout = SolLayout(seq, len(meta[0]), len(meta[1]), 0, C.cast(arrays[0], C.POINTER(SolBlock)),
+                                C.cast(arrays[1], C.POINTER(SolBlock)))
+
+
+def make_sol(seq, meta, q=32, minimum=0.5, tau=1.0, radius=1, exact=False):
+    g = Gpu()
+    lib = g.lib
+    lib.h3_cuda_sol_exchange.restype = SolOptions
+    lib.h3_cuda_sol_exchange.argtypes = [SolOptions]
+    saved = lib.h3_cuda_sol_exchange(SolOptions(q, 64, 1, 1, radius, tau, minimum, -1.0))
+    try:
+        g.check(lib.h3_gpu_dit_attention_configure(g.handle, 3), "configure")
+    finally:
+        lib.h3_cuda_sol_exchange(saved)
+    g.sol_layout = Layout(seq, meta)
+    g.check(lib.h3_gpu_dit_sol_layout(g.handle, C.byref(g.sol_layout.layout)), "layout")
+    g.check(lib.h3_gpu_dit_attention_noise(g.handle, STEP, 0.2, 0.2), "noise")
+    if exact:
+        g.check(lib.h3_hip_dit_sol_force_exact(g.handle, 1), "force exact")
+    return g
+
+
+def capture(g, seq, heads, q):
+    QB, KB = (seq + q - 1) // q, (seq + 63) // 64
+    routes = np.zeros(heads * QB * KB, np.uint8)
+    qc = np.zeros(heads * QB * 128, np.uint16)
+    kc = np.zeros(heads * KB * 128, np.uint16)
+    vc = np.zeros(heads * KB * 128, np.uint16)
+    g.check(g.lib.h3_hip_sol_routes(g.handle, routes.ctypes.data, routes.size, qc.ctypes.data, qc.size,
+                                    kc.ctypes.data, vc.ctypes.data, kc.size), "routes")
+    return routes.reshape(heads, QB, KB), qc, kc, vc
+
+
+def run_case(seq, heads=2, q=32, minimum=0.5, tau=1.0, radius=1, exact=False, head_major=False, pattern="random",
+             protected=False, all_protected=False, seed=1701):
+    print(f"[sol] seq={seq} heads={heads} q={q} min={minimum} tau={tau} exact={exact} pattern={pattern} "
+          f"protected={protected or all_protected}", flush=True)
+    qx, kx, vx = inputs(seq, heads, seed=seed, pattern=pattern)
+    meta = metadata(seq, q, protected, all_protected)
+    g = make_sol(seq, meta, q, minimum, tau, radius, exact)
+    try:
+        out = bf16(sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK, head_major=head_major))
+        routes, qc, kc, vc = capture(g, seq, heads, q)
+        assert np.array_equal(qc, oracle.sol_summary(qx, seq, heads, q)), "Q centroids"
+        assert np.array_equal(kc, oracle.sol_summary(kx, seq, heads, 64)), "K centroids"
+        assert np.array_equal(vc, oracle.sol_summary(vx, seq, heads, 64)), "V centroids"
+        KB = (seq + 63) // 64
+        mom = oracle.sol_moments(kc, heads, KB)
+        floor_count = int(np.ceil(float(np.float32(minimum)) * KB))
+        want, _ = oracle.sol_route(qc, kc, mom, meta[0], meta[1], heads, radius, floor_count, SCALE, tau, exact)
+        assert np.array_equal(routes, want), "routes"
+        qcf = synth.bf16_to_f32(qc).reshape(heads, -1, 128)
+        kcf = synth.bf16_to_f32(kc).reshape(heads, -1, 128)
+        for h in range(heads):
+            r64, dots, thr = routes64(qcf[h], kcf[h], meta, SCALE, minimum, tau, radius, exact)
+            sep = np.abs(dots - thr[:, None]) > 1e-5
+            assert np.array_equal(routes[h][sep], r64[sep]), h
+        rows = list(range(seq)) if seq <= 1025 else sorted({0, 1, 31, 32, seq // 3, seq // 2, seq - 2, seq - 1})
+        ref = np.concatenate([oracle.sol_attention(qx, kx, vx, kc, vc, routes, seq, heads, q, SCALE, (r, r + 1))
+                              for r in rows]).reshape(len(rows), heads, 128)
+        got = out[rows]
+        d = got.astype(np.float64) - ref
+        if np.any(ref):
+            rel = np.linalg.norm(d) / np.linalg.norm(ref)
+            max_rel = np.abs(d).max() / np.abs(ref).max()
+            assert rel <= 0.01 and max_rel <= 0.02, (rel, max_rel)
+            assert metrics(got, ref)["cosine"] >= ATTN_COSINE
+        else:
+            assert np.abs(d).max() <= 1e-5
+        return out, routes
+    finally:
+        g.close()
+
+
+EXACT = [(s, q) for s in (1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 257, 1025) for q in (32, 64)]
+
+
+@pytest.mark.parametrize("seq,q", EXACT)
+def test_exact_cases_equal_dense(seq, q):
+    """tests/cuda_sol_acceptance.json exact-S*-Q*: every block exact, so the
+    result is dense attention (Q64 cases use the head-major output)."""
+    out, routes = run_case(seq, q=q, exact=True, head_major=(q == 64))
+    assert routes.all()
+    qx, kx, vx = inputs(seq, 2)
+    dense = oracle.attention(bf16(qx), bf16(kx), bf16(vx), seq, 2, SCALE).reshape(seq, 2, 128)
+    m = metrics(out, dense)
+    assert m["max_abs"] <= 2e-2 and m["cosine"] >= ATTN_COSINE, m
+
+
+@pytest.mark.parametrize("case", [
+    dict(seq=513, protected=True),                                   # mixed
+    dict(seq=513, head_major=True, q=64),                            # head-major
+    dict(seq=257, all_protected=True),                               # all-protected
+    dict(seq=257, pattern="constant", minimum=0.0, tau=16.0),        # constant
+    dict(seq=128, minimum=0.0, tau=16.0),                            # all-approximate
+    dict(seq=257, pattern="zero", minimum=0.0),                      # zero
+    dict(seq=257, pattern="extreme"),                                # extreme
+    dict(seq=257, pattern="spike"),                                  # spike
+    dict(seq=4103, heads=9, q=32),                                   # multiple slabs / heads
+    dict(seq=4103, heads=3, q=64, minimum=0.0, radius=0),
+], ids=["mixed", "head-major", "all-protected", "constant", "all-approximate", "zero", "extreme", "spike",
+        "multi-heads", "q64-tau"])
+def test_acceptance_cases(case):
+    out, routes = run_case(**case)
+    if case.get("all_protected"):
+        assert routes.all()
+    if case.get("pattern") == "constant":
+        assert np.all(np.abs(out - 0.69921875) <= 4e-3)    # V = bf16(0.7) everywhere
+    if case.get("seq") == 128 and case.get("tau") == 16.0:
+        assert not routes.all()                            # approximate blocks were used
+
+
+def test_nonfinite_rejected():
+    seq = 65
+    qx, kx, vx = inputs(seq, 2, pattern="nan")
+    g = make_sol(seq, metadata(seq, 32))
+    try:
+        with pytest.raises(Exception) as e:
+            sdpa(g, qx, kx, vx, seq, 2, step=STEP, block=BLOCK)
+        assert "nonfinite" in str(e.value)
+    finally:
+        g.close()
+
+
+def test_dense_bypass_and_layout_rules():
+    """Early steps and layers run dense (cuda_sol_policy.c:30-37); layouts are
+    validated like the reference's configure; step must be bound."""
+    seq = 300
+    qx, kx, vx = inputs(seq, 2, seed=4)
+    d = Gpu()
+    g = make_sol(seq, metadata(seq, 32))
+    try:
+        dense = sdpa(d, qx, kx, vx, seq, 2)
+        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.2, 0.2), "noise")
+        assert np.array_equal(sdpa(g, qx, kx, vx, seq, 2, step=0, block=5), dense)     # early-evaluation
+        g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, STEP, 0.2, 0.2), "noise")
+        assert np.array_equal(sdpa(g, qx, kx, vx, seq, 2, step=STEP, block=0), dense)  # early-layer
+        with pytest.raises(RuntimeError):
+            sdpa(g, qx, kx, vx, seq, 2, step=STEP + 1, block=BLOCK)                   # step not bound
+    finally:
+        g.close()
+        d.close()
+    bad = metadata(seq, 32)
+    bad[0][0, 3] = 31
+    g = Gpu()
+    try:
+        g.check(g.lib.h3_gpu_dit_attention_configure(g.handle, 3), "configure")
+        lay = Layout(seq, bad)
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(lay.layout))
+        assert "protection metadata" in g.error()
+        wrong = Layout(seq, metadata(seq, 64))       # 64-row query blocks under the default Q=32
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(wrong.layout))
+        good = Layout(seq, metadata(seq, 32))
+        g.check(g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(good.layout)), "layout")
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(good.layout))        # already configured
+    finally:
+        g.close()
