@@ -181,6 +181,71 @@ def subblock_leg(steps, warmup, sparsity=0.75):
                 "router_and_transpose_ms": round(ms - kernel_ms, 4)}
 
 
+def sol_leg(steps, warmup):
+    """SOL routed attention (mode 3) at S = 32400, H = 40 with the reference's
+    default options (tau 1, local radius 1, min-exact 0) and a layout built as
+    h3_sol_layout_build does for one video segment (src/denoise/sol.c:10-58):
+    27 frames of 1200 rows, first and last frames protected. Per call:
+    centroids, moments, routing and lists, V transpose and the listed kernel
+    (timed on its own)."""
+    import ctypes as C
+    from h3cli_amd._lib import SolBlock, SolLayout
+    from h3cli_amd.runtime import Gpu
+
+    class Opts(C.Structure):
+        _fields_ = [("q_block", C.c_int), ("kv_block", C.c_int), ("dense_layers", C.c_int),
+                    ("dense_steps", C.c_int), ("local_radius", C.c_int), ("tau", C.c_float),
+                    ("min_exact", C.c_float), ("dense_sigma", C.c_float)]
+
+    frame_rows, frames = 1200, SEQ // 1200
+    out = {"workload": "SOL routed attention, S=32400 H=40, tau 1, radius 1, frames 0 and 26 protected"}
+    for qblock in (32, 64):
+        with Gpu() as gpu:
+            lib = gpu.lib
+            lib.h3_cuda_sol_exchange.restype = Opts
+            lib.h3_cuda_sol_exchange.argtypes = [Opts]
+            saved = lib.h3_cuda_sol_exchange(Opts(qblock, 64, 1, 1, 1, 1.0, 0.0, -1.0))
+            try:
+                gpu.check(lib.h3_gpu_dit_attention_configure(gpu.handle, 3), "configure sol")
+            finally:
+                lib.h3_cuda_sol_exchange(saved)
+            arrays = []
+            for block in (qblock, 64):
+                nb = (SEQ + block - 1) // block
+                arr = (SolBlock * nb)()
+                for b in range(nb):
+                    r0, r1 = b * block, min(SEQ, b * block + block) - 1
+                    f0, f1 = r0 // frame_rows, r1 // frame_rows
+                    arr[b].rows = r1 - r0 + 1
+                    arr[b].first_frame, arr[b].last_frame = f0, f1
+                    arr[b].protect = int(f0 == 0 or f1 == frames - 1)
+                arrays.append(arr)
+            layout = SolLayout(SEQ, len(arrays[0]), len(arrays[1]), 0, C.cast(arrays[0], C.POINTER(SolBlock)),
+                               C.cast(arrays[1], C.POINTER(SolBlock)))
+            gpu.check(lib.h3_gpu_dit_sol_layout(gpu.handle, C.byref(layout)), "layout")
+            gpu.check(lib.h3_gpu_dit_attention_noise(gpu.handle, 5, 0.2, 0.2), "noise")
+            w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=True)
+
+            def call():
+                return lib.h3_gpu_dit_sdpa_bf16(gpu.handle, w.out.handle, w.q.handle, w.k.handle, w.v.handle, SEQ,
+                                                HEADS, DIM, 1.0 / math.sqrt(DIM), 0, 1, 5)
+            kt = []
+            ms, _ = time_calls(gpu, call, steps, warmup, kt)
+            QB, KB = (SEQ + qblock - 1) // qblock, (SEQ + 63) // 64
+            routes = np.zeros(HEADS * QB * KB, np.uint8)
+            gpu.check(lib.h3_hip_sol_routes(gpu.handle, routes.ctypes.data, routes.size, None, 0, None, None, 0),
+                      "routes")
+            density = float(routes.mean())
+        kernel_ms = kt[0][0]
+        tf = attention_flops(SEQ, HEADS, density=density) / (kernel_ms * 1e-3) / 1e12
+        log(f"[bench] sol q{qblock}: {ms:.3f} ms/call, exact density {density:.4f}, listed kernel {kernel_ms:.3f} ms "
+            f"({tf:.1f} TFLOP/s on exact tiles), routing + transpose {ms - kernel_ms:.3f} ms")
+        out[f"q{qblock}"] = {"ms_per_call": round(ms, 4), "exact_density": round(density, 5),
+                             "kernel_ms": round(kernel_ms, 4), "kernel_tflops_on_exact_tiles": round(tf, 2),
+                             "routing_and_transpose_ms": round(ms - kernel_ms, 4)}
+    return out
+
+
 GEMM_SHAPES = [("qkv", 5120, 15360, False), ("out", 5120, 5120, False), ("up_gelu", 5120, 13824, True),
                ("down", 13824, 5120, False)]
 
@@ -393,7 +458,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,subblock,gemm,step,h3_attention,h3_proj,h3_step")
+    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_step")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -469,6 +534,8 @@ def main():
                               "frac_of_fp8_peak": round(eff / PEAK_FP8, 4)}
     if "subblock" in legs:
         result["subblock"] = subblock_leg(args.steps, args.warmup)
+    if "sol" in legs:
+        result["sol"] = sol_leg(args.steps, args.warmup)
     if "gemm" in legs:
         result["gemm"] = gemm_leg(args.steps, args.warmup)
     if "h3_attention" in legs:

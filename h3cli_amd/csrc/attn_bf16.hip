@@ -585,8 +585,10 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 //  * CENT (SOL): after the exact tiles, centroid tiles: tile t holds the
 //    centroids of key blocks 64t .. 64t+63 (K centroids in K's row layout, V
 //    centroids transposed like V^T); only the approximate blocks of the query
-//    block (a 64-bit mask per tile) take part, each with the bias ln 64 (6 in
-//    the kernel's log2 units), in the same online softmax.
+//    block (a 64-bit mask per tile and half) take part, each with the bias
+//    ln 64 (6 in the kernel's log2 units), in the same online softmax. SOL
+//    entries carry a bit per 32-query half (HALF_BIT << wave): a wave skips
+//    the entries its half's query block does not route.
 //  * SPLIT: 32 KB of LDS hold one K tile and one V^T tile; the phases are
 //    offset so that the next K tile loads during this tile's softmax and P.V,
 //    and the next V^T tile during the next scores. Barriers: one after the
@@ -597,7 +599,7 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 // outstanding load, the tile loads included. Fragments are read from LDS as
 // they are consumed (requesting all 16 ahead, as the dense kernel does, costs
 // 42 more VGPRs and spills here). Row sums of P are VALU adds.
-constexpr uint32_t CENT_BIT = 0x80000000u;
+constexpr uint32_t CENT_BIT = 0x80000000u, HALF_BIT = 1u << 29, TILE_BITS = HALF_BIT - 1;
 
 template <bool SPLIT, int OCC, int QW, bool CENT>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * QW, 64 * QW), amdgpu_waves_per_eu(OCC, OCC)))
@@ -624,7 +626,8 @@ void attn_bf16_listed(Args a) {
     const unsigned total = count + ccount;
     const uint32_t *list = a.kv_list + lq * a.list_stride;
     const uint32_t *clist = CENT ? a.cent_list + lq * a.cent_stride : nullptr;
-    const uint64_t *cmask = CENT ? a.cent_mask + lq * a.cent_stride : nullptr;
+    const uint64_t *cmask = CENT ? a.cent_mask + lq * a.cent_stride * 2 : nullptr;
+    const uint32_t half_bit = HALF_BIT << wave;     // SOL: this wave's query block routes the entry
 
     bf16x8 qf[8];
     {
@@ -650,7 +653,7 @@ void attn_bf16_listed(Args a) {
     };
     auto load_k = [&](uint32_t e, uint8_t *ks) {
         const bool cent = CENT && (e & CENT_BIT);
-        const unsigned key0 = (e & ~CENT_BIT) * BN, limit = cent ? a.key_blocks : a.seq;
+        const unsigned key0 = (CENT ? e & TILE_BITS : e) * BN, limit = cent ? a.key_blocks : a.seq;
         const uint16_t *base = cent ? kch : kh;
 #pragma unroll
         for (unsigned b = wave; b < BLOCKS; b += QW) {
@@ -664,7 +667,7 @@ void attn_bf16_listed(Args a) {
     auto load_v = [&](uint32_t e, uint8_t *vs) {
         const bool cent = CENT && (e & CENT_BIT);
         const unsigned padded = cent ? a.kc_padded : a.padded;
-        const unsigned col = min((e & ~CENT_BIT) * BN, padded - BN);
+        const unsigned col = min((CENT ? e & TILE_BITS : e) * BN, padded - BN);
         const uint16_t *base = cent ? vcth : vth;
 #pragma unroll
         for (unsigned b = wave; b < BLOCKS; b += QW) {
@@ -691,15 +694,12 @@ void attn_bf16_listed(Args a) {
     // s[mb][r] takes part; the bias is added in log2 units.
     auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, uint32_t e, uint32_t bits) {
         const bool cent = CENT && (e & CENT_BIT);
-        const unsigned tile = e & ~CENT_BIT;
+        const unsigned tile = CENT ? e & TILE_BITS : e;
         const float bias = cent ? 6.0f : 0.0f;      // log2(64)
-        if (cent) {
-#pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                    if (!((bits >> (mb * 16 + r)) & 1u)) s[mb][r] = -INFINITY;
-        } else if (tile * BN + BN > a.seq) {
+        // A centroid tile is masked in the P domain below (its max may then
+        // include excluded centroids: an upper bound, harmless to the softmax);
+        // a key tile crossing the sequence end masks keys >= seq here.
+        if (!cent && tile * BN + BN > a.seq) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
@@ -732,6 +732,10 @@ void attn_bf16_listed(Args a) {
             for (int r = 0; r < 16; r += 2) {
                 float p0 = exp2f_fast(fmaf(s[mb][r], c, neg));
                 float p1 = exp2f_fast(fmaf(s[mb][r + 1], c, neg));
+                if (cent) {
+                    p0 = (bits >> (mb * 16 + r)) & 1u ? p0 : 0.f;
+                    p1 = (bits >> (mb * 16 + r + 1)) & 1u ? p1 : 0.f;
+                }
                 psum += p0 + p1;
                 pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
                 pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
@@ -746,11 +750,22 @@ void attn_bf16_listed(Args a) {
                 o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kk], o[md], 0, 0, 0);
             }
     };
-    // This lane's 32 bits of the approximate-block mask of entry i (centroid
-    // entries only): keys mb * 32 + g * 8 + hf * 4 + (0..3) -> bits mb * 16 + g * 4.
-    auto bits_at = [&](unsigned i) -> uint32_t {
-        if (!CENT || i < count) return 0u;
-        const uint64_t w = cmask[i - count];
+    // The approximate-block mask of entry i for this wave's half (centroid
+    // entries only), read with the ids, one entry ahead; wave-uniform.
+    auto mask_at = [&](unsigned i) -> uint64_t {
+        if (!CENT || i >= total || i < count) return 0ull;
+        return cmask[2 * (i - count) + wave];
+    };
+    auto uniform64 = [](uint64_t w) -> uint64_t {
+        // readfirstlane returns int: widen through uint32_t, or the low word
+        // sign-extends over the high one.
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)w);
+        return ((uint64_t)hi << 32) | lo;
+    };
+    // This lane's 32 bits of a mask: keys mb * 32 + g * 8 + hf * 4 + (0..3)
+    // -> bits mb * 16 + g * 4 + (0..3), the accumulator element order.
+    auto lane_bits = [&](uint64_t w) -> uint32_t {
         uint32_t bits = 0;
 #pragma unroll
         for (int mb = 0; mb < 2; mb++)
@@ -761,8 +776,10 @@ void attn_bf16_listed(Args a) {
     };
 
     uint32_t tile = 0, next = 0;
+    uint64_t mask = 0;
     if (total) tile = __builtin_amdgcn_readfirstlane(entry_at(0));
     if (total > 1) next = __builtin_amdgcn_readfirstlane(entry_at(1));
+    if (CENT) mask = uniform64(mask_at(0));
     if constexpr (SPLIT) {
         uint8_t *ks = smem, *vs = smem + K_BYTES;
         if (total) { load_k(tile, ks); load_v(tile, vs); }
@@ -771,18 +788,19 @@ void attn_bf16_listed(Args a) {
         for (unsigned it = 0; it < total; it++) {
             const bool has_next = it + 1 < total;
             f32x16 s[2];
-            scores(ks, s);
+            if (!CENT || (tile & half_bit)) scores(ks, s);
             wait_vm_loads();               // this tile's V^T (own share)
             __syncthreads();               // K free; every share of V^T landed
             if (has_next) load_k(next, ks);
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
-            const uint32_t bits = bits_at(it);
-            softmax_pv(s, vs, tile, bits);
-            wait_vm_loads();               // next K and the id after it (own share)
+            const uint64_t mask_after = mask_at(it + 1);
+            if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT ? lane_bits(mask) : 0u);
+            wait_vm_loads();               // next K, the id after it and the next mask (own share)
             __syncthreads();               // V^T free; every share of the next K landed
             if (has_next) load_v(next, vs);
             tile = next;
             next = __builtin_amdgcn_readfirstlane(later);
+            if (CENT) mask = uniform64(mask_after);
         }
     } else {
         if (total) { load_k(tile, smem); load_v(tile, smem + K_BYTES); }
@@ -797,14 +815,17 @@ void attn_bf16_listed(Args a) {
                 load_v(next, nk + K_BYTES);
             }
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
-            const uint32_t bits = bits_at(it);
-            f32x16 s[2];
-            scores(ks, s);
-            softmax_pv(s, ks + K_BYTES, tile, bits);
+            const uint64_t mask_after = mask_at(it + 1);
+            if (!CENT || (tile & half_bit)) {
+                f32x16 s[2];
+                scores(ks, s);
+                softmax_pv(s, ks + K_BYTES, tile, CENT ? lane_bits(mask) : 0u);
+            }
             wait_vm_loads();
             __syncthreads();
             tile = next;
             next = __builtin_amdgcn_readfirstlane(later);
+            if (CENT) mask = uniform64(mask_after);
         }
     }
 
@@ -912,6 +933,6 @@ int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uin
     hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
-    if (q_block == 64) return launch_listed<true, 2, 2, true>(g, a, (seq + 63) / 64 * heads);
-    return launch_listed<true, 2, 1, true>(g, a, (seq + 31) / 32 * heads);
+    (void)q_block;   // 32-row blocks come paired in the lists: one 64-query workgroup either way
+    return launch_listed<true, 2, 2, true>(g, a, (seq + 63) / 64 * heads);
 }

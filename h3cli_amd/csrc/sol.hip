@@ -66,8 +66,17 @@ __global__ __launch_bounds__(128) void sol_moments(const uint16_t *kc, float *ou
     out[h * 256 + 128 + d] = var > 0.f ? var : 0.f;
 }
 
-// One workgroup per (query block, head). m, v and each dot are fmaf chains
-// over the 128 channels in order (the oracle's order); see oracle_sol_route.
+// One workgroup per (pair of query blocks, head) for 32-row query blocks, or
+// per (query block, head) for 64-row ones: the unit a listed-kernel workgroup
+// of 64 queries covers. For each of its PAIR query blocks, m, v and each dot
+// are fmaf chains over the 128 channels in order (the oracle's order; see
+// oracle_sol_route). Lists, per unit: exact tiles either block routes, with
+// HALF_BIT << i set when block i routes the tile; then centroid tiles holding
+// an approximate block of either, with the same half bits and one 64-bit
+// approximate mask per half (for 64-row blocks both halves are the block).
+constexpr uint32_t HALF_BIT = 1u << 29;
+
+template <int PAIR>
 __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint16_t *kc, const float *moments,
                                                  const h3_sol_block *qmeta, const h3_sol_block *kmeta,
                                                  uint8_t *routes, uint32_t *exact_list, uint32_t *exact_count,
@@ -75,62 +84,83 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                                                  unsigned heads, unsigned qblocks, unsigned kblocks, unsigned tiles,
                                                  unsigned radius, unsigned minimum, float scale, float tau,
                                                  int force_exact) {
-    __shared__ float q[D];
-    __shared__ float limit;
+    __shared__ float q[PAIR][D];
+    __shared__ float limit[PAIR];
     __shared__ unsigned wave_total[4][2];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned qb = blockIdx.x, h = blockIdx.y;
+    const unsigned unit = blockIdx.x, h = blockIdx.y, units = gridDim.x;
+    const unsigned qb0 = unit * PAIR;
+    const unsigned present = min((unsigned)PAIR, qblocks - qb0);
     const float a = __fmul_rn(scale, 1.4426950408889634f);
-    if (tid < D) q[tid] = bf16_to_f32(qc[((size_t)h * qblocks + qb) * D + tid]);
+    for (unsigned i = tid; i < present * D; i += 256) q[i / D][i % D] = bf16_to_f32(qc[((size_t)h * qblocks + qb0) * D + i]);
     __syncthreads();
-    if (tid == 0) {
+    if (tid < present) {
         float m = 0.f, v = 0.f;
         for (unsigned d = 0; d < D; d++) {
-            m = fmaf(q[d], moments[h * 256 + d], m);
-            v = fmaf(__fmul_rn(q[d], q[d]), moments[h * 256 + 128 + d], v);
+            m = fmaf(q[tid][d], moments[h * 256 + d], m);
+            v = fmaf(__fmul_rn(q[tid][d], q[tid][d]), moments[h * 256 + 128 + d], v);
         }
         const float mean = __fmul_rn(m, a), var = __fmul_rn(__fmul_rn(v > 0.f ? v : 0.f, a), a);
-        limit = __fadd_rn(mean, __fmul_rn(tau, __fsqrt_rn(__fadd_rn(var, 1e-6f))));
+        limit[tid] = __fadd_rn(mean, __fmul_rn(tau, __fsqrt_rn(__fadd_rn(var, 1e-6f))));
     }
     __syncthreads();
-    const float threshold = limit;
-    const h3_sol_block qm = qmeta[qb];
-    const size_t row = (size_t)h * qblocks + qb;
+    h3_sol_block qm[PAIR];
+    for (unsigned i = 0; i < PAIR; i++) qm[i] = qmeta[qb0 + (i < present ? i : 0)];
+    const size_t row = (size_t)h * units + unit;
     uint32_t *exact_row = exact_list + row * kblocks;
     uint32_t *cent_row = cent_list + row * tiles;
-    uint64_t *mask_row = cent_mask + row * tiles;
+    uint64_t *mask_row = cent_mask + row * tiles * 2;
     unsigned n_exact = 0, n_cent = 0;
     for (unsigned base = 0; base < kblocks; base += 256) {
         const unsigned b = base + tid;
         const bool valid = b < kblocks;
-        bool exact = false;
+        bool exact[2] = {false, false};
         if (valid) {
             const uint16_t *kr = kc + ((size_t)b * heads + h) * D;
-            float dot = 0.f;
+            float dot[PAIR];
+            for (unsigned i = 0; i < PAIR; i++) dot[i] = 0.f;
             for (unsigned c8 = 0; c8 < D / 8; c8++) {
                 const u16x8 w = *reinterpret_cast<const u16x8 *>(kr + c8 * 8);
 #pragma unroll
-                for (int i = 0; i < 8; i++) dot = fmaf(q[c8 * 8 + i], bf16_to_f32(w[i]), dot);
+                for (int j = 0; j < 8; j++) {
+                    const float kv = bf16_to_f32(w[j]);
+#pragma unroll
+                    for (int i = 0; i < PAIR; i++) dot[i] = fmaf(q[i][c8 * 8 + j], kv, dot[i]);
+                }
             }
-            dot = __fmul_rn(dot, a);
             const h3_sol_block km = kmeta[b];
-            const bool protect = qm.protect || km.protect;
-            const bool local = qm.first_frame >= 0 && km.first_frame >= 0 &&
-                               qm.first_frame <= km.last_frame + (int)radius && km.first_frame <= qm.last_frame + (int)radius;
             const bool floor_ = (uint64_t)(b + 1) * minimum / kblocks != (uint64_t)b * minimum / kblocks;
-            const bool recovery = !finite_f32(dot) || !finite_f32(threshold), tail = km.rows < 64;
-            exact = force_exact || protect || local || floor_ || recovery || tail || dot > threshold;
-            routes[row * kblocks + b] = (uint8_t)exact;
+            const bool tail = km.rows < 64;
+#pragma unroll
+            for (int i = 0; i < PAIR; i++) {
+                if ((unsigned)i >= present) break;
+                const float di = __fmul_rn(dot[i], a), t = limit[i];
+                const bool protect = qm[i].protect || km.protect;
+                const bool local = qm[i].first_frame >= 0 && km.first_frame >= 0 &&
+                                   qm[i].first_frame <= km.last_frame + (int)radius &&
+                                   km.first_frame <= qm[i].last_frame + (int)radius;
+                const bool recovery = !finite_f32(di) || !finite_f32(t);
+                exact[i] = force_exact || protect || local || floor_ || recovery || tail || di > t;
+                routes[((size_t)h * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
+            }
+            if (PAIR == 1) exact[1] = exact[0];
         }
-        // Ordered compaction of the exact blocks; wave w's approximate blocks
-        // are the mask of centroid tile base / 64 + w.
-        const unsigned long long ex = __ballot(exact), approx = __ballot(valid && !exact);
-        if (lane == 0) { wave_total[wave][0] = __popcll(ex); wave_total[wave][1] = approx != 0; }
+        // Ordered compaction of the tiles either block routes exactly; wave
+        // w's approximate blocks are the masks of centroid tile base / 64 + w.
+        const bool any = exact[0] || exact[1];
+        const unsigned long long ex = __ballot(any);
+        const unsigned long long m0 = __ballot(valid && !exact[0]);
+        const unsigned long long m1 = PAIR == 1 ? m0 : __ballot(valid && present > 1 && !exact[1]);
+        if (lane == 0) { wave_total[wave][0] = __popcll(ex); wave_total[wave][1] = (m0 | m1) != 0; }
         __syncthreads();
         unsigned pos = n_exact + __popcll(ex & ((1ull << lane) - 1ull)), cpos = n_cent;
         for (unsigned w = 0; w < wave; w++) { pos += wave_total[w][0]; cpos += wave_total[w][1]; }
-        if (exact) exact_row[pos] = b;
-        if (lane == 0 && approx) { cent_row[cpos] = base / 64 + wave; mask_row[cpos] = approx; }
+        if (any) exact_row[pos] = b | (exact[0] ? HALF_BIT : 0u) | (exact[1] ? HALF_BIT << 1 : 0u);
+        if (lane == 0 && (m0 | m1)) {
+            cent_row[cpos] = (base / 64 + wave) | (m0 ? HALF_BIT : 0u) | (m1 ? HALF_BIT << 1 : 0u);
+            mask_row[2 * cpos] = m0;
+            mask_row[2 * cpos + 1] = m1;
+        }
         for (unsigned w = 0; w < 4; w++) { n_exact += wave_total[w][0]; n_cent += wave_total[w][1]; }
         __syncthreads();
     }
@@ -183,7 +213,7 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     r->off_exact_count = off; off = align256(off + (size_t)heads * QB * 4);
     r->off_cent = off; off = align256(off + (size_t)heads * QB * tiles * 4);
     r->off_cent_count = off; off = align256(off + (size_t)heads * QB * 4);
-    r->off_cent_mask = off; off = align256(off + (size_t)heads * QB * tiles * 8);
+    r->off_cent_mask = off; off = align256(off + (size_t)heads * QB * tiles * 16);
     if (!h3_buffer_reserve(g, &r->ws, off, "SOL workspace")) return 0;
     r->heads = heads; r->kpad = kpad; r->tiles = tiles;
     auto *base = (uint8_t *)r->ws.ptr;
@@ -202,7 +232,10 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     hipLaunchKernelGGL(sol_moments, dim3(heads), dim3(128), 0, g->compute, kc, moments, heads, KB);
     if (!h3_launch_status(g, "SOL summaries")) return 0;
     const unsigned minimum = (unsigned)std::ceil((double)r->options.min_exact * KB);
-    hipLaunchKernelGGL(sol_route, dim3(QB, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta, kmeta,
+    // Lists per 64-query unit: pairs of 32-row blocks, or single 64-row blocks.
+    const uint32_t units = (seq + 63) / 64;
+    auto route = qblock == 32 ? sol_route<2> : sol_route<1>;
+    hipLaunchKernelGGL(route, dim3(units, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta, kmeta,
                        base + r->off_routes, (uint32_t *)(base + r->off_exact), (uint32_t *)(base + r->off_exact_count),
                        (uint32_t *)(base + r->off_cent), (uint32_t *)(base + r->off_cent_count),
                        (uint64_t *)(base + r->off_cent_mask), heads, QB, KB, tiles,
@@ -215,7 +248,7 @@ h3_sol_lists h3_sol_lists_of(const h3_sol_router *r) {
     h3_sol_lists l{};
     l.exact = (const uint32_t *)(base + r->off_exact);
     l.exact_count = (const uint32_t *)(base + r->off_exact_count);
-    l.exact_stride = r->kblocks;
+    l.exact_stride = r->kblocks;       // per 64-query unit (ceil(seq / 64) per head)
     l.cent = (const uint32_t *)(base + r->off_cent);
     l.cent_count = (const uint32_t *)(base + r->off_cent_count);
     l.cent_mask = (const uint64_t *)(base + r->off_cent_mask);
