@@ -66,6 +66,7 @@ void h3_attention_collect_timing(h3_gpu *g) {
     auto *s = g->attention;
     if (!s) return;
     h3_subblock_collect(g, &s->router);
+    h3_sol_collect(g, &s->sol);
     for (auto &p : s->pending) {
         float ms = 0;
         if (hipEventElapsedTime(&ms, p.first, p.second) == hipSuccess) {
@@ -211,8 +212,10 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
         // reference gpu_cuda.cu:1643-1662: the bypass rules run dense; routed
         // calls use the BF16-rounded scale.
         if (step != s->step) return h3_set_error(g, "SOL absolute step was not bound");
-        if (h3_cuda_sol_dense_reason(s->sol.options, block, step, s->sigma_video, s->sigma_audio))
+        if (h3_cuda_sol_dense_reason(s->sol.options, block, step, s->sigma_video, s->sigma_audio)) {
+            s->sol.bypass++;
             return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), head_major != 0, MODE_DEFAULT, false);
+        }
         const float rounded = round_scale_bf16(scale);
         if (!h3_sol_route(g, &s->sol, (const uint16_t *)q->data, (const uint16_t *)k->data, (const uint16_t *)v->data,
                           seq, heads, rounded))
@@ -270,6 +273,23 @@ extern "C" int h3_hip_dit_subblock_policy(h3_gpu *g, float sparsity, int warmup)
     if (!(sparsity >= 0.f) || sparsity >= 1.f) return h3_set_error(g, "SubBlock sparsity must be in [0, 1)");
     g->attention->subblock_sparsity = sparsity;
     g->attention->subblock_warmup = warmup;
+    return 1;
+}
+
+// SOL counters (the reference's per-synchronize "SOL counters" report,
+// gpu_cuda.cu:452-460): out[0] routed calls, out[1] dense bypasses, out[2..8]
+// pair counts exact, approximate, protected, local, floor, recovery, tail.
+// Counts of calls not yet synchronized are collected first.
+extern "C" int h3_hip_sol_counters(h3_gpu *g, uint64_t *out, size_t count) {
+    if (!g || !g->attention) return 0;
+    if (!out || count != 9) return h3_set_error(g, "SOL counters: expected 9 values");
+    auto &r = g->attention->sol;
+    if (r.pending) {
+        if (!h3_hip_check(g, hipStreamSynchronize(g->compute), "SOL counters")) return 0;
+        h3_sol_collect(g, &r);
+    }
+    out[0] = r.calls; out[1] = r.bypass;
+    for (int j = 0; j < 7; j++) out[2 + j] = r.pairs[j];
     return 1;
 }
 

@@ -15,10 +15,15 @@ struct h3_sol_router {
     uint32_t seq = 0, qblocks = 0, kblocks = 0;
     h3_device_buffer meta;                 // h3_sol_block query [qblocks], key [kblocks]
     h3_device_buffer ws;
+    h3_device_buffer counters;             // u64 [7] pair counts, summed on the device per call
+    // Collected counters (the reference's h3_cuda_sol_stats calls and pairs)
+    // and the calls the dense bypass rules took.
+    uint64_t calls = 0, bypass = 0, pairs[7] = {0, 0, 0, 0, 0, 0, 0};
+    bool pending = false;
     // Geometry of the workspace for the last routed call.
     uint32_t heads = 0, kpad = 0, tiles = 0;
     size_t off_qc = 0, off_kc = 0, off_vct = 0, off_moments = 0, off_routes = 0, off_exact = 0, off_exact_count = 0,
-           off_cent = 0, off_cent_count = 0, off_cent_mask = 0;
+           off_cent = 0, off_cent_count = 0, off_cent_mask = 0, off_row_counts = 0;
 };
 
 // Validates a layout as the reference's configure (cuda_sol.cu:356-364):
@@ -30,4 +35,7 @@ int h3_sol_bind(h3_gpu *g, h3_sol_router *r, const h3_sol_layout *layout, const 
 int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint32_t seq,
                  uint32_t heads, float scale);
 h3_sol_lists h3_sol_lists_of(const h3_sol_router *r);
+// Folds the device pair counters of the calls since the last collect into
+// r->pairs (after the compute stream has drained).
+void h3_sol_collect(h3_gpu *g, h3_sol_router *r);
 void h3_sol_free(h3_sol_router *r);

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                                                  uint32_t *cent_list, uint32_t *cent_count, uint64_t *cent_mask,
                                                  unsigned heads, unsigned qblocks, unsigned kblocks, unsigned tiles,
                                                  unsigned radius, unsigned minimum, float scale, float tau,
-                                                 int force_exact) {
+                                                 int force_exact, uint32_t *row_counts) {
     __shared__ float q[PAIR][D];
     __shared__ float limit[PAIR];
     __shared__ unsigned wave_total[4][2];
@@ -111,6 +111,9 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
     uint32_t *cent_row = cent_list + row * tiles;
     uint64_t *mask_row = cent_mask + row * tiles * 2;
     unsigned n_exact = 0, n_cent = 0;
+    // This thread's pair counts: exact, approximate, protected, local (not
+    // protected), floor, recovery, tail (the reference's h3_cuda_sol_stats.pairs).
+    uint32_t tally[7] = {0, 0, 0, 0, 0, 0, 0};
     for (unsigned base = 0; base < kblocks; base += 256) {
         const unsigned b = base + tid;
         const bool valid = b < kblocks;
@@ -142,6 +145,12 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                 const bool recovery = !finite_f32(di) || !finite_f32(t);
                 exact[i] = force_exact || protect || local || floor_ || recovery || tail || di > t;
                 routes[((size_t)h * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
+                tally[exact[i] ? 0 : 1]++;
+                tally[2] += protect;
+                tally[3] += local && !protect;
+                tally[4] += floor_;
+                tally[5] += recovery;
+                tally[6] += tail;
             }
             if (PAIR == 1) exact[1] = exact[0];
         }
@@ -165,6 +174,38 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
         __syncthreads();
     }
     if (tid == 0) { exact_count[row] = n_exact; cent_count[row] = n_cent; }
+    __shared__ uint32_t wave_tally[4][7];
+#pragma unroll
+    for (int j = 0; j < 7; j++) {
+        uint32_t x = tally[j];
+        for (int off = 32; off; off >>= 1) x += __shfl_xor(x, off, 64);
+        if (lane == 0) wave_tally[wave][j] = x;
+    }
+    __syncthreads();
+    if (tid < 7)
+        row_counts[row * 8 + tid] = wave_tally[0][tid] + wave_tally[1][tid] + wave_tally[2][tid] + wave_tally[3][tid];
+}
+
+// Sums the per-unit pair counts of one call into the router's u64 counters
+// (one workgroup: tens of thousands of same-address atomics would serialize).
+__global__ __launch_bounds__(1024) void sol_count(const uint32_t *row_counts, size_t rows,
+                                                  unsigned long long *counters) {
+    __shared__ unsigned long long red[16][7];
+    unsigned long long c[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (size_t r = threadIdx.x; r < rows; r += 1024)
+#pragma unroll
+        for (int j = 0; j < 7; j++) c[j] += row_counts[r * 8 + j];
+#pragma unroll
+    for (int j = 0; j < 7; j++) {
+        for (int off = 32; off; off >>= 1) c[j] += __shfl_xor(c[j], off, 64);
+        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][j] = c[j];
+    }
+    __syncthreads();
+    if (threadIdx.x < 7) {
+        unsigned long long t = 0;
+        for (int w = 0; w < 16; w++) t += red[w][threadIdx.x];
+        counters[threadIdx.x] += t;
+    }
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -192,6 +233,9 @@ int h3_sol_bind(h3_gpu *g, h3_sol_router *r, const h3_sol_layout *layout, const 
         !h3_hip_check(g, hipMemcpy((uint8_t *)r->meta.ptr + qbytes, layout->key, kbytes, hipMemcpyHostToDevice),
                       "SOL layout"))
         return 0;
+    if (!h3_buffer_reserve(g, &r->counters, 64, "SOL counters") ||
+        !h3_hip_check(g, hipMemset(r->counters.ptr, 0, 64), "SOL counters"))
+        return 0;
     r->options = o;
     r->seq = seq; r->qblocks = qblocks; r->kblocks = kblocks;
     r->bound = true;
@@ -214,6 +258,8 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     r->off_cent = off; off = align256(off + (size_t)heads * QB * tiles * 4);
     r->off_cent_count = off; off = align256(off + (size_t)heads * QB * 4);
     r->off_cent_mask = off; off = align256(off + (size_t)heads * QB * tiles * 16);
+    const uint32_t units = (seq + 63) / 64;
+    r->off_row_counts = off; off = align256(off + (size_t)heads * units * 8 * 4);
     if (!h3_buffer_reserve(g, &r->ws, off, "SOL workspace")) return 0;
     r->heads = heads; r->kpad = kpad; r->tiles = tiles;
     auto *base = (uint8_t *)r->ws.ptr;
@@ -233,14 +279,30 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     if (!h3_launch_status(g, "SOL summaries")) return 0;
     const unsigned minimum = (unsigned)std::ceil((double)r->options.min_exact * KB);
     // Lists per 64-query unit: pairs of 32-row blocks, or single 64-row blocks.
-    const uint32_t units = (seq + 63) / 64;
     auto route = qblock == 32 ? sol_route<2> : sol_route<1>;
     hipLaunchKernelGGL(route, dim3(units, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta, kmeta,
                        base + r->off_routes, (uint32_t *)(base + r->off_exact), (uint32_t *)(base + r->off_exact_count),
                        (uint32_t *)(base + r->off_cent), (uint32_t *)(base + r->off_cent_count),
                        (uint64_t *)(base + r->off_cent_mask), heads, QB, KB, tiles,
-                       (unsigned)r->options.local_radius, minimum, scale, r->options.tau, r->force_exact ? 1 : 0);
-    return h3_launch_status(g, "SOL route");
+                       (unsigned)r->options.local_radius, minimum, scale, r->options.tau, r->force_exact ? 1 : 0,
+                       (uint32_t *)(base + r->off_row_counts));
+    if (!h3_launch_status(g, "SOL route")) return 0;
+    hipLaunchKernelGGL(sol_count, dim3(1), dim3(1024), 0, g->compute, (const uint32_t *)(base + r->off_row_counts),
+                       (size_t)heads * units, (unsigned long long *)r->counters.ptr);
+    if (!h3_launch_status(g, "SOL counters")) return 0;
+    r->calls++;
+    r->pending = true;
+    return 1;
+}
+
+void h3_sol_collect(h3_gpu *g, h3_sol_router *r) {
+    (void)g;
+    if (!r->pending) return;
+    unsigned long long c[7];
+    if (hipMemcpy(c, r->counters.ptr, sizeof(c), hipMemcpyDeviceToHost) != hipSuccess) return;
+    if (hipMemset(r->counters.ptr, 0, sizeof(c)) != hipSuccess) return;
+    for (int j = 0; j < 7; j++) r->pairs[j] += c[j];
+    r->pending = false;
 }
 
 h3_sol_lists h3_sol_lists_of(const h3_sol_router *r) {
@@ -263,6 +325,7 @@ h3_sol_lists h3_sol_lists_of(const h3_sol_router *r) {
 void h3_sol_free(h3_sol_router *r) {
     h3_buffer_free(&r->ws);
     h3_buffer_free(&r->meta);
+    h3_buffer_free(&r->counters);
     r->bound = false;
 }
 

@@ -85,6 +85,13 @@ int h3_hip_sol_routes(h3_gpu *gpu, uint8_t *routes, size_t route_count, uint16_t
 /* SOL operator tests: route every key block exact (the reference's run-time
  * force_exact, h3_cuda_sol_run). */
 int h3_hip_dit_sol_force_exact(h3_gpu *gpu, int on);
+/* SOL counters, the values of the reference's "SOL counters" report at
+ * synchronize (src/cuda/gpu_cuda.cu:452-460, h3_cuda_sol_stats in
+ * src/cuda/cuda_sol.h:6-10): out[0] routed calls, out[1] calls the dense
+ * bypass rules took, out[2..8] (query block, key block) pairs exact,
+ * approximate, protected, local, floor, recovery, tail, summed over heads and
+ * calls. count must be 9. Waits for the stream if calls are not yet counted. */
+int h3_hip_sol_counters(h3_gpu *gpu, uint64_t *out, size_t count);
 
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded

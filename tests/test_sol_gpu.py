@@ -84,8 +84,11 @@ def run_case(seq, heads=2, q=32, minimum=0.5, tau=1.0, radius=1, exact=False, he
         KB = (seq + 63) // 64
         mom = oracle.sol_moments(kc, heads, KB)
         floor_count = int(np.ceil(float(np.float32(minimum)) * KB))
-        want, _ = oracle.sol_route(qc, kc, mom, meta[0], meta[1], heads, radius, floor_count, SCALE, tau, exact)
+        want, counts = oracle.sol_route(qc, kc, mom, meta[0], meta[1], heads, radius, floor_count, SCALE, tau, exact)
         assert np.array_equal(routes, want), "routes"
+        got = np.zeros(9, np.uint64)
+        g.check(g.lib.h3_hip_sol_counters(g.handle, got.ctypes.data, 9), "counters")
+        assert got[0] == 1 and got[1] == 0 and np.array_equal(got[2:], np.asarray(counts, np.uint64)), (got, counts)
         qcf = synth.bf16_to_f32(qc).reshape(heads, -1, 128)
         kcf = synth.bf16_to_f32(kc).reshape(heads, -1, 128)
         for h in range(heads):
@@ -135,8 +138,9 @@ def test_exact_cases_equal_dense(seq, q):
     dict(seq=257, pattern="spike"),                                  # spike
     dict(seq=4103, heads=9, q=32),                                   # multiple slabs / heads
     dict(seq=4103, heads=3, q=64, minimum=0.0, radius=0),
+    dict(seq=4103, heads=3, q=32, minimum=0.0, radius=0),            # approximate block 31 (mask bit 31)
 ], ids=["mixed", "head-major", "all-protected", "constant", "all-approximate", "zero", "extreme", "spike",
-        "multi-heads", "q64-tau"])
+        "multi-heads", "q64-tau", "q32-tau"])
 def test_acceptance_cases(case):
     out, routes = run_case(**case)
     if case.get("all_protected"):
@@ -172,6 +176,11 @@ def test_dense_bypass_and_layout_rules():
         assert np.array_equal(sdpa(g, qx, kx, vx, seq, 2, step=0, block=5), dense)     # early-evaluation
         g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, STEP, 0.2, 0.2), "noise")
         assert np.array_equal(sdpa(g, qx, kx, vx, seq, 2, step=STEP, block=0), dense)  # early-layer
+        sdpa(g, qx, kx, vx, seq, 2, step=STEP, block=BLOCK)                            # routed
+        counters = np.zeros(9, np.uint64)
+        g.check(g.lib.h3_hip_sol_counters(g.handle, counters.ctypes.data, 9), "counters")
+        QB, KB = (seq + 31) // 32, (seq + 63) // 64
+        assert counters[0] == 1 and counters[1] == 2 and counters[2] + counters[3] == 2 * QB * KB, counters
         with pytest.raises(RuntimeError):
             sdpa(g, qx, kx, vx, seq, 2, step=STEP + 1, block=BLOCK)                   # step not bound
     finally:
