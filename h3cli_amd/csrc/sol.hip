@@ -253,12 +253,12 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     r->off_vct = off; off = align256(off + (size_t)heads * D * kpad * 2);
     r->off_moments = off; off = align256(off + (size_t)heads * 256 * 4);
     r->off_routes = off; off = align256(off + (size_t)heads * QB * KB);
-    r->off_exact = off; off = align256(off + (size_t)heads * QB * KB * 4);
-    r->off_exact_count = off; off = align256(off + (size_t)heads * QB * 4);
-    r->off_cent = off; off = align256(off + (size_t)heads * QB * tiles * 4);
-    r->off_cent_count = off; off = align256(off + (size_t)heads * QB * 4);
-    r->off_cent_mask = off; off = align256(off + (size_t)heads * QB * tiles * 16);
-    const uint32_t units = (seq + 63) / 64;
+    const uint32_t units = (seq + 63) / 64;     // lists are per 64-query unit
+    r->off_exact = off; off = align256(off + (size_t)heads * units * KB * 4);
+    r->off_exact_count = off; off = align256(off + (size_t)heads * units * 4);
+    r->off_cent = off; off = align256(off + (size_t)heads * units * tiles * 4);
+    r->off_cent_count = off; off = align256(off + (size_t)heads * units * 4);
+    r->off_cent_mask = off; off = align256(off + (size_t)heads * units * tiles * 16);
     r->off_row_counts = off; off = align256(off + (size_t)heads * units * 8 * 4);
     if (!h3_buffer_reserve(g, &r->ws, off, "SOL workspace")) return 0;
     r->heads = heads; r->kpad = kpad; r->tiles = tiles;

@@ -153,8 +153,10 @@ h3_gpu_tensor *h3_gpu_q8_load(h3_gpu *gpu, const char *path, uint64_t offset,
 
 /* ---- DiT attention ---------------------------------------------------- */
 /* gpu.h:52. mode: 0 default (dense BF16), 1 sage2++ (int8 QK / fp8 PV),
- * 4 subblock (block-sparse); 2 sage3 and 3 sol are rejected as unsupported
- * (reference src/denoise/attention.h:7). Once per context. */
+ * 3 sol (centroid-routed; reads the thread-current h3_cuda_sol_options as
+ * gpu_cuda.cu:1553-1555 does), 4 subblock (block-sparse); 2 sage3 is
+ * rejected as unsupported (reference src/denoise/attention.h:7). Once per
+ * context. */
 int h3_gpu_dit_attention_configure(h3_gpu *gpu, int mode);
 /* gpu.h:53-55. Q,K,V sequence-major BF16 [seq,heads,dim]; out [seq,heads,dim]
  * or head-major [heads,seq,dim]. dim must be 128; heads is any value >= 1
