@@ -400,6 +400,54 @@ def h3_proj_leg(steps, warmup, m=8193, seed=9):
     return res
 
 
+def h3_proj_fp8_leg(steps, warmup, m=8193, seed=9):
+    """The same four real-H3 projections as FP8 W8A8 (reference
+    cuda_quant.cuh:339-398, the mode behind the published FP8 figure): tensorwide
+    E4M3 weights packed once, the activation packed per call (max, scale,
+    encode), then the FP8 GEMM. ms is the whole call; gemm_ms the GEMM kernel."""
+    from h3cli_amd.runtime import Gpu, Tensor
+    shapes = [("qkv", 5376, 21504), ("out", 7168, 5376), ("fc1", 5376, 28672), ("fc2", 14336, 5376)]
+    res = {"workload": "real-H3 block-0 projections, 8193 rows, FP8 W8A8 (tensorwide E4M3)", "rows": m, "shapes": {},
+           "published": H3_PUBLISHED["proj_8193"]}
+    total_flops, total_ms, total_gemm = 0.0, 0.0, 0.0
+    with Gpu() as gpu:
+        lib = gpu.lib
+        gpu.check(lib.h3_gpu_quant_configure(gpu.handle, 1, os.environ.get("TMPDIR", "/tmp").encode() + b"/h3-fp8",
+                                             2 * (4 * 7168 * 5376 + 3 * 14336 * 5376), 1 << 30, 0), "quant configure")
+        x = gpu.empty(m * 14336)
+        gpu.begin()
+        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, seed * 16, 1.0, m * 14336), "fill")
+        gpu.submit()
+        for i, (name, k, n) in enumerate(shapes):
+            wb = gpu.empty(n * k)
+            gpu.begin()
+            gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, wb.handle, seed * 8 + i, 0.02, n * k), "fill w")
+            gpu.submit()
+            h = lib.h3_hip_fp8_weight_from_bf16(gpu.handle, wb.handle, n, k)
+            gpu.check(h, "fp8 weight")
+            w = Tensor(gpu, h, n * k, 2)
+            gpu.tensors.append(w)
+            gpu.free(wb)
+            y = gpu.empty(m * n)
+            call = lambda: lib.h3_gpu_linear_bf16(gpu.handle, y.handle, x.handle, w.handle, None, m, k, n)
+            kt = []
+            ms, _ = time_calls(gpu, call, steps, warmup, kt)
+            flops = 2.0 * m * k * n
+            total_flops += flops
+            total_ms += ms
+            total_gemm += kt[0][0]
+            res["shapes"][name] = {"k": k, "n": n, "ms": round(ms, 4), "gemm_ms": round(kt[0][0], 4),
+                                   "tflops": round(flops / ms / 1e9, 2), "gemm_tflops": round(flops / kt[0][0] / 1e9, 2)}
+            log(f"[bench] h3 fp8 proj {name} {m}x{k}x{n}: {ms:.3f} ms per call, GEMM {kt[0][0]:.3f} ms "
+                f"({flops / kt[0][0] / 1e9:.1f} TFLOP/s)")
+            gpu.free(y)
+            gpu.free(w)
+    res["ms_total"] = round(total_ms, 4)
+    res["gemm_ms_total"] = round(total_gemm, 4)
+    res["tflops"] = round(total_flops / total_ms / 1e9, 2)
+    return res
+
+
 def h3_step_leg(steps, warmup):
     """One real-H3-geometry denoise step (include/h3_dit_synth.h
     h3_hip_dit_synth_h3): 50 blocks, 18225 video rows, hidden 5376, 56 heads,
@@ -458,7 +506,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_step")
+    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_proj_fp8,h3_step")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -542,6 +590,8 @@ def main():
         result["h3_attention"] = h3_attention_leg()
     if "h3_proj" in legs:
         result["h3_proj"] = h3_proj_leg(args.steps, args.warmup)
+    if "h3_proj_fp8" in legs:
+        result["h3_proj_fp8"] = h3_proj_fp8_leg(args.steps, args.warmup)
     if "h3_step" in legs:
         result["h3_step"] = h3_step_leg(2, 1)
     if "step" in legs:

@@ -90,6 +90,12 @@ struct h3_gpu_tensor {
     int q8;
     uint32_t q8_rows, q8_cols, q8_group;
     float *q8_scales;
+    // FP8 packed projection weight (h3_gpu_quant_load): data holds the packed
+    // descriptor (codes [quant_n, quant_k], scale at quant_scale, global slot at
+    // quant_global), in device memory or, for streamed weights, pinned host memory.
+    int quant_mode;
+    uint32_t quant_n, quant_k;
+    size_t quant_scale, quant_global;
     // Streaming fences (copy stream fills, compute stream reads).
     hipEvent_t ready, released;
     bool ready_pending, release_recorded;
@@ -106,8 +112,9 @@ struct h3_gpu {
     bool active, deferred_error;
     char error[1024];
     h3_gpu_stats stats;
-    unsigned *fault;        // device flags: [0] nonfinite attention, [1] quantizer nonfinite
+    unsigned *fault;        // device flags: [0] nonfinite attention, [1] Sage quantizer, [2] FP8 projection input
     int quant_mode;
+    struct h3_quant_state *quant;   // quant.hip: artifact cache and FP8 workspaces (mode 1)
     h3_attention_state *attention;
     h3_stream_state *streaming;
     std::mutex copy_mutex;

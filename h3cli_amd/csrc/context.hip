@@ -121,6 +121,7 @@ extern "C" void h3_gpu_free(h3_gpu *g) {
     if (g->copy) hipStreamSynchronize(g->copy);
     h3_attention_destroy(g);
     h3_streaming_destroy(g);
+    h3_quant_destroy(g);
     kernel_events_clear(g);
     delete g->kernel_events;
     if (g->fault) hipFree(g->fault);
@@ -153,7 +154,8 @@ extern "C" int h3_gpu_synchronize(h3_gpu *g) {
         ok = h3_hip_check(g, hipMemcpy(flags, g->fault, sizeof(flags), hipMemcpyDeviceToHost), "fault flags");
         if (ok && flags[0]) ok = h3_set_error(g, "nonfinite attention input or output");
         else if (ok && flags[1]) ok = h3_set_error(g, "nonfinite input encountered in Sage quantization");
-        if (flags[0] || flags[1]) {
+        else if (ok && flags[2]) ok = h3_set_error(g, "nonfinite input encountered in quantized DiT projection");
+        if (flags[0] || flags[1] || flags[2]) {
             // Sticky until cancel, like the reference's deferred faults.
             g->deferred_error = true;
         }

@@ -40,6 +40,11 @@ int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uin
                             uint32_t q_block, const h3_sol_lists *lists);
 
 // Grow-only device buffer; growing waits for queued work that may read the old one.
+// FP8 projections (quant.hip): y = FP8 GEMM of x with a packed weight; teardown.
+int h3_quant_gemm(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w, uint32_t rows,
+                  uint32_t k, uint32_t n);
+void h3_quant_destroy(h3_gpu *g);
+
 struct h3_device_buffer {
     void *ptr = nullptr;
     size_t bytes = 0;

@@ -21,6 +21,12 @@ static int linear(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const 
         !h3_require(g, out, H3_GPU_BF16, (size_t)rows * n, "linear output") ||
         (bias && !h3_require(g, bias, H3_GPU_BF16, n, "linear bias")))
         return 0;
+    if (w->quant_mode) {
+        // Reference gpu_cuda.cu:928-930: packed FP8 weights take no bias or epilogue.
+        if (bias || gelu) return h3_set_error(g, "unsupported quantized projection offset/bias/type");
+        if (out == in) return h3_set_error(g, "linear: output aliases input");
+        return h3_quant_gemm(g, out, in, w, rows, k, n);
+    }
     if (w->q8) {
         if (w->q8_rows != n || w->q8_cols != k)
             return h3_set_error(g, "linear: q8 weight is %ux%u, need %ux%u", w->q8_rows, w->q8_cols, n, k);
@@ -168,19 +174,4 @@ extern "C" h3_gpu_tensor *h3_gpu_q8_load(h3_gpu *g, const char *path, uint64_t o
     if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
     g->stats.q8_source_bytes += n * 2;
     return t;
-}
-
-extern "C" int h3_gpu_quant_configure(h3_gpu *g, int mode, const char *cache, uint64_t bf16_weights,
-                                      uint64_t activations, int force_stream) {
-    (void)cache; (void)bf16_weights; (void)activations; (void)force_stream;
-    if (!g) return 0;
-    if (mode < 0 || mode > 1) return h3_set_error(g, "quantization mode %d is unsupported on HIP (0 bf16, 1 q8)", mode);
-    g->quant_mode = mode;
-    return 1;
-}
-
-extern "C" h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *g, const char *path, uint64_t offset, uint32_t rows, uint32_t columns) {
-    if (!g) return nullptr;
-    if (g->quant_mode != 1) { h3_set_error(g, "quantized projections are not configured"); return nullptr; }
-    return h3_gpu_q8_load(g, path, offset, rows, columns);
 }

@@ -1,0 +1,692 @@
+// FP8 W8A8 DiT projections (reference src/cuda/cuda_quant.cuh): tensorwide
+// E4M3 packing of weights and activations, the packed-weight caches (metadata
+// keyed H3QMT002, and the strict content-hashed H3QWT001), and an FP8 GEMM on
+// gfx950's v_mfma_f32_32x32x64_f8f6f4 in place of cuBLASLt.
+//
+// Arithmetic contract (cuda_quant.cuh:26-49, 362-394):
+//   scale = max(max|x| / 448, 1e-20), code = E4M3(x / scale), RNE, saturating;
+//   y = bf16(sx * sw * sum_k x8[m,k] * w8[n,k]), FP32 accumulation.
+// Packed weight descriptor (src/weights/residency.c:39-51): n*k codes, the
+// 4-byte scale at the 256-aligned `scale` offset, and a 16-byte global slot
+// {scale, 1, 0, 0} at the 256-aligned `global` offset, zero elsewhere; this is
+// the artifact payload, so caches written by either build are interchangeable.
+//
+// MI355X design:
+//  * packing is HBM-bound: a max pass (16-byte loads, per-workgroup maxima),
+//    a one-workgroup finish, and an encode pass (16-byte loads, 8-byte stores);
+//  * the GEMM computes C^T = W . X^T with 256 x 256 output tiles, 8 waves (two
+//    per SIMD, 128 x 64 each), 128-byte K stages of both operands loaded
+//    global -> LDS directly (XOR-swizzled 16-byte chunks), double buffered;
+//    each K stage is two 32x32x64 FP8 MFMA steps per accumulator block, the
+//    fragments of the next step read during the current one; workgroup ids are
+//    XCD-remapped and grouped along M, as in the BF16 GEMM.
+#include "common.h"
+#include "internal.h"
+#include "sage.h"
+#include "../../include/h3_quant.h"
+#include "../../include/h3_quant_cache.h"
+#include "../../include/h3_residency.h"
+#include "../../include/h3_gpu_surface.h"
+#include "../host/sha256.h"
+#include <algorithm>
+#include <cerrno>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fcntl.h>
+#include <string>
+#include <sys/file.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <vector>
+
+struct h3_quant_state {
+    std::string cache;                 // artifact directory
+    bool verify = false;               // H3QWT001 content-hashed artifacts
+    bool streaming = false;            // packed weights stay in pinned host memory
+    h3_device_buffer activation;       // packed activation codes + maxima + global slot
+    h3_device_buffer streamed;         // device copy of a streamed packed weight
+};
+
+namespace {
+
+constexpr unsigned MAX_PARTIALS = 1024;
+constexpr unsigned FAULT_QUANT = 2;    // g->fault index: nonfinite projection input
+
+// ---------------------------------------------------------------- packing
+// Maximum |x| of BF16 values as the integer maximum of their magnitude bits
+// (equal to the float maximum for finite values); a non-finite value sets the
+// fault flag and is left out.
+__global__ __launch_bounds__(256) void fp8_amax(const uint16_t *x, size_t chunks, unsigned *partials,
+                                                unsigned *fault) {
+    unsigned best = 0;
+    bool bad = false;
+    for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (size_t)gridDim.x * 256) {
+        const u16x8 v = *reinterpret_cast<const u16x8 *>(x + c * 8);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const unsigned mag = v[j] & 0x7fffu;
+            if (mag >= 0x7f80u) bad = true;
+            else best = max(best, mag);
+        }
+    }
+    if (bad) fault[FAULT_QUANT] = 1u;
+    for (int off = 32; off; off >>= 1) best = max(best, (unsigned)__shfl_xor((int)best, off, 64));
+    __shared__ unsigned waves[4];
+    if (threadIdx.x % 64 == 0) waves[threadIdx.x / 64] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) partials[blockIdx.x] = max(max(waves[0], waves[1]), max(waves[2], waves[3]));
+}
+
+// scale = max(amax / 448, 1e-20) (IEEE division); global slot {scale, 1, 0, 0}
+// and the scale plane's single value (cuda_quant.cuh:36-39, 43).
+__global__ __launch_bounds__(256) void fp8_finish(const unsigned *partials, unsigned count, float *global,
+                                                  float *scale_slot) {
+    unsigned best = 0;
+    for (unsigned i = threadIdx.x; i < count; i += 256) best = max(best, partials[i]);
+    for (int off = 32; off; off >>= 1) best = max(best, (unsigned)__shfl_xor((int)best, off, 64));
+    __shared__ unsigned waves[4];
+    if (threadIdx.x % 64 == 0) waves[threadIdx.x / 64] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float amax = bf16_to_f32((uint16_t)max(max(waves[0], waves[1]), max(waves[2], waves[3])));
+        const float scale = fmaxf(__fdiv_rn(amax, 448.f), 1e-20f);
+        global[0] = scale; global[1] = 1.f; global[2] = 0.f; global[3] = 0.f;
+        if (scale_slot) scale_slot[0] = scale;
+    }
+}
+
+// code = E4M3(x / scale), eight values per thread.
+__global__ __launch_bounds__(256) void fp8_encode(const uint16_t *x, size_t chunks, const float *global,
+                                                  uint8_t *codes) {
+    const float scale = global[0];
+    for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (size_t)gridDim.x * 256) {
+        const u16x8 v = *reinterpret_cast<const u16x8 *>(x + c * 8);
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            lo |= (uint32_t)f32_to_e4m3(__fdiv_rn(bf16_to_f32(v[j]), scale)) << (8 * j);
+            hi |= (uint32_t)f32_to_e4m3(__fdiv_rn(bf16_to_f32(v[j + 4]), scale)) << (8 * j);
+        }
+        *reinterpret_cast<uint2 *>(codes + c * 8) = make_uint2(lo, hi);
+    }
+}
+
+unsigned pack_grid(size_t chunks) {
+    return (unsigned)std::min<size_t>(MAX_PARTIALS, std::max<size_t>(1, (chunks + 255) / 256));
+}
+
+// Packs count BF16 values (count % 8 == 0) into codes, with the global slot at
+// global and, for weights, the scale plane at scale_slot. partials: MAX_PARTIALS.
+int fp8_pack(h3_gpu *g, const uint16_t *x, size_t count, uint8_t *codes, unsigned *partials, float *global,
+             float *scale_slot) {
+    const size_t chunks = count / 8;
+    const unsigned grid = pack_grid(chunks);
+    hipLaunchKernelGGL(fp8_amax, dim3(grid), dim3(256), 0, g->compute, x, chunks, partials, g->fault);
+    hipLaunchKernelGGL(fp8_finish, dim3(1), dim3(256), 0, g->compute, partials, grid, global, scale_slot);
+    hipLaunchKernelGGL(fp8_encode, dim3(grid), dim3(256), 0, g->compute, x, chunks, global, codes);
+    return h3_launch_status(g, "FP8 packing");
+}
+
+// ---------------------------------------------------------------- GEMM
+constexpr int TM = 256, TN = 256, TK = 128;          // TK in FP8 bytes
+constexpr int ROW = TK;                              // 128 B per LDS row
+constexpr int TILE = 256 * ROW;                      // 32 KB per operand tile
+constexpr int STAGE = 2 * TILE;
+constexpr int GROUP_M = 8;
+
+__device__ inline unsigned swz(unsigned row, unsigned ch) { return ch ^ ((row >> 1) & 7); }
+
+struct Fp8Args {
+    uint16_t *y;
+    const uint8_t *x, *w;
+    const float *sx, *sw;     // device scalars: activation and weight scales
+    unsigned m, n, k;
+};
+
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+void fp8_gemm(Fp8Args a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
+    const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
+    const unsigned pid = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned band = pid / (GROUP_M * tiles_n), first_m = band * GROUP_M;
+    const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)GROUP_M);
+    const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
+    const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
+    const unsigned m0 = tm * TM, n0 = tn * TN;
+    const unsigned wm = wave / 4, wn = wave % 4;   // rows m0 + wm*128, columns n0 + wn*64
+    const unsigned ksteps = a.k / TK;
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+
+    // 256 rows x 128 B of each operand: 32 groups of 8 rows, 16 B per lane.
+    auto load = [&](unsigned kt, int stage) {
+        uint8_t *xs = lds + stage * STAGE;
+#pragma unroll
+        for (unsigned b = wave; b < 32; b += 8) {
+            const unsigned row = 8 * b + lane / 8, ph = lane % 8;
+            const unsigned gm = min(m0 + row, a.m - 1);
+            const uint8_t *xsrc = a.x + (size_t)gm * a.k + kt * TK + swz(row, ph) * 16;
+            const uint8_t *wsrc = a.w + (size_t)(n0 + row) * a.k + kt * TK + swz(row, ph) * 16;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)xsrc,
+                                             (__attribute__((address_space(3))) void *)(xs + b * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)wsrc,
+                                             (__attribute__((address_space(3))) void *)(xs + TILE + b * 1024), 16, 0, 0);
+        }
+    };
+    // MFMA step s (64 K bytes): lane half hf supplies bytes 32 hf .. 32 hf + 31,
+    // chunks 4 s + 2 hf and 4 s + 2 hf + 1 of its row.
+    auto fragment = [&](const uint8_t *tile, unsigned row, int s) -> i32x8 {
+        const unsigned c0 = 4 * s + 2 * hf;
+        const i32x4 lo = *reinterpret_cast<const i32x4 *>(tile + row * ROW + swz(row, c0) * 16);
+        const i32x4 hi = *reinterpret_cast<const i32x4 *>(tile + row * ROW + swz(row, c0 + 1) * 16);
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    load(0, 0);
+    wait_vm_loads();
+    __syncthreads();
+    for (unsigned kt = 0; kt < ksteps; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ksteps) load(kt + 1, cur ^ 1);
+        const uint8_t *xs = lds + cur * STAGE, *ws = xs + TILE;
+        i32x8 wf[2][2], xf[2][4];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) wf[s][i] = fragment(ws, wn * 64 + i * 32 + n32, s);
+#pragma unroll
+            for (int j = 0; j < 4; j++) xf[s][j] = fragment(xs, wm * 128 + j * 32 + n32, s);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[s][i], xf[s][j], acc[i][j], 0, 0,
+                                                                                0, 0, 0, 0);
+        wait_vm_loads();
+        __syncthreads();
+    }
+
+    const float scale = a.sx[0] * a.sw[0];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const unsigned row = m0 + wm * 128 + j * 32 + n32;
+        if (row >= a.m) continue;
+        uint16_t *dst = a.y + (size_t)row * a.n;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const unsigned col = n0 + wn * 64 + i * 32 + g4 * 8 + hf * 4;
+                u16x4 out;
+#pragma unroll
+                for (int e = 0; e < 4; e++) out[e] = f32_to_bf16(acc[i][j][g4 * 4 + e] * scale);
+                *reinterpret_cast<u16x4 *>(dst + col) = out;
+            }
+    }
+}
+
+// E4M3 value of a code (0x7f / 0xff are NaN; packed codes never hold them).
+__device__ inline float e4m3_value(uint8_t c) {
+    const unsigned e = (c >> 3) & 15u, m = c & 7u;
+    const float mag = e ? __builtin_ldexpf(1.f + m * 0.125f, (int)e - 7) : m * 0.001953125f;
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// Shapes the tiled kernel does not take (N not a multiple of 256): one thread
+// per output, FP32 accumulation in K order.
+__global__ __launch_bounds__(256) void fp8_gemm_small(Fp8Args a) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)a.m * a.n) return;
+    const unsigned row = idx / a.n, col = idx % a.n;
+    const uint8_t *xr = a.x + (size_t)row * a.k, *wr = a.w + (size_t)col * a.k;
+    float acc = 0.f;
+    for (unsigned i = 0; i < a.k; i++) acc = fmaf(e4m3_value(xr[i]), e4m3_value(wr[i]), acc);
+    a.y[idx] = f32_to_bf16(acc * (a.sx[0] * a.sw[0]));
+}
+
+int launch_gemm(h3_gpu *g, const Fp8Args &a) {
+    if (a.n % TN == 0) {
+        static bool configured = false;
+        if (!configured) {
+            if (!h3_hip_check(g, hipFuncSetAttribute((const void *)fp8_gemm, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     2 * STAGE), "FP8 GEMM shared memory"))
+                return 0;
+            configured = true;
+        }
+        const unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
+        hipEvent_t timing = h3_kernel_timing_begin(g);
+        hipLaunchKernelGGL(fp8_gemm, dim3(tiles), dim3(512), 2 * STAGE, g->compute, a);
+        h3_kernel_timing_end(g, timing);
+    } else {
+        const size_t total = (size_t)a.m * a.n;
+        hipLaunchKernelGGL(fp8_gemm_small, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, a);
+    }
+    return h3_launch_status(g, "native fp8 projection");
+}
+
+// ---------------------------------------------------------------- host helpers
+std::string hex32(const unsigned char d[32]) {
+    static const char digits[] = "0123456789abcdef";
+    std::string s(64, '0');
+    for (int i = 0; i < 32; i++) { s[2 * i] = digits[d[i] >> 4]; s[2 * i + 1] = digits[d[i] & 15]; }
+    return s;
+}
+
+void sha256_of(const void *data, size_t bytes, unsigned char out[32]) {
+    h3hip_sha256 s;
+    h3hip_sha256_init(&s);
+    h3hip_sha256_update(&s, data, bytes);
+    h3hip_sha256_final(&s, out);
+}
+
+void put_le(unsigned char *p, uint64_t v, unsigned n) { for (unsigned i = 0; i < n; i++) p[i] = (unsigned char)(v >> (8 * i)); }
+uint64_t get_le(const unsigned char *p, unsigned n) {
+    uint64_t v = 0;
+    for (unsigned i = 0; i < n; i++) v |= (uint64_t)p[i] << (8 * i);
+    return v;
+}
+
+bool file_io(int fd, void *data, size_t bytes, bool writing) {
+    auto *p = (unsigned char *)data;
+    while (bytes) {
+        ssize_t n = writing ? ::write(fd, p, bytes) : ::read(fd, p, bytes);
+        if (n < 0 && errno == EINTR) continue;
+        if (n <= 0) return false;
+        p += n; bytes -= (size_t)n;
+    }
+    return true;
+}
+
+bool same_source(const char *path, const struct stat &before) {
+    struct stat now;
+    return stat(path, &now) == 0 && before.st_dev == now.st_dev && before.st_ino == now.st_ino &&
+           before.st_size == now.st_size && before.st_mtim.tv_sec == now.st_mtim.tv_sec &&
+           before.st_mtim.tv_nsec == now.st_mtim.tv_nsec && before.st_ctim.tv_sec == now.st_ctim.tv_sec &&
+           before.st_ctim.tv_nsec == now.st_ctim.tv_nsec;
+}
+
+int make_dirs(const std::string &path) {
+    if (path.empty()) return 0;
+    for (size_t i = 1; i <= path.size(); i++)
+        if (i == path.size() || path[i] == '/') {
+            const std::string part = path.substr(0, i);
+            if (mkdir(part.c_str(), 0755) != 0 && errno != EEXIST) return 0;
+            struct stat st;
+            if (stat(part.c_str(), &st) != 0 || !S_ISDIR(st.st_mode)) return 0;
+        }
+    return 1;
+}
+
+// A read-only mapping of [offset, offset + bytes) of a file.
+struct Mapping {
+    void *base = MAP_FAILED;
+    size_t length = 0, delta = 0;
+    const uint16_t *data() const { return (const uint16_t *)((const char *)base + delta); }
+    ~Mapping() { if (base != MAP_FAILED) munmap(base, length); }
+    bool map(int fd, uint64_t offset, size_t bytes) {
+        const size_t page = (size_t)sysconf(_SC_PAGESIZE);
+        delta = offset % page;
+        length = bytes + delta;
+        base = mmap(nullptr, length, PROT_READ, MAP_PRIVATE, fd, (off_t)(offset - delta));
+        return base != MAP_FAILED;
+    }
+};
+
+// Packs n x k BF16 weights (host) into the descriptor layout on the device and
+// copies it back: packed receives `bytes` bytes.
+int prepare_packed(h3_gpu *g, const uint16_t *source, uint32_t n, uint32_t k, size_t bytes, size_t scale,
+                   size_t global, unsigned char *packed) {
+    const size_t count = (size_t)n * k, partial_bytes = MAX_PARTIALS * 4;
+    void *staging = nullptr, *device = nullptr, *partials = nullptr;
+    int ok = h3_hip_check(g, hipMalloc(&staging, count * 2), "quantization source upload") &&
+             h3_hip_check(g, hipMalloc(&device, bytes), "packed weight") &&
+             h3_hip_check(g, hipMalloc(&partials, partial_bytes), "packed weight maxima") &&
+             h3_hip_check(g, hipMemcpyAsync(staging, source, count * 2, hipMemcpyHostToDevice, g->compute),
+                          "quantization source upload") &&
+             h3_hip_check(g, hipMemsetAsync(device, 0, bytes, g->compute), "packed weight initialization") &&
+             fp8_pack(g, (const uint16_t *)staging, count, (uint8_t *)device, (unsigned *)partials,
+                      (float *)((char *)device + global), (float *)((char *)device + scale)) &&
+             h3_hip_check(g, hipStreamSynchronize(g->compute), "prepare quantized weight") &&
+             h3_hip_check(g, hipMemcpy(packed, device, bytes, hipMemcpyDeviceToHost), "download packed artifact");
+    if (staging) hipFree(staging);
+    if (device) hipFree(device);
+    if (partials) hipFree(partials);
+    g->stats.h2d_bytes += count * 2;
+    g->stats.d2h_bytes += bytes;
+    // A non-finite weight raised the quantizer fault: report it now.
+    return ok && h3_gpu_synchronize(g);
+}
+
+h3_gpu_tensor *finish_weight(h3_gpu *g, std::vector<unsigned char> &packed, uint32_t n, uint32_t k, size_t scale,
+                             size_t global, bool hit) {
+    float gs, ss;
+    memcpy(&gs, packed.data() + global, 4);
+    if (!std::isfinite(gs) || gs <= 0) { h3_set_error(g, "invalid quantized weight global scale"); return nullptr; }
+    memcpy(&ss, packed.data() + scale, 4);
+    if (ss != gs) { h3_set_error(g, "invalid FP8 weight scale"); return nullptr; }
+    for (size_t i = 0; i < (size_t)n * k; i++)
+        if ((packed[i] & 0x7f) == 0x7f) { h3_set_error(g, "nonfinite FP8 weight"); return nullptr; }
+    const h3_gpu_storage storage = g->quant->streaming ? H3_GPU_HOST_PINNED : H3_GPU_DEVICE_ONLY;
+    h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, packed.size(), H3_GPU_I8, storage);
+    if (!t) return nullptr;
+    bool ok;
+    if (storage == H3_GPU_DEVICE_ONLY) {
+        ok = h3_hip_check(g, hipMemcpy(t->data, packed.data(), packed.size(), hipMemcpyHostToDevice), "packed weight upload");
+        g->stats.h2d_bytes += packed.size();
+    } else {
+        memcpy(t->data, packed.data(), packed.size());
+        ok = true;
+    }
+    if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
+    t->elements = (size_t)n * k;
+    t->quant_mode = H3_QUANT_FP8; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    if (hit) g->stats.quant_cache_hits++; else g->stats.quant_cache_misses++;
+    return t;
+}
+
+// Strict content-hashed artifacts (reference cuda_quant.cuh:169-248, selected by
+// H3_QUANT_VERIFY=1): <cache>/v<recipe>-fp8-<n>x<k>-<sha256(source)>.h3q with a
+// 128-byte H3QWT001 header: recipe u32 @8, mode u32 @12, n u32 @16, k u32 @20,
+// bytes u64 @24, scale @32, global @40, source SHA-256 @48, payload SHA-256 @80,
+// zero @112-127.
+h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
+                           size_t scale, size_t global) {
+    const size_t source_bytes = (size_t)n * k * 2;
+    int fd = open(path, O_RDONLY);
+    struct stat st;
+    if (fd < 0 || fstat(fd, &st) != 0 || offset > (uint64_t)st.st_size || source_bytes > (uint64_t)st.st_size - offset) {
+        if (fd >= 0) close(fd);
+        h3_set_error(g, "invalid quantized source range: %s", path);
+        return nullptr;
+    }
+    const struct stat source_status = st;
+    Mapping map;
+    const bool mapped = map.map(fd, offset, source_bytes);
+    close(fd);
+    if (!mapped) { h3_set_error(g, "cannot map quantized source: %s", strerror(errno)); return nullptr; }
+    unsigned char source_hash[32];
+    sha256_of(map.data(), source_bytes, source_hash);
+    const std::string artifact = g->quant->cache + "/v" + std::to_string(H3_QUANT_VERSION) + "-" +
+                                 h3_quant_name(H3_QUANT_FP8) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
+                                 hex32(source_hash) + ".h3q";
+    int lock = open((artifact + ".lock").c_str(), O_CREAT | O_RDWR, 0600);
+    if (lock < 0 || flock(lock, LOCK_EX) != 0) {
+        if (lock >= 0) close(lock);
+        h3_set_error(g, "cannot lock quantization artifact: %s", strerror(errno));
+        return nullptr;
+    }
+    std::vector<unsigned char> packed(bytes);
+    unsigned char header[128];
+    bool ok = true, hit = false;
+    fd = open(artifact.c_str(), O_RDONLY);
+    if (fd >= 0) {
+        ok = fstat(fd, &st) == 0 && (uint64_t)st.st_size == 128 + bytes && file_io(fd, header, 128, false) &&
+             memcmp(header, "H3QWT001", 8) == 0 && get_le(header + 8, 4) == H3_QUANT_VERSION &&
+             get_le(header + 12, 4) == H3_QUANT_FP8 && get_le(header + 16, 4) == n && get_le(header + 20, 4) == k &&
+             get_le(header + 24, 8) == bytes && get_le(header + 32, 8) == scale && get_le(header + 40, 8) == global &&
+             memcmp(header + 48, source_hash, 32) == 0 && file_io(fd, packed.data(), bytes, false);
+        close(fd);
+        if (ok) {
+            unsigned char digest[32];
+            sha256_of(packed.data(), bytes, digest);
+            ok = memcmp(header + 80, digest, 32) == 0;
+        }
+        for (unsigned i = 112; ok && i < 128; i++) ok = header[i] == 0;
+        if (!ok) h3_set_error(g, "corrupt/incompatible quantization artifact %s; remove it and prepare again", artifact.c_str());
+        hit = ok;
+    } else if (errno != ENOENT) {
+        ok = false;
+        h3_set_error(g, "cannot read quantization artifact: %s", strerror(errno));
+    }
+    if (ok && !hit) {
+        ok = prepare_packed(g, map.data(), n, k, bytes, scale, global, packed.data());
+        if (ok && !same_source(path, source_status)) {
+            ok = false;
+            h3_set_error(g, "source weight changed during quantization; retry with immutable model files");
+        }
+        if (ok) {
+            memset(header, 0, sizeof(header));
+            memcpy(header, "H3QWT001", 8);
+            put_le(header + 8, H3_QUANT_VERSION, 4); put_le(header + 12, H3_QUANT_FP8, 4);
+            put_le(header + 16, n, 4); put_le(header + 20, k, 4);
+            put_le(header + 24, bytes, 8); put_le(header + 32, scale, 8); put_le(header + 40, global, 8);
+            memcpy(header + 48, source_hash, 32);
+            sha256_of(packed.data(), bytes, header + 80);
+            std::string staging = artifact + ".tmp.XXXXXX";
+            std::vector<char> name(staging.begin(), staging.end());
+            name.push_back(0);
+            fd = mkstemp(name.data());
+            ok = fd >= 0;
+            if (ok) {
+                ok = file_io(fd, header, 128, true) && file_io(fd, packed.data(), bytes, true) && fsync(fd) == 0;
+                if (close(fd) != 0) ok = false;
+            }
+            if (ok) ok = rename(name.data(), artifact.c_str()) == 0;
+            if (!ok) {
+                unlink(name.data());
+                h3_set_error(g, "cannot commit quantization artifact: %s", strerror(errno));
+            }
+        }
+    }
+    flock(lock, LOCK_UN);
+    close(lock);
+    if (!ok) return nullptr;
+    if (!same_source(path, source_status)) {
+        h3_set_error(g, "source weight changed during artifact verification; retry with immutable model files");
+        return nullptr;
+    }
+    return finish_weight(g, packed, n, k, scale, global, hit);
+}
+
+// Metadata-keyed artifacts (reference cuda_quant.cuh:292-330): the source is
+// only opened on a miss.
+h3_gpu_tensor *load_metadata(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
+                             size_t scale, size_t global) {
+    h3_quant_cache *cache = h3_quant_cache_open(g->quant->cache.c_str(), path, offset, n, k, H3_QUANT_FP8, bytes,
+                                                scale, global, g->error, sizeof(g->error));
+    if (!cache) return nullptr;
+    std::vector<unsigned char> packed(bytes);
+    const int status = h3_quant_cache_read(cache, packed.data(), g->error, sizeof(g->error));
+    bool ok = status >= 0;
+    if (ok && status == 0) {
+        const size_t source_bytes = (size_t)n * k * 2;
+        int fd = open(cache->source, O_RDONLY);
+        struct stat st;
+        Mapping map;
+        bool mapped = fd >= 0 && fstat(fd, &st) == 0 && st.st_dev == cache->stamp.st_dev &&
+                      st.st_ino == cache->stamp.st_ino && st.st_size == cache->stamp.st_size &&
+                      h3_quant_cache_unchanged(cache, g->error, sizeof(g->error)) && map.map(fd, offset, source_bytes);
+        if (fd >= 0) close(fd);
+        if (!mapped) {
+            h3_set_error(g, "cannot map metadata-cache source: %s", path);
+            ok = false;
+        } else {
+            ok = prepare_packed(g, map.data(), n, k, bytes, scale, global, packed.data()) &&
+                 h3_quant_cache_write(cache, packed.data(), g->error, sizeof(g->error));
+        }
+    }
+    if (ok) ok = h3_quant_cache_unchanged(cache, g->error, sizeof(g->error));
+    h3_quant_cache_close(cache);
+    return ok ? finish_weight(g, packed, n, k, scale, global, status == 1) : nullptr;
+}
+
+}  // namespace
+
+void h3_quant_destroy(h3_gpu *g) {
+    if (!g->quant) return;
+    h3_buffer_free(&g->quant->activation);
+    h3_buffer_free(&g->quant->streamed);
+    delete g->quant;
+    g->quant = nullptr;
+}
+
+extern "C" int h3_quant_preflight(int mode, char *error, size_t size) {
+    if (!mode) return 1;
+    hipDeviceProp_t prop;
+    int device = 0;
+    if (mode < 1 || mode > 2 || hipGetDevice(&device) != hipSuccess ||
+        hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        if (error && size) snprintf(error, size, "cannot query HIP quantization device");
+        return 0;
+    }
+    if (mode == H3_QUANT_NVFP4) {
+        if (error && size) snprintf(error, size, "cuda-denoise-quant nvfp4 is not available on the HIP backend (fp8 is)");
+        return 0;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (error && size)
+            snprintf(error, size, "cuda-denoise-quant fp8 requires gfx950 FP8 matrix cores (MI355X) (device %s)",
+                     prop.gcnArchName);
+        return 0;
+    }
+    return 1;
+}
+
+// gpu.h:44-45 (reference cuda_quant.cuh:120-162).
+extern "C" int h3_gpu_quant_configure(h3_gpu *g, int mode, const char *cache, uint64_t weights, uint64_t activations,
+                                      int force_stream) {
+    if (!g || !h3_quant_preflight(mode, g->error, sizeof(g->error))) return 0;
+    if (!mode) return 1;      // BF16 projections never touch packed-weight caches
+    if (g->quant_mode) return h3_set_error(g, "quantized GPU context already configured");
+    const char *home = getenv("HOME");
+    std::string dir = cache ? cache : std::string(home ? home : ".") + "/.cache/h3/denoise-quant";
+    if (!make_dirs(dir)) return h3_set_error(g, "cannot create quantization cache %s: %s", dir.c_str(), strerror(errno));
+    // Admission counts whole H3 blocks: the BF16 bytes of the four projections
+    // (qkv 3 x 7168 x 5376, out 5376 x 7168, fc1 2 x 14336 x 5376, fc2 5376 x 14336).
+    const uint64_t bf16_block = 2ull * (4ull * 7168 * 5376 + 3ull * 14336 * 5376);
+    if (weights % bf16_block) return h3_set_error(g, "invalid packed DiT core geometry");
+    const uint32_t shapes[4][2] = {{3 * 7168, 5376}, {5376, 7168}, {2 * 14336, 5376}, {5376, 14336}};
+    uint64_t packed_block = 0;
+    for (auto &s : shapes) {
+        uint64_t sc, gl, by;
+        h3_weight_packed_size(s[0], s[1], mode, &sc, &gl, &by);
+        packed_block += by;
+    }
+    const uint64_t packed = weights / bf16_block * packed_block;
+    h3_weight_options o;
+    if (!h3_weight_options_read(&o, 0, g->error, sizeof(g->error))) return 0;
+    if (force_stream && o.mode == H3_WEIGHTS_RESIDENT)
+        return h3_set_error(g, "--ssd-streaming conflicts with CUDA resident weight mode");
+    const int stream = h3_gpu_plan_weights(g, packed + (1ull << 30), activations + (2ull << 30));
+    if (stream < 0) return 0;
+    g->quant = new (std::nothrow) h3_quant_state();
+    if (!g->quant) return h3_set_error(g, "quantization: out of host memory");
+    g->quant->cache = dir;
+    g->quant->verify = h3_quant_verify() != 0;
+    g->quant->streaming = stream != 0 || force_stream;
+    g->quant_mode = mode;
+    return 1;
+}
+
+// gpu.h:46-47 (reference cuda_quant.cuh:249-330): a packed FP8 weight from
+// rows x columns BF16 values at offset of a file, through the artifact cache.
+extern "C" h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k) {
+    if (!g) return nullptr;
+    if (!g->quant_mode || !n || !k || n % 128 || k % 128 || (uint64_t)n * k > UINT32_MAX) {
+        h3_set_error(g, "quantized weight shape must be nonzero and a multiple of 128");
+        return nullptr;
+    }
+    if (!path) { h3_set_error(g, "invalid quantized source range: (null)"); return nullptr; }
+    uint64_t scale, global, bytes;
+    h3_weight_packed_size(n, k, g->quant_mode, &scale, &global, &bytes);
+    return g->quant->verify ? load_strict(g, path, offset, n, k, bytes, scale, global)
+                            : load_metadata(g, path, offset, n, k, bytes, scale, global);
+}
+
+// y[rows, n] = FP8 projection of x[rows, k] with a packed weight (reference
+// quant_gemm, cuda_quant.cuh:339-398): the activation is packed per call with
+// its own tensorwide scale.
+int h3_quant_gemm(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w, uint32_t rows,
+                  uint32_t k, uint32_t n) {
+    if (!g->quant || w->quant_k != k || w->quant_n != n || !rows)
+        return h3_set_error(g, "quantized projection %ux%ux%u does not match its %ux%u weight", rows, n, k, w->quant_n,
+                            w->quant_k);
+    const size_t count = (size_t)rows * k;
+    const size_t codes = (count + 255) / 256 * 256;
+    if (!h3_buffer_reserve(g, &g->quant->activation, codes + MAX_PARTIALS * 4 + 16, "quantized activation"))
+        return 0;
+    auto *base = (uint8_t *)g->quant->activation.ptr;
+    auto *partials = (unsigned *)(base + codes);
+    auto *global = (float *)(base + codes + MAX_PARTIALS * 4);
+    const uint8_t *weight = (const uint8_t *)w->data;
+    if (w->storage != H3_GPU_DEVICE_ONLY) {
+        if (!h3_buffer_reserve(g, &g->quant->streamed, w->bytes, "packed weight stream") ||
+            !h3_hip_check(g, hipMemcpyAsync(g->quant->streamed.ptr, w->data, w->bytes, hipMemcpyHostToDevice, g->compute),
+                          "packed weight stream"))
+            return 0;
+        g->stats.h2d_bytes += w->bytes;
+        g->stats.streamed_bytes += w->bytes;
+        weight = (const uint8_t *)g->quant->streamed.ptr;
+    }
+    if (!fp8_pack(g, (const uint16_t *)in->data, count, base, partials, global, nullptr)) return 0;
+    Fp8Args a;
+    a.y = (uint16_t *)out->data; a.x = base; a.w = weight;
+    a.sx = global; a.sw = (const float *)(weight + w->quant_scale);
+    a.m = rows; a.n = n; a.k = k;
+    if (!launch_gemm(g, a)) return 0;
+    g->stats.quant_projection_dispatches++;
+    g->stats.linear_dispatches++;
+    return 1;
+}
+
+// A resident packed FP8 weight from n x k BF16 device values (the descriptor
+// h3_gpu_quant_load builds, without a file or an artifact): synthetic models
+// and benchmarks. Needs h3_gpu_quant_configure(mode 1).
+extern "C" h3_gpu_tensor *h3_hip_fp8_weight_from_bf16(h3_gpu *g, const h3_gpu_tensor *w, uint32_t n, uint32_t k) {
+    if (!g) return nullptr;
+    if (g->quant_mode != H3_QUANT_FP8 || !n || !k || n % 128 || k % 128 || (uint64_t)n * k > UINT32_MAX) {
+        h3_set_error(g, "quantized weight shape must be nonzero and a multiple of 128");
+        return nullptr;
+    }
+    if (!h3_require(g, w, H3_GPU_BF16, (size_t)n * k, "FP8 weight source")) return nullptr;
+    uint64_t scale, global, bytes;
+    h3_weight_packed_size(n, k, H3_QUANT_FP8, &scale, &global, &bytes);
+    h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, bytes, H3_GPU_I8, H3_GPU_DEVICE_ONLY);
+    if (!t) return nullptr;
+    void *partials = nullptr;
+    int ok = h3_hip_check(g, hipMalloc(&partials, MAX_PARTIALS * 4), "FP8 weight maxima") &&
+             h3_hip_check(g, hipMemsetAsync(t->data, 0, bytes, g->compute), "packed weight initialization") &&
+             fp8_pack(g, (const uint16_t *)w->data, (size_t)n * k, (uint8_t *)t->data, (unsigned *)partials,
+                      (float *)((char *)t->data + global), (float *)((char *)t->data + scale)) &&
+             h3_hip_check(g, hipStreamSynchronize(g->compute), "FP8 weight");
+    if (partials) hipFree(partials);
+    if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
+    t->elements = (size_t)n * k;
+    t->quant_mode = H3_QUANT_FP8; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    return t;
+}
+
+// Test entry: SHA-256 of a buffer with the library's own digest.
+extern "C" int h3_hip_sha256(const void *data, size_t bytes, uint8_t digest[32]) {
+    if ((!data && bytes) || !digest) return 0;
+    sha256_of(data, bytes, digest);
+    return 1;
+}
+
+// Test entry: FP8-pack count BF16 device values (count % 8 == 0) into codes
+// (count bytes) and the global slot (4 floats), as a projection input is packed.
+extern "C" int h3_hip_fp8_pack(h3_gpu *g, const h3_gpu_tensor *x, h3_gpu_tensor *codes, h3_gpu_tensor *global,
+                               size_t count) {
+    if (!g || !x || !codes || !global) return 0;
+    if (!count || count % 8) return h3_set_error(g, "FP8 pack: count must be a positive multiple of 8");
+    if (!h3_require(g, x, H3_GPU_BF16, count, "FP8 pack input") || codes->bytes < count || global->bytes < 16)
+        return h3_set_error(g, "FP8 pack: tensors too small");
+    void *partials = nullptr;
+    int ok = h3_hip_check(g, hipMalloc(&partials, MAX_PARTIALS * 4), "FP8 pack maxima") &&
+             fp8_pack(g, (const uint16_t *)x->data, count, (uint8_t *)codes->data, (unsigned *)partials,
+                      (float *)global->data, nullptr) &&
+             h3_hip_check(g, hipStreamSynchronize(g->compute), "FP8 pack");
+    if (partials) hipFree(partials);
+    return ok;
+}

@@ -120,3 +120,23 @@ WEAK int h3_weight_plan_build(h3_weight_plan *p, h3_weight_options o, uint64_t m
         if (mask & (UINT64_C(1) << i)) { p->resident_mask |= UINT64_C(1) << i; keep--; }
     return 1;
 }
+
+/* Packed projection descriptor (reference residency.c:39-51): the payload
+ * (rows x columns FP8 bytes, or half that for NVFP4), then at `scale` (next
+ * 256-byte boundary) the scale plane (4 bytes for FP8; for NVFP4 one E4M3 byte
+ * per 16 columns, rows padded to 128 and block columns to 4), then at `global`
+ * (next 256-byte boundary) 16 bytes of global scale; bytes = global + 16. */
+WEAK int h3_weight_packed_size(uint32_t rows, uint32_t columns, int mode, uint64_t *scale, uint64_t *global,
+                               uint64_t *bytes) {
+    uint64_t payload, plane, end;
+    if (!rows || !columns || (mode != 1 && mode != 2) || !scale || !global || !bytes || (mode == 2 && columns % 16) ||
+        !mul_u64(rows, columns, &payload))
+        return 0;
+    if (mode == 2) payload /= 2;
+    if (!add_u64(payload, 255, &end)) return 0;
+    *scale = end / 256 * 256;
+    plane = mode == 1 ? 4 : ((uint64_t)rows + 127) / 128 * 128 * (((uint64_t)columns / 16 + 3) / 4 * 4);
+    if (!add_u64(*scale, plane, &end) || !add_u64(end, 255, &end)) return 0;
+    *global = end / 256 * 256;
+    return add_u64(*global, 16, bytes);
+}

@@ -93,6 +93,20 @@ int h3_hip_dit_sol_force_exact(h3_gpu *gpu, int on);
  * calls. count must be 9. Waits for the stream if calls are not yet counted. */
 int h3_hip_sol_counters(h3_gpu *gpu, uint64_t *out, size_t count);
 
+/* FP8 projections (quant.hip). SHA-256 (FIPS 180-4) of a buffer with the
+ * library's own digest, the one its packed-weight caches key and verify with. */
+int h3_hip_sha256(const void *data, size_t bytes, uint8_t digest[32]);
+/* Tensorwide E4M3 packing of count BF16 device values (count a positive
+ * multiple of 8), as a projection input is packed per call
+ * (reference src/cuda/cuda_quant.cuh:26-49): codes (>= count bytes) and the
+ * 16-byte global slot {scale, 1, 0, 0}. Waits for the stream. */
+int h3_hip_fp8_pack(h3_gpu *gpu, const h3_gpu_tensor *x, h3_gpu_tensor *codes, h3_gpu_tensor *global,
+                    size_t count);
+/* A resident packed FP8 weight (the h3_gpu_quant_load descriptor) from n x k
+ * BF16 device values, without a file or artifact, for synthetic models and
+ * benchmarks. Requires h3_gpu_quant_configure(mode 1); n, k multiples of 128. */
+h3_gpu_tensor *h3_hip_fp8_weight_from_bf16(h3_gpu *gpu, const h3_gpu_tensor *w, uint32_t n, uint32_t k);
+
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded
  * to a multiple of 64, padded rows zero):

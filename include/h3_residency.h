@@ -33,6 +33,11 @@ int h3_weight_options_equal(const h3_weight_options *a, const h3_weight_options 
 int h3_weight_plan_build(h3_weight_plan *out, h3_weight_options options, uint64_t active_mask, uint64_t block_bytes,
                          uint64_t available, uint64_t live, uint64_t future, uint64_t reserve, char *error, size_t size);
 int h3_weight_retry_cap(unsigned count);                                              /* residency.h:30 */
+/* residency.h:31-33: packed projection descriptor sizes (payload, 256-aligned
+ * scale plane at *scale, 16-byte global slot at *global; *bytes in total).
+ * mode 1 FP8, 2 NVFP4. */
+int h3_weight_packed_size(uint32_t rows, uint32_t columns, int mode, uint64_t *scale, uint64_t *global,
+                          uint64_t *bytes);
 #ifdef __cplusplus
 }
 #endif

@@ -122,4 +122,9 @@ void oracle_xorshift_bf16(uint16_t *out, size_t count, uint32_t *seed);
 void oracle_xorshift_native_bf16(uint16_t *out, size_t count, uint32_t *state);
 
 int oracle_threads(void);
+
+/* quant.c: FP8 W8A8 projection (cuda_quant.cuh:26-104, 339-398) */
+int oracle_fp8_pack(uint8_t *codes, float *scale_out, const uint16_t *x, size_t count, size_t padded_count);
+void oracle_fp8_gemm(uint16_t *y, const uint8_t *x8, float sx, const uint8_t *w8, float sw, unsigned m, unsigned n,
+                     unsigned k);
 #endif

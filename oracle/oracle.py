@@ -357,3 +357,28 @@ def sol_attention(q, k, v, kc, vc, routes, seq, heads, qblock, scale, rows=None)
                                 _ptr(_u16(vc)), _ptr(np.ascontiguousarray(routes, np.uint8)), seq, heads, qblock,
                                 scale, r0, r1)
     return out
+
+
+def fp8_pack(x, count=None, padded=None):
+    """Tensorwide E4M3 packing (cuda_quant.cuh:26-49). Returns (codes u8
+    [padded], scale f32, nonfinite)."""
+    x = _u16(x).reshape(-1)
+    count = x.size if count is None else count
+    padded = count if padded is None else padded
+    codes = np.zeros(padded, np.uint8)
+    scale = np.zeros(1, np.float32)
+    lib = load()
+    lib.oracle_fp8_pack.restype = C.c_int
+    lib.oracle_fp8_pack.argtypes = [_p, _p, _p, C.c_size_t, C.c_size_t]
+    bad = lib.oracle_fp8_pack(_ptr(codes), _ptr(scale), _ptr(x), count, padded)
+    return codes, np.float32(scale[0]), bool(bad)
+
+
+def fp8_gemm(x8, sx, w8, sw, m, n, k):
+    """y [m, n] BF16 bits = bf16(sx * sw * sum x8 . w8^T) (cuda_quant.cuh:362-394)."""
+    y = np.zeros(m * n, np.uint16)
+    lib = load()
+    lib.oracle_fp8_gemm.argtypes = [_p, _p, C.c_float, _p, C.c_float, _u, _u, _u]
+    lib.oracle_fp8_gemm(_ptr(y), _ptr(np.ascontiguousarray(x8, np.uint8)), float(sx),
+                        _ptr(np.ascontiguousarray(w8, np.uint8)), float(sw), m, n, k)
+    return y.reshape(m, n)
