@@ -98,19 +98,23 @@ __global__ __launch_bounds__(256) void fp8_finish(const unsigned *partials, unsi
     }
 }
 
-// code = E4M3(x / scale), eight values per thread.
+// code = E4M3(x / scale), eight values per thread. The quotient is the IEEE
+// one; the encode is v_cvt_pk_fp8_f32 (OCP E4M3, round to nearest even). Its
+// saturation differs from the reference's only above 464, and |x| / scale <=
+// amax / RN(amax / 448) < 449 here (or x / 1e-20 < 448 when the floor applies).
 __global__ __launch_bounds__(256) void fp8_encode(const uint16_t *x, size_t chunks, const float *global,
                                                   uint8_t *codes) {
     const float scale = global[0];
     for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (size_t)gridDim.x * 256) {
         const u16x8 v = *reinterpret_cast<const u16x8 *>(x + c * 8);
-        uint32_t lo = 0, hi = 0;
+        float q[8];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            lo |= (uint32_t)f32_to_e4m3(__fdiv_rn(bf16_to_f32(v[j]), scale)) << (8 * j);
-            hi |= (uint32_t)f32_to_e4m3(__fdiv_rn(bf16_to_f32(v[j + 4]), scale)) << (8 * j);
-        }
-        *reinterpret_cast<uint2 *>(codes + c * 8) = make_uint2(lo, hi);
+        for (int j = 0; j < 8; j++) q[j] = __fdiv_rn(bf16_to_f32(v[j]), scale);
+        int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+        int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+        *reinterpret_cast<uint2 *>(codes + c * 8) = make_uint2((unsigned)lo, (unsigned)hi);
     }
 }
 
@@ -150,7 +154,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
 void fp8_gemm(Fp8Args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
-    const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
+    const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = (a.n + TN - 1) / TN;
     const unsigned pid = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned band = pid / (GROUP_M * tiles_n), first_m = band * GROUP_M;
     const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)GROUP_M);
@@ -174,7 +178,7 @@ void fp8_gemm(Fp8Args a) {
             const unsigned row = 8 * b + lane / 8, ph = lane % 8;
             const unsigned gm = min(m0 + row, a.m - 1);
             const uint8_t *xsrc = a.x + (size_t)gm * a.k + kt * TK + swz(row, ph) * 16;
-            const uint8_t *wsrc = a.w + (size_t)(n0 + row) * a.k + kt * TK + swz(row, ph) * 16;
+            const uint8_t *wsrc = a.w + (size_t)min(n0 + row, a.n - 1) * a.k + kt * TK + swz(row, ph) * 16;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)xsrc,
                                              (__attribute__((address_space(3))) void *)(xs + b * 1024), 16, 0, 0);
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)wsrc,
@@ -228,6 +232,7 @@ void fp8_gemm(Fp8Args a) {
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
                 const unsigned col = n0 + wn * 64 + i * 32 + g4 * 8 + hf * 4;
+                if (col >= a.n) continue;     // N is a multiple of 128: the last tile may be half full
                 u16x4 out;
 #pragma unroll
                 for (int e = 0; e < 4; e++) out[e] = f32_to_bf16(acc[i][j][g4 * 4 + e] * scale);
@@ -236,42 +241,19 @@ void fp8_gemm(Fp8Args a) {
     }
 }
 
-// E4M3 value of a code (0x7f / 0xff are NaN; packed codes never hold them).
-__device__ inline float e4m3_value(uint8_t c) {
-    const unsigned e = (c >> 3) & 15u, m = c & 7u;
-    const float mag = e ? __builtin_ldexpf(1.f + m * 0.125f, (int)e - 7) : m * 0.001953125f;
-    return (c & 0x80u) ? -mag : mag;
-}
-
-// Shapes the tiled kernel does not take (N not a multiple of 256): one thread
-// per output, FP32 accumulation in K order.
-__global__ __launch_bounds__(256) void fp8_gemm_small(Fp8Args a) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)a.m * a.n) return;
-    const unsigned row = idx / a.n, col = idx % a.n;
-    const uint8_t *xr = a.x + (size_t)row * a.k, *wr = a.w + (size_t)col * a.k;
-    float acc = 0.f;
-    for (unsigned i = 0; i < a.k; i++) acc = fmaf(e4m3_value(xr[i]), e4m3_value(wr[i]), acc);
-    a.y[idx] = f32_to_bf16(acc * (a.sx[0] * a.sw[0]));
-}
-
+// Packed weights have N and K multiples of 128 (h3_gpu_quant_load); any M.
 int launch_gemm(h3_gpu *g, const Fp8Args &a) {
-    if (a.n % TN == 0) {
-        static bool configured = false;
-        if (!configured) {
-            if (!h3_hip_check(g, hipFuncSetAttribute((const void *)fp8_gemm, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     2 * STAGE), "FP8 GEMM shared memory"))
-                return 0;
-            configured = true;
-        }
-        const unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
-        hipEvent_t timing = h3_kernel_timing_begin(g);
-        hipLaunchKernelGGL(fp8_gemm, dim3(tiles), dim3(512), 2 * STAGE, g->compute, a);
-        h3_kernel_timing_end(g, timing);
-    } else {
-        const size_t total = (size_t)a.m * a.n;
-        hipLaunchKernelGGL(fp8_gemm_small, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, a);
+    static bool configured = false;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)fp8_gemm, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 2 * STAGE), "FP8 GEMM shared memory"))
+            return 0;
+        configured = true;
     }
+    const unsigned tiles = (a.m + TM - 1) / TM * ((a.n + TN - 1) / TN);
+    hipEvent_t timing = h3_kernel_timing_begin(g);
+    hipLaunchKernelGGL(fp8_gemm, dim3(tiles), dim3(512), 2 * STAGE, g->compute, a);
+    h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "native fp8 projection");
 }
 

@@ -101,10 +101,9 @@ extern "C" int h3_gpu_weight_plan_compatible(h3_gpu *g, int force_stream) {
     return hipMemGetInfo(&available, &total) == hipSuccess && available >= reserve_bytes(total);
 }
 
-// ---- SOL / SubBlock layout (gpu.h:66). The learned SubBlock router and SOL
-// attention are not built on this backend; block-sparse attention takes its mask
-// from h3_hip_dit_block_mask. The layout is validated and its protected rows
-// counted so that callers driving SubBlock see the same acceptance rules.
+// ---- SOL / SubBlock layout (gpu.h:66): bound for the SubBlock router in
+// attention mode 4 and for SOL routing in mode 3; other modes check only that
+// the tables are present.
 extern "C" int h3_gpu_dit_sol_layout(h3_gpu *g, const h3_sol_layout *layout) {
     if (!g || !layout) return 0;
     if (!layout->sequence || !layout->query_blocks || !layout->key_blocks || !layout->query || !layout->key)

@@ -137,17 +137,24 @@ int h3_gpu_event_wait(h3_gpu *gpu, h3_gpu_event *event);        /* gpu.h:32 */
 void h3_gpu_event_free(h3_gpu_event *event);                    /* gpu.h:33 */
 
 /* ---- quantized projection weights -------------------------------------- */
-/* gpu.h:44. mode 0 = BF16 projections, 1 = W8A16 (int8 weights, per-group
- * fp32 scales, BF16 activations and output). The remaining arguments are
- * accepted for signature compatibility; the packed-artifact cache is not used. */
+/* gpu.h:44 (reference src/cuda/cuda_quant.cuh:120-162). mode 0 = BF16
+ * projections (no cache is touched), 1 = FP8 W8A8 (tensorwide E4M3 weights
+ * and activations, FP32 accumulation, BF16 output); 2 (NVFP4) fails
+ * h3_quant_preflight. cache: artifact directory (NULL: $HOME/.cache/h3/
+ * denoise-quant), created if missing. bf16_weights: BF16 bytes of whole H3
+ * blocks' four projections, for the resident/streamed plan; force_stream
+ * keeps packed weights in pinned host memory. */
 int h3_gpu_quant_configure(h3_gpu *gpu, int mode, const char *cache,
                            uint64_t bf16_weights, uint64_t activations, int force_stream);
-/* gpu.h:46 and gpu.h:74. Read rows x columns BF16 weights from a file at
- * offset and pack them as q8 (int8 [rows,columns] + fp32 scale per 64-wide
- * column group, round-half-even; reference src/weights/q8.c:26-56). The
- * returned tensor is passed to h3_gpu_linear_bf16 like a BF16 weight. */
+/* gpu.h:46 (cuda_quant.cuh:249-330). rows x columns BF16 weights at offset
+ * of a file (multiples of 128), packed to the FP8 descriptor through the
+ * artifact cache (H3QMT002, or H3QWT001 with H3_QUANT_VERIFY=1). The result is
+ * passed to h3_gpu_linear_bf16 like a BF16 weight (no bias). */
 h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *gpu, const char *path, uint64_t offset,
                                  uint32_t rows, uint32_t columns);
+/* gpu.h:74. rows x columns BF16 weights from a file packed as q8 (int8
+ * [rows, columns] + fp32 scale per 64-wide column group, round-half-even;
+ * reference src/weights/q8.c:26-56) for W8A16 projections. */
 h3_gpu_tensor *h3_gpu_q8_load(h3_gpu *gpu, const char *path, uint64_t offset,
                               uint32_t rows, uint32_t columns);
 

@@ -205,8 +205,8 @@ def test_gemm_against_oracle(tmp_path, m, n, k):
     2^12 plus 64 products of 2^-9 is exact), so the bound is
     |got - want| <= 2^-8 |want| + 2^-14 s sum_chunks max|x| max|w|.
     Independently, the result equals hipBLASLt's FP8 GEMM (torch._scaled_mm,
-    tensorwide scales, BF16 output) bit for bit. n = 384 takes the untiled
-    kernel."""
+    tensorwide scales, BF16 output) bit for bit. n = 384 fills half of its
+    last 256-column tile."""
     say(f"gemm m={m} n={n} k={k}")
     rng = np.random.default_rng(m * 7 + n)
     w = synth.f32_to_bf16((rng.standard_normal(n * k) * 0.03).astype(np.float32))
