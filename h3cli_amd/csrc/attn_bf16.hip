@@ -607,7 +607,9 @@ void attn_bf16_listed(Args a) {
     constexpr int BLOCKS = K_BYTES / 1024;
     constexpr unsigned QROWS = 32 * QW;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    // wave is read as a wave-uniform value so that per-wave loops and LDS
+    // addresses stay scalar.
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
     const unsigned nqb = (a.seq + QROWS - 1) / QROWS;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
@@ -646,6 +648,19 @@ void attn_bf16_listed(Args a) {
     for (int md = 0; md < 4; md++) o[md] = f32x16{};
     float m = -1e30f, l = 0.f;
 
+    // Byte offsets, inside a full tile, of this lane's 16-byte load t (LDS
+    // block wave + QW t): a full exact tile is then a uniform base plus these,
+    // with no per-load address arithmetic.
+    constexpr int LOADS = BLOCKS / QW;
+    uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+    for (int t = 0; t < LOADS; t++) {
+        const unsigned b = wave + QW * t;
+        const unsigned key = 4 * b + lane / 16, d = 8 * b + lane / 8;
+        koff[t] = (key * (uint32_t)stride + k_chunk(key, lane % 16) * 8) * 2;
+        voff[t] = (d * a.padded + v_chunk(d, lane % 8) * 8) * 2;
+    }
+
     // Entry i of the walk: an exact tile id, or a centroid tile (CENT_BIT | t).
     auto entry_at = [&](unsigned i) -> uint32_t {
         if (!CENT || i < count) return list[i];
@@ -655,6 +670,16 @@ void attn_bf16_listed(Args a) {
         const bool cent = CENT && (e & CENT_BIT);
         const unsigned key0 = (CENT ? e & TILE_BITS : e) * BN, limit = cent ? a.key_blocks : a.seq;
         const uint16_t *base = cent ? kch : kh;
+        if (!cent && key0 + BN <= limit) {
+            const __attribute__((address_space(1))) char *tile =
+                (const __attribute__((address_space(1))) char *)(base + (size_t)key0 * stride);
+#pragma unroll
+            for (int t = 0; t < LOADS; t++)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(tile + koff[t]),
+                                                 (__attribute__((address_space(3))) void *)(ks + (wave + QW * t) * 1024),
+                                                 16, 0, 0);
+            return;
+        }
 #pragma unroll
         for (unsigned b = wave; b < BLOCKS; b += QW) {
             unsigned key = 4 * b + lane / 16, phys = lane % 16;
@@ -669,6 +694,16 @@ void attn_bf16_listed(Args a) {
         const unsigned padded = cent ? a.kc_padded : a.padded;
         const unsigned col = min((CENT ? e & TILE_BITS : e) * BN, padded - BN);
         const uint16_t *base = cent ? vcth : vth;
+        if (!cent) {                               // exact tiles: col + BN <= padded always
+            const __attribute__((address_space(1))) char *tile =
+                (const __attribute__((address_space(1))) char *)(base + col);
+#pragma unroll
+            for (int t = 0; t < LOADS; t++)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(tile + voff[t]),
+                                                 (__attribute__((address_space(3))) void *)(vs + (wave + QW * t) * 1024),
+                                                 16, 0, 0);
+            return;
+        }
 #pragma unroll
         for (unsigned b = wave; b < BLOCKS; b += QW) {
             unsigned d = 8 * b + lane / 8, vph = lane % 8;
