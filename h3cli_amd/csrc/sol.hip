@@ -31,23 +31,39 @@ enum { SUM_Q = 0, SUM_K = 1, SUM_V = 2 };
 // Centroid of block b, head h, channel d: fp32 sum of the block's rows in
 // order, divided by the row count, rounded to BF16. Q -> qc [heads][qblocks][128];
 // K -> kc [kblocks][heads][128]; V -> vct [heads][128][kpad] at the V^T key
-// position (blocks kblocks .. kpad-1 write zeros).
+// position (blocks kblocks .. kpad-1 write zeros). A workgroup covers one
+// block of 16 heads: 16 lanes per head, 8 channels (one 16-byte load per row)
+// per lane.
 template <int WHICH>
-__global__ __launch_bounds__(128) void sol_summary(const uint16_t *x, uint16_t *out, unsigned seq, unsigned heads,
+__global__ __launch_bounds__(256) void sol_summary(const uint16_t *x, uint16_t *out, unsigned seq, unsigned heads,
                                                    unsigned block, unsigned blocks, unsigned kpad, unsigned *fault) {
-    const unsigned b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-    uint16_t value = 0;
+    const unsigned b = blockIdx.x, h = blockIdx.y * 16 + threadIdx.x / 16, d0 = (threadIdx.x % 16) * 8;
+    if (h >= heads) return;
+    u16x8 value = {};
     if (b < blocks) {
         const unsigned start = b * block, len = min(block, seq - start);
-        float sum = 0.f;
-        for (unsigned i = 0; i < len; i++) sum += bf16_to_f32(x[((size_t)(start + i) * heads + h) * D + d]);
-        const float mean = __fdiv_rn(sum, (float)len);
-        value = f32_to_bf16(mean);
-        if (!finite_f32(mean) || !finite_f32(bf16_to_f32(value))) fault[0] = 1u;
+        float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const uint16_t *p = x + ((size_t)start * heads + h) * D + d0;
+        for (unsigned i = 0; i < len; i++) {
+            const u16x8 v = *reinterpret_cast<const u16x8 *>(p + (size_t)i * heads * D);
+#pragma unroll
+            for (int c = 0; c < 8; c++) sum[c] = __fadd_rn(sum[c], bf16_to_f32(v[c]));
+        }
+        bool bad = false;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float mean = __fdiv_rn(sum[c], (float)len);
+            value[c] = f32_to_bf16(mean);
+            bad |= !finite_f32(mean) || !finite_f32(bf16_to_f32(value[c]));
+        }
+        if (bad) fault[0] = 1u;
     }
-    if (WHICH == SUM_Q) out[((size_t)h * blocks + b) * D + d] = value;
-    else if (WHICH == SUM_K) out[((size_t)b * heads + h) * D + d] = value;
-    else out[((size_t)h * D + d) * kpad + (b & ~63u) + vt_position(b & 63u)] = value;
+    if (WHICH == SUM_Q) *reinterpret_cast<u16x8 *>(out + ((size_t)h * blocks + b) * D + d0) = value;
+    else if (WHICH == SUM_K) *reinterpret_cast<u16x8 *>(out + ((size_t)b * heads + h) * D + d0) = value;
+    else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) out[((size_t)h * D + d0 + c) * kpad + (b & ~63u) + vt_position(b & 63u)] = value[c];
+    }
 }
 
 // Per head and channel: mean and variance of the K centroids over the key
@@ -55,8 +71,22 @@ __global__ __launch_bounds__(128) void sol_summary(const uint16_t *x, uint16_t *
 __global__ __launch_bounds__(128) void sol_moments(const uint16_t *kc, float *out, unsigned heads, unsigned blocks) {
     const unsigned h = blockIdx.x, d = threadIdx.x;
     float sum = 0.f, sq = 0.f;
-    for (unsigned b = 0; b < blocks; b++) {
-        const float x = bf16_to_f32(kc[((size_t)b * heads + h) * D + d]);
+    const uint16_t *p = kc + (size_t)h * D + d;
+    const size_t stride = (size_t)heads * D;
+    unsigned b = 0;
+    // Sixteen loads in flight ahead of the in-order sums.
+    for (; b + 16 <= blocks; b += 16) {
+        float x[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) x[j] = bf16_to_f32(p[(size_t)(b + j) * stride]);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            sum = __fadd_rn(sum, x[j]);
+            sq = __fadd_rn(sq, __fmul_rn(x[j], x[j]));
+        }
+    }
+    for (; b < blocks; b++) {
+        const float x = bf16_to_f32(p[(size_t)b * stride]);
         sum = __fadd_rn(sum, x);
         sq = __fadd_rn(sq, __fmul_rn(x, x));
     }
@@ -66,15 +96,18 @@ __global__ __launch_bounds__(128) void sol_moments(const uint16_t *kc, float *ou
     out[h * 256 + 128 + d] = var > 0.f ? var : 0.f;
 }
 
-// One workgroup per (pair of query blocks, head) for 32-row query blocks, or
-// per (query block, head) for 64-row ones: the unit a listed-kernel workgroup
-// of 64 queries covers. For each of its PAIR query blocks, m, v and each dot
-// are fmaf chains over the 128 channels in order (the oracle's order; see
-// oracle_sol_route). Lists, per unit: exact tiles either block routes, with
-// HALF_BIT << i set when block i routes the tile; then centroid tiles holding
-// an approximate block of either, with the same half bits and one 64-bit
-// approximate mask per half (for 64-row blocks both halves are the block).
+// Units: a pair of 32-row query blocks, or one 64-row block: the 64 queries a
+// listed-kernel workgroup covers. One workgroup routes UPW consecutive units
+// of one head. Per 256-key-block chunk each thread loads its key block's
+// centroid row once into registers and scores it against every unit's query
+// blocks (their centroids broadcast from LDS). For each query block, m, v and
+// each dot are fmaf chains over the 128 channels in order (the oracle's order;
+// see oracle_sol_route). Lists, per unit: exact tiles either block routes,
+// with HALF_BIT << i set when block i routes the tile; then centroid tiles
+// holding an approximate block of either, with the same half bits and one
+// 64-bit approximate mask per half (for 64-row blocks both halves are the block).
 constexpr uint32_t HALF_BIT = 1u << 29;
+constexpr unsigned UPW = 8;
 
 template <int PAIR>
 __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint16_t *kc, const float *moments,
@@ -82,99 +115,121 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                                                  uint8_t *routes, uint32_t *exact_list, uint32_t *exact_count,
                                                  uint32_t *cent_list, uint32_t *cent_count, uint64_t *cent_mask,
                                                  unsigned heads, unsigned qblocks, unsigned kblocks, unsigned tiles,
-                                                 unsigned radius, unsigned minimum, float scale, float tau,
-                                                 int force_exact, uint32_t *row_counts) {
-    __shared__ float q[PAIR][D];
-    __shared__ float limit[PAIR];
-    __shared__ unsigned wave_total[4][2];
+                                                 unsigned units, unsigned radius, unsigned minimum, float scale,
+                                                 float tau, int force_exact, uint32_t *row_counts) {
+    __shared__ float q[UPW][PAIR][D];
+    __shared__ float limit[UPW][PAIR];
+    __shared__ unsigned wave_total[1][4][2];
+    __shared__ uint32_t wave_tally[4][7];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned unit = blockIdx.x, h = blockIdx.y, units = gridDim.x;
-    const unsigned qb0 = unit * PAIR;
-    const unsigned present = min((unsigned)PAIR, qblocks - qb0);
+    const unsigned h = blockIdx.y, u0 = blockIdx.x * UPW, nu = min(UPW, units - u0);
     const float a = __fmul_rn(scale, 1.4426950408889634f);
-    for (unsigned i = tid; i < present * D; i += 256) q[i / D][i % D] = bf16_to_f32(qc[((size_t)h * qblocks + qb0) * D + i]);
-    __syncthreads();
-    if (tid < present) {
-        float m = 0.f, v = 0.f;
-        for (unsigned d = 0; d < D; d++) {
-            m = fmaf(q[tid][d], moments[h * 256 + d], m);
-            v = fmaf(__fmul_rn(q[tid][d], q[tid][d]), moments[h * 256 + 128 + d], v);
-        }
-        const float mean = __fmul_rn(m, a), var = __fmul_rn(__fmul_rn(v > 0.f ? v : 0.f, a), a);
-        limit[tid] = __fadd_rn(mean, __fmul_rn(tau, __fsqrt_rn(__fadd_rn(var, 1e-6f))));
+    for (unsigned i = tid; i < UPW * PAIR * D; i += 256) {
+        const unsigned u = i / (PAIR * D), qb = (u0 + u) * PAIR + (i / D) % PAIR;
+        (&q[0][0][0])[i] = u < nu && qb < qblocks ? bf16_to_f32(qc[((size_t)h * qblocks + qb) * D + i % D]) : 0.f;
     }
     __syncthreads();
-    h3_sol_block qm[PAIR];
-    for (unsigned i = 0; i < PAIR; i++) qm[i] = qmeta[qb0 + (i < present ? i : 0)];
-    const size_t row = (size_t)h * units + unit;
-    uint32_t *exact_row = exact_list + row * kblocks;
-    uint32_t *cent_row = cent_list + row * tiles;
-    uint64_t *mask_row = cent_mask + row * tiles * 2;
-    unsigned n_exact = 0, n_cent = 0;
-    // This thread's pair counts: exact, approximate, protected, local (not
-    // protected), floor, recovery, tail (the reference's h3_cuda_sol_stats.pairs).
+    if (tid < UPW * PAIR) {
+        const unsigned u = tid / PAIR, pi = tid % PAIR;
+        float m = 0.f, v = 0.f;
+        for (unsigned d = 0; d < D; d++) {
+            m = fmaf(q[u][pi][d], moments[h * 256 + d], m);
+            v = fmaf(__fmul_rn(q[u][pi][d], q[u][pi][d]), moments[h * 256 + 128 + d], v);
+        }
+        const float mean = __fmul_rn(m, a), var = __fmul_rn(__fmul_rn(v > 0.f ? v : 0.f, a), a);
+        limit[u][pi] = __fadd_rn(mean, __fmul_rn(tau, __fsqrt_rn(__fadd_rn(var, 1e-6f))));
+    }
+    __syncthreads();
+    // Running list lengths per unit (exact, centroid).
+    __shared__ unsigned lengths[UPW][2];
+    if (tid < UPW * 2) (&lengths[0][0])[tid] = 0;
+    // This thread's pair counts over all units: exact, approximate, protected,
+    // local (not protected), floor, recovery, tail (the reference's
+    // h3_cuda_sol_stats.pairs); summed per workgroup into its first unit's row.
     uint32_t tally[7] = {0, 0, 0, 0, 0, 0, 0};
+    __syncthreads();
     for (unsigned base = 0; base < kblocks; base += 256) {
         const unsigned b = base + tid;
         const bool valid = b < kblocks;
-        bool exact[2] = {false, false};
+        u16x8 kr[D / 8];
+        h3_sol_block km = {};
         if (valid) {
-            const uint16_t *kr = kc + ((size_t)b * heads + h) * D;
-            float dot[PAIR];
-            for (unsigned i = 0; i < PAIR; i++) dot[i] = 0.f;
-            for (unsigned c8 = 0; c8 < D / 8; c8++) {
-                const u16x8 w = *reinterpret_cast<const u16x8 *>(kr + c8 * 8);
+            const uint16_t *row = kc + ((size_t)b * heads + h) * D;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float kv = bf16_to_f32(w[j]);
+            for (unsigned c8 = 0; c8 < D / 8; c8++) kr[c8] = *reinterpret_cast<const u16x8 *>(row + c8 * 8);
+            km = kmeta[b];
+        }
+        const bool floor_ = valid && (uint64_t)(b + 1) * minimum / kblocks != (uint64_t)b * minimum / kblocks;
+        const bool tail = valid && km.rows < 64;
+#pragma unroll 1
+        for (unsigned u = 0; u < nu; u++) {
+            const unsigned qb0 = (u0 + u) * PAIR;
+            const unsigned present = min((unsigned)PAIR, qblocks - qb0);
+            bool exact[2] = {false, false};
+            if (valid) {
+                float dot[PAIR];
 #pragma unroll
-                    for (int i = 0; i < PAIR; i++) dot[i] = fmaf(q[i][c8 * 8 + j], kv, dot[i]);
+                for (int i = 0; i < PAIR; i++) dot[i] = 0.f;
+#pragma unroll
+                for (unsigned c8 = 0; c8 < D / 8; c8++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float kv = bf16_to_f32(kr[c8][j]);
+#pragma unroll
+                        for (int i = 0; i < PAIR; i++) dot[i] = fmaf(q[u][i][c8 * 8 + j], kv, dot[i]);
+                    }
+#pragma unroll
+                for (int i = 0; i < PAIR; i++) {
+                    if ((unsigned)i >= present) break;
+                    const h3_sol_block qm = qmeta[qb0 + i];
+                    const float di = __fmul_rn(dot[i], a), t = limit[u][i];
+                    const bool protect = qm.protect || km.protect;
+                    const bool local = qm.first_frame >= 0 && km.first_frame >= 0 &&
+                                       qm.first_frame <= km.last_frame + (int)radius &&
+                                       km.first_frame <= qm.last_frame + (int)radius;
+                    const bool recovery = !finite_f32(di) || !finite_f32(t);
+                    exact[i] = force_exact || protect || local || floor_ || recovery || tail || di > t;
+                    routes[((size_t)h * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
+                    tally[exact[i] ? 0 : 1]++;
+                    tally[2] += protect;
+                    tally[3] += local && !protect;
+                    tally[4] += floor_;
+                    tally[5] += recovery;
+                    tally[6] += tail;
                 }
             }
-            const h3_sol_block km = kmeta[b];
-            const bool floor_ = (uint64_t)(b + 1) * minimum / kblocks != (uint64_t)b * minimum / kblocks;
-            const bool tail = km.rows < 64;
-#pragma unroll
-            for (int i = 0; i < PAIR; i++) {
-                if ((unsigned)i >= present) break;
-                const float di = __fmul_rn(dot[i], a), t = limit[i];
-                const bool protect = qm[i].protect || km.protect;
-                const bool local = qm[i].first_frame >= 0 && km.first_frame >= 0 &&
-                                   qm[i].first_frame <= km.last_frame + (int)radius &&
-                                   km.first_frame <= qm[i].last_frame + (int)radius;
-                const bool recovery = !finite_f32(di) || !finite_f32(t);
-                exact[i] = force_exact || protect || local || floor_ || recovery || tail || di > t;
-                routes[((size_t)h * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
-                tally[exact[i] ? 0 : 1]++;
-                tally[2] += protect;
-                tally[3] += local && !protect;
-                tally[4] += floor_;
-                tally[5] += recovery;
-                tally[6] += tail;
-            }
             if (PAIR == 1) exact[1] = exact[0];
+            // Ordered compaction of the tiles either block routes exactly; wave
+            // w's approximate blocks are the masks of centroid tile base / 64 + w.
+            const bool any = exact[0] || exact[1];
+            const unsigned long long ex = __ballot(any);
+            const unsigned long long m0 = __ballot(valid && !exact[0]);
+            const unsigned long long m1 = PAIR == 1 ? m0 : __ballot(valid && present > 1 && !exact[1]);
+            if (lane == 0) { wave_total[0][wave][0] = __popcll(ex); wave_total[0][wave][1] = (m0 | m1) != 0; }
+            __syncthreads();
+            const size_t row = (size_t)h * units + u0 + u;
+            unsigned pos = lengths[u][0] + __popcll(ex & ((1ull << lane) - 1ull)), cpos = lengths[u][1];
+            unsigned add_exact = 0, add_cent = 0;
+            for (unsigned w = 0; w < 4; w++) {
+                if (w < wave) { pos += wave_total[0][w][0]; cpos += wave_total[0][w][1]; }
+                add_exact += wave_total[0][w][0];
+                add_cent += wave_total[0][w][1];
+            }
+            if (any) exact_list[row * kblocks + pos] = b | (exact[0] ? HALF_BIT : 0u) | (exact[1] ? HALF_BIT << 1 : 0u);
+            if (lane == 0 && (m0 | m1)) {
+                cent_list[row * tiles + cpos] = (base / 64 + wave) | (m0 ? HALF_BIT : 0u) | (m1 ? HALF_BIT << 1 : 0u);
+                cent_mask[(row * tiles + cpos) * 2] = m0;
+                cent_mask[(row * tiles + cpos) * 2 + 1] = m1;
+            }
+            __syncthreads();           // lengths[u] and wave_total read by everyone
+            if (tid == 0) { lengths[u][0] += add_exact; lengths[u][1] += add_cent; }
         }
-        // Ordered compaction of the tiles either block routes exactly; wave
-        // w's approximate blocks are the masks of centroid tile base / 64 + w.
-        const bool any = exact[0] || exact[1];
-        const unsigned long long ex = __ballot(any);
-        const unsigned long long m0 = __ballot(valid && !exact[0]);
-        const unsigned long long m1 = PAIR == 1 ? m0 : __ballot(valid && present > 1 && !exact[1]);
-        if (lane == 0) { wave_total[wave][0] = __popcll(ex); wave_total[wave][1] = (m0 | m1) != 0; }
-        __syncthreads();
-        unsigned pos = n_exact + __popcll(ex & ((1ull << lane) - 1ull)), cpos = n_cent;
-        for (unsigned w = 0; w < wave; w++) { pos += wave_total[w][0]; cpos += wave_total[w][1]; }
-        if (any) exact_row[pos] = b | (exact[0] ? HALF_BIT : 0u) | (exact[1] ? HALF_BIT << 1 : 0u);
-        if (lane == 0 && (m0 | m1)) {
-            cent_row[cpos] = (base / 64 + wave) | (m0 ? HALF_BIT : 0u) | (m1 ? HALF_BIT << 1 : 0u);
-            mask_row[2 * cpos] = m0;
-            mask_row[2 * cpos + 1] = m1;
-        }
-        for (unsigned w = 0; w < 4; w++) { n_exact += wave_total[w][0]; n_cent += wave_total[w][1]; }
-        __syncthreads();
     }
-    if (tid == 0) { exact_count[row] = n_exact; cent_count[row] = n_cent; }
-    __shared__ uint32_t wave_tally[4][7];
+    __syncthreads();
+    if (tid < nu) {
+        exact_count[(size_t)h * units + u0 + tid] = lengths[tid][0];
+        cent_count[(size_t)h * units + u0 + tid] = lengths[tid][1];
+    }
 #pragma unroll
     for (int j = 0; j < 7; j++) {
         uint32_t x = tally[j];
@@ -182,8 +237,13 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
         if (lane == 0) wave_tally[wave][j] = x;
     }
     __syncthreads();
-    if (tid < 7)
-        row_counts[row * 8 + tid] = wave_tally[0][tid] + wave_tally[1][tid] + wave_tally[2][tid] + wave_tally[3][tid];
+    if (tid < 8) {
+        const size_t row = (size_t)h * units + u0;
+        // The workgroup's counts land in its first unit's row; the others hold zeros.
+        for (unsigned u = 0; u < nu; u++)
+            row_counts[(row + u) * 8 + tid] =
+                u == 0 && tid < 7 ? wave_tally[0][tid] + wave_tally[1][tid] + wave_tally[2][tid] + wave_tally[3][tid] : 0u;
+    }
 }
 
 // Sums the per-unit pair counts of one call into the router's u64 counters
@@ -269,22 +329,24 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
     const auto *qmeta = (const h3_sol_block *)r->meta.ptr;
     const auto *kmeta = qmeta + QB;
     const uint32_t qblock = (uint32_t)r->options.q_block;
-    hipLaunchKernelGGL(sol_summary<SUM_Q>, dim3(QB, heads), dim3(128), 0, g->compute, q, qc, seq, heads, qblock, QB,
+    const unsigned head_groups = (heads + 15) / 16;
+    hipLaunchKernelGGL(sol_summary<SUM_Q>, dim3(QB, head_groups), dim3(256), 0, g->compute, q, qc, seq, heads, qblock, QB,
                        kpad, g->fault);
-    hipLaunchKernelGGL(sol_summary<SUM_K>, dim3(KB, heads), dim3(128), 0, g->compute, k, kc, seq, heads, 64u, KB,
+    hipLaunchKernelGGL(sol_summary<SUM_K>, dim3(KB, head_groups), dim3(256), 0, g->compute, k, kc, seq, heads, 64u, KB,
                        kpad, g->fault);
-    hipLaunchKernelGGL(sol_summary<SUM_V>, dim3(kpad, heads), dim3(128), 0, g->compute, v, vct, seq, heads, 64u, KB,
+    hipLaunchKernelGGL(sol_summary<SUM_V>, dim3(kpad, head_groups), dim3(256), 0, g->compute, v, vct, seq, heads, 64u, KB,
                        kpad, g->fault);
     hipLaunchKernelGGL(sol_moments, dim3(heads), dim3(128), 0, g->compute, kc, moments, heads, KB);
     if (!h3_launch_status(g, "SOL summaries")) return 0;
     const unsigned minimum = (unsigned)std::ceil((double)r->options.min_exact * KB);
     // Lists per 64-query unit: pairs of 32-row blocks, or single 64-row blocks.
     auto route = qblock == 32 ? sol_route<2> : sol_route<1>;
-    hipLaunchKernelGGL(route, dim3(units, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta, kmeta,
-                       base + r->off_routes, (uint32_t *)(base + r->off_exact), (uint32_t *)(base + r->off_exact_count),
-                       (uint32_t *)(base + r->off_cent), (uint32_t *)(base + r->off_cent_count),
-                       (uint64_t *)(base + r->off_cent_mask), heads, QB, KB, tiles,
-                       (unsigned)r->options.local_radius, minimum, scale, r->options.tau, r->force_exact ? 1 : 0,
+    hipLaunchKernelGGL(route, dim3((units + UPW - 1) / UPW, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta,
+                       kmeta, base + r->off_routes, (uint32_t *)(base + r->off_exact),
+                       (uint32_t *)(base + r->off_exact_count), (uint32_t *)(base + r->off_cent),
+                       (uint32_t *)(base + r->off_cent_count), (uint64_t *)(base + r->off_cent_mask), heads, QB, KB,
+                       tiles, units, (unsigned)r->options.local_radius, minimum, scale, r->options.tau,
+                       r->force_exact ? 1 : 0,
                        (uint32_t *)(base + r->off_row_counts));
     if (!h3_launch_status(g, "SOL route")) return 0;
     hipLaunchKernelGGL(sol_count, dim3(1), dim3(1024), 0, g->compute, (const uint32_t *)(base + r->off_row_counts),
