@@ -448,14 +448,15 @@ def h3_proj_fp8_leg(steps, warmup, m=8193, seed=9):
     return res
 
 
-def h3_step_leg(steps, warmup):
+def h3_step_leg(steps, warmup, fp8=False):
     """One real-H3-geometry denoise step (include/h3_dit_synth.h
     h3_hip_dit_synth_h3): 50 blocks, 18225 video rows, hidden 5376, 56 heads,
-    grouped QKV with Q/K norm, 48 RoPE pairs, SwiGLU 14336, W8A16 weights all
-    resident, dense BF16 attention."""
+    grouped QKV with Q/K norm, 48 RoPE pairs, SwiGLU 14336, all weights
+    resident, dense BF16 attention; projections W8A16, or FP8 W8A8 (tensorwide
+    E4M3, activations packed per call) with fp8."""
     from h3cli_amd.runtime import DitSynth
     t0 = time.perf_counter()
-    with DitSynth(geometry="h3") as m:
+    with DitSynth(geometry="h3", projection_quant=1 if fp8 else 0) as m:
         setup = time.perf_counter() - t0
         rows, cfg = m.rows, m.config
         for i in range(warmup):
@@ -470,8 +471,9 @@ def h3_step_leg(steps, warmup):
     H, I, F = cfg.hidden, cfg.heads * 128, cfg.mlp
     gemm = 2.0 * rows * (H * 3 * I + I * H + H * 2 * F + F * H) * cfg.blocks
     attn = attention_flops(rows, cfg.heads) * cfg.blocks
-    log(f"[bench] h3 step: {sec:.3f} s/step over {rows} rows (setup {setup:.1f} s), finite={finite}")
-    return {"workload": "real-H3-geometry 50-block denoise step, 18225 rows, dense BF16 attention",
+    kind = "FP8 W8A8" if fp8 else "W8A16"
+    log(f"[bench] h3 step ({kind}): {sec:.3f} s/step over {rows} rows (setup {setup:.1f} s), finite={finite}")
+    return {"workload": f"real-H3-geometry 50-block denoise step, 18225 rows, dense BF16 attention, {kind} projections",
             "s_per_step": round(sec, 4), "steps": steps, "rows": rows, "blocks": cfg.blocks,
             "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
             "achieved_tflops": round((gemm + attn) / sec / 1e12, 2), "latent_finite": finite,
@@ -506,7 +508,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_proj_fp8,h3_step")
+    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_proj_fp8,h3_step,h3_step_fp8")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -594,6 +596,8 @@ def main():
         result["h3_proj_fp8"] = h3_proj_fp8_leg(args.steps, args.warmup)
     if "h3_step" in legs:
         result["h3_step"] = h3_step_leg(2, 1)
+    if "h3_step_fp8" in legs:
+        result["h3_step_fp8"] = h3_step_leg(2, 1, fp8=True)
     if "step" in legs:
         result["step"] = step_leg(args.step_count, 1)
     print(json.dumps(result), flush=True)

@@ -117,7 +117,7 @@ class DitSynthConfig(C.Structure):
                 ("latent", _u32), ("streamed_first", _u32), ("mask_density", _f),
                 ("attention_mode", _i), ("eps", _f), ("time", _f), ("seed", C.c_uint64),
                 ("rope_half", _u32), ("swiglu", _i), ("qk_norm", _i), ("grouped_qkv", _i),
-                ("subblock_sparsity", _f)]
+                ("subblock_sparsity", _f), ("projection_quant", _i)]
 
 
 _SIGNATURES.update({

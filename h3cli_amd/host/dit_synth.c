@@ -16,6 +16,7 @@
 #include "h3_gpu_surface.h"
 #include "h3_safetensors.h"
 #include "h3_hip_ext.h"
+#include "h3_quant.h"
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -191,6 +192,16 @@ static h3_gpu_tensor *q8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed
     return t;
 }
 
+/* FP8 projection weight (projection_quant 1): N(0, 1/k) BF16 values packed to
+ * the tensorwide E4M3 descriptor. */
+static h3_gpu_tensor *fp8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed) {
+    h3_gpu_tensor *b = normal_tensor(g, (size_t)n * k, seed, 1.0f / sqrtf((float)k), 0.f);
+    if (!b) return NULL;
+    h3_gpu_tensor *t = h3_gpu_synchronize(g) ? h3_hip_fp8_weight_from_bf16(g, b, n, k) : NULL;
+    h3_gpu_tensor_free(b);
+    return t;
+}
+
 static int weights(h3_hip_dit_synth *m, char *error, size_t size) {
     h3_gpu *g = m->gpu;
     const h3_hip_dit_synth_config *c = &m->c;
@@ -213,7 +224,8 @@ static int weights(h3_hip_dit_synth *m, char *error, size_t size) {
         for (int j = 0; j < PROJ; j++) {
             uint32_t n, k;
             proj_shape(c, j, &n, &k);
-            h3_gpu_tensor *t = q8_random(g, n, k, c->seed * 7919ull + b * 8 + j);
+            h3_gpu_tensor *t = c->projection_quant ? fp8_random(g, n, k, c->seed * 7919ull + b * 8 + j)
+                                                   : q8_random(g, n, k, c->seed * 7919ull + b * 8 + j);
             if (!t) return fail(error, size, "block %u weight %d: %s", b, j, h3_gpu_error(g));
             if (resident) m->proj[(size_t)b * PROJ + j] = t;
             else {
@@ -247,9 +259,14 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
     if (!c->blocks || !c->heads || !c->mlp || c->mlp % 256 || !c->hidden || c->hidden % 256 || !c->latent ||
         c->latent % 256 || !c->frames || !c->height || !c->width ||
         (c->rope_half != 64 && (!c->rope_half || c->rope_half > 64 || c->rope_half % 3)) ||
-        (c->attention_mode != 0 && c->attention_mode != 1 && c->attention_mode != 4)) {
+        (c->attention_mode != 0 && c->attention_mode != 1 && c->attention_mode != 4) ||
+        (c->projection_quant != 0 && c->projection_quant != 1)) {
         fail(error, size, "synthetic DiT: hidden/mlp/latent multiples of 256, rope_half 64 or a multiple of 3 "
-                          "below it, attention mode 0/1/4");
+                          "below it, attention mode 0/1/4, projection_quant 0/1");
+        return NULL;
+    }
+    if (c->projection_quant && c->streamed_first < c->blocks) {
+        fail(error, size, "synthetic DiT: FP8 projections need every block resident");
         return NULL;
     }
     h3_hip_dit_synth *m = calloc(1, sizeof(*m));
@@ -273,6 +290,17 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         fail(error, size, "attention configure: %s", h3_gpu_error(g));
         goto bad;
     }
+    if (c->projection_quant) {
+        /* Synthetic weights are packed in place; checkpoints go through the
+         * artifact cache. No H3 admission bytes: every block is resident. */
+        const char *tmp = getenv("TMPDIR");
+        char cache[512];
+        snprintf(cache, sizeof(cache), "%s/h3cli-amd-quant", tmp && *tmp ? tmp : "/tmp");
+        if (!h3_gpu_quant_configure(g, H3_QUANT_FP8, cache, 0, 0, 0)) {
+            fail(error, size, "quant configure: %s", h3_gpu_error(g));
+            goto bad;
+        }
+    }
     if (!h3_gpu_begin(g)) { fail(error, size, "begin: %s", h3_gpu_error(g)); goto bad; }
     if (!weights(m, error, size) || !modulation(m, error, size) || !rope_tables(m)) { h3_gpu_cancel(g); goto bad; }
     {
@@ -289,10 +317,10 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         m->q = bf16_buffer(g, R * I); m->k = bf16_buffer(g, R * I); m->v = bf16_buffer(g, R * I);
         m->attn = bf16_buffer(g, R * I); m->o = bf16_buffer(g, R * H);
         m->h = bf16_buffer(g, R * c->mlp * (c->swiglu ? 2 : 1)); m->f = bf16_buffer(g, R * H);
-        m->act = c->swiglu ? bf16_buffer(g, R * c->mlp) : NULL;
+        m->act = c->swiglu || c->projection_quant ? bf16_buffer(g, R * c->mlp) : NULL;
         m->vel = bf16_buffer(g, R * c->latent);
         if (!m->row_map || !m->latent || !m->latent_bf16 || !m->x || !m->xn || !m->qkv || !m->q || !m->k || !m->v ||
-            !m->attn || !m->o || !m->h || !m->f || !m->vel || (c->swiglu && !m->act)) {
+            !m->attn || !m->o || !m->h || !m->f || !m->vel || ((c->swiglu || c->projection_quant) && !m->act)) {
             fail(error, size, "activations: %s", h3_gpu_error(g));
             h3_gpu_cancel(g);
             goto bad;
@@ -398,13 +426,19 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
              h3_gpu_linear_bf16(g, m->o, m->attn, w[1], NULL, R, I, H) &&
              h3_gpu_gate_adaln_bf16(g, m->x, m->xn, m->x, m->o, m->norm2[b], m->mod[b], m->mod[b], m->row_map, R, H,
                                     SLOTS, 2, 3, 4, c->eps);
-        if (c->swiglu)
+        if (c->swiglu) {
             ok = ok && h3_gpu_linear_bf16(g, m->h, m->xn, w[2], NULL, R, H, 2 * c->mlp) &&
                  h3_gpu_swiglu_bf16(g, m->act, m->h, R, c->mlp) &&
                  h3_gpu_linear_bf16(g, m->f, m->act, w[3], NULL, R, c->mlp, H);
-        else
+        } else if (c->projection_quant) {
+            /* Packed FP8 weights take no epilogue: GELU-tanh separately. */
+            ok = ok && h3_gpu_linear_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
+                 h3_gpu_gelu_bf16(g, m->act, m->h, (uint32_t)(R * c->mlp), 1) &&
+                 h3_gpu_linear_bf16(g, m->f, m->act, w[3], NULL, R, c->mlp, H);
+        } else {
             ok = ok && h3_hip_linear_gelu_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
                  h3_gpu_linear_bf16(g, m->f, m->h, w[3], NULL, R, c->mlp, H);
+        }
         ok = ok && h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5);
     }
     ok = ok && h3_gpu_adaln_bf16(g, m->xn, m->x, m->head_norm, m->head_mod, m->row_map, R, H, 2, 0, 1, c->eps) &&
@@ -469,8 +503,9 @@ int h3_hip_dit_synth_load(h3_hip_dit_synth *m, const char *path, char *error, si
             block_shape(c, i, &rows, &cols);
             snprintf(name, sizeof(name), "blocks.%u.%s", b, BLOCK_NAMES[i]);
             const h3_st_tensor *t = h3_st_find(&header, name);
-            h3_gpu_tensor *loaded = cols ? h3_gpu_q8_load(g, path, t->file_offset, rows, cols)
-                                         : h3_gpu_tensor_load_bf16(g, path, t->file_offset, rows);
+            h3_gpu_tensor *loaded = !cols ? h3_gpu_tensor_load_bf16(g, path, t->file_offset, rows)
+                                    : c->projection_quant ? h3_gpu_quant_load(g, path, t->file_offset, rows, cols)
+                                                          : h3_gpu_q8_load(g, path, t->file_offset, rows, cols);
             if (!loaded) { ok = fail(error, size, "%s: %s", name, h3_gpu_error(g)); break; }
             h3_gpu_tensor **slot = block_slot(m, b, i);
             h3_gpu_tensor_free(*slot);

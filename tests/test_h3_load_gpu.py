@@ -4,6 +4,8 @@ written by the `safetensors` package. Loaded projections must equal the
 reference q8 recipe applied to the file's BF16 weights bit for bit, norms must
 equal the file, the loaded model must step deterministically, and missing or
 mismatched tensors must be named in the error."""
+import os
+
 import numpy as np
 import pytest
 
@@ -68,7 +70,7 @@ def test_load_weights_bit_exact_and_step(tmp_path):
                     assert np.array_equal(m.read(name), ref[name]), name
             m.step(step=0, dt=-0.1)
             runs.append((m.read("latent"), m.read("hidden")))
-    assert np.all(np.isfinite(runs[0][0])) and np.all(np.isfinite(runs[0][1]))
+    assert np.all(np.isfinite(runs[0][0])) and np.all(np.isfinite(synth.bf16_to_f32(runs[0][1])))
     assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
     with DitSynth(geometry="h3", **SMALL) as m:
         m.step(step=0, dt=-0.1)
@@ -93,3 +95,40 @@ def test_load_needs_resident_blocks(tmp_path):
         with pytest.raises(H3Error) as e:
             m.load(path)
         assert "resident" in str(e.value)
+
+
+def test_load_fp8_projections(tmp_path, monkeypatch):
+    """projection_quant 1: the checkpoint's projections go through
+    h3_gpu_quant_load (the artifact cache under $TMPDIR) and equal the
+    reference's FP8 descriptor of the file's BF16 weights byte for byte; the
+    step is deterministic and tracks the W8A16 model loaded from the same file."""
+    from tests.test_quant_gpu import descriptor, packed_size
+    monkeypatch.setenv("TMPDIR", str(tmp_path))
+    path = tmp_path / "h3.safetensors"
+    ref = checkpoint(path)
+    shapes = {"attn.qkv_proj.weight": (3 * 384, 512), "attn.out_proj.weight": (512, 384),
+              "mlp.fc1.weight": (1536, 512), "mlp.fc2.weight": (512, 768)}
+    hidden = []
+    for run in range(2):
+        with DitSynth(geometry="h3", projection_quant=1, **dict(SMALL, streamed_first=SMALL["blocks"])) as m:
+            m.load(path)
+            if run == 0:
+                for b in range(SMALL["blocks"]):
+                    for suffix, (n, k) in shapes.items():
+                        name = f"blocks.{b}.{suffix}"
+                        h = m.lib.h3_hip_dit_synth_tensor(m.handle, name.encode())
+                        want, _ = descriptor(ref[name], n, k)
+                        raw = np.zeros(packed_size(n, k)[2], np.uint8)
+                        assert m.lib.h3_hip_tensor_copy_to_host(h, raw.ctypes.data, raw.size), m.gpu.error()
+                        assert np.array_equal(raw, want), name
+            m.step(step=0, dt=-0.1)
+            hidden.append(m.read("hidden"))
+    assert any(f.endswith(".h3q") for f in os.listdir(tmp_path / "h3cli-amd-quant"))
+    assert np.array_equal(hidden[0], hidden[1]) and np.all(np.isfinite(synth.bf16_to_f32(hidden[0])))
+    with DitSynth(geometry="h3", **SMALL) as m:
+        m.load(path)
+        m.step(step=0, dt=-0.1)
+        q8 = synth.bf16_to_f32(m.read("hidden")).astype(np.float64)
+    f8 = synth.bf16_to_f32(hidden[0]).astype(np.float64)
+    cos = np.dot(f8, q8) / np.sqrt(np.dot(f8, f8) * np.dot(q8, q8))
+    assert cos > 0.99, cos
