@@ -400,19 +400,23 @@ def h3_proj_leg(steps, warmup, m=8193, seed=9):
     return res
 
 
-def h3_proj_fp8_leg(steps, warmup, m=8193, seed=9):
-    """The same four real-H3 projections as FP8 W8A8 (reference
-    cuda_quant.cuh:339-398, the mode behind the published FP8 figure): tensorwide
-    E4M3 weights packed once, the activation packed per call (max, scale,
-    encode), then the FP8 GEMM. ms is the whole call; gemm_ms the GEMM kernel."""
+def h3_proj_quant_leg(steps, warmup, mode=1, m=8193, seed=9):
+    """The same four real-H3 projections quantized (reference
+    cuda_quant.cuh:339-398, the modes behind the published FP8 and NVFP4
+    figures). mode 1, FP8 W8A8: tensorwide E4M3 weights packed once, the
+    activation packed per call (max, scale, encode), then the FP8 GEMM. mode 2,
+    NVFP4 W4A4: weights packed and dequantized to BF16 once, the activation
+    packed and dequantized per call, then the BF16 GEMM with alpha. ms is the
+    whole call; gemm_ms the GEMM kernel."""
     from h3cli_amd.runtime import Gpu, Tensor
     shapes = [("qkv", 5376, 21504), ("out", 7168, 5376), ("fc1", 5376, 28672), ("fc2", 14336, 5376)]
-    res = {"workload": "real-H3 block-0 projections, 8193 rows, FP8 W8A8 (tensorwide E4M3)", "rows": m, "shapes": {},
+    kind = "FP8 W8A8 (tensorwide E4M3)" if mode == 1 else "NVFP4 W4A4 (UE4M3 per 16, dequantized to BF16)"
+    res = {"workload": f"real-H3 block-0 projections, 8193 rows, {kind}", "rows": m, "shapes": {},
            "published": H3_PUBLISHED["proj_8193"]}
     total_flops, total_ms, total_gemm = 0.0, 0.0, 0.0
     with Gpu() as gpu:
         lib = gpu.lib
-        gpu.check(lib.h3_gpu_quant_configure(gpu.handle, 1, os.environ.get("TMPDIR", "/tmp").encode() + b"/h3-fp8",
+        gpu.check(lib.h3_gpu_quant_configure(gpu.handle, mode, os.environ.get("TMPDIR", "/tmp").encode() + b"/h3-quant",
                                              2 * (4 * 7168 * 5376 + 3 * 14336 * 5376), 1 << 30, 0), "quant configure")
         x = gpu.empty(m * 14336)
         gpu.begin()
@@ -423,8 +427,8 @@ def h3_proj_fp8_leg(steps, warmup, m=8193, seed=9):
             gpu.begin()
             gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, wb.handle, seed * 8 + i, 0.02, n * k), "fill w")
             gpu.submit()
-            h = lib.h3_hip_fp8_weight_from_bf16(gpu.handle, wb.handle, n, k)
-            gpu.check(h, "fp8 weight")
+            h = lib.h3_hip_quant_weight_from_bf16(gpu.handle, wb.handle, n, k)
+            gpu.check(h, "quantized weight")
             w = Tensor(gpu, h, n * k, 2)
             gpu.tensors.append(w)
             gpu.free(wb)
@@ -438,7 +442,7 @@ def h3_proj_fp8_leg(steps, warmup, m=8193, seed=9):
             total_gemm += kt[0][0]
             res["shapes"][name] = {"k": k, "n": n, "ms": round(ms, 4), "gemm_ms": round(kt[0][0], 4),
                                    "tflops": round(flops / ms / 1e9, 2), "gemm_tflops": round(flops / kt[0][0] / 1e9, 2)}
-            log(f"[bench] h3 fp8 proj {name} {m}x{k}x{n}: {ms:.3f} ms per call, GEMM {kt[0][0]:.3f} ms "
+            log(f"[bench] h3 {'fp8' if mode == 1 else 'nvfp4'} proj {name} {m}x{k}x{n}: {ms:.3f} ms per call, GEMM {kt[0][0]:.3f} ms "
                 f"({flops / kt[0][0] / 1e9:.1f} TFLOP/s)")
             gpu.free(y)
             gpu.free(w)
@@ -508,7 +512,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_proj_fp8,h3_step,h3_step_fp8")
+    ap.add_argument("--legs", default="attention,sage,subblock,sol,gemm,step,h3_attention,h3_proj,h3_proj_fp8,h3_proj_nvfp4,h3_step,h3_step_fp8")
     ap.add_argument("--step-count", type=int, default=3, help="timed full DiT steps (step leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=int(os.environ.get("H3_BENCH_CPU_ROWS", "576")))
@@ -593,7 +597,9 @@ def main():
     if "h3_proj" in legs:
         result["h3_proj"] = h3_proj_leg(args.steps, args.warmup)
     if "h3_proj_fp8" in legs:
-        result["h3_proj_fp8"] = h3_proj_fp8_leg(args.steps, args.warmup)
+        result["h3_proj_fp8"] = h3_proj_quant_leg(args.steps, args.warmup, mode=1)
+    if "h3_proj_nvfp4" in legs:
+        result["h3_proj_nvfp4"] = h3_proj_quant_leg(args.steps, args.warmup, mode=2)
     if "h3_step" in legs:
         result["h3_step"] = h3_step_leg(2, 1)
     if "h3_step_fp8" in legs:

@@ -144,7 +144,7 @@ _SIGNATURES.update({
     "h3_hip_sol_counters": (_i, [_p, _p, C.c_size_t]),
     "h3_hip_sha256": (_i, [_p, C.c_size_t, _p]),
     "h3_hip_fp8_pack": (_i, [_p, _p, _p, _p, C.c_size_t]),
-    "h3_hip_fp8_weight_from_bf16": (_p, [_p, _p, _u32, _u32]),
+    "h3_hip_quant_weight_from_bf16": (_p, [_p, _p, _u32, _u32]),
     # the rest of the reference surface implemented here (include/h3_gpu_surface.h)
     "h3_gpu_adaln_bf16_offset": (_i, [_p, _p, _p, _sz, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _f]),
     "h3_gpu_rms_norm_bf16": (_i, [_p, _p, _p, _p, _u32, _u32, _f]),

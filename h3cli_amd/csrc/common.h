@@ -96,6 +96,7 @@ struct h3_gpu_tensor {
     int quant_mode;
     uint32_t quant_n, quant_k;
     size_t quant_scale, quant_global;
+    void *quant_dequant;    // NVFP4 resident weight: BF16 code * block scale [quant_n, quant_k]
     // Streaming fences (copy stream fills, compute stream reads).
     hipEvent_t ready, released;
     bool ready_pending, release_recorded;

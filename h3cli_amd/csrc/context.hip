@@ -262,6 +262,7 @@ extern "C" void h3_gpu_tensor_free(h3_gpu_tensor *t) {
     if (t->storage == H3_GPU_DEVICE_ONLY) { hipFree(t->data); h3_stats_track_alloc(g, t->bytes_alloc, -1); }
     else { hipHostFree(t->data); g->stats.pinned_bytes -= std::min<uint64_t>(g->stats.pinned_bytes, t->bytes_alloc); }
     if (t->q8_scales) hipFree(t->q8_scales);
+    if (t->quant_dequant) { hipFree(t->quant_dequant); t->quant_dequant = nullptr; }
     delete t;
 }
 

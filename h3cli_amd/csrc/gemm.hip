@@ -52,6 +52,7 @@ struct GemmArgs {
     const void *w;            // bf16 [N,K] or int8 [N,K]
     const float *scales;      // q8: [N, groups]
     const uint16_t *bias;     // optional [N]
+    const float *alpha;       // EPI bit 2: device scalar multiplying the accumulator
     unsigned m, n, k, group, groups;
     int gelu;
 };
@@ -70,7 +71,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // 8 waves as 2 (M) x 4 (N); each wave owns a 128 x 64 output tile (8 MFMA
 // blocks), two waves per SIMD. CHANNEL: one scale per output row (group == K),
-// loaded once. EPI bit 0: bias, bit 1: GELU.
+// loaded once. EPI bit 0: bias, bit 1: GELU, bit 2: alpha (before the bias).
 template <bool Q8, bool CHANNEL, int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void gemm_kernel(GemmArgs a) {
@@ -210,6 +211,7 @@ void gemm_kernel(GemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float v = acc[i][j][g4 * 4 + e];
+                    if constexpr (EPI & 4) v *= a.alpha[0];
                     if constexpr (EPI & 1) v += bf16_to_f32(bias4[e]);
                     uint16_t b = f32_to_bf16(v);
                     if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
@@ -238,6 +240,7 @@ __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
         }
         acc = fmaf(bf16_to_f32(xr[kk]), w, acc);
     }
+    if (a.alpha) acc *= a.alpha[0];
     if (a.bias) acc += bf16_to_f32(a.bias[col]);
     uint16_t b = f32_to_bf16(acc);
     if (a.gelu) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
@@ -275,9 +278,21 @@ int launch_epi(h3_gpu *g, const GemmArgs &a) {
 
 }  // namespace
 
+// y[M,N] = bf16(alpha[0] * x[M,K] . w[N,K]^T) with BF16 device operands and a
+// device scalar alpha (the NVFP4 projections' dequantized operands).
+int h3_gemm_bf16_alpha(h3_gpu *g, uint16_t *y, const uint16_t *x, const uint16_t *w, const float *alpha, uint32_t m,
+                       uint32_t k, uint32_t n) {
+    GemmArgs a{};
+    a.y = y; a.x = x; a.w = w; a.alpha = alpha; a.m = m; a.n = n; a.k = k; a.group = 1; a.groups = 1;
+    if (n % TN == 0 && k % TK == 0 && m >= 32) return launch_tiled<false, false, 4>(g, a);
+    const size_t total = (size_t)m * n;
+    hipLaunchKernelGGL(gemm_small, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, a, 0);
+    return h3_launch_status(g, "small scaled GEMM");
+}
+
 int h3_gemm(h3_gpu *g, uint16_t *y, const uint16_t *x, const h3_gpu_tensor *w, const uint16_t *bias, uint32_t m,
             uint32_t k, uint32_t n, int gelu) {
-    GemmArgs a;
+    GemmArgs a{};
     a.y = y; a.x = x; a.w = w->data; a.bias = bias; a.m = m; a.n = n; a.k = k; a.gelu = gelu;
     a.scales = w->q8 ? w->q8_scales : nullptr;
     a.group = w->q8 ? w->q8_group : 1;

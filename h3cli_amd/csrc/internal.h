@@ -44,6 +44,9 @@ int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uin
 int h3_quant_gemm(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const h3_gpu_tensor *w, uint32_t rows,
                   uint32_t k, uint32_t n);
 void h3_quant_destroy(h3_gpu *g);
+// y[M,N] = bf16(alpha[0] * x . w^T), BF16 device operands, device scalar alpha (gemm.hip).
+int h3_gemm_bf16_alpha(h3_gpu *g, uint16_t *y, const uint16_t *x, const uint16_t *w, const float *alpha, uint32_t m,
+                       uint32_t k, uint32_t n);
 
 struct h3_device_buffer {
     void *ptr = nullptr;

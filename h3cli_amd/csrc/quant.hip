@@ -48,6 +48,8 @@ struct h3_quant_state {
     bool streaming = false;            // packed weights stay in pinned host memory
     h3_device_buffer activation;       // packed activation codes + maxima + global slot
     h3_device_buffer streamed;         // device copy of a streamed packed weight
+    h3_device_buffer dequant_x;        // NVFP4: the activation's dequantized BF16 values
+    h3_device_buffer dequant_w;        // NVFP4: a streamed weight's dequantized BF16 values
 };
 
 namespace {
@@ -80,10 +82,12 @@ __global__ __launch_bounds__(256) void fp8_amax(const uint16_t *x, size_t chunks
     if (threadIdx.x == 0) partials[blockIdx.x] = max(max(waves[0], waves[1]), max(waves[2], waves[3]));
 }
 
-// scale = max(amax / 448, 1e-20) (IEEE division); global slot {scale, 1, 0, 0}
-// and the scale plane's single value (cuda_quant.cuh:36-39, 43).
+// scale = max(amax / divisor, 1e-20) (IEEE division; 448 for FP8, 2688 for
+// NVFP4); global slot {scale, scale * weight_global[0] (an NVFP4 activation)
+// or 1, 0, 0} and, for FP8 weights, the scale plane's single value
+// (cuda_quant.cuh:36-39, 43).
 __global__ __launch_bounds__(256) void fp8_finish(const unsigned *partials, unsigned count, float *global,
-                                                  float *scale_slot) {
+                                                  float *scale_slot, float divisor, const float *weight_global) {
     unsigned best = 0;
     for (unsigned i = threadIdx.x; i < count; i += 256) best = max(best, partials[i]);
     for (int off = 32; off; off >>= 1) best = max(best, (unsigned)__shfl_xor((int)best, off, 64));
@@ -92,8 +96,9 @@ __global__ __launch_bounds__(256) void fp8_finish(const unsigned *partials, unsi
     __syncthreads();
     if (threadIdx.x == 0) {
         const float amax = bf16_to_f32((uint16_t)max(max(waves[0], waves[1]), max(waves[2], waves[3])));
-        const float scale = fmaxf(__fdiv_rn(amax, 448.f), 1e-20f);
-        global[0] = scale; global[1] = 1.f; global[2] = 0.f; global[3] = 0.f;
+        const float scale = fmaxf(__fdiv_rn(amax, divisor), 1e-20f);
+        global[0] = scale; global[1] = weight_global ? __fmul_rn(scale, weight_global[0]) : 1.f;
+        global[2] = 0.f; global[3] = 0.f;
         if (scale_slot) scale_slot[0] = scale;
     }
 }
@@ -129,9 +134,128 @@ int fp8_pack(h3_gpu *g, const uint16_t *x, size_t count, uint8_t *codes, unsigne
     const size_t chunks = count / 8;
     const unsigned grid = pack_grid(chunks);
     hipLaunchKernelGGL(fp8_amax, dim3(grid), dim3(256), 0, g->compute, x, chunks, partials, g->fault);
-    hipLaunchKernelGGL(fp8_finish, dim3(1), dim3(256), 0, g->compute, partials, grid, global, scale_slot);
+    hipLaunchKernelGGL(fp8_finish, dim3(1), dim3(256), 0, g->compute, partials, grid, global, scale_slot, 448.f,
+                       (const float *)nullptr);
     hipLaunchKernelGGL(fp8_encode, dim3(grid), dim3(256), 0, g->compute, x, chunks, global, codes);
     return h3_launch_status(g, "FP8 packing");
+}
+
+// ---------------------------------------------------------------- NVFP4
+// NVFP4 (cuda_quant.cuh:50-72): per 16-column block a UE4M3 scale
+// sf = E4M3(max(blockmax / (6 g), 2^-9)) and E2M1 codes of x / (sf g), both
+// round to nearest even; scales in cuBLASLt's VEC16 tiled layout. MI355X has no
+// NVFP4 matrix path (its FP4 MFMAs take E8M0 scales per 32 values), so the
+// projection dequantizes: a code times its block scale has at most 6
+// significant bits and is exact in BF16, and y = bf16(gx gw sum (x4 sfx)(w4 sfw))
+// runs on the BF16 GEMM with gx gw as its alpha.
+__host__ __device__ inline size_t nvfp4_scale_index(unsigned row, unsigned block, unsigned k) {
+    const unsigned tiles = (k / 16 + 3) / 4;
+    return ((size_t)(row / 128) * tiles + block / 4) * 512 + (row % 32) * 16 + ((row % 128) / 32) * 4 + block % 4;
+}
+
+// E2M1 code of |x| (ties to the even code, saturating at 6) with x's sign.
+__device__ inline uint8_t f32_to_e2m1(float x) {
+    const float a = fabsf(x);
+    uint8_t c;
+    if (a <= 0.25f) c = 0;
+    else if (a < 0.75f) c = 1;
+    else if (a <= 1.25f) c = 2;
+    else if (a < 1.75f) c = 3;
+    else if (a <= 2.5f) c = 4;
+    else if (a < 3.5f) c = 5;
+    else if (a <= 5.f) c = 6;
+    else c = 7;
+    return (__builtin_bit_cast(uint32_t, x) >> 28 & 8u) | c;
+}
+
+__device__ inline float e2m1_value(unsigned c) {
+    const float mag = (c & 7) < 2 ? (c & 7) * 0.5f : __builtin_ldexpf(1.f + ((c & 1) ? 0.5f : 0.f), (int)((c & 6) >> 1) - 1);
+    return (c & 8) ? -mag : mag;
+}
+
+__device__ inline float e4m3_value(uint8_t c) {
+    const unsigned e = (c >> 3) & 15u, m = c & 7u;
+    const float mag = e ? __builtin_ldexpf(1.f + m * 0.125f, (int)e - 7) : m * 0.001953125f;
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// One thread per (row, 16-column block). With codes/scales: the packed
+// descriptor (weights at load). With deq: the dequantized BF16 values code * sf
+// (activations per call; the global scale goes into the GEMM's alpha).
+__global__ __launch_bounds__(256) void nvfp4_pack(const uint16_t *x, unsigned rows, unsigned k, const float *global,
+                                                  uint8_t *codes, uint8_t *scales, uint16_t *deq) {
+    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const unsigned blocks = k / 16;
+    if (b >= (size_t)rows * blocks) return;
+    const unsigned row = (unsigned)(b / blocks), col = (unsigned)(b % blocks);
+    const u16x8 *src = reinterpret_cast<const u16x8 *>(x + (size_t)row * k + col * 16);
+    const u16x8 lo = src[0], hi = src[1];
+    float v[16], m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) { v[j] = bf16_to_f32(lo[j]); v[j + 8] = bf16_to_f32(hi[j]); }
+#pragma unroll
+    for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(v[j]));
+    const float g = global[0];
+    const uint8_t sf = f32_to_e4m3(fmaxf(__fdiv_rn(m, __fmul_rn(6.f, g)), 0.001953125f));
+    const float sv = e4m3_value(sf), r = __fdiv_rn(1.f, __fmul_rn(sv, g));
+    uint8_t c[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) c[j] = f32_to_e2m1(__fmul_rn(v[j], r));
+    if (codes) {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            w0 |= (uint32_t)(c[2 * j] | c[2 * j + 1] << 4) << (8 * j);
+            w1 |= (uint32_t)(c[8 + 2 * j] | c[8 + 2 * j + 1] << 4) << (8 * j);
+        }
+        *reinterpret_cast<uint2 *>(codes + b * 8) = make_uint2(w0, w1);
+        scales[nvfp4_scale_index(row, col, k)] = sf;
+    }
+    if (deq) {
+        u16x8 o0, o1;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            o0[j] = f32_to_bf16(e2m1_value(c[j]) * sv);
+            o1[j] = f32_to_bf16(e2m1_value(c[j + 8]) * sv);
+        }
+        u16x8 *dst = reinterpret_cast<u16x8 *>(deq + (size_t)row * k + col * 16);
+        dst[0] = o0; dst[1] = o1;
+    }
+}
+
+// BF16 values code * sf of a packed NVFP4 descriptor [n, k] (weights).
+__global__ __launch_bounds__(256) void nvfp4_dequant(const uint8_t *codes, const uint8_t *scales, unsigned n,
+                                                     unsigned k, uint16_t *out) {
+    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const unsigned blocks = k / 16;
+    if (b >= (size_t)n * blocks) return;
+    const unsigned row = (unsigned)(b / blocks), col = (unsigned)(b % blocks);
+    const float sv = e4m3_value(scales[nvfp4_scale_index(row, col, k)]);
+    const uint2 w = *reinterpret_cast<const uint2 *>(codes + b * 8);
+    u16x8 o0, o1;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        o0[j] = f32_to_bf16(e2m1_value((w.x >> (4 * j)) & 15u) * sv);
+        o1[j] = f32_to_bf16(e2m1_value((w.y >> (4 * j)) & 15u) * sv);
+    }
+    u16x8 *dst = reinterpret_cast<u16x8 *>(out + (size_t)row * k + col * 16);
+    dst[0] = o0; dst[1] = o1;
+}
+
+// NVFP4-packs count = rows * k BF16 values: global g from the tensor's max,
+// then codes and tiled scales (weights, weight_global null) or the dequantized
+// BF16 values (activations, alpha = g * weight_global[0] in global[1]).
+int nvfp4_pack_all(h3_gpu *g, const uint16_t *x, unsigned rows, unsigned k, unsigned *partials, float *global,
+                   const float *weight_global, uint8_t *codes, uint8_t *scales, uint16_t *deq) {
+    const size_t count = (size_t)rows * k, chunks = count / 8;
+    const unsigned grid = pack_grid(chunks);
+    hipLaunchKernelGGL(fp8_amax, dim3(grid), dim3(256), 0, g->compute, x, chunks, partials, g->fault);
+    hipLaunchKernelGGL(fp8_finish, dim3(1), dim3(256), 0, g->compute, partials, grid, global, (float *)nullptr,
+                       2688.f, weight_global);
+    const size_t blocks = count / 16;
+    hipLaunchKernelGGL(nvfp4_pack, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, g->compute, x, rows, k,
+                       (const float *)global, codes, scales, deq);
+    return h3_launch_status(g, "NVFP4 packing");
 }
 
 // ---------------------------------------------------------------- GEMM
@@ -329,6 +453,7 @@ struct Mapping {
 // copies it back: packed receives `bytes` bytes.
 int prepare_packed(h3_gpu *g, const uint16_t *source, uint32_t n, uint32_t k, size_t bytes, size_t scale,
                    size_t global, unsigned char *packed) {
+    const int mode = g->quant_mode;
     const size_t count = (size_t)n * k, partial_bytes = MAX_PARTIALS * 4;
     void *staging = nullptr, *device = nullptr, *partials = nullptr;
     int ok = h3_hip_check(g, hipMalloc(&staging, count * 2), "quantization source upload") &&
@@ -337,8 +462,12 @@ int prepare_packed(h3_gpu *g, const uint16_t *source, uint32_t n, uint32_t k, si
              h3_hip_check(g, hipMemcpyAsync(staging, source, count * 2, hipMemcpyHostToDevice, g->compute),
                           "quantization source upload") &&
              h3_hip_check(g, hipMemsetAsync(device, 0, bytes, g->compute), "packed weight initialization") &&
-             fp8_pack(g, (const uint16_t *)staging, count, (uint8_t *)device, (unsigned *)partials,
-                      (float *)((char *)device + global), (float *)((char *)device + scale)) &&
+             (mode == H3_QUANT_FP8
+                  ? fp8_pack(g, (const uint16_t *)staging, count, (uint8_t *)device, (unsigned *)partials,
+                             (float *)((char *)device + global), (float *)((char *)device + scale))
+                  : nvfp4_pack_all(g, (const uint16_t *)staging, n, k, (unsigned *)partials,
+                                   (float *)((char *)device + global), nullptr, (uint8_t *)device,
+                                   (uint8_t *)device + scale, nullptr)) &&
              h3_hip_check(g, hipStreamSynchronize(g->compute), "prepare quantized weight") &&
              h3_hip_check(g, hipMemcpy(packed, device, bytes, hipMemcpyDeviceToHost), "download packed artifact");
     if (staging) hipFree(staging);
@@ -350,15 +479,41 @@ int prepare_packed(h3_gpu *g, const uint16_t *source, uint32_t n, uint32_t k, si
     return ok && h3_gpu_synchronize(g);
 }
 
+// The BF16 values code * sf of a resident NVFP4 weight, kept beside its
+// descriptor for the GEMM.
+int nvfp4_resident_dequant(h3_gpu *g, h3_gpu_tensor *t) {
+    const size_t count = (size_t)t->quant_n * t->quant_k;
+    if (!h3_hip_check(g, hipMalloc(&t->quant_dequant, count * 2 + 256), "NVFP4 dequantized weight")) {
+        t->quant_dequant = nullptr;
+        return 0;
+    }
+    const size_t blocks = count / 16;
+    hipLaunchKernelGGL(nvfp4_dequant, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, g->compute,
+                       (const uint8_t *)t->data, (const uint8_t *)t->data + t->quant_scale, t->quant_n, t->quant_k,
+                       (uint16_t *)t->quant_dequant);
+    return h3_launch_status(g, "NVFP4 dequantization") && h3_hip_check(g, hipStreamSynchronize(g->compute), "NVFP4 dequantization");
+}
+
 h3_gpu_tensor *finish_weight(h3_gpu *g, std::vector<unsigned char> &packed, uint32_t n, uint32_t k, size_t scale,
                              size_t global, bool hit) {
-    float gs, ss;
+    const int mode = g->quant_mode;
+    float gs;
     memcpy(&gs, packed.data() + global, 4);
     if (!std::isfinite(gs) || gs <= 0) { h3_set_error(g, "invalid quantized weight global scale"); return nullptr; }
-    memcpy(&ss, packed.data() + scale, 4);
-    if (ss != gs) { h3_set_error(g, "invalid FP8 weight scale"); return nullptr; }
-    for (size_t i = 0; i < (size_t)n * k; i++)
-        if ((packed[i] & 0x7f) == 0x7f) { h3_set_error(g, "nonfinite FP8 weight"); return nullptr; }
+    if (mode == H3_QUANT_FP8) {
+        float ss;
+        memcpy(&ss, packed.data() + scale, 4);
+        if (ss != gs) { h3_set_error(g, "invalid FP8 weight scale"); return nullptr; }
+        for (size_t i = 0; i < (size_t)n * k; i++)
+            if ((packed[i] & 0x7f) == 0x7f) { h3_set_error(g, "nonfinite FP8 weight"); return nullptr; }
+    } else {
+        const size_t plane = (size_t)(n + 127) / 128 * 128 * ((k / 16 + 3) / 4 * 4);
+        for (size_t i = 0; i < plane; i++)
+            if (!packed[scale + i] || packed[scale + i] >= 127) {
+                h3_set_error(g, "invalid NVFP4 weight block scale");
+                return nullptr;
+            }
+    }
     const h3_gpu_storage storage = g->quant->streaming ? H3_GPU_HOST_PINNED : H3_GPU_DEVICE_ONLY;
     h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, packed.size(), H3_GPU_I8, storage);
     if (!t) return nullptr;
@@ -372,7 +527,11 @@ h3_gpu_tensor *finish_weight(h3_gpu *g, std::vector<unsigned char> &packed, uint
     }
     if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
     t->elements = (size_t)n * k;
-    t->quant_mode = H3_QUANT_FP8; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    t->quant_mode = mode; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    if (mode == H3_QUANT_NVFP4 && storage == H3_GPU_DEVICE_ONLY && !nvfp4_resident_dequant(g, t)) {
+        h3_gpu_tensor_free(t);
+        return nullptr;
+    }
     if (hit) g->stats.quant_cache_hits++; else g->stats.quant_cache_misses++;
     return t;
 }
@@ -400,7 +559,7 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
     unsigned char source_hash[32];
     sha256_of(map.data(), source_bytes, source_hash);
     const std::string artifact = g->quant->cache + "/v" + std::to_string(H3_QUANT_VERSION) + "-" +
-                                 h3_quant_name(H3_QUANT_FP8) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
+                                 h3_quant_name(g->quant_mode) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
                                  hex32(source_hash) + ".h3q";
     int lock = open((artifact + ".lock").c_str(), O_CREAT | O_RDWR, 0600);
     if (lock < 0 || flock(lock, LOCK_EX) != 0) {
@@ -415,7 +574,7 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
     if (fd >= 0) {
         ok = fstat(fd, &st) == 0 && (uint64_t)st.st_size == 128 + bytes && file_io(fd, header, 128, false) &&
              memcmp(header, "H3QWT001", 8) == 0 && get_le(header + 8, 4) == H3_QUANT_VERSION &&
-             get_le(header + 12, 4) == H3_QUANT_FP8 && get_le(header + 16, 4) == n && get_le(header + 20, 4) == k &&
+             get_le(header + 12, 4) == (unsigned)g->quant_mode && get_le(header + 16, 4) == n && get_le(header + 20, 4) == k &&
              get_le(header + 24, 8) == bytes && get_le(header + 32, 8) == scale && get_le(header + 40, 8) == global &&
              memcmp(header + 48, source_hash, 32) == 0 && file_io(fd, packed.data(), bytes, false);
         close(fd);
@@ -440,7 +599,7 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
         if (ok) {
             memset(header, 0, sizeof(header));
             memcpy(header, "H3QWT001", 8);
-            put_le(header + 8, H3_QUANT_VERSION, 4); put_le(header + 12, H3_QUANT_FP8, 4);
+            put_le(header + 8, H3_QUANT_VERSION, 4); put_le(header + 12, (unsigned)g->quant_mode, 4);
             put_le(header + 16, n, 4); put_le(header + 20, k, 4);
             put_le(header + 24, bytes, 8); put_le(header + 32, scale, 8); put_le(header + 40, global, 8);
             memcpy(header + 48, source_hash, 32);
@@ -475,7 +634,7 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
 // only opened on a miss.
 h3_gpu_tensor *load_metadata(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
                              size_t scale, size_t global) {
-    h3_quant_cache *cache = h3_quant_cache_open(g->quant->cache.c_str(), path, offset, n, k, H3_QUANT_FP8, bytes,
+    h3_quant_cache *cache = h3_quant_cache_open(g->quant->cache.c_str(), path, offset, n, k, g->quant_mode, bytes,
                                                 scale, global, g->error, sizeof(g->error));
     if (!cache) return nullptr;
     std::vector<unsigned char> packed(bytes);
@@ -509,6 +668,8 @@ void h3_quant_destroy(h3_gpu *g) {
     if (!g->quant) return;
     h3_buffer_free(&g->quant->activation);
     h3_buffer_free(&g->quant->streamed);
+    h3_buffer_free(&g->quant->dequant_x);
+    h3_buffer_free(&g->quant->dequant_w);
     delete g->quant;
     g->quant = nullptr;
 }
@@ -522,13 +683,9 @@ extern "C" int h3_quant_preflight(int mode, char *error, size_t size) {
         if (error && size) snprintf(error, size, "cannot query HIP quantization device");
         return 0;
     }
-    if (mode == H3_QUANT_NVFP4) {
-        if (error && size) snprintf(error, size, "cuda-denoise-quant nvfp4 is not available on the HIP backend (fp8 is)");
-        return 0;
-    }
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         if (error && size)
-            snprintf(error, size, "cuda-denoise-quant fp8 requires gfx950 FP8 matrix cores (MI355X) (device %s)",
+            snprintf(error, size, "cuda-denoise-quant %s requires gfx950 (MI355X) (device %s)", h3_quant_name(mode),
                      prop.gcnArchName);
         return 0;
     }
@@ -611,6 +768,30 @@ int h3_quant_gemm(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const 
         g->stats.streamed_bytes += w->bytes;
         weight = (const uint8_t *)g->quant->streamed.ptr;
     }
+    if (w->quant_mode == H3_QUANT_NVFP4) {
+        // Activation quantized and dequantized in one pass (BF16 code * sf), the
+        // weight's BF16 values (resident, or dequantized from the streamed
+        // copy), alpha = gx * gw.
+        if (!h3_buffer_reserve(g, &g->quant->dequant_x, count * 2 + 256, "NVFP4 activation")) return 0;
+        const uint16_t *wdeq = (const uint16_t *)w->quant_dequant;
+        if (!wdeq) {
+            const size_t wcount = (size_t)n * k;
+            if (!h3_buffer_reserve(g, &g->quant->dequant_w, wcount * 2 + 256, "NVFP4 streamed weight")) return 0;
+            hipLaunchKernelGGL(nvfp4_dequant, dim3((unsigned)((wcount / 16 + 255) / 256)), dim3(256), 0, g->compute,
+                               weight, weight + w->quant_scale, n, k, (uint16_t *)g->quant->dequant_w.ptr);
+            if (!h3_launch_status(g, "NVFP4 dequantization")) return 0;
+            wdeq = (const uint16_t *)g->quant->dequant_w.ptr;
+        }
+        if (!nvfp4_pack_all(g, (const uint16_t *)in->data, rows, k, partials, global,
+                            (const float *)(weight + w->quant_global), nullptr, nullptr,
+                            (uint16_t *)g->quant->dequant_x.ptr) ||
+            !h3_gemm_bf16_alpha(g, (uint16_t *)out->data, (const uint16_t *)g->quant->dequant_x.ptr, wdeq, global + 1,
+                                rows, k, n))
+            return 0;
+        g->stats.quant_projection_dispatches++;
+        g->stats.linear_dispatches++;
+        return 1;
+    }
     if (!fp8_pack(g, (const uint16_t *)in->data, count, base, partials, global, nullptr)) return 0;
     Fp8Args a;
     a.y = (uint16_t *)out->data; a.x = base; a.w = weight;
@@ -622,30 +803,36 @@ int h3_quant_gemm(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in, const 
     return 1;
 }
 
-// A resident packed FP8 weight from n x k BF16 device values (the descriptor
-// h3_gpu_quant_load builds, without a file or an artifact): synthetic models
-// and benchmarks. Needs h3_gpu_quant_configure(mode 1).
-extern "C" h3_gpu_tensor *h3_hip_fp8_weight_from_bf16(h3_gpu *g, const h3_gpu_tensor *w, uint32_t n, uint32_t k) {
+// A resident packed weight of the configured mode (FP8 or NVFP4) from n x k
+// BF16 device values: the descriptor h3_gpu_quant_load builds, without a file
+// or an artifact, for synthetic models and benchmarks.
+extern "C" h3_gpu_tensor *h3_hip_quant_weight_from_bf16(h3_gpu *g, const h3_gpu_tensor *w, uint32_t n, uint32_t k) {
     if (!g) return nullptr;
-    if (g->quant_mode != H3_QUANT_FP8 || !n || !k || n % 128 || k % 128 || (uint64_t)n * k > UINT32_MAX) {
+    const int mode = g->quant_mode;
+    if (!mode || !n || !k || n % 128 || k % 128 || (uint64_t)n * k > UINT32_MAX) {
         h3_set_error(g, "quantized weight shape must be nonzero and a multiple of 128");
         return nullptr;
     }
-    if (!h3_require(g, w, H3_GPU_BF16, (size_t)n * k, "FP8 weight source")) return nullptr;
+    if (!h3_require(g, w, H3_GPU_BF16, (size_t)n * k, "quantized weight source")) return nullptr;
     uint64_t scale, global, bytes;
-    h3_weight_packed_size(n, k, H3_QUANT_FP8, &scale, &global, &bytes);
+    h3_weight_packed_size(n, k, mode, &scale, &global, &bytes);
     h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, bytes, H3_GPU_I8, H3_GPU_DEVICE_ONLY);
     if (!t) return nullptr;
     void *partials = nullptr;
-    int ok = h3_hip_check(g, hipMalloc(&partials, MAX_PARTIALS * 4), "FP8 weight maxima") &&
+    uint8_t *base = (uint8_t *)t->data;
+    int ok = h3_hip_check(g, hipMalloc(&partials, MAX_PARTIALS * 4), "quantized weight maxima") &&
              h3_hip_check(g, hipMemsetAsync(t->data, 0, bytes, g->compute), "packed weight initialization") &&
-             fp8_pack(g, (const uint16_t *)w->data, (size_t)n * k, (uint8_t *)t->data, (unsigned *)partials,
-                      (float *)((char *)t->data + global), (float *)((char *)t->data + scale)) &&
-             h3_hip_check(g, hipStreamSynchronize(g->compute), "FP8 weight");
+             (mode == H3_QUANT_FP8
+                  ? fp8_pack(g, (const uint16_t *)w->data, (size_t)n * k, base, (unsigned *)partials,
+                             (float *)(base + global), (float *)(base + scale))
+                  : nvfp4_pack_all(g, (const uint16_t *)w->data, n, k, (unsigned *)partials, (float *)(base + global),
+                                   nullptr, base, base + scale, nullptr)) &&
+             h3_hip_check(g, hipStreamSynchronize(g->compute), "quantized weight");
     if (partials) hipFree(partials);
     if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
     t->elements = (size_t)n * k;
-    t->quant_mode = H3_QUANT_FP8; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    t->quant_mode = mode; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
+    if (mode == H3_QUANT_NVFP4 && !nvfp4_resident_dequant(g, t)) { h3_gpu_tensor_free(t); return nullptr; }
     return t;
 }
 

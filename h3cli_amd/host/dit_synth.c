@@ -197,7 +197,7 @@ static h3_gpu_tensor *q8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed
 static h3_gpu_tensor *fp8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed) {
     h3_gpu_tensor *b = normal_tensor(g, (size_t)n * k, seed, 1.0f / sqrtf((float)k), 0.f);
     if (!b) return NULL;
-    h3_gpu_tensor *t = h3_gpu_synchronize(g) ? h3_hip_fp8_weight_from_bf16(g, b, n, k) : NULL;
+    h3_gpu_tensor *t = h3_gpu_synchronize(g) ? h3_hip_quant_weight_from_bf16(g, b, n, k) : NULL;
     h3_gpu_tensor_free(b);
     return t;
 }

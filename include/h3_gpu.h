@@ -139,8 +139,9 @@ void h3_gpu_event_free(h3_gpu_event *event);                    /* gpu.h:33 */
 /* ---- quantized projection weights -------------------------------------- */
 /* gpu.h:44 (reference src/cuda/cuda_quant.cuh:120-162). mode 0 = BF16
  * projections (no cache is touched), 1 = FP8 W8A8 (tensorwide E4M3 weights
- * and activations, FP32 accumulation, BF16 output); 2 (NVFP4) fails
- * h3_quant_preflight. cache: artifact directory (NULL: $HOME/.cache/h3/
+ * and activations, FP32 accumulation, BF16 output), 2 = NVFP4 W4A4 (E2M1 with
+ * UE4M3 scales per 16 values and a tensorwide scale; the same packed format,
+ * multiplied as exact BF16 dequantized values). cache: artifact directory (NULL: $HOME/.cache/h3/
  * denoise-quant), created if missing. bf16_weights: BF16 bytes of whole H3
  * blocks' four projections, for the resident/streamed plan; force_stream
  * keeps packed weights in pinned host memory. */

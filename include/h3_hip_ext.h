@@ -102,10 +102,11 @@ int h3_hip_sha256(const void *data, size_t bytes, uint8_t digest[32]);
  * 16-byte global slot {scale, 1, 0, 0}. Waits for the stream. */
 int h3_hip_fp8_pack(h3_gpu *gpu, const h3_gpu_tensor *x, h3_gpu_tensor *codes, h3_gpu_tensor *global,
                     size_t count);
-/* A resident packed FP8 weight (the h3_gpu_quant_load descriptor) from n x k
- * BF16 device values, without a file or artifact, for synthetic models and
- * benchmarks. Requires h3_gpu_quant_configure(mode 1); n, k multiples of 128. */
-h3_gpu_tensor *h3_hip_fp8_weight_from_bf16(h3_gpu *gpu, const h3_gpu_tensor *w, uint32_t n, uint32_t k);
+/* A resident packed weight of the configured quantization mode (FP8 or NVFP4;
+ * the h3_gpu_quant_load descriptor) from n x k BF16 device values, without a
+ * file or artifact, for synthetic models and benchmarks. Requires
+ * h3_gpu_quant_configure(mode 1 or 2); n, k multiples of 128. */
+h3_gpu_tensor *h3_hip_quant_weight_from_bf16(h3_gpu *gpu, const h3_gpu_tensor *w, uint32_t n, uint32_t k);
 
 /* Sage quantization of sequence-major BF16 Q, K, V [seq, heads, 128] into the
  * layouts the quantized attention kernel consumes (all head-major, rows padded

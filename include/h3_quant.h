@@ -31,8 +31,8 @@ unsigned h3_quant_execution_recipe(int mode, int adaptive_cache, int attention);
 int h3_quant_projection_policy(const char *name, int requested, int adaptive_cache);
 h3_quant_scope h3_quant_exchange(h3_quant_scope next);              /* thread-local; returns the previous */
 h3_quant_scope h3_quant_current(void);
-/* Backend capability: mode 0 always; mode 1 (FP8) on a gfx950 device; mode 2
- * (NVFP4) is not available on this backend. */
+/* Backend capability: mode 0 always; modes 1 (FP8) and 2 (NVFP4, computed by
+ * exact dequantization to BF16) on a gfx950 device. */
 int h3_quant_preflight(int mode, char *error, size_t size);
 
 #ifdef __cplusplus

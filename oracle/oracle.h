@@ -127,4 +127,11 @@ int oracle_threads(void);
 int oracle_fp8_pack(uint8_t *codes, float *scale_out, const uint16_t *x, size_t count, size_t padded_count);
 void oracle_fp8_gemm(uint16_t *y, const uint8_t *x8, float sx, const uint8_t *w8, float sw, unsigned m, unsigned n,
                      unsigned k);
+float oracle_e2m1_to_f32(uint8_t c);
+uint8_t oracle_f32_to_e2m1(float x);
+size_t oracle_nvfp4_scale_index(unsigned row, unsigned block, unsigned k);
+int oracle_nvfp4_pack(uint8_t *codes, uint8_t *scales, float *global_out, const uint16_t *x, unsigned rows,
+                      unsigned padded, unsigned k, float weight_global);
+void oracle_nvfp4_gemm(uint16_t *y, const uint8_t *x4, const uint8_t *xs, const uint8_t *w4, const uint8_t *ws,
+                       float alpha, unsigned m, unsigned n, unsigned k);
 #endif

@@ -382,3 +382,47 @@ def fp8_gemm(x8, sx, w8, sw, m, n, k):
     lib.oracle_fp8_gemm(_ptr(y), _ptr(np.ascontiguousarray(x8, np.uint8)), float(sx),
                         _ptr(np.ascontiguousarray(w8, np.uint8)), float(sw), m, n, k)
     return y.reshape(m, n)
+
+
+def nvfp4_scale_bytes(rows, k):
+    """Bytes of the VEC16 tiled scale plane (cuda_quant.cuh:14-16)."""
+    return ((rows + 127) // 128 * 128) * ((k // 16 + 3) // 4 * 4)
+
+
+def nvfp4_pack(x, rows, k, padded=None, weight_global=0.0):
+    """NVFP4 packing (cuda_quant.cuh:50-72). Returns (codes u8 [padded*k/2],
+    scales u8 tiled plane, global f32[4], nonfinite)."""
+    x = _u16(x).reshape(-1)
+    padded = rows if padded is None else padded
+    codes = np.zeros(padded * k // 2, np.uint8)
+    scales = np.zeros(nvfp4_scale_bytes(padded, k), np.uint8)
+    glob = np.zeros(4, np.float32)
+    lib = load()
+    lib.oracle_nvfp4_pack.restype = C.c_int
+    lib.oracle_nvfp4_pack.argtypes = [_p, _p, _p, _p, _u, _u, _u, C.c_float]
+    bad = lib.oracle_nvfp4_pack(_ptr(codes), _ptr(scales), _ptr(glob), _ptr(x), rows, padded, k, float(weight_global))
+    return codes, scales, glob, bool(bad)
+
+
+def nvfp4_gemm(x4, xs, w4, ws, alpha, m, n, k):
+    y = np.zeros(m * n, np.uint16)
+    lib = load()
+    lib.oracle_nvfp4_gemm.argtypes = [_p, _p, _p, _p, _p, C.c_float, _u, _u, _u]
+    lib.oracle_nvfp4_gemm(_ptr(y), _ptr(np.ascontiguousarray(x4, np.uint8)), _ptr(np.ascontiguousarray(xs, np.uint8)),
+                          _ptr(np.ascontiguousarray(w4, np.uint8)), _ptr(np.ascontiguousarray(ws, np.uint8)),
+                          float(alpha), m, n, k)
+    return y.reshape(m, n)
+
+
+def e2m1_decode(codes):
+    lib = load()
+    lib.oracle_e2m1_to_f32.restype = C.c_float
+    lib.oracle_e2m1_to_f32.argtypes = [C.c_uint8]
+    return np.array([lib.oracle_e2m1_to_f32(int(c)) for c in np.asarray(codes).reshape(-1)], np.float32)
+
+
+def nvfp4_scale_index(row, block, k):
+    lib = load()
+    lib.oracle_nvfp4_scale_index.restype = C.c_size_t
+    lib.oracle_nvfp4_scale_index.argtypes = [_u, _u, _u]
+    return lib.oracle_nvfp4_scale_index(row, block, k)

@@ -36,20 +36,32 @@ def write_weight(path, w, offset=0):
         f.write(np.ascontiguousarray(w, np.uint16).tobytes())
 
 
-def packed_size(rows, cols):
+def packed_size(rows, cols, mode=1):
     lib = _lib.load()
     s, g, b = C.c_uint64(), C.c_uint64(), C.c_uint64()
     lib.h3_weight_packed_size.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [C.POINTER(C.c_uint64)] * 3
-    assert lib.h3_weight_packed_size(rows, cols, 1, C.byref(s), C.byref(g), C.byref(b))
+    assert lib.h3_weight_packed_size(rows, cols, mode, C.byref(s), C.byref(g), C.byref(b))
     return s.value, g.value, b.value
 
 
-def load(g, path, n, k, offset=0):
+def load(g, path, n, k, offset=0, mode=1):
     h = g.lib.h3_gpu_quant_load(g.handle, str(path).encode(), offset, n, k)
     if not h:
         raise H3Error(g.error())
-    scale, glob, nbytes = packed_size(n, k)
+    scale, glob, nbytes = packed_size(n, k, mode)
     return g._track(h, nbytes, _lib.I8)
+
+
+def nvfp4_descriptor(w, n, k):
+    """The reference's NVFP4 descriptor: codes, the tiled UE4M3 scale plane at
+    `scale`, {g, 1, 0, 0} at `global` (cuda_quant.cuh:88-104)."""
+    scale, glob, nbytes = packed_size(n, k, 2)
+    codes, scales, g, _ = oracle.nvfp4_pack(w, n, k)
+    out = np.zeros(nbytes, np.uint8)
+    out[:n * k // 2] = codes
+    out[scale:scale + scales.size] = scales
+    out[glob:glob + 16] = g.view(np.uint8)
+    return out, g
 
 
 def descriptor(w, n, k):
@@ -100,10 +112,11 @@ def test_pack_bit_exact():
         assert glob[0] == np.float32(1e-20) and not codes.any()
 
 
-def test_reference_exact_pattern(tmp_path):
-    """tests/quant_native.c:29-66: pattern weights and inputs, row counts
-    1/17/129/3 bit-equal to bf16 of the exact sum; a second load hits the
-    artifact cache; zero input gives zeros."""
+@pytest.mark.parametrize("mode", [1, 2], ids=["fp8", "nvfp4"])
+def test_reference_exact_pattern(tmp_path, mode):
+    """tests/quant_native.c:29-66 (run there for fp8 and nvfp4): pattern
+    weights and inputs, row counts 1/17/129/3 bit-equal to bf16 of the exact
+    sum; a second load hits the artifact cache; zero input gives zeros."""
     n, k, rows = 256, 256, 129
     j, c = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
     w = synth.f32_to_bf16(np.ldexp(1.0, (j % 3) - 1 + (c // 16) % 3).astype(np.float32)).reshape(-1)
@@ -114,15 +127,15 @@ def test_reference_exact_pattern(tmp_path):
     path = tmp_path / "w.bin"
     write_weight(path, w)
     with Gpu() as g:
-        g.check(configure(g, tmp_path / "cache"), "configure")
-        weight = load(g, path, n, k)
+        g.check(configure(g, tmp_path / "cache", mode=mode), "configure")
+        weight = load(g, path, n, k, mode=mode)
         assert stats(g).quant_cache_misses == 1
         xin, out = g.from_bf16(x), g.empty(rows * n)
         for count in (1, 17, 129, 3):
-            say(f"pattern rows={count}")
+            say(f"pattern mode={mode} rows={count}")
             assert np.array_equal(linear(g, out, xin, weight, count, k, n), want[:count]), count
         g.free(weight)
-        weight = load(g, path, n, k)
+        weight = load(g, path, n, k, mode=mode)
         st = stats(g)
         assert st.quant_cache_hits == 1 and st.quant_cache_misses == 1 and st.quant_projection_dispatches == 4
         assert np.array_equal(linear(g, out, xin, weight, rows, k, n), want)
@@ -130,7 +143,8 @@ def test_reference_exact_pattern(tmp_path):
         assert not (linear(g, out, zero, weight, rows, k, n) & 0x7fff).any()
 
 
-def test_descriptor_and_metadata_artifact(tmp_path):
+@pytest.mark.parametrize("mode", [1, 2], ids=["fp8", "nvfp4"])
+def test_descriptor_and_metadata_artifact(tmp_path, mode):
     """The loaded weight is the reference's packed descriptor byte for byte,
     and the H3QMT002 artifact is its 128-byte header plus that payload."""
     rng = np.random.default_rng(2)
@@ -140,19 +154,19 @@ def test_descriptor_and_metadata_artifact(tmp_path):
     write_weight(path, w, offset)
     cache = tmp_path / "cache"
     with Gpu() as g:
-        g.check(configure(g, cache), "configure")
-        weight = load(g, path, n, k, offset)
-        want, _ = descriptor(w, n, k)
+        g.check(configure(g, cache, mode=mode), "configure")
+        weight = load(g, path, n, k, offset, mode=mode)
+        want, _ = descriptor(w, n, k) if mode == 1 else nvfp4_descriptor(w, n, k)
         assert np.array_equal(weight.read_bytes(), want)
     names = [f for f in os.listdir(cache) if f.endswith(".h3q")]
-    assert len(names) == 1 and names[0].startswith(f"m2-fp8-{n}x{k}-")
+    assert len(names) == 1 and names[0].startswith(f"m2-{['', 'fp8', 'nvfp4'][mode]}-{n}x{k}-")
     data = (cache / names[0]).read_bytes()
     h = np.frombuffer(data[:128], np.uint8)
-    scale, glob, nbytes = packed_size(n, k)
+    scale, glob, nbytes = packed_size(n, k, mode)
     assert data[:8] == b"H3QMT002" and len(data) == 128 + nbytes
     u32 = lambda o: int.from_bytes(data[o:o + 4], "little")
     u64 = lambda o: int.from_bytes(data[o:o + 8], "little")
-    assert (u32(8), u32(12), u32(16), u32(20), u32(24)) == (2, 2, 1, n, k)
+    assert (u32(8), u32(12), u32(16), u32(20), u32(24)) == (2, 2, mode, n, k)
     assert (u64(32), u64(40), u64(48), u64(88)) == (nbytes, scale, glob, offset)
     assert data[56:88].hex() == names[0].split("-")[-1][:-4] and not h[96:].any()
     assert np.array_equal(np.frombuffer(data[128:], np.uint8), want)
@@ -240,7 +254,8 @@ def test_gemm_against_oracle(tmp_path, m, n, k):
         assert np.array_equal(yt.view(torch.int16).cpu().numpy().view(np.uint16), got)
 
 
-def test_streamed_weights_equal_resident(tmp_path):
+@pytest.mark.parametrize("mode", [1, 2], ids=["fp8", "nvfp4"])
+def test_streamed_weights_equal_resident(tmp_path, mode):
     rng = np.random.default_rng(4)
     m, n, k = 200, 512, 256
     w = synth.f32_to_bf16((rng.standard_normal(n * k) * 0.05).astype(np.float32))
@@ -250,12 +265,12 @@ def test_streamed_weights_equal_resident(tmp_path):
     outs = []
     for force in (0, 1):
         with Gpu() as g:
-            g.check(configure(g, tmp_path / "cache", force_stream=force), "configure")
-            weight = load(g, path, n, k)
+            g.check(configure(g, tmp_path / "cache", mode=mode, force_stream=force), "configure")
+            weight = load(g, path, n, k, mode=mode)
             outs.append(linear(g, g.empty(m * n), g.from_bf16(x), weight, m, k, n))
             if force:
                 st = stats(g)
-                assert st.streamed_bytes >= packed_size(n, k)[2] and st.quant_cache_hits == 1
+                assert st.streamed_bytes >= packed_size(n, k, mode)[2] and st.quant_cache_hits == 1
     assert np.array_equal(outs[0], outs[1])
 
 
@@ -265,7 +280,7 @@ def test_errors_and_nonfinite(tmp_path):
     path = tmp_path / "w.bin"
     write_weight(path, w)
     with Gpu() as g:
-        assert not configure(g, tmp_path / "c", mode=2) and "nvfp4" in g.error()
+        assert not configure(g, tmp_path / "c", mode=3) and "quantization device" in g.error()
         assert not configure(g, tmp_path / "c", weights=BLOCK_BYTES + 2) and "geometry" in g.error()
         assert configure(g, tmp_path / "c", mode=0)
         assert not g.lib.h3_gpu_quant_load(g.handle, str(path).encode(), 0, n, k)     # not configured
@@ -298,3 +313,35 @@ def test_errors_and_nonfinite(tmp_path):
         g.check(configure(g, tmp_path / "c2"), "configure")
         with pytest.raises(H3Error, match="nonfinite"):
             load(g, tmp_path / "bad.bin", n, k)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 384), (7, 256, 256), (257, 768, 1024)])
+def test_nvfp4_gemm_against_oracle(tmp_path, m, n, k):
+    """NVFP4 projections: the activation packs exactly as the oracle does
+    (weight descriptor checks pin the packer), and y = bf16(gx gw sum (x4 sfx)
+    (w4 sfw)) is within one BF16 step plus FP32 accumulation in another order
+    (k 2^-24 alpha sum|x w|) of the oracle's exact sum."""
+    say(f"nvfp4 gemm m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 11 + n)
+    w = synth.f32_to_bf16((rng.standard_normal(n * k) * 0.03).astype(np.float32))
+    x = synth.f32_to_bf16((rng.standard_normal(m * k) * 1.5).astype(np.float32))
+    path = tmp_path / "w.bin"
+    write_weight(path, w)
+    with Gpu() as g:
+        g.check(configure(g, tmp_path / "cache", mode=2), "configure")
+        weight = load(g, path, n, k, mode=2)
+        got = linear(g, g.empty(m * n), g.from_bf16(x), weight, m, k, n)
+    w4, ws, wg, _ = oracle.nvfp4_pack(w, n, k)
+    x4, xs, xg, _ = oracle.nvfp4_pack(x, m, k, weight_global=wg[0])
+    want = oracle.nvfp4_gemm(x4, xs, w4, ws, xg[1], m, n, k)
+    dx = (oracle.e2m1_decode(np.stack([x4 & 15, x4 >> 4], 1).reshape(-1)).reshape(m, k // 16, 16) *
+          oracle.e4m3_decode(xs)[[oracle.nvfp4_scale_index(r, b, k) for r in range(m) for b in range(k // 16)]]
+          .reshape(m, k // 16, 1)).reshape(m, k)
+    dw = (oracle.e2m1_decode(np.stack([w4 & 15, w4 >> 4], 1).reshape(-1)).reshape(n, k // 16, 16) *
+          oracle.e4m3_decode(ws)[[oracle.nvfp4_scale_index(r, b, k) for r in range(n) for b in range(k // 16)]]
+          .reshape(n, k // 16, 1)).reshape(n, k)
+    mag = np.abs(dx.astype(np.float64)) @ np.abs(dw.astype(np.float64)).T * float(xg[1])
+    g32, w32 = synth.bf16_to_f32(got).astype(np.float64), synth.bf16_to_f32(want).astype(np.float64)
+    bound = 2.0 ** -7 * np.maximum(np.abs(g32), np.abs(w32)) + k * 2.0 ** -24 * mag
+    assert np.all(np.abs(g32 - w32) <= bound), np.max(np.abs(g32 - w32) - bound)
+    assert (got == want).mean() > 0.95, (got == want).mean()

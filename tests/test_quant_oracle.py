@@ -2,6 +2,8 @@
 E4M3 packing against torch's float8_e4m3fn cast, its scale closed forms, and
 the GEMM against a float64 matrix product of torch-decoded codes; plus the
 reference's exact-pattern case (tests/quant_native.c:29-52)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -78,3 +80,83 @@ def test_reference_exact_pattern():
     got = oracle.fp8_gemm(x8, sx, w8, sw, rows, n, k)
     exact = synth.bf16_to_f32(x).reshape(rows, k).astype(np.float64) @ synth.bf16_to_f32(w).reshape(n, k).astype(np.float64).T
     assert np.array_equal(got, synth.f32_to_bf16(exact.astype(np.float32)))
+
+
+def test_e2m1_encoder_closed_forms():
+    """E2M1 values {0, .5, 1, 1.5, 2, 3, 4, 6}: exact values, every midpoint
+    tied to the even code, saturation at 6, the sign bit."""
+    values = [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+    assert list(oracle.e2m1_decode(np.arange(16))) == values + [-v for v in values]
+    enc = lambda x: int(oracle.load().oracle_f32_to_e2m1(C.c_float(x)))
+    oracle.load().oracle_f32_to_e2m1.argtypes = [C.c_float]
+    oracle.load().oracle_f32_to_e2m1.restype = C.c_uint8
+    for c, v in enumerate(values):
+        assert enc(v) == c
+    ties = {0.25: 0, 0.75: 2, 1.25: 2, 1.75: 4, 2.5: 4, 3.5: 6, 5.0: 6}
+    for x, c in ties.items():
+        assert enc(x) == c, x
+    assert enc(0.26) == 1 and enc(5.01) == 7 and enc(7.0) == 7 and enc(1e9) == 7
+    assert enc(-0.75) == 8 | 2 and enc(-6.0) == 15
+
+
+def test_nvfp4_scale_layout_is_a_bijection():
+    """Every (row, block) of padded rows x blocks padded to 4 maps to its own
+    byte of the plane, 512-byte tiles hold 128 rows x 4 blocks."""
+    for rows, k in ((128, 64), (256, 512), (384, 1024)):
+        blocks = (k // 16 + 3) // 4 * 4
+        seen = {oracle.nvfp4_scale_index(r, b, k) for r in range(rows) for b in range(blocks)}
+        assert len(seen) == rows * blocks and max(seen) == oracle.nvfp4_scale_bytes(rows, k) - 1
+        for r in (0, 31, 32, 127):
+            assert oracle.nvfp4_scale_index(r, 3, k) // 512 == 0
+
+
+def test_nvfp4_exact_pattern_round_trips():
+    """tests/quant_native.c's pattern: every value is 2^e with one e per 16
+    columns, so g = amax / 2688, each block scale is 448 * 2^(e - emax), every
+    code is 6 and the dequantized value code * sf * g is 2^e exactly."""
+    n, k = 256, 256
+    j, c = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    e = (j % 3) - 1 + (c // 16) % 3
+    w = synth.f32_to_bf16(np.ldexp(1.0, e).astype(np.float32)).reshape(-1)
+    codes, scales, glob, _ = oracle.nvfp4_pack(w, n, k)
+    assert glob[0] == np.float32(8.0 / 2688) and glob[1] == 1.0
+    assert np.all(codes == 0x77)
+    sf = oracle.e4m3_decode(scales)
+    for r in (0, 1, 2, 200):
+        for b in range(k // 16):
+            assert sf[oracle.nvfp4_scale_index(r, b, k)] == 448 * 2.0 ** (e[r, b * 16] - 3)
+    x = synth.f32_to_bf16(np.ldexp(np.where(j[:129] % 2, -1.0, 1.0), (j[:129] % 3) - 1 + (c[:129] // 16) % 2)
+                          .astype(np.float32)).reshape(-1)
+    x4, xs, xg, _ = oracle.nvfp4_pack(x, 129, k, weight_global=glob[0])
+    assert xg[1] == np.float32(xg[0] * glob[0])
+    y = oracle.nvfp4_gemm(x4, xs, codes, scales, xg[1], 129, n, k)
+    exact = synth.bf16_to_f32(x).reshape(129, k).astype(np.float64) @ synth.bf16_to_f32(w).reshape(n, k).astype(np.float64).T
+    assert np.array_equal(y, synth.f32_to_bf16(exact.astype(np.float32)))
+
+
+def test_nvfp4_pack_error_bounds():
+    """Random rows: each block scale is the E4M3 rounding of blockmax / (6 g)
+    (floored at 2^-9); each dequantized value is within half an E2M1 step (or
+    saturated at 6) of x / (sf g)."""
+    rng = np.random.default_rng(13)
+    rows, k = 128, 256
+    x = synth.f32_to_bf16((rng.standard_normal(rows * k) * np.repeat(rng.uniform(0.01, 3, rows * k // 16), 16))
+                          .astype(np.float32))
+    codes, scales, glob, _ = oracle.nvfp4_pack(x, rows, k)
+    xf = synth.bf16_to_f32(x).reshape(rows, k).astype(np.float64)
+    g = float(glob[0])
+    assert glob[0] == np.float32(max(np.float32(np.abs(xf).max()) / np.float32(2688), np.float32(1e-20)))
+    sf = oracle.e4m3_decode(scales).astype(np.float64)
+    vals = oracle.e2m1_decode(np.stack([codes & 15, codes >> 4], 1).reshape(-1)).astype(np.float64).reshape(rows, k)
+    grid = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.5, -1, -1.5, -2, -3, -4, -6])
+    for r in range(0, rows, 7):
+        for b in range(k // 16):
+            s = sf[oracle.nvfp4_scale_index(r, b, k)]
+            m = np.abs(xf[r, b * 16:(b + 1) * 16]).max()
+            t = max(m / (6 * g), 2.0 ** -9)
+            assert abs(s - t) <= t * 2.0 ** -4 + 2.0 ** -10          # E4M3 rounding (3 mantissa bits)
+            q = xf[r, b * 16:(b + 1) * 16] / (s * g)
+            v = vals[r, b * 16:(b + 1) * 16]
+            qc = np.clip(q, -6, 6)
+            nearest = np.abs(grid[None, :] - qc[:, None]).min(axis=1)
+            assert np.all(np.abs(v - qc) <= nearest + 1e-6), (r, b)         # a nearest E2M1 value
