@@ -192,9 +192,9 @@ static h3_gpu_tensor *q8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed
     return t;
 }
 
-/* FP8 projection weight (projection_quant 1): N(0, 1/k) BF16 values packed to
- * the tensorwide E4M3 descriptor. */
-static h3_gpu_tensor *fp8_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed) {
+/* Quantized projection weight (projection_quant 1 FP8, 2 NVFP4): N(0, 1/k)
+ * BF16 values packed to the mode's descriptor. */
+static h3_gpu_tensor *quant_random(h3_gpu *g, uint32_t n, uint32_t k, uint64_t seed) {
     h3_gpu_tensor *b = normal_tensor(g, (size_t)n * k, seed, 1.0f / sqrtf((float)k), 0.f);
     if (!b) return NULL;
     h3_gpu_tensor *t = h3_gpu_synchronize(g) ? h3_hip_quant_weight_from_bf16(g, b, n, k) : NULL;
@@ -224,7 +224,7 @@ static int weights(h3_hip_dit_synth *m, char *error, size_t size) {
         for (int j = 0; j < PROJ; j++) {
             uint32_t n, k;
             proj_shape(c, j, &n, &k);
-            h3_gpu_tensor *t = c->projection_quant ? fp8_random(g, n, k, c->seed * 7919ull + b * 8 + j)
+            h3_gpu_tensor *t = c->projection_quant ? quant_random(g, n, k, c->seed * 7919ull + b * 8 + j)
                                                    : q8_random(g, n, k, c->seed * 7919ull + b * 8 + j);
             if (!t) return fail(error, size, "block %u weight %d: %s", b, j, h3_gpu_error(g));
             if (resident) m->proj[(size_t)b * PROJ + j] = t;
@@ -260,13 +260,13 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         c->latent % 256 || !c->frames || !c->height || !c->width ||
         (c->rope_half != 64 && (!c->rope_half || c->rope_half > 64 || c->rope_half % 3)) ||
         (c->attention_mode != 0 && c->attention_mode != 1 && c->attention_mode != 4) ||
-        (c->projection_quant != 0 && c->projection_quant != 1)) {
+        (c->projection_quant < 0 || c->projection_quant > 2)) {
         fail(error, size, "synthetic DiT: hidden/mlp/latent multiples of 256, rope_half 64 or a multiple of 3 "
-                          "below it, attention mode 0/1/4, projection_quant 0/1");
+                          "below it, attention mode 0/1/4, projection_quant 0/1/2");
         return NULL;
     }
     if (c->projection_quant && c->streamed_first < c->blocks) {
-        fail(error, size, "synthetic DiT: FP8 projections need every block resident");
+        fail(error, size, "synthetic DiT: quantized projections need every block resident");
         return NULL;
     }
     h3_hip_dit_synth *m = calloc(1, sizeof(*m));
@@ -296,7 +296,7 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         const char *tmp = getenv("TMPDIR");
         char cache[512];
         snprintf(cache, sizeof(cache), "%s/h3cli-amd-quant", tmp && *tmp ? tmp : "/tmp");
-        if (!h3_gpu_quant_configure(g, H3_QUANT_FP8, cache, 0, 0, 0)) {
+        if (!h3_gpu_quant_configure(g, c->projection_quant, cache, 0, 0, 0)) {
             fail(error, size, "quant configure: %s", h3_gpu_error(g));
             goto bad;
         }
@@ -431,7 +431,7 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
                  h3_gpu_swiglu_bf16(g, m->act, m->h, R, c->mlp) &&
                  h3_gpu_linear_bf16(g, m->f, m->act, w[3], NULL, R, c->mlp, H);
         } else if (c->projection_quant) {
-            /* Packed FP8 weights take no epilogue: GELU-tanh separately. */
+            /* Packed weights take no epilogue: GELU-tanh separately. */
             ok = ok && h3_gpu_linear_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
                  h3_gpu_gelu_bf16(g, m->act, m->h, (uint32_t)(R * c->mlp), 1) &&
                  h3_gpu_linear_bf16(g, m->f, m->act, w[3], NULL, R, c->mlp, H);

@@ -34,8 +34,8 @@ typedef struct {
     int qk_norm;                /* 1: per-head RMSNorm of Q and K with learned [128] weights */
     int grouped_qkv;            /* 1: QKV rows grouped per head [heads, 3, 128] (H3 checkpoint layout) */
     float subblock_sparsity;    /* attention_mode 4: the request's sparsity (0.75) */
-    int projection_quant;       /* 0: W8A16 q8 projections; 1: FP8 W8A8 (h3_gpu_quant_configure mode 1,
-                                   every block resident) */
+    int projection_quant;       /* 0: W8A16 q8 projections; 1: FP8 W8A8, 2: NVFP4 W4A4
+                                   (h3_gpu_quant_configure mode 1/2, every block resident) */
 } h3_hip_dit_synth_config;
 
 /* The benchmark geometry. */
@@ -50,8 +50,8 @@ typedef struct h3_hip_dit_synth h3_hip_dit_synth;
 
 /* Build the model on a fresh context (configures its DiT attention mode, binds
  * the block mask): seeded W8A16 projection weights (int8 U[-127,127], per-output
- * channel fp32 scales U[1e-3,1e-2]) or, with projection_quant 1, FP8 weights
- * packed from N(0, 1/k) BF16 values (the context's quantization is configured,
+ * channel fp32 scales U[1e-3,1e-2]) or, with projection_quant 1 or 2, FP8 or
+ * NVFP4 weights packed from N(0, 1/k) BF16 values (the context's quantization is configured,
  * artifacts under $TMPDIR/h3cli-amd-quant), AdaLN norms and modulation from a 256-d
  * sinusoidal timestep embedding, 3D RoPE tables, a seeded latent. Blocks from
  * streamed_first on live in pinned host memory and are copied into two device
@@ -72,8 +72,8 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *model, int step, float dt);
  * "attn.out_proj.weight" [hidden, heads * 128], "mlp.fc1.weight" [2 * mlp
  * (SwiGLU) or mlp, hidden], "mlp.fc2.weight" [hidden, mlp]; all BF16. The four
  * projections are packed to W8A16 on the device with the reference q8 recipe
- * (group 64), or with projection_quant 1 to FP8 through h3_gpu_quant_load and
- * its artifact cache. Every block must be resident (streamed_first >= blocks); no
+ * (group 64), or with projection_quant 1 / 2 to FP8 / NVFP4 through
+ * h3_gpu_quant_load and its artifact cache. Every block must be resident (streamed_first >= blocks); no
  * command may be active. Errors name the first missing or mismatched tensor. */
 int h3_hip_dit_synth_load(h3_hip_dit_synth *model, const char *path, char *error, size_t error_size);
 

@@ -97,12 +97,13 @@ def test_load_needs_resident_blocks(tmp_path):
         assert "resident" in str(e.value)
 
 
-def test_load_fp8_projections(tmp_path, monkeypatch):
-    """projection_quant 1: the checkpoint's projections go through
-    h3_gpu_quant_load (the artifact cache under $TMPDIR) and equal the
-    reference's FP8 descriptor of the file's BF16 weights byte for byte; the
-    step is deterministic and tracks the W8A16 model loaded from the same file."""
-    from tests.test_quant_gpu import descriptor, packed_size
+@pytest.mark.parametrize("mode", [1, 2], ids=["fp8", "nvfp4"])
+def test_load_quantized_projections(tmp_path, monkeypatch, mode):
+    """projection_quant 1 (FP8) / 2 (NVFP4): the checkpoint's projections go
+    through h3_gpu_quant_load (the artifact cache under $TMPDIR) and equal the
+    reference's descriptor of the file's BF16 weights byte for byte; the step
+    is deterministic and tracks the W8A16 model loaded from the same file."""
+    from tests.test_quant_gpu import descriptor, nvfp4_descriptor, packed_size
     monkeypatch.setenv("TMPDIR", str(tmp_path))
     path = tmp_path / "h3.safetensors"
     ref = checkpoint(path)
@@ -110,15 +111,15 @@ def test_load_fp8_projections(tmp_path, monkeypatch):
               "mlp.fc1.weight": (1536, 512), "mlp.fc2.weight": (512, 768)}
     hidden = []
     for run in range(2):
-        with DitSynth(geometry="h3", projection_quant=1, **dict(SMALL, streamed_first=SMALL["blocks"])) as m:
+        with DitSynth(geometry="h3", projection_quant=mode, **dict(SMALL, streamed_first=SMALL["blocks"])) as m:
             m.load(path)
             if run == 0:
                 for b in range(SMALL["blocks"]):
                     for suffix, (n, k) in shapes.items():
                         name = f"blocks.{b}.{suffix}"
                         h = m.lib.h3_hip_dit_synth_tensor(m.handle, name.encode())
-                        want, _ = descriptor(ref[name], n, k)
-                        raw = np.zeros(packed_size(n, k)[2], np.uint8)
+                        want, _ = descriptor(ref[name], n, k) if mode == 1 else nvfp4_descriptor(ref[name], n, k)
+                        raw = np.zeros(packed_size(n, k, mode)[2], np.uint8)
                         assert m.lib.h3_hip_tensor_copy_to_host(h, raw.ctypes.data, raw.size), m.gpu.error()
                         assert np.array_equal(raw, want), name
             m.step(step=0, dt=-0.1)
@@ -131,4 +132,4 @@ def test_load_fp8_projections(tmp_path, monkeypatch):
         q8 = synth.bf16_to_f32(m.read("hidden")).astype(np.float64)
     f8 = synth.bf16_to_f32(hidden[0]).astype(np.float64)
     cos = np.dot(f8, q8) / np.sqrt(np.dot(f8, f8) * np.dot(q8, q8))
-    assert cos > 0.99, cos
+    assert cos > (0.99 if mode == 1 else 0.95), cos
