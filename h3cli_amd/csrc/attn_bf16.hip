@@ -41,6 +41,7 @@ constexpr int K_BYTES = BN * D * 2;        // K tile: 64 rows x 256 B, 16-byte c
 constexpr int V_BYTES = D * BN * 2;        // V^T tile: 128 rows x 128 B, 16-byte chunks XOR-swizzled
 constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
 constexpr float RESCALE_SLACK = 8.0f;      // log2 units the running max may lag
+constexpr float PSUM_LIMIT = 1048576.0f;   // 2^20: bound on a lane's 32-key partial row sum
 
 // LDS chunk swizzles (16-byte chunks): every 16-lane group of a ds_read_b128
 // touches 16 distinct 4-bank groups for both operand reads.
@@ -60,6 +61,9 @@ struct Args {
     const uint32_t *kv_count;              // sparse: number of entries per list
     unsigned list_stride;
     unsigned *fault;
+    // Dense kernel: one byte per (head, 256-query block, wave), set when the
+    // wave's rows need the recomputation launch.
+    uint8_t *retry;
     // SOL centroid phase (listed kernel with CENT): per (head, query block) the
     // centroid tile list, its length and the approximate-block mask of each
     // tile; centroid K rows [key_blocks][heads][128] and transposed V
@@ -365,9 +369,10 @@ int launch(h3_gpu *g, const Args &a, unsigned groups) {
 // Wide tiles: each barrier interval covers KT consecutive 64-key sub-tiles, so
 // the per-interval fixed costs (the barrier, the load wait and the serial
 // max / ballot chain) are paid once per KT * 64 keys.
-template <int KT, bool SPARSE, bool MSUM>
+template <int KT, bool SPARSE, bool MSUM, bool NOMAX>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void attn_bf16_wide(Args a) {
+    static_assert(!(NOMAX && MSUM), "the overflow test reads the VALU row sums");
     constexpr int WAVES = 8;
     constexpr int BM = 32 * WAVES;
     constexpr int BLOCKS = K_BYTES / 1024;
@@ -380,6 +385,11 @@ void attn_bf16_wide(Args a) {
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned head = id / nqb, qb = id % nqb;
     const unsigned q0 = qb * BM;
+    uint8_t *const retry = a.retry ? a.retry + ((size_t)head * nqb + qb) * WAVES : nullptr;
+    // The recomputation launch runs only the workgroups the fast kernel flagged.
+    if constexpr (!NOMAX) {
+        if (retry && *reinterpret_cast<const uint64_t *>(retry) == 0) return;
+    }
     const size_t stride = (size_t)a.heads * D;
     const uint16_t *qh = a.q + (size_t)head * D;
     const uint16_t *kh = a.k + (size_t)head * D;
@@ -439,6 +449,7 @@ void attn_bf16_wide(Args a) {
 #pragma unroll
     for (int md = 0; md < 4; md++) o[md] = f32x16{};
     float m = -1e30f, l = 0.f;
+    bool failed = false;   // a P overflowed: these rows are recomputed
     f32x16 lsum = f32x16{};
     bf16x8 ones;
 #pragma unroll
@@ -484,6 +495,7 @@ void attn_bf16_wide(Args a) {
                     }
             }
         }
+        if (!NOMAX || g == 0) {
         float mx0 = -INFINITY, mx1 = -INFINITY;
 #pragma unroll
         for (int j = 0; j < KT; j++)
@@ -502,16 +514,21 @@ void attn_bf16_wide(Args a) {
 #pragma unroll
             for (int md = 0; md < 4; md++) o[md] *= alpha;
         }
+        }
         const float neg = -m;
+        int raise = 0;   // exponent m rises by after this group (0 or more)
 #pragma unroll
         for (int j = 0; j < KT; j++) {
             const uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
             bf16x8 vfr[16];
+            auto load_v = [&]() {
 #pragma unroll
-            for (int x = 0; x < 16; x++) {
-                const unsigned d = (x % 4) * 32 + n;
-                vfr[x] = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, (x / 4) * 2 + hf) * 16);
-            }
+                for (int x = 0; x < 16; x++) {
+                    const unsigned d = (x % 4) * 32 + n;
+                    vfr[x] = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, (x / 4) * 2 + hf) * 16);
+                }
+            };
+            load_v();
             bf16x8 pb[4];
             float psum = 0.f;
 #pragma unroll
@@ -524,6 +541,19 @@ void attn_bf16_wide(Args a) {
                     pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
                     pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
                 }
+            if constexpr (NOMAX) {
+                // Past the first group the running max is raised only when the
+                // row's 32-key partial sums leave [0, PSUM_LIMIT], so no
+                // per-tile max is computed. Then m rises by e, the largest
+                // exponent of the row's partial sums (a bound on every P of the
+                // row), after the group's P.V, scaling l and O by 2^-e exactly. A partial sum at or above 2^64 (or not finite)
+                // could overflow O: the wave flags its rows and the launch that
+                // follows recomputes them.
+                // Branch-free: a branch here would keep the exponentials from
+                // overlapping the P.V products.
+                // An infinite or NaN sum has exponent 128.
+                if (!(psum <= PSUM_LIMIT)) raise = max(raise, (int)((__builtin_bit_cast(uint32_t, psum) >> 23) & 0xFF) - 127);
+            }
             if constexpr (!MSUM) l += psum;
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
@@ -531,6 +561,19 @@ void attn_bf16_wide(Args a) {
                 for (int md = 0; md < 4; md++)
                     o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[kk * 4 + md], pb[kk], o[md], 0, 0, 0);
                 if constexpr (MSUM) lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[kk], lsum, 0, 0, 0);
+            }
+        }
+        if constexpr (NOMAX) {
+            if (__builtin_amdgcn_ballot_w64(raise != 0)) {
+                // Both lanes of a query (one per 32-key half) take the larger.
+                raise = (int)half_max_swap((float)raise);
+                failed |= raise >= 64;
+                if (raise >= 64) raise = 0;
+                const float alpha = ldexpf(1.f, -raise);
+                m += (float)raise;
+                l *= alpha;
+#pragma unroll
+                for (int md = 0; md < 4; md++) o[md] *= alpha;
             }
         }
         wait_vm_loads();
@@ -557,22 +600,41 @@ void attn_bf16_wide(Args a) {
                 *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
             }
     }
+    if constexpr (NOMAX) {
+        const bool any = __builtin_amdgcn_ballot_w64(failed) != 0;
+        if (lane == 0) retry[wave] = any ? 1 : 0;
+        if (any) return;
+    }
     if (bad) a.fault[0] = 1u;
 }
 
-template <int KT, bool SPARSE, bool MSUM>
-int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
-    constexpr size_t shared = 2 * KT * STAGE_BYTES;
+template <int KT, bool SPARSE, bool MSUM, bool NOMAX>
+int configure_wide(h3_gpu *g) {
     static bool configured = false;
-    auto kernel = attn_bf16_wide<KT, SPARSE, MSUM>;
     if (!configured) {
-        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)attn_bf16_wide<KT, SPARSE, MSUM, NOMAX>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * KT * STAGE_BYTES)),
                           "attention shared memory"))
             return 0;
         configured = true;
     }
+    return 1;
+}
+
+// NOMAX: the fast kernel, then the per-tile-max kernel over the workgroups
+// the fast one flagged (most of its workgroups exit at once); both inside one
+// timing window.
+template <int KT, bool SPARSE, bool MSUM, bool NOMAX = false>
+int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
+    constexpr size_t shared = 2 * KT * STAGE_BYTES;
+    if (!configure_wide<KT, SPARSE, MSUM, false>(g)) return 0;
+    if (NOMAX && !configure_wide<KT, SPARSE, MSUM, true>(g)) return 0;
     hipEvent_t timing = h3_kernel_timing_begin(g);
-    hipLaunchKernelGGL(kernel, dim3(groups), dim3(512), shared, g->compute, a);
+    hipLaunchKernelGGL((attn_bf16_wide<KT, SPARSE, MSUM, NOMAX>), dim3(groups), dim3(512), shared, g->compute, a);
+    if (NOMAX) {
+        if (!h3_launch_status(g, "BF16 attention")) return 0;
+        hipLaunchKernelGGL((attn_bf16_wide<KT, SPARSE, MSUM, false>), dim3(groups), dim3(512), shared, g->compute, a);
+    }
     h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "BF16 attention");
 }
@@ -906,14 +968,19 @@ int launch_listed(h3_gpu *g, const Args &a, unsigned groups) {
 
 }  // namespace
 
+// V^T, then (256-byte aligned) one retry byte per (head, 256-query block, wave).
+static size_t retry_offset(uint32_t seq, uint32_t heads) {
+    return ((size_t)heads * D * ((seq + 63) / 64 * 64) * sizeof(uint16_t) + 255) / 256 * 256;
+}
+
 size_t h3_attention_bf16_workspace(uint32_t seq, uint32_t heads) {
-    return (size_t)heads * D * ((seq + 63) / 64 * 64) * sizeof(uint16_t);
+    return retry_offset(seq, heads) + (size_t)heads * ((seq + 255) / 256) * 8;
 }
 
 int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
                              const uint32_t *kv_list, const uint32_t *kv_count, uint32_t list_stride) {
-    Args a;
+    Args a{};
     a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
     a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;
@@ -929,13 +996,16 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     if (kv_list) return launch<4, 1, 2, true, true>(g, a, (seq + 127) / 128 * heads);
     if (g->attention_variant == 1) return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
     if (g->attention_variant == 2) return launch<12, 1, 3, false, false>(g, a, (seq + 383) / 384 * heads);
-    return launch_wide<2, false, false>(g, a, (seq + 255) / 256 * heads);
+    // Variant 3: a tile max every 128 keys instead of the row-sum test.
+    if (g->attention_variant == 3) return launch_wide<2, false, false, false>(g, a, (seq + 255) / 256 * heads);
+    a.retry = (uint8_t *)workspace + retry_offset(seq, heads);
+    return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
 }
 
 int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                                const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
                                const uint32_t *lists, const uint32_t *counts, uint32_t list_stride) {
-    Args a;
+    Args a{};
     a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
     a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;

@@ -61,6 +61,40 @@ def test_plain_entry_points(gpu):
     _check(gpu, q, k, v, seq, heads, head_major=True, dit=False)
 
 
+def _growth_inputs(seq, heads, pattern):
+    """Scores that rise across the keys (the running max is raised many times),
+    fall (the first tile holds the max), or jump at one late key by more than
+    128 in log2 units (its P overflows FP32 until the max is raised)."""
+    rng = np.random.default_rng(21)
+    n = seq * heads * 128
+    one = np.float32(1.0)
+    q = np.full((seq, heads, 128), one, np.float32)
+    if pattern == "rise":
+        k = np.repeat(np.linspace(0, 20, seq, dtype=np.float32)[:, None, None], heads, 1).repeat(128, 2)
+    elif pattern == "fall":
+        k = np.repeat(np.linspace(20, 0, seq, dtype=np.float32)[:, None, None], heads, 1).repeat(128, 2)
+    else:
+        k = rng.normal(0, 0.25, (seq, heads, 128)).astype(np.float32)
+        k[seq - 100] = 8.0
+    v = rng.normal(0, 1, (seq, heads, 128)).astype(np.float32)
+    return tuple(synth.f32_to_bf16(x.reshape(n)) for x in (q, k, v))
+
+
+@pytest.mark.parametrize("pattern", ["rise", "fall", "spike"])
+def test_score_growth(gpu, pattern):
+    """Large, moving score ranges: the lazily raised running max must keep every
+    P finite and the result equal to the oracle's and to a direct FP64 softmax."""
+    seq, heads = 1500, 2
+    q, k, v = _growth_inputs(seq, heads, pattern)
+    _check(gpu, q, k, v, seq, heads)
+    out = bf16(sdpa(gpu, q, k, v, seq, heads))
+    scale = scale_bf16(1 / math.sqrt(128))
+    for r0 in (0, 700, seq - 10):
+        ref = oracle.attention_f64(bf16(q), bf16(k), bf16(v), seq, heads, scale, rows=(r0, r0 + 10))
+        m = metrics(out[r0:r0 + 10], ref)
+        assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+
+
 def test_f64_bruteforce_rows(gpu):
     """Sampled rows against a direct FP64 softmax (tests/metal_attention.c:55-67)."""
     seq, heads = 3000, 2
