@@ -421,6 +421,20 @@ void attn_bf16_wide(Args a) {
         if (bad) a.fault[0] = 1u;
     }
 
+    // Byte offsets, inside a full tile, of this lane's first 16-byte load (LDS
+    // block wave). Load t (block wave + WAVES t) sits 4 WAVES t keys / 8 WAVES t
+    // channels further on, with the same swizzle (it depends on key % 16 and
+    // channel / 2 % 8 only): a full tile is a uniform base plus one offset per
+    // lane, with no per-load address arithmetic.
+    constexpr int LOADS = BLOCKS / WAVES;
+    static_assert((4 * WAVES) % 16 == 0 && (8 * WAVES) % 16 == 0, "load steps keep the swizzle");
+    uint32_t koff, voff;
+    {
+        const unsigned key = 4 * wave + lane / 16, d = 8 * wave + lane / 8;
+        koff = (key * (uint32_t)stride + k_chunk(key, lane % 16) * 8) * 2;
+        voff = (d * a.padded + v_chunk(d, lane % 8) * 8) * 2;
+    }
+
     auto load_group = [&](unsigned g, int stage) {
         uint8_t *base = smem + stage * STAGE;
 #pragma unroll
@@ -429,18 +443,33 @@ void attn_bf16_wide(Args a) {
             const unsigned key0 = tile * BN;
             uint8_t *ks = base + j * K_BYTES;
             uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
+            if (key0 + BN <= a.seq) {
 #pragma unroll
-            for (unsigned b = wave; b < BLOCKS; b += WAVES) {
-                unsigned key = 4 * b + lane / 16, phys = lane % 16;
-                unsigned row = min(key0 + key, a.seq - 1);
-                const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                                 (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
-                unsigned d = 8 * b + lane / 8, vph = lane % 8;
-                unsigned col = min(key0, a.padded - BN);
-                const uint16_t *vsrc = vth + (size_t)d * a.padded + col + v_chunk(d, vph) * 8;
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vsrc,
-                                                 (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, 0, 0);
+                for (int t = 0; t < LOADS; t++) {
+                    const __attribute__((address_space(1))) char *kt =
+                        (const __attribute__((address_space(1))) char *)(kh + ((size_t)key0 + 4 * WAVES * t) * stride);
+                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(kt + koff),
+                                                     (__attribute__((address_space(3))) void *)(ks + (wave + WAVES * t) * 1024),
+                                                     16, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (unsigned b = wave; b < BLOCKS; b += WAVES) {
+                    unsigned key = 4 * b + lane / 16, phys = lane % 16;
+                    unsigned row = min(key0 + key, a.seq - 1);
+                    const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, phys) * 8;
+                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                                     (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
+                }
+            }
+            // V^T is padded to whole tiles: always a uniform base plus offsets.
+#pragma unroll
+            for (int t = 0; t < LOADS; t++) {
+                const __attribute__((address_space(1))) char *vt = (const __attribute__((address_space(1))) char *)(
+                    vth + (size_t)8 * WAVES * t * a.padded + min(key0, a.padded - BN));
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(vt + voff),
+                                                 (__attribute__((address_space(3))) void *)(vs + (wave + WAVES * t) * 1024),
+                                                 16, 0, 0);
             }
         }
     };
