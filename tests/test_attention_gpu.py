@@ -95,6 +95,26 @@ def test_score_growth(gpu, pattern):
         assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
 
 
+def test_recomputation_launch_matches_tile_max_kernel(gpu, monkeypatch):
+    """A 130-log2-unit spike overflows P in every workgroup of the default
+    kernel, so the recomputation launch redoes all rows with the per-tile-max
+    kernel (attention variant 3): the two outputs agree bit for bit. A rising
+    ramp, which only raises the max by exponent shifts, stays within tolerance
+    of variant 3."""
+    seq, heads = 1500, 2
+    q, k, v = _growth_inputs(seq, heads, "spike")
+    fast = sdpa(gpu, q, k, v, seq, heads)
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", "3")
+    g3 = Gpu()
+    try:
+        assert np.array_equal(sdpa(g3, q, k, v, seq, heads), fast)
+        q, k, v = _growth_inputs(seq, heads, "rise")
+        m = metrics(bf16(sdpa(gpu, q, k, v, seq, heads)), bf16(sdpa(g3, q, k, v, seq, heads)))
+        assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+    finally:
+        g3.close()
+
+
 def test_f64_bruteforce_rows(gpu):
     """Sampled rows against a direct FP64 softmax (tests/metal_attention.c:55-67)."""
     seq, heads = 3000, 2
