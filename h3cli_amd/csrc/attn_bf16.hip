@@ -42,6 +42,7 @@ constexpr int V_BYTES = D * BN * 2;        // V^T tile: 128 rows x 128 B, 16-byt
 constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
 constexpr float RESCALE_SLACK = 8.0f;      // log2 units the running max may lag
 constexpr float PSUM_LIMIT = 1048576.0f;   // 2^20: bound on a lane's 32-key partial row sum
+constexpr int RETRY_EXP = 32;              // partial sums from 2^32 up send the rows to the recomputation
 
 // LDS chunk swizzles (16-byte chunks): every 16-lane group of a ds_read_b128
 // touches 16 distinct 4-bank groups for both operand reads.
@@ -575,12 +576,13 @@ void attn_bf16_wide(Args a) {
                 // row's 32-key partial sums leave [0, PSUM_LIMIT], so no
                 // per-tile max is computed. Then m rises by e, the largest
                 // exponent of the row's partial sums (a bound on every P of the
-                // row), after the group's P.V, scaling l and O by 2^-e exactly. A partial sum at or above 2^64 (or not finite)
-                // could overflow O: the wave flags its rows and the launch that
-                // follows recomputes them.
+                // row), after the group's P.V, scaling l and O by 2^-e exactly.
+                // A partial sum at or above 2^RETRY_EXP (or not finite: its
+                // exponent reads 128) has already put P that large into O,
+                // which for large |V| could overflow: the wave flags its rows
+                // and the launch that follows recomputes them.
                 // Branch-free: a branch here would keep the exponentials from
                 // overlapping the P.V products.
-                // An infinite or NaN sum has exponent 128.
                 if (!(psum <= PSUM_LIMIT)) raise = max(raise, (int)((__builtin_bit_cast(uint32_t, psum) >> 23) & 0xFF) - 127);
             }
             if constexpr (!MSUM) l += psum;
@@ -596,8 +598,8 @@ void attn_bf16_wide(Args a) {
             if (__builtin_amdgcn_ballot_w64(raise != 0)) {
                 // Both lanes of a query (one per 32-key half) take the larger.
                 raise = (int)half_max_swap((float)raise);
-                failed |= raise >= 64;
-                if (raise >= 64) raise = 0;
+                failed |= raise >= RETRY_EXP;
+                if (raise >= RETRY_EXP) raise = 0;
                 const float alpha = ldexpf(1.f, -raise);
                 m += (float)raise;
                 l *= alpha;

@@ -115,6 +115,23 @@ def test_recomputation_launch_matches_tile_max_kernel(gpu, monkeypatch):
         g3.close()
 
 
+def test_large_values_after_score_jump(gpu):
+    """A 41-log2-unit score jump with |V| near 1e26: P that large must not
+    reach O unscaled (it would overflow FP32). The rows go to the
+    recomputation launch, and with constant V the output is V."""
+    seq, heads = 1500, 2
+    rng = np.random.default_rng(5)
+    q = np.ones((seq, heads, 128), np.float32)
+    k = rng.normal(0, 0.25, (seq, heads, 128)).astype(np.float32)
+    k[seq - 300] = 2.5
+    big = synth.bf16_to_f32(synth.f32_to_bf16(np.float32(1e26)))
+    v = np.full((seq, heads, 128), big, np.float32)
+    q, k, v = (synth.f32_to_bf16(x.reshape(-1)) for x in (q, k, v))
+    out = bf16(sdpa(gpu, q, k, v, seq, heads))
+    assert np.all(np.isfinite(out))
+    assert np.max(np.abs(out / big - 1)) < 2e-2
+
+
 def test_f64_bruteforce_rows(gpu):
     """Sampled rows against a direct FP64 softmax (tests/metal_attention.c:55-67)."""
     seq, heads = 3000, 2
