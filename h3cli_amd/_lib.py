@@ -117,7 +117,7 @@ class DitSynthConfig(C.Structure):
                 ("latent", _u32), ("streamed_first", _u32), ("mask_density", _f),
                 ("attention_mode", _i), ("eps", _f), ("time", _f), ("seed", C.c_uint64),
                 ("rope_half", _u32), ("swiglu", _i), ("qk_norm", _i), ("grouped_qkv", _i),
-                ("subblock_sparsity", _f), ("projection_quant", _i)]
+                ("subblock_sparsity", _f), ("projection_quant", _i), ("trace_block", _u32)]
 
 
 _SIGNATURES.update({
@@ -125,6 +125,8 @@ _SIGNATURES.update({
     "h3_hip_dit_synth_h3": (DitSynthConfig, []),
     "h3_hip_dit_synth_create": (_p, [_p, C.POINTER(DitSynthConfig), C.c_char_p, _sz]),
     "h3_hip_dit_synth_free": (None, [_p]),
+    "h3_hip_dit_time_features": (None, [_p, _u32, _p]),
+    "h3_hip_dit_rope_tables": (_i, [_u32, _u32, _u32, _u32, _u32, _p, _p]),
     "h3_hip_dit_synth_load": (_i, [_p, C.c_char_p, C.c_char_p, _sz]),
     "h3_hip_dit_synth_step": (_i, [_p, _i, _f]),
     "h3_hip_dit_synth_tensor": (_p, [_p, C.c_char_p]),

@@ -632,6 +632,11 @@ void attn_bf16_wide(Args a) {
             }
     }
     if constexpr (NOMAX) {
+        // A non-finite output with no flagged partial sum comes from P below
+        // 2^RETRY_EXP times a large |V| (or from a non-finite input): the
+        // per-tile-max launch recomputes those rows too, and raises the
+        // fault only if its own output is not finite.
+        failed |= bad;
         const bool any = __builtin_amdgcn_ballot_w64(failed) != 0;
         if (lane == 0) retry[wave] = any ? 1 : 0;
         if (any) return;

@@ -27,6 +27,11 @@
 #define TIME_FEATURES 256u
 #define PROJ 4 /* qkv, out, up, down */
 
+/* Stages of one block kept when config.trace_block selects it, in op order. */
+enum { T_X0, T_XN1, T_QKV, T_Q, T_K, T_V, T_ATTN, T_O, T_X1, T_XN2, T_H, T_ACT, T_F, T_X2, TRACE_COUNT };
+static const char *const TRACE_NAMES[TRACE_COUNT] = {"x0", "xn1", "qkv", "q", "k", "v", "attn", "o", "x1",
+                                                     "xn2", "h", "act", "f", "x2"};
+
 struct h3_hip_dit_synth {
     h3_gpu *gpu;
     h3_hip_dit_synth_config c;
@@ -44,6 +49,7 @@ struct h3_hip_dit_synth {
     h3_sol_block *layout_blocks;   /* attention_mode 4: the bound 64-row layout */
     h3_gpu_tensor *cos_t, *sin_t, *row_map;
     uint64_t kept, total;
+    h3_gpu_tensor *trace[TRACE_COUNT]; /* copies of the traced block's stages */
 };
 
 static int fail(char *error, size_t size, const char *fmt, ...) {
@@ -105,36 +111,58 @@ static h3_gpu_tensor *normal_tensor(h3_gpu *g, size_t n, uint64_t seed, float sp
     return t;
 }
 
-/* 3D RoPE tables over the video grid (rotate-half pairs d <-> d + half; half 64:
- * frame / row / column split 44/42/42 channels, half 48: 16 frequencies per axis
- * as dit.c ROPE_FREQS; theta 1e4); audio rows get angle 0. */
-static int rope_tables(h3_hip_dit_synth *m) {
-    const uint32_t half = m->c.rope_half;
+int h3_hip_dit_rope_tables(uint32_t frames, uint32_t height, uint32_t width, uint32_t audio_rows, uint32_t half,
+                           uint16_t *cosines, uint16_t *sines) {
+    if (!frames || !height || !width || !cosines || !sines || (half != 64 && (!half || half > 64 || half % 3)))
+        return 0;
+    /* Pairs per axis (frame, row, column): 22/21/21 for half 64 (44/42/42
+     * channels), else half / 3 each. */
     uint32_t split[3] = {22, 21, 21};
     if (half != 64) split[0] = split[1] = split[2] = half / 3;
-    size_t n = (size_t)m->rows * half;
-    uint16_t *c = malloc(n * 2), *s = malloc(n * 2);
-    if (!c || !s) { free(c); free(s); return 0; }
-    for (uint32_t r = 0; r < m->rows; r++) {
-        uint32_t pos[3] = {0, 0, 0};
-        if (r < m->video_rows) {
-            pos[0] = r / (m->c.height * m->c.width);
-            pos[1] = (r / m->c.width) % m->c.height;
-            pos[2] = r % m->c.width;
+    float inv[64];
+    for (uint32_t axis = 0, j = 0; axis < 3; axis++)
+        for (uint32_t i = 0; i < split[axis]; i++, j++)
+            inv[j] = (float)pow(10000.0, -2.0 * (double)i / (2.0 * split[axis]));
+    const uint32_t video = frames * height * width;
+    for (uint32_t r = 0; r < video + audio_rows; r++) {
+        float pos[3] = {0.f, 0.f, 0.f};
+        if (r < video) {
+            pos[0] = (float)(r / (height * width));
+            pos[1] = (float)((r / width) % height);
+            pos[2] = (float)(r % width);
         }
-        uint32_t j = 0;
-        for (int axis = 0; axis < 3; axis++)
+        for (uint32_t axis = 0, j = 0; axis < 3; axis++)
             for (uint32_t i = 0; i < split[axis]; i++, j++) {
-                double inv = pow(10000.0, -2.0 * i / (2.0 * split[axis]));
-                double angle = pos[axis] * inv;
-                c[(size_t)r * half + j] = to_bf16((float)cos(angle));
-                s[(size_t)r * half + j] = to_bf16((float)sin(angle));
+                float angle = pos[axis] * inv[j];
+                cosines[(size_t)r * half + j] = to_bf16(cosf(angle));
+                sines[(size_t)r * half + j] = to_bf16(sinf(angle));
             }
     }
-    m->cos_t = h3_gpu_tensor_from_bf16(m->gpu, c, n);
-    m->sin_t = h3_gpu_tensor_from_bf16(m->gpu, s, n);
+    return 1;
+}
+
+void h3_hip_dit_time_features(const float *times, uint32_t rows, float *features) {
+    for (uint32_t row = 0; row < rows; row++)
+        for (uint32_t i = 0; i < TIME_FEATURES / 2; i++) {
+            float freq = expf(-logf(10000.0f) * (float)i / (float)(TIME_FEATURES / 2));
+            float angle = times[row] * freq;
+            features[(size_t)row * TIME_FEATURES + i] = cosf(angle);
+            features[(size_t)row * TIME_FEATURES + TIME_FEATURES / 2 + i] = sinf(angle);
+        }
+}
+
+/* 3D RoPE tables over the video grid; audio rows get angle 0. */
+static int rope_tables(h3_hip_dit_synth *m) {
+    const uint32_t half = m->c.rope_half;
+    size_t n = (size_t)m->rows * half;
+    uint16_t *c = malloc(n * 2), *s = malloc(n * 2);
+    int ok = c && s && h3_hip_dit_rope_tables(m->c.frames, m->c.height, m->c.width, m->c.audio_rows, half, c, s);
+    if (ok) {
+        m->cos_t = h3_gpu_tensor_from_bf16(m->gpu, c, n);
+        m->sin_t = h3_gpu_tensor_from_bf16(m->gpu, s, n);
+    }
     free(c); free(s);
-    return m->cos_t && m->sin_t;
+    return ok && m->cos_t && m->sin_t;
 }
 
 /* Modulation [2 rows (video, audio), 6 slots, hidden] per block = a shared time
@@ -143,15 +171,9 @@ static int rope_tables(h3_hip_dit_synth *m) {
 static int modulation(h3_hip_dit_synth *m, char *error, size_t size) {
     h3_gpu *g = m->gpu;
     const uint32_t H = m->c.hidden;
-    float feat[2 * TIME_FEATURES];
+    float feat[2 * TIME_FEATURES], times[2] = {m->c.time, m->c.time};
     uint16_t featb[2 * TIME_FEATURES];
-    for (int row = 0; row < 2; row++)
-        for (uint32_t i = 0; i < TIME_FEATURES / 2; i++) {
-            float freq = expf(-logf(10000.0f) * (float)i / (float)(TIME_FEATURES / 2));
-            float angle = m->c.time * freq;
-            feat[row * TIME_FEATURES + i] = cosf(angle);
-            feat[row * TIME_FEATURES + TIME_FEATURES / 2 + i] = sinf(angle);
-        }
+    h3_hip_dit_time_features(times, 2, feat);
     for (uint32_t i = 0; i < 2 * TIME_FEATURES; i++) featb[i] = to_bf16(feat[i]);
     uint64_t sd = m->c.seed * 1000003ull;
     h3_gpu_tensor *tf = h3_gpu_tensor_from_bf16(g, featb, 2 * TIME_FEATURES);
@@ -260,9 +282,9 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
         c->latent % 256 || !c->frames || !c->height || !c->width ||
         (c->rope_half != 64 && (!c->rope_half || c->rope_half > 64 || c->rope_half % 3)) ||
         (c->attention_mode != 0 && c->attention_mode != 1 && c->attention_mode != 4) ||
-        (c->projection_quant < 0 || c->projection_quant > 2)) {
+        (c->projection_quant < 0 || c->projection_quant > 2) || c->trace_block > c->blocks) {
         fail(error, size, "synthetic DiT: hidden/mlp/latent multiples of 256, rope_half 64 or a multiple of 3 "
-                          "below it, attention mode 0/1/4, projection_quant 0/1/2");
+                          "below it, attention mode 0/1/4, projection_quant 0/1/2, trace_block <= blocks");
         return NULL;
     }
     if (c->projection_quant && c->streamed_first < c->blocks) {
@@ -325,6 +347,17 @@ h3_hip_dit_synth *h3_hip_dit_synth_create(h3_gpu *g, const h3_hip_dit_synth_conf
             h3_gpu_cancel(g);
             goto bad;
         }
+        if (c->trace_block) {
+            const size_t sizes[TRACE_COUNT] = {R * H, R * H, R * I * 3, R * I, R * I, R * I, R * I, R * H, R * H,
+                                               R * H, R * c->mlp * (c->swiglu ? 2 : 1), m->act ? R * c->mlp : 0,
+                                               R * H, R * H};
+            for (int i = 0; i < TRACE_COUNT; i++)
+                if (sizes[i] && !(m->trace[i] = bf16_buffer(g, sizes[i]))) {
+                    fail(error, size, "trace: %s", h3_gpu_error(g));
+                    h3_gpu_cancel(g);
+                    goto bad;
+                }
+        }
         /* Seeded N(0,1) latent. */
         h3_gpu_tensor *init = normal_tensor(g, R * c->latent, c->seed * 41 + 1, 1.0f, 0.f);
         int ok = init && h3_gpu_cast_bf16_to_f32(g, m->latent, init, (uint32_t)(R * c->latent)) && h3_gpu_synchronize(g);
@@ -383,9 +416,16 @@ void h3_hip_dit_synth_free(h3_hip_dit_synth *m) {
                             m->qkv, m->q, m->k, m->v, m->attn, m->o, m->h, m->act, m->f, m->vel, m->cos_t, m->sin_t,
                             m->row_map};
     for (size_t i = 0; i < sizeof(all) / sizeof(*all); i++) h3_gpu_tensor_free(all[i]);
+    for (int i = 0; i < TRACE_COUNT; i++) h3_gpu_tensor_free(m->trace[i]);
     free(m->proj); free(m->host); free(m->norm1); free(m->norm2); free(m->mod); free(m->qn); free(m->kn);
     free(m->layout_blocks);
     free(m);
+}
+
+/* Device copy of a stage of the traced block into its trace tensor. */
+static int keep(h3_hip_dit_synth *m, int stage, const h3_gpu_tensor *src) {
+    h3_gpu_tensor *t = m->trace[stage];
+    return !t || h3_gpu_copy_bf16(m->gpu, t, 0, src, 0, h3_gpu_tensor_elements(t));
 }
 
 /* Queue the copy of streamed block b into its slot (b % 2) on the copy stream. */
@@ -414,7 +454,9 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
         /* The next streamed block's copy overlaps this block's compute. */
         if (b + 1 > c->streamed_first && !prefetch(m, b + 1)) { ok = 0; break; }
         const h3_gpu_tensor *qn = c->qk_norm ? m->qn[b] : NULL, *kn = c->qk_norm ? m->kn[b] : NULL;
-        ok = h3_gpu_adaln_bf16(g, m->xn, m->x, m->norm1[b], m->mod[b], m->row_map, R, H, SLOTS, 0, 1, c->eps);
+        const int tr = c->trace_block == b + 1;
+        ok = (!tr || keep(m, T_X0, m->x)) &&
+             h3_gpu_adaln_bf16(g, m->xn, m->x, m->norm1[b], m->mod[b], m->row_map, R, H, SLOTS, 0, 1, c->eps);
         if (c->grouped_qkv)
             ok = ok && h3_gpu_grouped_qkv_linear_rope_bf16(g, m->q, m->k, m->v, m->qkv, m->xn, w[0], qn, kn, m->cos_t,
                                                            m->sin_t, R, H, c->heads, 128, c->rope_half, c->eps);
@@ -422,10 +464,14 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
             ok = ok && h3_gpu_linear_bf16(g, m->qkv, m->xn, w[0], NULL, R, H, 3 * I) &&
                  h3_gpu_qkv_rope_bf16(g, m->q, m->k, m->v, m->qkv, qn, kn, m->cos_t, m->sin_t, R, c->heads, 128,
                                       c->rope_half, c->eps);
+        ok = ok && (!tr || (keep(m, T_XN1, m->xn) && keep(m, T_QKV, m->qkv) && keep(m, T_Q, m->q) &&
+                            keep(m, T_K, m->k) && keep(m, T_V, m->v)));
         ok = ok && h3_gpu_dit_sdpa_bf16(g, m->attn, m->q, m->k, m->v, R, c->heads, 128, scale, 0, b, step) &&
              h3_gpu_linear_bf16(g, m->o, m->attn, w[1], NULL, R, I, H) &&
+             (!tr || (keep(m, T_ATTN, m->attn) && keep(m, T_O, m->o))) &&
              h3_gpu_gate_adaln_bf16(g, m->x, m->xn, m->x, m->o, m->norm2[b], m->mod[b], m->mod[b], m->row_map, R, H,
-                                    SLOTS, 2, 3, 4, c->eps);
+                                    SLOTS, 2, 3, 4, c->eps) &&
+             (!tr || (keep(m, T_X1, m->x) && keep(m, T_XN2, m->xn)));
         if (c->swiglu) {
             ok = ok && h3_gpu_linear_bf16(g, m->h, m->xn, w[2], NULL, R, H, 2 * c->mlp) &&
                  h3_gpu_swiglu_bf16(g, m->act, m->h, R, c->mlp) &&
@@ -439,7 +485,9 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *m, int step, float dt) {
             ok = ok && h3_hip_linear_gelu_bf16(g, m->h, m->xn, w[2], NULL, R, H, c->mlp) &&
                  h3_gpu_linear_bf16(g, m->f, m->h, w[3], NULL, R, c->mlp, H);
         }
-        ok = ok && h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5);
+        ok = ok && (!tr || (keep(m, T_H, m->h) && (!m->act || keep(m, T_ACT, m->act)) && keep(m, T_F, m->f))) &&
+             h3_gpu_gate_bf16(g, m->x, m->x, m->f, m->mod[b], m->row_map, R, H, SLOTS, 5) &&
+             (!tr || keep(m, T_X2, m->x));
     }
     ok = ok && h3_gpu_adaln_bf16(g, m->xn, m->x, m->head_norm, m->head_mod, m->row_map, R, H, 2, 0, 1, c->eps) &&
          h3_gpu_linear_bf16(g, m->vel, m->xn, m->head, NULL, R, H, L) &&
@@ -520,13 +568,27 @@ h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *m, const char *name) {
     if (!strcmp(name, "latent")) return m->latent;
     if (!strcmp(name, "hidden")) return m->x;
     if (!strcmp(name, "velocity")) return m->vel;
+    if (!strcmp(name, "latent_bf16")) return m->latent_bf16;
+    if (!strcmp(name, "patch")) return m->patch;
+    if (!strcmp(name, "head")) return m->head;
+    if (!strcmp(name, "head_norm")) return m->head_norm;
+    if (!strcmp(name, "head_mod")) return m->head_mod;
+    if (!strcmp(name, "rope_cos")) return m->cos_t;
+    if (!strcmp(name, "rope_sin")) return m->sin_t;
+    if (!strcmp(name, "row_map")) return m->row_map;
+    if (!strncmp(name, "trace.", 6)) {
+        for (int i = 0; i < TRACE_COUNT; i++)
+            if (!strcmp(name + 6, TRACE_NAMES[i])) return m->trace[i];
+        return NULL;
+    }
     unsigned b, used = 0;
-    if (sscanf(name, "blocks.%u.%n", &b, &used) == 1 && used && b < m->c.blocks)
-        for (int i = 0; i < 8; i++)
-            if (!strcmp(name + used, BLOCK_NAMES[i])) {
-                h3_gpu_tensor **slot = block_slot(m, b, i);
-                return slot ? *slot : NULL;
-            }
+    if (sscanf(name, "blocks.%u.%n", &b, &used) != 1 || !used || b >= m->c.blocks) return NULL;
+    if (!strcmp(name + used, "modulation")) return m->mod[b];
+    for (int i = 0; i < 8; i++)
+        if (!strcmp(name + used, BLOCK_NAMES[i])) {
+            h3_gpu_tensor **slot = block_slot(m, b, i);
+            return slot ? *slot : NULL;
+        }
     return NULL;
 }
 

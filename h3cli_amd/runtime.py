@@ -176,10 +176,22 @@ class DitSynth:
         n = self.lib.h3_gpu_tensor_elements(h)
         dtype = self.lib.h3_gpu_tensor_dtype(h)
         out = np.empty(n, dtype=_DTYPE_NP[dtype])
-        fn = {F32: self.lib.h3_gpu_tensor_read_f32, BF16: self.lib.h3_gpu_tensor_read_bf16}[dtype]
+        fn = {F32: self.lib.h3_gpu_tensor_read_f32, BF16: self.lib.h3_gpu_tensor_read_bf16,
+              U32: self.lib.h3_gpu_tensor_read_u32}[dtype]
         if not fn(h, out.ctypes.data, n):
             raise H3Error(self.gpu.error())
         return out
+
+    def read_q8(self, name, rows, columns):
+        """A resident per-output-channel W8A16 weight: (int8 codes [rows *
+        columns], fp32 scales [rows])."""
+        h = self.lib.h3_hip_dit_synth_tensor(self.handle, name.encode())
+        if not h:
+            raise H3Error(f"no tensor {name}")
+        raw = np.empty(rows * columns + rows * 4, np.uint8)
+        if not self.lib.h3_hip_tensor_copy_to_host(h, raw.ctypes.data, raw.size):
+            raise H3Error(self.gpu.error())
+        return raw[:rows * columns].view(np.int8).copy(), raw[rows * columns:].view(np.float32).copy()
 
     def close(self):
         if self.handle:

@@ -36,6 +36,8 @@ typedef struct {
     float subblock_sparsity;    /* attention_mode 4: the request's sparsity (0.75) */
     int projection_quant;       /* 0: W8A16 q8 projections; 1: FP8 W8A8, 2: NVFP4 W4A4
                                    (h3_gpu_quant_configure mode 1/2, every block resident) */
+    uint32_t trace_block;       /* 0: off; b + 1: each step keeps device copies of block b's stage
+                                   tensors, read back as "trace.<stage>" (h3_hip_dit_synth_tensor) */
 } h3_hip_dit_synth_config;
 
 /* The benchmark geometry. */
@@ -45,6 +47,23 @@ h3_hip_dit_synth_config h3_hip_dit_synth_default(void);
  * axis), eps 1e-5, BF16 attention; video grid 25 x 27 x 27 = 18225 rows (the
  * reference's 18,225-token attention case), no audio rows, all blocks resident. */
 h3_hip_dit_synth_config h3_hip_dit_synth_h3(void);
+
+/* The 256-d timestep features of reference dit_schedule.c:152-162 for rows
+ * of times: features[row, i] = cos(t * f_i) for i < 128 and
+ * features[row, 128 + i] = sin(t * f_i), f_i = exp(-ln(1e4) * i / 128), in
+ * FP32 as the reference computes them. */
+void h3_hip_dit_time_features(const float *times, uint32_t rows, float *features);
+
+/* 3D RoPE cos/sin tables [frames * height * width + audio_rows, half] as BF16
+ * bits, rows frame-major then row then column, audio rows angle 0. Pair j of
+ * axis a (frame, row, column) has inv_freq theta^(-2 i / dim_a), theta 1e4,
+ * i = j - first pair of the axis; half 64 splits 22/21/21 pairs (44/42/42
+ * channels), a multiple of 3 below 64 splits evenly (reference dit.c:1051-1090
+ * with ROPE_FREQS = half / 3). angle = position * inv_freq in FP32 (inv_freq
+ * rounded to FP32, as read from the reference's rope.inv_freq weights), then
+ * cosf / sinf and BF16 rounding. Returns 0 on invalid arguments. */
+int h3_hip_dit_rope_tables(uint32_t frames, uint32_t height, uint32_t width, uint32_t audio_rows, uint32_t half,
+                           uint16_t *cosines, uint16_t *sines);
 
 typedef struct h3_hip_dit_synth h3_hip_dit_synth;
 
@@ -78,9 +97,17 @@ int h3_hip_dit_synth_step(h3_hip_dit_synth *model, int step, float dt);
 int h3_hip_dit_synth_load(h3_hip_dit_synth *model, const char *path, char *error, size_t error_size);
 
 /* Model tensors for inspection: "latent" (F32 [rows, latent]), "hidden" (BF16
- * [rows, hidden], the residual stream after the last block), "velocity", and a
- * resident block's weights under the checkpoint names above
- * ("blocks.0.attn.qkv_proj.weight": a W8A16 tensor; norms BF16). */
+ * [rows, hidden], the residual stream after the last block), "velocity",
+ * "latent_bf16" (the patch-embedding input), "patch" [hidden, latent], "head"
+ * [latent, hidden], "head_norm", "head_mod" [2, 2, hidden], "rope_cos" and
+ * "rope_sin" [rows, rope_half], "row_map" (U32 [rows]: 0 video, 1 audio), a
+ * block's modulation "blocks.<b>.modulation" [2, 6, hidden], a resident
+ * block's weights under the checkpoint names above
+ * ("blocks.0.attn.qkv_proj.weight": a W8A16 tensor; norms BF16), and with
+ * trace_block the traced block's stages "trace.x0" (block input), "xn1"
+ * (AdaLN), "qkv", "q", "k", "v", "attn", "o" (out projection), "x1" (gated
+ * residual), "xn2" (second AdaLN), "h" (fc1, GELU applied when fused),
+ * "act" (SwiGLU or separate GELU), "f" (fc2) and "x2" (block output). */
 h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *model, const char *name);
 uint32_t h3_hip_dit_synth_rows(const h3_hip_dit_synth *model);
 /* Kept 128x128 blocks of the bound mask and the total (for FLOP accounting). */

@@ -132,6 +132,33 @@ def test_large_values_after_score_jump(gpu):
     assert np.max(np.abs(out / big - 1)) < 2e-2
 
 
+def test_large_values_after_small_score_jump(gpu):
+    """A score jump of about 30 log2 units (below the 32-unit retry bound on
+    partial sums) with |V| = 1e30: P near 2^30 times V overflows FP32 in the
+    fast kernel's O before the max is raised. The non-finite output sends
+    those rows to the per-tile-max launch, whose P <= 256 keeps O finite; with
+    constant V the output is V, and the call does not fail."""
+    seq, heads = 1500, 2
+    rng = np.random.default_rng(8)
+    q = np.ones((seq, heads, 128), np.float32)
+    k = rng.normal(0, 0.25, (seq, heads, 128)).astype(np.float32)
+    k[seq - 300] = 1.90625
+    big = synth.bf16_to_f32(synth.f32_to_bf16(np.float32(1e30)))
+    v = np.full((seq, heads, 128), big, np.float32)
+    qb, kb, vb = (synth.f32_to_bf16(x.reshape(-1)) for x in (q, k, v))
+    # The jump stays below 32 log2 units over every row's running max.
+    scale = scale_bf16(1 / math.sqrt(128))
+    s = bf16(kb).reshape(seq, heads, 128).sum(-1) * scale * math.log2(math.e)
+    jump = s[seq - 300] - s[:128].max(0)
+    assert np.all((jump > 28) & (jump < 32)), jump
+    out = bf16(sdpa(gpu, qb, kb, vb, seq, heads))
+    assert np.all(np.isfinite(out))
+    assert np.max(np.abs(out / big - 1)) < 2e-2
+    ref = oracle.attention(bf16(qb), bf16(kb), bf16(vb), seq, heads, scale, rows=(seq - 310, seq - 290))
+    m = metrics(out[seq - 310:seq - 290] / big, ref / big)
+    assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+
+
 def test_f64_bruteforce_rows(gpu):
     """Sampled rows against a direct FP64 softmax (tests/metal_attention.c:55-67)."""
     seq, heads = 3000, 2
