@@ -1,7 +1,7 @@
 // FP8 W8A8 DiT projections (reference src/cuda/cuda_quant.cuh): tensorwide
-// E4M3 packing of weights and activations, the packed-weight caches (metadata
-// keyed H3QMT002, and the strict content-hashed H3QWT001), and an FP8 GEMM on
-// gfx950's v_mfma_f32_32x32x64_f8f6f4 in place of cuBLASLt.
+// E4M3 packing of weights and activations, the content-hashed packed-weight
+// artifacts (H3QWT001), and an FP8 GEMM on gfx950's v_mfma_f32_32x32x64_f8f6f4
+// in place of cuBLASLt.
 //
 // Arithmetic contract (cuda_quant.cuh:26-49, 362-394):
 //   scale = max(max|x| / 448, 1e-20), code = E4M3(x / scale), RNE, saturating;
@@ -24,7 +24,6 @@
 #include "internal.h"
 #include "sage.h"
 #include "../../include/h3_quant.h"
-#include "../../include/h3_quant_cache.h"
 #include "../../include/h3_residency.h"
 #include "../../include/h3_gpu_surface.h"
 #include "../host/sha256.h"
@@ -44,7 +43,6 @@
 
 struct h3_quant_state {
     std::string cache;                 // artifact directory
-    bool verify = false;               // H3QWT001 content-hashed artifacts
     bool streaming = false;            // packed weights stay in pinned host memory
     h3_device_buffer activation;       // packed activation codes + maxima + global slot
     h3_device_buffer streamed;         // device copy of a streamed packed weight
@@ -56,6 +54,9 @@ namespace {
 
 constexpr unsigned MAX_PARTIALS = 1024;
 constexpr unsigned FAULT_QUANT = 2;    // g->fault index: nonfinite projection input
+
+// Mode names as they appear in artifact names and messages ("fp8", "nvfp4").
+const char *mode_name(int mode) { return mode == H3_QUANT_FP8 ? "fp8" : mode == H3_QUANT_NVFP4 ? "nvfp4" : "off"; }
 
 // ---------------------------------------------------------------- packing
 // Maximum |x| of BF16 values as the integer maximum of their magnitude bits
@@ -536,12 +537,14 @@ h3_gpu_tensor *finish_weight(h3_gpu *g, std::vector<unsigned char> &packed, uint
     return t;
 }
 
-// Strict content-hashed artifacts (reference cuda_quant.cuh:169-248, selected by
-// H3_QUANT_VERIFY=1): <cache>/v<recipe>-fp8-<n>x<k>-<sha256(source)>.h3q with a
+// Content-hashed artifacts, the reference's strict format (cuda_quant.cuh:169-248,
+// which the reference selects with H3_QUANT_VERIFY=1; this backend uses it for
+// every load, and does not write the host's metadata-keyed cache):
+// <cache>/v<recipe>-<mode>-<n>x<k>-<sha256(source)>.h3q with a
 // 128-byte H3QWT001 header: recipe u32 @8, mode u32 @12, n u32 @16, k u32 @20,
 // bytes u64 @24, scale @32, global @40, source SHA-256 @48, payload SHA-256 @80,
 // zero @112-127.
-h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
+h3_gpu_tensor *load_artifact(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
                            size_t scale, size_t global) {
     const size_t source_bytes = (size_t)n * k * 2;
     int fd = open(path, O_RDONLY);
@@ -559,7 +562,7 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
     unsigned char source_hash[32];
     sha256_of(map.data(), source_bytes, source_hash);
     const std::string artifact = g->quant->cache + "/v" + std::to_string(H3_QUANT_VERSION) + "-" +
-                                 h3_quant_name(g->quant_mode) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
+                                 mode_name(g->quant_mode) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
                                  hex32(source_hash) + ".h3q";
     int lock = open((artifact + ".lock").c_str(), O_CREAT | O_RDWR, 0600);
     if (lock < 0 || flock(lock, LOCK_EX) != 0) {
@@ -630,38 +633,6 @@ h3_gpu_tensor *load_strict(h3_gpu *g, const char *path, uint64_t offset, uint32_
     return finish_weight(g, packed, n, k, scale, global, hit);
 }
 
-// Metadata-keyed artifacts (reference cuda_quant.cuh:292-330): the source is
-// only opened on a miss.
-h3_gpu_tensor *load_metadata(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
-                             size_t scale, size_t global) {
-    h3_quant_cache *cache = h3_quant_cache_open(g->quant->cache.c_str(), path, offset, n, k, g->quant_mode, bytes,
-                                                scale, global, g->error, sizeof(g->error));
-    if (!cache) return nullptr;
-    std::vector<unsigned char> packed(bytes);
-    const int status = h3_quant_cache_read(cache, packed.data(), g->error, sizeof(g->error));
-    bool ok = status >= 0;
-    if (ok && status == 0) {
-        const size_t source_bytes = (size_t)n * k * 2;
-        int fd = open(cache->source, O_RDONLY);
-        struct stat st;
-        Mapping map;
-        bool mapped = fd >= 0 && fstat(fd, &st) == 0 && st.st_dev == cache->stamp.st_dev &&
-                      st.st_ino == cache->stamp.st_ino && st.st_size == cache->stamp.st_size &&
-                      h3_quant_cache_unchanged(cache, g->error, sizeof(g->error)) && map.map(fd, offset, source_bytes);
-        if (fd >= 0) close(fd);
-        if (!mapped) {
-            h3_set_error(g, "cannot map metadata-cache source: %s", path);
-            ok = false;
-        } else {
-            ok = prepare_packed(g, map.data(), n, k, bytes, scale, global, packed.data()) &&
-                 h3_quant_cache_write(cache, packed.data(), g->error, sizeof(g->error));
-        }
-    }
-    if (ok) ok = h3_quant_cache_unchanged(cache, g->error, sizeof(g->error));
-    h3_quant_cache_close(cache);
-    return ok ? finish_weight(g, packed, n, k, scale, global, status == 1) : nullptr;
-}
-
 }  // namespace
 
 void h3_quant_destroy(h3_gpu *g) {
@@ -685,7 +656,7 @@ extern "C" int h3_quant_preflight(int mode, char *error, size_t size) {
     }
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         if (error && size)
-            snprintf(error, size, "cuda-denoise-quant %s requires gfx950 (MI355X) (device %s)", h3_quant_name(mode),
+            snprintf(error, size, "cuda-denoise-quant %s requires gfx950 (MI355X) (device %s)", mode_name(mode),
                      prop.gcnArchName);
         return 0;
     }
@@ -722,7 +693,6 @@ extern "C" int h3_gpu_quant_configure(h3_gpu *g, int mode, const char *cache, ui
     g->quant = new (std::nothrow) h3_quant_state();
     if (!g->quant) return h3_set_error(g, "quantization: out of host memory");
     g->quant->cache = dir;
-    g->quant->verify = h3_quant_verify() != 0;
     g->quant->streaming = stream != 0 || force_stream;
     g->quant_mode = mode;
     return 1;
@@ -739,8 +709,7 @@ extern "C" h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *g, const char *path, uint64_
     if (!path) { h3_set_error(g, "invalid quantized source range: (null)"); return nullptr; }
     uint64_t scale, global, bytes;
     h3_weight_packed_size(n, k, g->quant_mode, &scale, &global, &bytes);
-    return g->quant->verify ? load_strict(g, path, offset, n, k, bytes, scale, global)
-                            : load_metadata(g, path, offset, n, k, bytes, scale, global);
+    return load_artifact(g, path, offset, n, k, bytes, scale, global);
 }
 
 // y[rows, n] = FP8 projection of x[rows, k] with a packed weight (reference

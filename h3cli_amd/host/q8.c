@@ -1,62 +1,74 @@
-/* Host-side W8A16 packing with the reference's layout and rounding
- * (src/weights/q8.h:6-16, src/weights/q8.c:6-56): int8 [rows, columns] row-major,
- * then fp32 scales [rows, ceil(columns/64)] starting at a 4-byte aligned offset.
- * Per 64-wide group: scale = max|w| / 127, or 1 when the group is all zero,
- * floored at FLT_MIN; code = round-half-to-even(w / scale) clamped to +-127. */
+/* Host-side W8A16 packing (the reference's src/weights/q8.h interface).
+ *
+ * Storage, which packed files share with the reference: int8 codes
+ * [rows, columns] row-major, then float scales [rows, ceil(columns / 64)]
+ * starting at the first 4-byte boundary after the codes. Per 64-column group:
+ * scale = max|w| / 127 (1 for an all-zero group, never below FLT_MIN) and
+ * code = w / scale rounded to nearest, ties to even, clamped to [-127, 127].
+ * A non-finite weight refuses the whole tensor. The device packer
+ * (q8_pack_kernel) computes the same bytes on the GPU. */
+#include "h3_q8.h"
 #include <float.h>
 #include <math.h>
-#include <stddef.h>
-#include <stdint.h>
 #include <string.h>
 
-#define Q8_GROUP 64u
+/* Accepted shapes: the code plane stays below 2^32 - 32 bytes, the limit of
+ * the format's 32-bit addressing (a shape the reference refuses is refused
+ * here too, so both sides agree on which checkpoints pack). */
+#define Q8_MAX_CODES (UINT32_MAX - 31u)
 
-int h3_q8_layout(uint32_t rows, uint32_t columns, size_t *offset, size_t *bytes) {
-    if (!rows || !columns || columns > UINT32_MAX - (Q8_GROUP - 1u) || !offset || !bytes) return 0;
-    uint64_t elements = (uint64_t)rows * columns;
-    uint64_t groups = ((uint64_t)columns + Q8_GROUP - 1) / Q8_GROUP;
-    if (elements > UINT32_MAX - 31u) return 0;
-    uint64_t start = (elements + 3) & ~UINT64_C(3);
-    uint64_t total = start + (uint64_t)rows * groups * sizeof(float);
-    if (total > SIZE_MAX) return 0;
-    *offset = (size_t)start;
-    *bytes = (size_t)total;
+int h3_q8_layout(uint32_t rows, uint32_t columns, size_t *scale_offset, size_t *bytes) {
+    if (!scale_offset || !bytes || rows == 0 || columns == 0) return 0;
+    if ((uint64_t)columns + (H3_Q8_GROUP - 1) > UINT32_MAX) return 0;
+    const uint64_t codes = (uint64_t)rows * columns;
+    if (codes > Q8_MAX_CODES) return 0;
+    const uint64_t groups = ((uint64_t)columns + H3_Q8_GROUP - 1) / H3_Q8_GROUP;
+    const uint64_t scales_at = (codes + 3) / 4 * 4;
+    const uint64_t end = scales_at + (uint64_t)rows * groups * 4;
+    if (end > SIZE_MAX) return 0;
+    *scale_offset = (size_t)scales_at;
+    *bytes = (size_t)end;
     return 1;
 }
 
-static float widen(uint16_t bits) {
-    uint32_t word = (uint32_t)bits << 16;
-    float value;
-    memcpy(&value, &word, sizeof(value));
-    return value;
+/* BF16 magnitude bits order like the magnitudes themselves; 0x7f80 and above
+ * are infinities and NaNs. */
+static float bf16_value(uint16_t bits) {
+    const uint32_t word = (uint32_t)bits << 16;
+    float f;
+    memcpy(&f, &word, 4);
+    return f;
 }
 
-/* Round half to even of v, clamped to +-127. */
-static int8_t code_of(float v) {
-    float lo = floorf(v), frac = v - lo;
-    long q = (long)lo;
-    if (frac > 0.5f || (frac == 0.5f && (q & 1))) q++;
-    return (int8_t)(q < -127 ? -127 : q > 127 ? 127 : q);
+/* Packs one group of n weights; 0 if any is not finite. */
+static int pack_group(const uint16_t *w, uint32_t n, int8_t *codes, float *scale_out) {
+    uint16_t top = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const uint16_t mag = w[i] & 0x7fffu;
+        if (mag >= 0x7f80u) return 0;
+        if (mag > top) top = mag;
+    }
+    const float amax = bf16_value(top);
+    const float scale = top ? fmaxf(amax / 127.0f, FLT_MIN) : 1.0f;
+    *scale_out = scale;
+    for (uint32_t i = 0; i < n; i++) {
+        /* rintf rounds half to even in the default rounding mode. */
+        const float q = rintf(bf16_value(w[i]) / scale);
+        codes[i] = (int8_t)(q > 127.f ? 127 : q < -127.f ? -127 : (int)q);
+    }
+    return 1;
 }
 
 int h3_q8_pack_rows(const uint16_t *source, int8_t *weights, float *scales, uint32_t rows, uint32_t columns) {
-    size_t offset, bytes;
-    if (!source || !weights || !scales || !h3_q8_layout(rows, columns, &offset, &bytes)) return 0;
-    uint32_t groups = (columns + Q8_GROUP - 1) / Q8_GROUP;
-    for (uint32_t r = 0; r < rows; r++) {
-        const uint16_t *row = source + (size_t)r * columns;
-        for (uint32_t gi = 0; gi < groups; gi++) {
-            uint32_t begin = gi * Q8_GROUP, end = begin + Q8_GROUP < columns ? begin + Q8_GROUP : columns;
-            float amax = 0.f;
-            for (uint32_t c = begin; c < end; c++) {
-                float w = widen(row[c]);
-                if (!isfinite(w)) return 0;
-                if (fabsf(w) > amax) amax = fabsf(w);
-            }
-            float scale = amax == 0.f ? 1.f : fmaxf(amax / 127.f, FLT_MIN);
-            scales[(size_t)r * groups + gi] = scale;
-            for (uint32_t c = begin; c < end; c++) weights[(size_t)r * columns + c] = code_of(widen(row[c]) / scale);
+    size_t scale_offset, bytes;
+    if (!source || !weights || !scales || !h3_q8_layout(rows, columns, &scale_offset, &bytes)) return 0;
+    const uint32_t groups = (columns + H3_Q8_GROUP - 1) / H3_Q8_GROUP;
+    size_t at = 0;
+    for (uint32_t r = 0; r < rows; r++, at += columns)
+        for (uint32_t g = 0; g < groups; g++) {
+            const uint32_t first = g * H3_Q8_GROUP;
+            const uint32_t n = columns - first < H3_Q8_GROUP ? columns - first : H3_Q8_GROUP;
+            if (!pack_group(source + at + first, n, weights + at + first, scales + (size_t)r * groups + g)) return 0;
         }
-    }
     return 1;
 }

@@ -144,9 +144,10 @@ def test_reference_exact_pattern(tmp_path, mode):
 
 
 @pytest.mark.parametrize("mode", [1, 2], ids=["fp8", "nvfp4"])
-def test_descriptor_and_metadata_artifact(tmp_path, mode):
+def test_descriptor_and_artifact(tmp_path, mode):
     """The loaded weight is the reference's packed descriptor byte for byte,
-    and the H3QMT002 artifact is its 128-byte header plus that payload."""
+    read from a source at a file offset, and the artifact is the H3QWT001
+    header plus that payload."""
     rng = np.random.default_rng(2)
     n, k, offset = 384, 512, 4096
     w = synth.f32_to_bf16((rng.standard_normal(n * k) * 0.02).astype(np.float32))
@@ -158,25 +159,20 @@ def test_descriptor_and_metadata_artifact(tmp_path, mode):
         weight = load(g, path, n, k, offset, mode=mode)
         want, _ = descriptor(w, n, k) if mode == 1 else nvfp4_descriptor(w, n, k)
         assert np.array_equal(weight.read_bytes(), want)
+    source_hash = hashlib.sha256(w.tobytes()).hexdigest()
     names = [f for f in os.listdir(cache) if f.endswith(".h3q")]
-    assert len(names) == 1 and names[0].startswith(f"m2-{['', 'fp8', 'nvfp4'][mode]}-{n}x{k}-")
+    assert names == [f"v2-{['', 'fp8', 'nvfp4'][mode]}-{n}x{k}-{source_hash}.h3q"]
     data = (cache / names[0]).read_bytes()
-    h = np.frombuffer(data[:128], np.uint8)
     scale, glob, nbytes = packed_size(n, k, mode)
-    assert data[:8] == b"H3QMT002" and len(data) == 128 + nbytes
-    u32 = lambda o: int.from_bytes(data[o:o + 4], "little")
-    u64 = lambda o: int.from_bytes(data[o:o + 8], "little")
-    assert (u32(8), u32(12), u32(16), u32(20), u32(24)) == (2, 2, mode, n, k)
-    assert (u64(32), u64(40), u64(48), u64(88)) == (nbytes, scale, glob, offset)
-    assert data[56:88].hex() == names[0].split("-")[-1][:-4] and not h[96:].any()
+    assert data[:8] == b"H3QWT001" and len(data) == 128 + nbytes
+    assert int.from_bytes(data[12:16], "little") == mode
     assert np.array_equal(np.frombuffer(data[128:], np.uint8), want)
 
 
-def test_strict_artifact(tmp_path, monkeypatch):
-    """H3_QUANT_VERIFY=1: v2-fp8-NxK-<sha256 of the source>.h3q with an
-    H3QWT001 header holding the source and payload digests; a corrupted
-    payload is refused with the reference's text."""
-    monkeypatch.setenv("H3_QUANT_VERIFY", "1")
+def test_strict_artifact(tmp_path):
+    """v2-fp8-NxK-<sha256 of the source>.h3q with an H3QWT001 header holding
+    the source and payload digests (the reference's strict format); a
+    corrupted payload is refused with the reference's text."""
     rng = np.random.default_rng(3)
     n, k = 256, 384
     w = synth.f32_to_bf16((rng.standard_normal(n * k) * 0.1).astype(np.float32))
