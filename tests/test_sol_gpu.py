@@ -1,10 +1,12 @@
 """SOL routed attention (mode 3) on the GPU against oracle/sol.c, over the
 reference's operator acceptance cases (tests/cuda_sol_acceptance.json,
-tests/cuda_sol_oracle.py:58-98): centroids bit-exact, routes equal to the
-oracle's on the same centroids (and to the float64 rule where separated),
-outputs within the reference's gates (rel-L2 <= 0.01, max relative <= 0.02)
-of the float64 SOL softmax, force-exact calls equal to dense attention, NaN
-inputs rejected, dense bypass for early steps and layers."""
+tests/cuda_sol_oracle.py:58-98, with the layouts its oracle builds, from the
+golden vectors): centroids bit-exact, routes equal to the oracle's on the same
+centroids (the oracle's routes are pinned to the reference's float64 rule in
+tests/test_sol_oracle.py), outputs within the reference's gates (rel-L2 <=
+0.01, max relative <= 0.02) of the oracle's SOL softmax, force-exact calls
+equal to dense attention, NaN inputs rejected, dense bypass for early steps
+and layers."""
 import ctypes as C
 import math
 
@@ -12,31 +14,16 @@ import numpy as np
 import pytest
 
 from h3cli_amd import synth
-from h3cli_amd._lib import SolBlock, SolLayout
 from h3cli_amd.runtime import Gpu
 from oracle import oracle
 from tests.helpers import ATTN_COSINE, bf16, metrics, scale_bf16, sdpa
-from tests.sol_fixtures import inputs, metadata, routes64
+from tests.router_inputs import Layout, sol_inputs, sol_layout
 from tests.test_ref_host import SolOptions
 
 pytestmark = pytest.mark.gpu
 
 SCALE = scale_bf16(1 / math.sqrt(128))
 STEP, BLOCK = 5, 1
-
-
-class Layout:
-    def __init__(self, seq, meta):
-        self.blocks = []
-        arrays = []
-        for m in meta:
-            arr = (SolBlock * len(m))()
-            for i, (p, f0, f1, rows) in enumerate(m):
-                arr[i].protect, arr[i].first_frame, arr[i].last_frame, arr[i].rows = int(p), int(f0), int(f1), int(rows)
-            arrays.append(arr)
-        self.arrays = arrays
-        self.layout = SolLayout(seq, len(meta[0]), len(meta[1]), 0, C.cast(arrays[0], C.POINTER(SolBlock)),
-                                C.cast(arrays[1], C.POINTER(SolBlock)))
 
 
 def make_sol(seq, meta, q=32, minimum=0.5, tau=1.0, radius=1, exact=False):
@@ -50,7 +37,7 @@ def make_sol(seq, meta, q=32, minimum=0.5, tau=1.0, radius=1, exact=False):
     finally:
         lib.h3_cuda_sol_exchange(saved)
     g.sol_layout = Layout(seq, meta)
-    g.check(lib.h3_gpu_dit_sol_layout(g.handle, C.byref(g.sol_layout.layout)), "layout")
+    g.check(lib.h3_gpu_dit_sol_layout(g.handle, g.sol_layout.ptr), "layout")
     g.check(lib.h3_gpu_dit_attention_noise(g.handle, STEP, 0.2, 0.2), "noise")
     if exact:
         g.check(lib.h3_hip_dit_sol_force_exact(g.handle, 1), "force exact")
@@ -72,8 +59,8 @@ def run_case(seq, heads=2, q=32, minimum=0.5, tau=1.0, radius=1, exact=False, he
              protected=False, all_protected=False, seed=1701):
     print(f"[sol] seq={seq} heads={heads} q={q} min={minimum} tau={tau} exact={exact} pattern={pattern} "
           f"protected={protected or all_protected}", flush=True)
-    qx, kx, vx = inputs(seq, heads, seed=seed, pattern=pattern)
-    meta = metadata(seq, q, protected, all_protected)
+    qx, kx, vx = sol_inputs(seq, heads, seed=seed, pattern=pattern)
+    meta = sol_layout(seq, q, protected, all_protected)
     g = make_sol(seq, meta, q, minimum, tau, radius, exact)
     try:
         out = bf16(sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK, head_major=head_major))
@@ -89,12 +76,6 @@ def run_case(seq, heads=2, q=32, minimum=0.5, tau=1.0, radius=1, exact=False, he
         got = np.zeros(9, np.uint64)
         g.check(g.lib.h3_hip_sol_counters(g.handle, got.ctypes.data, 9), "counters")
         assert got[0] == 1 and got[1] == 0 and np.array_equal(got[2:], np.asarray(counts, np.uint64)), (got, counts)
-        qcf = synth.bf16_to_f32(qc).reshape(heads, -1, 128)
-        kcf = synth.bf16_to_f32(kc).reshape(heads, -1, 128)
-        for h in range(heads):
-            r64, dots, thr = routes64(qcf[h], kcf[h], meta, SCALE, minimum, tau, radius, exact)
-            sep = np.abs(dots - thr[:, None]) > 1e-5
-            assert np.array_equal(routes[h][sep], r64[sep]), h
         rows = list(range(seq)) if seq <= 1025 else sorted({0, 1, 31, 32, seq // 3, seq // 2, seq - 2, seq - 1})
         ref = np.concatenate([oracle.sol_attention(qx, kx, vx, kc, vc, routes, seq, heads, q, SCALE, (r, r + 1))
                               for r in rows]).reshape(len(rows), heads, 128)
@@ -121,7 +102,7 @@ def test_exact_cases_equal_dense(seq, q):
     result is dense attention (Q64 cases use the head-major output)."""
     out, routes = run_case(seq, q=q, exact=True, head_major=(q == 64))
     assert routes.all()
-    qx, kx, vx = inputs(seq, 2)
+    qx, kx, vx = sol_inputs(seq, 2)
     dense = oracle.attention(bf16(qx), bf16(kx), bf16(vx), seq, 2, SCALE).reshape(seq, 2, 128)
     m = metrics(out, dense)
     assert m["max_abs"] <= 2e-2 and m["cosine"] >= ATTN_COSINE, m
@@ -153,8 +134,8 @@ def test_acceptance_cases(case):
 
 def test_nonfinite_rejected():
     seq = 65
-    qx, kx, vx = inputs(seq, 2, pattern="nan")
-    g = make_sol(seq, metadata(seq, 32))
+    qx, kx, vx = sol_inputs(seq, 2, pattern="nan")
+    g = make_sol(seq, sol_layout(seq, 32))
     try:
         with pytest.raises(Exception) as e:
             sdpa(g, qx, kx, vx, seq, 2, step=STEP, block=BLOCK)
@@ -167,9 +148,9 @@ def test_dense_bypass_and_layout_rules():
     """Early steps and layers run dense (cuda_sol_policy.c:30-37); layouts are
     validated like the reference's configure; step must be bound."""
     seq = 300
-    qx, kx, vx = inputs(seq, 2, seed=4)
+    qx, kx, vx = sol_inputs(seq, 2, seed=4)
     d = Gpu()
-    g = make_sol(seq, metadata(seq, 32))
+    g = make_sol(seq, sol_layout(seq, 32))
     try:
         dense = sdpa(d, qx, kx, vx, seq, 2)
         g.check(g.lib.h3_gpu_dit_attention_noise(g.handle, 0, 0.2, 0.2), "noise")
@@ -186,18 +167,18 @@ def test_dense_bypass_and_layout_rules():
     finally:
         g.close()
         d.close()
-    bad = metadata(seq, 32)
+    bad = [m.copy() for m in sol_layout(seq, 32)]
     bad[0][0, 3] = 31
     g = Gpu()
     try:
         g.check(g.lib.h3_gpu_dit_attention_configure(g.handle, 3), "configure")
         lay = Layout(seq, bad)
-        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(lay.layout))
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, lay.ptr)
         assert "protection metadata" in g.error()
-        wrong = Layout(seq, metadata(seq, 64))       # 64-row query blocks under the default Q=32
-        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(wrong.layout))
-        good = Layout(seq, metadata(seq, 32))
-        g.check(g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(good.layout)), "layout")
-        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, C.byref(good.layout))        # already configured
+        wrong = Layout(seq, sol_layout(seq, 64))     # 64-row query blocks under the default Q=32
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, wrong.ptr)
+        good = Layout(seq, sol_layout(seq, 32))
+        g.check(g.lib.h3_gpu_dit_sol_layout(g.handle, good.ptr), "layout")
+        assert not g.lib.h3_gpu_dit_sol_layout(g.handle, good.ptr)                    # already configured
     finally:
         g.close()

@@ -1,24 +1,23 @@
 """Pins of the SubBlock router's C restatement (oracle/block.c: oracle_sb_pool,
-oracle_sb_score, oracle_sb_select, oracle_attention_routed) against the
-reference's own float64 oracle formulation (tests/subblock_oracle.py), closed
-forms and brute force."""
+oracle_sb_score, oracle_sb_select, oracle_attention_routed) against vectors
+from the reference's own NumPy oracle (tests/subblock_oracle.py, run by
+tests/golden/make_router_vectors.py), closed forms and brute force."""
 import math
 
 import numpy as np
 
 from h3cli_amd import synth
 from oracle import oracle
-from tests.subblock_fixtures import (f64_pool, f64_scores, lexsort_routes, native_inputs, protect_ends,
-                                     score_tolerance)
+from tests.router_inputs import native_inputs, random_pool_inputs, select_inputs, vectors
+
+
+def score_tolerance(expected):
+    """The reference's contract tolerance of pooled scores (subblock_oracle.py:60)."""
+    return 2e-4 + 2e-5 * np.abs(expected)
+
 
 SCALE = np.float32(1 / math.sqrt(128))
 QSCALE = np.float32(SCALE * np.float32(math.log2(math.e)))
-
-
-def _pools(q, k, seq, heads):
-    qp = synth.bf16_to_f32(oracle.sb_pool(q, seq, heads, QSCALE)).reshape(heads, -1, 128)
-    kp = synth.bf16_to_f32(oracle.sb_pool(k, seq, heads, 1.0)).reshape(heads, -1, 128)
-    return qp, kp
 
 
 def test_pool_matches_float64_means():
@@ -28,7 +27,7 @@ def test_pool_matches_float64_means():
     seq, heads = 69, 3
     q, _, _ = native_inputs(seq, heads, 0)
     got = synth.bf16_to_f32(oracle.sb_pool(q, seq, heads, QSCALE)).reshape(heads, -1, 128)
-    want = f64_pool(synth.bf16_to_f32(q), seq, heads, QSCALE)
+    want = vectors()["sb_pool_69_q"]
     assert got.shape == want.shape == (heads, 8, 128)
     ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64)) >> 16
     assert ulp.max() <= 1
@@ -55,22 +54,18 @@ def test_score_within_reference_tolerance():
     included."""
     seq, heads = 300, 2
     q, k, _ = native_inputs(seq, heads, 0)
-    qp, kp = _pools(q, k, seq, heads)
     blocks = (seq + 63) // 64
     got = oracle.sb_score(oracle.sb_pool(q, seq, heads, QSCALE), oracle.sb_pool(k, seq, heads, 1.0), seq,
                           heads).reshape(heads, blocks, blocks)
-    want = f64_scores(qp, kp, seq)
+    want = vectors()["sb_scores_300"]
     assert np.all(np.abs(got - want) <= score_tolerance(want))
     # Random pools at a larger scale exercise the tolerance's relative term.
-    rng = np.random.default_rng(5)
     seq = 200
-    qr = synth.f32_to_bf16(rng.standard_normal((seq, 1, 128)).astype(np.float32) * 3)
-    kr = synth.f32_to_bf16(rng.standard_normal((seq, 1, 128)).astype(np.float32) * 3)
-    qp, kp = _pools(qr, kr, seq, 1)
+    qr, kr = random_pool_inputs()
     blocks = (seq + 63) // 64
     got = oracle.sb_score(oracle.sb_pool(qr, seq, 1, QSCALE), oracle.sb_pool(kr, seq, 1, 1.0), seq,
                           1).reshape(1, blocks, blocks)
-    want = f64_scores(qp, kp, seq)
+    want = vectors()["sb_scores_200r"]
     assert np.all(np.abs(got - want) <= score_tolerance(want))
 
 
@@ -94,14 +89,10 @@ def test_score_closed_form():
 
 
 def test_select_matches_lexsort_and_ties():
-    rng = np.random.default_rng(9)
-    heads, blocks, keep = 2, 37, 8
-    scores = rng.integers(-4, 4, (heads, blocks, blocks)).astype(np.float32)  # many ties
-    kp = np.zeros(blocks, np.uint8)
-    kp[[3, 30]] = 1
-    qp = protect_ends(blocks * 64)
+    scores, kp, qp, keep = select_inputs()
+    heads, blocks = scores.shape[:2]
     got = oracle.sb_select(scores, heads, blocks, keep, qp, kp).reshape(heads, blocks, blocks)
-    assert np.array_equal(got, lexsort_routes(scores, keep, qp, kp))
+    assert np.array_equal(got, vectors()["sb_select_routes"])
     # All scores equal: the first `keep` indices win.
     flat = np.zeros((1, blocks, blocks), np.float32)
     got = oracle.sb_select(flat, 1, blocks, keep).reshape(blocks, blocks)
