@@ -59,13 +59,10 @@ def attention_ok(mode, q, k, v, rows, heads, mask, got):
     assert m["cosine"] >= (ATTN_COSINE if mode == 0 else 0.9995) and m["max_abs"] <= bound, m
 
 
-def chained_attention(mode, q, k, v, rows, heads, mask):
+def bf16_attention(q, k, v, rows, heads, mask):
     scale = scale_bf16(1 / math.sqrt(128))
-    if mode == 0:
-        ref = oracle.attention(bf16(q), bf16(k), bf16(v), rows, heads, scale, mask=mask, block=128)
-    else:
-        ref = oracle.sage_attention(oracle.sage_pack(q, k, v, rows, heads), rows, heads, scale, mask=mask, block=128)
-    return synth.f32_to_bf16(ref.astype(np.float32).reshape(-1))
+    ref = oracle.attention(bf16(q), bf16(k), bf16(v), rows, heads, scale, mask=mask, block=128)
+    return synth.f32_to_bf16(ref.reshape(-1))
 
 
 @pytest.mark.parametrize("mode", [1, 0])
@@ -115,7 +112,13 @@ def test_block_composition_against_oracle(mode):
     xn1 = oracle.adaln(t["x0"], norm1, mod, rmap, R, H, SLOTS, 0, 1, eps)
     qkv, _ = linear(xn1, *w[0], R, H, 3 * I)
     q, k, v = oracle.qkv_rope(qkv, None, None, cos, sin, R, heads, 128, 64, eps, 0)
-    att = chained_attention(mode, q, k, v, R, heads, mask)
+    # BF16 attention is chained too. Sage is not: one-ulp differences in the
+    # chained projections change some int8 Q/K codes, and with the nearly
+    # one-hot softmax of these weights a changed code moves a whole row's
+    # winning key (2% rel-L2 measured), so in Sage mode the chain continues
+    # from the GPU's attention output, which the stage check above holds to
+    # the quantized-operand oracle.
+    att = bf16_attention(q, k, v, R, heads, mask) if mode == 0 else t["attn"]
     o, _ = linear(att, *w[1], R, I, H)
     x1 = oracle.gate(t["x0"], o, mod, rmap, R, H, SLOTS, 2)
     xn2 = oracle.adaln(x1, norm2, mod, rmap, R, H, SLOTS, 3, 4, eps)
@@ -126,14 +129,8 @@ def test_block_composition_against_oracle(mode):
         met = metrics(bf16(t[name]), bf16(ref))
         print(f"[dit block] chained {name}: {met}", flush=True)
         # One-ulp differences in the projections move the chained inputs of
-        # every later stage; the block output stays within the GEMM gate. In
-        # Sage mode those differences also change some int8 Q/K codes, and with
-        # the nearly one-hot softmax of these weights a changed code can move
-        # a whole row's winning key: the chained attention is held to the
-        # cosine gate and 5% rel-L2 (measured 2%), the residual stream after it
-        # to the GEMM gate.
-        rel = 0.05 if (mode == 1 and name == "attn") else GEMM_REL_L2
-        assert met["cosine"] >= ATTN_COSINE and met["rel_l2"] <= rel, (name, met)
+        # every later stage; each stays within the GEMM gate.
+        assert met["cosine"] >= ATTN_COSINE and met["rel_l2"] <= GEMM_REL_L2, (name, met)
 
     # Output head on the last block's output, then the Euler update.
     hn = oracle.adaln(hidden, head_norm, head_mod, rmap, R, H, 2, 0, 1, eps)
