@@ -10,6 +10,7 @@
 #include "sol.h"
 #include "../../include/h3_policy.h"
 #include <cmath>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -40,9 +41,45 @@ struct h3_attention_state {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
 };
 
+// ---------------------------------------------------------------- no-allocation scratch
+// Workspace of h3_hip_sdpa_bf16_noalloc: the transposed V and the retry bytes
+// of the dense BF16 kernel, in a fixed device array instead of a grow-only
+// allocation. 384 MiB holds S = 32400 x H = 40 (332 MB) and S = 18225 x
+// H = 56 (261 MB). The runtime gives every device its own copy of the array
+// when the code object loads, held until the process ends. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in for
+// the symbol): each device's address comes from hipGetSymbolAddress, taken
+// once per device at context creation with that device current.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(384) << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void *scratch_address[MAX_DEVICES];   // per device, once resolved
+bool scratch_resolved[MAX_DEVICES];
+}  // namespace
+
+// With g->device current (h3_gpu_create runs on it). A failure is remembered
+// and reported by the entry point; contexts that never use it are unaffected.
+static void resolve_scratch(h3_gpu *g) {
+    if (g->device < 0 || g->device >= MAX_DEVICES) return;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_resolved[g->device]) return;
+    void *ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
+        (void)hipGetLastError();
+        ptr = nullptr;
+    }
+    scratch_address[g->device] = ptr;
+    scratch_resolved[g->device] = true;
+}
+
 int h3_attention_init(h3_gpu *g) {
     g->attention = new (std::nothrow) h3_attention_state();
-    return g->attention ? 1 : h3_set_error(g, "attention: out of host memory");
+    if (!g->attention) return h3_set_error(g, "attention: out of host memory");
+    resolve_scratch(g);
+    return 1;
 }
 
 void h3_attention_destroy(h3_gpu *g) {
@@ -266,6 +303,34 @@ extern "C" int h3_gpu_sdpa_bf16_head_major_output(h3_gpu *g, h3_gpu_tensor *out,
                                                   uint32_t heads, uint32_t dim, float scale) {
     if (!g || !validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
     return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), true, MODE_DEFAULT, false);
+}
+
+// Dense BF16 SDPA (the kernels of h3_gpu_sdpa_bf16 / _head_major_output)
+// with its workspace in the fixed scratch array: no device allocation and no
+// allocating library call. Every call on one device shares that device's
+// array, so calls that overlap on one GPU (two contexts, or two streams) race.
+// Nothing in the array needs clearing: the V transpose writes every byte the
+// kernel reads, and every wave of the main launch writes its retry byte.
+extern "C" int h3_hip_sdpa_bf16_noalloc(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q,
+                                        const h3_gpu_tensor *k, const h3_gpu_tensor *v, uint32_t seq,
+                                        uint32_t heads, uint32_t dim, float scale, int head_major) {
+    if (!g || !validate(g, out, q, k, v, seq, heads, dim, scale)) return 0;
+    if (head_major != 0 && head_major != 1) return h3_set_error(g, "no-allocation attention: head_major must be 0/1");
+    const size_t need = h3_attention_bf16_workspace(seq, heads);
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return h3_set_error(g, "no-allocation attention: S=%u H=%u needs %zu workspace bytes, above the fixed %zu",
+                            seq, heads, need, NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(scratch_mutex);
+        if (g->device >= 0 && g->device < MAX_DEVICES && scratch_resolved[g->device]) ws = scratch_address[g->device];
+    }
+    if (!ws) return h3_set_error(g, "no-allocation attention: the scratch array of device %d is not available", g->device);
+    const int ok = h3_launch_attention_bf16(g, ws, (uint16_t *)out->data, (const uint16_t *)q->data,
+                                            (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads,
+                                            round_scale_bf16(scale), head_major != 0, nullptr, nullptr, 0);
+    if (ok) g->stats.attention_dispatches++;
+    return ok;
 }
 
 extern "C" int h3_hip_dit_subblock_policy(h3_gpu *g, float sparsity, int warmup) {

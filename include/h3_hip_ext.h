@@ -42,6 +42,20 @@ int h3_hip_fill_q8_random(h3_gpu *gpu, h3_gpu_tensor *weight, uint64_t seed, flo
  * codes followed by the scales (the h3_hip_tensor_stream_host layout). */
 int h3_hip_tensor_copy_to_host(h3_gpu_tensor *tensor, void *dst, size_t bytes);
 
+/* Dense BF16 SDPA that allocates nothing: the computation, arguments, errors
+ * and output of h3_gpu_sdpa_bf16 (head_major 0) or
+ * h3_gpu_sdpa_bf16_head_major_output (head_major 1), bit for bit, with the
+ * workspace (transposed V and retry bytes) in a fixed 384 MiB device array
+ * instead of a device allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Workspaces above 384 MiB are
+ * refused with an error (S * H up to about 1.5M rows, e.g. S = 32400 with
+ * H = 40). All calls on one GPU share its array: calls that overlap on one
+ * GPU race. Requires an active command (h3_gpu_begin). */
+int h3_hip_sdpa_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_tensor *query,
+                             const h3_gpu_tensor *key, const h3_gpu_tensor *value, uint32_t sequence,
+                             uint32_t heads, uint32_t head_dim, float scale, int head_major);
+
 /* Fixed block-sparse mask for main-DiT attention. mask is u8 [q_blocks, k_blocks]
  * (nonzero = keep) over block x block tiles; block must be 128 (or 64). While a
  * mask is bound, h3_gpu_dit_sdpa_bf16 computes softmax over the kept key tiles
