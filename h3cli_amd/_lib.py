@@ -126,6 +126,10 @@ _SIGNATURES.update({
     "h3_hip_dit_synth_create": (_p, [_p, C.POINTER(DitSynthConfig), C.c_char_p, _sz]),
     "h3_hip_dit_synth_free": (None, [_p]),
     "h3_hip_sdpa_bf16_noalloc": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _f, _i]),
+    "h3_sglang_flash": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _f, _i, _i, _p, C.c_char_p, _sz]),
+    "h3_sglang_flash_query_range": (_i, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _f, _i, _p, C.c_char_p, _sz]),
+    "h3_hip_tensor_device_pointer": (_p, [_p]),
+    "h3_hip_compute_stream": (_p, [_p]),
     "h3_hip_dit_time_features": (None, [_p, _u32, _p]),
     "h3_hip_dit_rope_tables": (_i, [_u32, _u32, _u32, _u32, _u32, _p, _p]),
     "h3_hip_dit_synth_load": (_i, [_p, C.c_char_p, C.c_char_p, _sz]),

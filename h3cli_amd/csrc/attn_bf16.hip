@@ -73,6 +73,12 @@ struct Args {
     const uint64_t *cent_mask;
     unsigned cent_stride, key_blocks, kc_padded;
     const uint16_t *kc, *vct;
+    // Dense kernel only: query rows when they are fewer than the keys (a query
+    // range; q and out point at its first row, the head-major output keeps the
+    // full sequence stride), 0 for all seq rows; and an optional FP32 log-sum-
+    // exp per (head, query row) of scale * q.k in natural-log units.
+    unsigned qrows;
+    float *lse;
 };
 
 // Position of key j (0..63) inside a transposed V row: keys are grouped by 16
@@ -382,7 +388,8 @@ void attn_bf16_wide(Args a) {
 
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
-    const unsigned nqb = (a.seq + BM - 1) / BM;
+    const unsigned qrows = a.qrows ? a.qrows : a.seq;
+    const unsigned nqb = (qrows + BM - 1) / BM;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned head = id / nqb, qb = id % nqb;
     const unsigned q0 = qb * BM;
@@ -415,7 +422,7 @@ void attn_bf16_wide(Args a) {
     bf16x8 qf[8];
     {
         unsigned row = q0 + wave * 32 + n;
-        row = row < a.seq ? row : a.seq - 1;
+        row = row < qrows ? row : qrows - 1;
         const uint16_t *p = qh + (size_t)row * stride + hf * 8;
         bool bad = false;
 #pragma unroll
@@ -619,7 +626,7 @@ void attn_bf16_wide(Args a) {
     const float inv = total > 0.f ? 1.f / total : 0.f;
     const unsigned q = q0 + wave * 32 + n;
     bool bad = false;
-    if (q < a.seq) {
+    if (q < qrows) {
         uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
 #pragma unroll
         for (int md = 0; md < 4; md++)
@@ -646,6 +653,8 @@ void attn_bf16_wide(Args a) {
         if (any) return;
     }
     if (bad) a.fault[0] = 1u;
+    // m + log2(total) is log2 of sum_j 2^(c s_j) = log2 sum_j e^(scale s_j).
+    if (a.lse && hf == 0 && q < qrows) a.lse[(size_t)head * qrows + q] = (m + log2f(total)) * 0.6931471805599453f;
 }
 
 template <int KT, bool SPARSE, bool MSUM, bool NOMAX, int WAVES = 8>
@@ -1045,6 +1054,27 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     // CU, whose barriers are independent, 64 keys per interval (6% slower).
     if (g->attention_variant == 4) return launch_wide<1, false, false, true, 4>(g, a, (seq + 127) / 128 * heads);
     return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
+}
+
+// Dense attention of query rows [first, first + qrows) (q and out already
+// offset to the first row) over all seq keys, with the FP32 log-sum-exp per
+// (head, query row) written to lse [heads, qrows]: the fast kernel and its
+// recomputation launch, whatever the variant selector says.
+int h3_launch_attention_flash(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, float *lse, uint32_t seq, uint32_t qrows, uint32_t heads,
+                              float scale, bool head_major) {
+    Args a{};
+    a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
+    a.seq = seq; a.qrows = qrows; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.head_major = head_major ? 1 : 0;
+    a.lse = lse;
+    a.fault = g->fault;
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
+                       seq, heads, a.padded, g->fault);
+    if (!h3_launch_status(g, "V transpose")) return 0;
+    a.retry = (uint8_t *)workspace + retry_offset(seq, heads);
+    return launch_wide<2, false, false, true>(g, a, (qrows + 255) / 256 * heads);
 }
 
 int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,

@@ -214,6 +214,12 @@ extern "C" h3_gpu_tensor *h3_gpu_tensor_alloc(h3_gpu *g, size_t elements, h3_gpu
     return t;
 }
 
+extern "C" void *h3_hip_tensor_device_pointer(h3_gpu_tensor *t) {
+    return t && t->storage == H3_GPU_DEVICE_ONLY ? t->data : nullptr;
+}
+
+extern "C" void *h3_hip_compute_stream(h3_gpu *g) { return g ? (void *)g->compute : nullptr; }
+
 extern "C" void *h3_gpu_tensor_contents(h3_gpu_tensor *t) {
     if (!t || t->storage == H3_GPU_DEVICE_ONLY) return nullptr;
     hipStreamSynchronize(t->owner->compute);

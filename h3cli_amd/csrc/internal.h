@@ -19,6 +19,11 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
                              const uint16_t *v, uint32_t seq, uint32_t heads, float scale,
                              bool head_major, const uint32_t *kv_list, const uint32_t *kv_count,
                              uint32_t list_stride);
+// Dense attention of qrows query rows (q, out offset to the first) over seq
+// keys with the FP32 natural-log LSE per (head, query row) into lse [heads, qrows].
+int h3_launch_attention_flash(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, float *lse, uint32_t seq, uint32_t qrows, uint32_t heads,
+                              float scale, bool head_major);
 // Routed attention over per-(head, 64-query block) lists of kept 64-key tiles:
 // lists [heads][ceil(seq/64)][list_stride], counts [heads][ceil(seq/64)].
 int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,

@@ -56,6 +56,13 @@ int h3_hip_sdpa_bf16_noalloc(h3_gpu *gpu, h3_gpu_tensor *output, const h3_gpu_te
                              const h3_gpu_tensor *key, const h3_gpu_tensor *value, uint32_t sequence,
                              uint32_t heads, uint32_t head_dim, float scale, int head_major);
 
+/* Interop with stream-level entry points (include/h3_sglang_flash.h): a
+ * tensor's device address (NULL for host-visible storage) and the context's
+ * compute stream (a hipStream_t), so such calls order with the context's
+ * own work. */
+void *h3_hip_tensor_device_pointer(h3_gpu_tensor *tensor);
+void *h3_hip_compute_stream(h3_gpu *gpu);
+
 /* Fixed block-sparse mask for main-DiT attention. mask is u8 [q_blocks, k_blocks]
  * (nonzero = keep) over block x block tiles; block must be 128 (or 64). While a
  * mask is bound, h3_gpu_dit_sdpa_bf16 computes softmax over the kept key tiles
