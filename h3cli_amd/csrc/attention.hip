@@ -184,7 +184,7 @@ static float round_scale_bf16(float scale) {
 
 static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
                     const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                    int mode, bool masked, bool routed = false) {
+                    int mode, bool masked) {
     auto *s = g->attention;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     if (g->profiling) {
@@ -195,13 +195,7 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
     const uint32_t *cnt = masked ? s->kv_count : nullptr;
     const uint32_t stride = s->list_stride;
     int ok;
-    if (routed) {
-        ok = h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") &&
-             h3_launch_attention_routed(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data,
-                                        (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads, scale,
-                                        head_major, h3_subblock_lists(&s->router), h3_subblock_counts(&s->router),
-                                        s->router.blocks);
-    } else if (mode == MODE_SAGE2) {
+    if (mode == MODE_SAGE2) {
         ok = h3_sage_attention(g, &s->sage, (uint16_t *)out->data, (const uint16_t *)q->data, (const uint16_t *)k->data,
                                (const uint16_t *)v->data, seq, heads, scale, head_major, list, cnt, stride);
         if (ok) g->stats.sage2_attention_dispatches++;
@@ -217,9 +211,55 @@ static int dispatch(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const
     }
     if (ok) {
         g->stats.attention_dispatches++;
-        if (routed) { g->stats.subblock_calls++; g->stats.subblock_protected_calls += s->router.protected_ranges; }
-        else if (masked) { g->stats.subblock_calls++; g->stats.subblock_selected += s->kept_tiles; g->stats.subblock_possible += s->total_tiles; }
+        if (masked) { g->stats.subblock_calls++; g->stats.subblock_selected += s->kept_tiles; g->stats.subblock_possible += s->total_tiles; }
         else if (mode == MODE_DEFAULT) g->stats.main_dense_calls++;
+    }
+    return ok;
+}
+
+// SubBlock routed attention (reference gpu_cuda.cu:1620-1639) under the fixed
+// workspace budget: heads in groups and 64-query blocks in slabs, as planned
+// by h3_subblock_plan; each chunk routes its slab (pooling its head group's
+// cells and transposing its V on the group's first slab) and runs the listed
+// kernel over it. Every (head, query block) is computed as in one whole call,
+// so the output does not depend on the split.
+static int routed(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q, const h3_gpu_tensor *k,
+                  const h3_gpu_tensor *v, uint32_t seq, uint32_t heads, float scale, bool head_major, unsigned keep) {
+    auto *s = g->attention;
+    auto *r = &s->router;
+    h3_subblock_chunking plan;
+    if (!h3_subblock_plan(g, r, seq, heads, &plan)) return 0;
+    if (!h3_buffer_reserve(g, &s->bf16_ws, plan.vt_bytes, "attention workspace")) return 0;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (g->profiling) {
+        hipEventCreate(&t0); hipEventCreate(&t1);
+        hipEventRecord(t0, g->compute);
+    }
+    const uint32_t blocks = r->blocks;
+    const auto *qd = (const uint16_t *)q->data, *kd = (const uint16_t *)k->data, *vd = (const uint16_t *)v->data;
+    r->plan = plan;
+    r->chunked = plan.group < heads || plan.slab < blocks;
+    int ok = 1;
+    for (uint32_t h0 = 0; ok && h0 < heads; h0 += plan.group) {
+        const uint32_t gh = std::min(plan.group, heads - h0);
+        for (uint32_t qb0 = 0; ok && qb0 < blocks; qb0 += plan.slab) {
+            const uint32_t qs = std::min(plan.slab, blocks - qb0);
+            ok = h3_subblock_route(g, r, qd, kd, seq, heads, h0, gh, qb0, qs, scale, keep, false, qb0 == 0) &&
+                 h3_launch_attention_routed(g, s->bf16_ws.ptr, (uint16_t *)out->data, qd, kd, vd, seq, heads, scale,
+                                            head_major, h3_subblock_lists(r), h3_subblock_counts(r), blocks, h0, gh,
+                                            qb0, qs, qb0 == 0);
+        }
+    }
+    g->stats.attention_workspace_bytes = s->sage.bytes + s->bf16_ws.bytes + r->ws.bytes;
+    if (g->profiling) {
+        hipEventRecord(t1, g->compute);
+        s->pending.emplace_back(t0, t1);
+    }
+    if (ok) {
+        g->stats.subblock_router_calls++;
+        g->stats.attention_dispatches++;
+        g->stats.subblock_calls++;
+        g->stats.subblock_protected_calls += r->protected_ranges;
     }
     return ok;
 }
@@ -278,10 +318,7 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
             // is the dense result the reference computes for them separately.
             const unsigned blocks = (seq + 63) / 64;
             const unsigned keep = h3_subblock_budget(blocks, s->subblock_sparsity);
-            if (!h3_subblock_route(g, &s->router, (const uint16_t *)q->data, (const uint16_t *)k->data, seq, heads,
-                                   scale, keep, false))
-                return 0;
-            return dispatch(g, out, q, k, v, seq, heads, scale, head_major != 0, MODE_DEFAULT, false, true);
+            return routed(g, out, q, k, v, seq, heads, scale, head_major != 0, keep);
         }
     }
     // A kept last 128-key block may list a 64-key tile wholly past the sequence
@@ -361,5 +398,23 @@ extern "C" int h3_hip_sol_counters(h3_gpu *g, uint64_t *out, size_t count) {
 extern "C" int h3_hip_dit_sol_force_exact(h3_gpu *g, int on) {
     if (!g) return 0;
     g->attention->sol.force_exact = on != 0;
+    return 1;
+}
+
+// Workspace budget of SubBlock routed calls on this context (0 restores the
+// fixed 512 MiB) and the split of the last routed call.
+extern "C" int h3_hip_subblock_workspace_cap(h3_gpu *g, size_t bytes) {
+    if (!g || !g->attention) return 0;
+    g->attention->router.cap = bytes ? bytes : H3_SUBBLOCK_WORKSPACE_CAP;
+    return 1;
+}
+
+extern "C" int h3_hip_subblock_plan_info(h3_gpu *g, uint32_t *group, uint32_t *slab, size_t *bytes) {
+    if (!g || !g->attention) return 0;
+    const auto &p = g->attention->router.plan;
+    if (!p.group) return h3_set_error(g, "SubBlock plan: no routed call yet");
+    if (group) *group = p.group;
+    if (slab) *slab = p.slab;
+    if (bytes) *bytes = p.bytes;
     return 1;
 }

@@ -124,6 +124,7 @@ struct h3_gpu {
     // Kernel-shape selector for measurement (H3_HIP_ATTENTION_VARIANT): 0 is the
     // default shape, other values pick the alternatives each kernel documents.
     int attention_variant;
+    int gemm_variant;
     char label[64];         // h3_gpu_profile_set_label
     double created;         // wall clock at creation (profile marks)
     bool allocation_failed; // a device allocation ran out of memory

@@ -99,6 +99,7 @@ extern "C" h3_gpu *h3_gpu_create(const char *shader_source_path, char *error, si
     g->created = now_seconds();
     g->profiling = getenv("H3_PROFILE") != nullptr;
     if (const char *v = getenv("H3_HIP_ATTENTION_VARIANT")) g->attention_variant = atoi(v);
+    if (const char *v = getenv("H3_HIP_GEMM_VARIANT")) g->gemm_variant = atoi(v);
     // Both streams keep the default priority.
     if ((e = hipStreamCreateWithFlags(&g->compute, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipStreamCreateWithFlags(&g->copy, hipStreamNonBlocking)) != hipSuccess) {

@@ -69,12 +69,23 @@ __device__ inline float gelu_tanh(float v) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// 8 waves as 2 (M) x 4 (N); each wave owns a 128 x 64 output tile (8 MFMA
-// blocks), two waves per SIMD. CHANNEL: one scale per output row (group == K),
+// WM x WN waves; each wave owns a (256 / WM) x (256 / WN) output tile of
+// 32 x 32 MFMA blocks. 2 x 4 waves (128 x 64 per wave, two waves per SIMD) or
+// 2 x 2 waves (128 x 128 per wave, one wave per SIMD: the 256 accumulator
+// registers sit in AGPRs, and each fragment read from LDS feeds four MFMAs
+// instead of two or four). CHANNEL: one scale per output row (group == K),
 // loaded once. EPI bit 0: bias, bit 1: GELU, bit 2: alpha (before the bias).
-template <bool Q8, bool CHANNEL, int EPI>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4, int XST = 2>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * WM * WN, 64 * WM * WN),
+                          amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_kernel(GemmArgs a) {
+    constexpr int T = 64 * WM * WN;            // threads
+    constexpr int NBM = TM / WM / 32, NBN = TN / WN / 32;
+    constexpr int WCH = 1024 / T;              // weight chunks per thread
+    // XST = 3 (q8 only): three X stages and two BF16 weight stages in LDS
+    // (160 KB), X and int8 W loads issued two k-steps ahead.
+    static_assert(XST == 2 || (XST == 3 && Q8), "three X stages need register-staged weights");
+    constexpr int VM_PER_STEP = 32 / (WM * WN) + WCH + (CHANNEL ? 0 : WCH);
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
     const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
@@ -85,40 +96,43 @@ void gemm_kernel(GemmArgs a) {
     const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
     const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
     const unsigned m0 = tm * TM, n0 = tn * TN;
-    const unsigned wm = wave / 4, wn = wave % 4;   // wave rows m0 + wm*128, columns n0 + wn*64
+    const unsigned wm = wave / WN, wn = wave % WN;   // wave rows m0 + wm*32*NBM, columns n0 + wn*32*NBN
     const unsigned ksteps = a.k / TK;
 
-    f32x16 acc[2][4];   // [n block][m block], C^T layout: lane = output row, regs = columns
+    f32x16 acc[NBN][NBM];   // [n block][m block], C^T layout: lane = output row, regs = columns
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < NBN; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+        for (int j = 0; j < NBM; j++) acc[i][j] = f32x16{};
 
-    // Weight staging (q8): 256 rows x 64 int8 = 1024 16-byte chunks, 2 per thread.
-    i32x4 wq[2];
-    float wscale[2];
+    // Weight staging (q8): 256 rows x 64 int8 = 1024 16-byte chunks, WCH per thread.
+    i32x4 wq[WCH], wq2[WCH];
+    float wscale[WCH], wscale2[WCH];
     if constexpr (Q8 && CHANNEL) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) wscale[j] = a.scales[n0 + w_row(tid + 512 * j)];
+        for (int j = 0; j < WCH; j++) wscale2[j] = wscale[j] = a.scales[n0 + w_row(tid + T * j)];
     }
-    auto load_w = [&](unsigned kt) {
+    auto load_w_into = [&](unsigned kt, i32x4 *dq, float *ds) {
         if constexpr (Q8) {
             const int8_t *w8 = reinterpret_cast<const int8_t *>(a.w);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                unsigned c = tid + 512 * j, row = w_row(c), part = w_part(c);
-                wq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
+            for (int j = 0; j < WCH; j++) {
+                unsigned c = tid + T * j, row = w_row(c), part = w_part(c);
+                dq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
                 if constexpr (!CHANNEL)
-                    wscale[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
+                    ds[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
             }
         }
     };
-    auto store_w = [&](int stage) {
+    auto load_w = [&](unsigned kt) { load_w_into(kt, wq, wscale); };
+    auto x_stage = [&](int stage) { return lds + stage * (XST == 3 ? TILE_BYTES : STAGE); };
+    auto w_stage = [&](int stage) { return XST == 3 ? lds + (3 + stage) * TILE_BYTES : lds + stage * STAGE + TILE_BYTES; };
+    auto store_w_from = [&](int stage, const i32x4 *wq, const float *wscale) {
         if constexpr (Q8) {
-            uint8_t *ws = lds + stage * STAGE + TILE_BYTES;
+            uint8_t *ws = w_stage(stage);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                unsigned c = tid + 512 * j, row = w_row(c), part = w_part(c);
+            for (int j = 0; j < WCH; j++) {
+                unsigned c = tid + T * j, row = w_row(c), part = w_part(c);
                 bf16x8 half[2];
 #pragma unroll
                 for (int e = 0; e < 16; e += 2) {
@@ -134,11 +148,12 @@ void gemm_kernel(GemmArgs a) {
             }
         }
     };
+    auto store_w = [&](int stage) { store_w_from(stage, wq, wscale); };
     // Direct global -> LDS loads: X rows (clamped at M) and, for BF16 weights, W rows.
     auto load_direct = [&](unsigned kt, int stage) {
-        uint8_t *xs = lds + stage * STAGE;
+        uint8_t *xs = x_stage(stage);
 #pragma unroll
-        for (unsigned b = wave; b < 32; b += 8) {
+        for (unsigned b = wave; b < 32; b += WM * WN) {
             unsigned row = 8 * b + lane / 8, ph = lane % 8;
             unsigned gm = min(m0 + row, a.m - 1);
             const uint16_t *src = a.x + (size_t)gm * a.k + kt * TK + swz(row, ph) * 8;
@@ -153,17 +168,60 @@ void gemm_kernel(GemmArgs a) {
     };
     auto frags = [&](const uint8_t *xs, const uint8_t *ws, int ks, bf16x8 *wf, bf16x8 *xf) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            unsigned wr = wn * 64 + i * 32 + n32;
+        for (int i = 0; i < NBN; i++) {
+            unsigned wr = wn * 32 * NBN + i * 32 + n32;
             wf[i] = *reinterpret_cast<const bf16x8 *>(ws + wr * ROW_BYTES + swz(wr, ks * 2 + hf) * 16);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            unsigned xr = wm * 128 + j * 32 + n32;
+        for (int j = 0; j < NBM; j++) {
+            unsigned xr = wm * 32 * NBM + j * 32 + n32;
             xf[j] = *reinterpret_cast<const bf16x8 *>(xs + xr * ROW_BYTES + swz(xr, ks * 2 + hf) * 16);
         }
     };
 
+    if constexpr (XST == 3) {
+        // Step kt: issue X(kt+2) and W(kt+2) (indices clamped, so the loads are
+        // unconditional; past the end they refill stages no step reads again),
+        // run the MFMAs of stage kt, then dequantize W(kt+1) into its LDS stage.
+        // The two register sets alternate roles by call site, so no loaded
+        // register is copied (a copy would wait for its load).
+        auto step = [&](unsigned kt, i32x4 *held, float *held_s, i32x4 *next, float *next_s) {
+            const unsigned k2 = min(kt + 2, ksteps - 1);
+            load_direct(k2, (kt + 2) % 3);
+            load_w_into(k2, next, next_s);
+            const uint8_t *xs = x_stage(kt % 3);
+            const uint8_t *ws = w_stage(kt & 1);
+            bf16x8 wf[2][NBN], xf[2][NBM];
+            frags(xs, ws, 0, wf[0], xf[0]);
+#pragma unroll
+            for (int ks = 0; ks < TK / 16; ks++) {
+                if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
+#pragma unroll
+                for (int i = 0; i < NBN; i++)
+#pragma unroll
+                    for (int j = 0; j < NBM; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
+            }
+            store_w_from((kt + 1) & 1, held, held_s);
+            // X(kt+1) has landed; the loads of step kt+2 stay in flight.
+            __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STEP);
+            __syncthreads();
+        };
+        load_direct(0, 0);
+        load_w_into(0, wq2, wscale2);
+        load_direct(min(1u, ksteps - 1), 1);
+        load_w_into(min(1u, ksteps - 1), wq, wscale);
+        store_w_from(0, wq2, wscale2);
+        __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STEP);
+        __syncthreads();
+        unsigned kt = 0;
+        for (; kt + 1 < ksteps; kt += 2) {
+            step(kt, wq, wscale, wq2, wscale2);
+            step(kt + 1, wq2, wscale2, wq, wscale);
+        }
+        if (kt < ksteps) step(kt, wq, wscale, wq2, wscale2);
+        wait_vm_loads();
+    } else {
     load_direct(0, 0);
     load_w(0);
     store_w(0);
@@ -174,37 +232,38 @@ void gemm_kernel(GemmArgs a) {
         const int cur = kt & 1;
         const bool more = kt + 1 < ksteps;
         if (more) { load_direct(kt + 1, cur ^ 1); load_w(kt + 1); }
-        const uint8_t *xs = lds + cur * STAGE;
-        const uint8_t *ws = xs + TILE_BYTES;
+        const uint8_t *xs = x_stage(cur);
+        const uint8_t *ws = w_stage(cur);
         // Fragments of k-step ks+1 are read while the MFMAs of ks run.
-        bf16x8 wf[2][2], xf[2][4];
+        bf16x8 wf[2][NBN], xf[2][NBM];
         frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ks++) {
             if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < NBN; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < NBM; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
         }
         if (more) store_w(cur ^ 1);
         wait_vm_loads();
         __syncthreads();
     }
+    }
 
-    // Epilogue: lane holds output row m = m0 + wm*128 + j*32 + n32 and columns
-    // n0 + wn*64 + i*32 + g*8 + hf*4 + 0..3 for register group g.
+    // Epilogue: lane holds output row m = m0 + wm*32*NBM + j*32 + n32 and columns
+    // n0 + wn*32*NBN + i*32 + g*8 + hf*4 + 0..3 for register group g.
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const unsigned row = m0 + wm * 128 + j * 32 + n32;
+    for (int j = 0; j < NBM; j++) {
+        const unsigned row = m0 + wm * 32 * NBM + j * 32 + n32;
         if (row >= a.m) continue;
         uint16_t *dst = a.y + (size_t)row * a.n;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < NBN; i++)
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
-                const unsigned col = n0 + wn * 64 + i * 32 + g4 * 8 + hf * 4;
+                const unsigned col = n0 + wn * 32 * NBN + i * 32 + g4 * 8 + hf * 4;
                 u16x4 out;
                 u16x4 bias4 = {};
                 if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
@@ -247,11 +306,11 @@ __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
     a.y[idx] = b;
 }
 
-template <bool Q8, bool CHANNEL, int EPI>
+template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4, int XST = 2>
 int launch_tiled(h3_gpu *g, const GemmArgs &a) {
-    constexpr size_t shared = 2 * STAGE;
+    constexpr size_t shared = XST == 3 ? 5 * TILE_BYTES : 2 * STAGE;
     static bool configured = false;
-    auto kernel = gemm_kernel<Q8, CHANNEL, EPI>;
+    auto kernel = gemm_kernel<Q8, CHANNEL, EPI, WM, WN, XST>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)shared), "GEMM shared memory"))
@@ -260,7 +319,7 @@ int launch_tiled(h3_gpu *g, const GemmArgs &a) {
     }
     unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
     hipEvent_t timing = h3_kernel_timing_begin(g);
-    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(512), shared, g->compute, a);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(64 * WM * WN), shared, g->compute, a);
     h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, Q8 ? "W8A16 GEMM" : "BF16 GEMM");
 }
@@ -268,6 +327,24 @@ int launch_tiled(h3_gpu *g, const GemmArgs &a) {
 template <bool Q8, bool CHANNEL>
 int launch_epi(h3_gpu *g, const GemmArgs &a) {
     const int epi = (a.bias ? 1 : 0) | (a.gelu ? 2 : 0);
+    if constexpr (Q8) {
+        if (g->gemm_variant == 2) {
+            switch (epi) {
+            case 0: return launch_tiled<Q8, CHANNEL, 0, 2, 4, 3>(g, a);
+            case 1: return launch_tiled<Q8, CHANNEL, 1, 2, 4, 3>(g, a);
+            case 2: return launch_tiled<Q8, CHANNEL, 2, 2, 4, 3>(g, a);
+            default: return launch_tiled<Q8, CHANNEL, 3, 2, 4, 3>(g, a);
+            }
+        }
+    }
+    if (g->gemm_variant == 1) {
+        switch (epi) {
+        case 0: return launch_tiled<Q8, CHANNEL, 0, 2, 2>(g, a);
+        case 1: return launch_tiled<Q8, CHANNEL, 1, 2, 2>(g, a);
+        case 2: return launch_tiled<Q8, CHANNEL, 2, 2, 2>(g, a);
+        default: return launch_tiled<Q8, CHANNEL, 3, 2, 2>(g, a);
+        }
+    }
     switch (epi) {
     case 0: return launch_tiled<Q8, CHANNEL, 0>(g, a);
     case 1: return launch_tiled<Q8, CHANNEL, 1>(g, a);

@@ -24,11 +24,14 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
 int h3_launch_attention_flash(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                               const uint16_t *v, float *lse, uint32_t seq, uint32_t qrows, uint32_t heads,
                               float scale, bool head_major);
-// Routed attention over per-(head, 64-query block) lists of kept 64-key tiles:
-// lists [heads][ceil(seq/64)][list_stride], counts [heads][ceil(seq/64)].
+// Routed attention of heads [head0, head0 + group) and 64-query blocks
+// [qb0, qb0 + qslab) over lists of kept 64-key tiles, slab-relative:
+// lists [group][qslab][list_stride], counts [group][qslab]. workspace holds
+// the group's transposed V (written first when transpose is set).
 int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                                const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                               const uint32_t *lists, const uint32_t *counts, uint32_t list_stride);
+                               const uint32_t *lists, const uint32_t *counts, uint32_t list_stride,
+                               uint32_t head0, uint32_t group, uint32_t qb0, uint32_t qslab, bool transpose);
 
 // SOL attention lists (see csrc/sol.hip): exact tiles per (head, query block),
 // centroid tiles with their approximate-block masks, and the centroid arrays.

@@ -72,15 +72,19 @@ __device__ inline float quad_sum(float x) {
 // of 32 key cells (8 key blocks each). S^T = Kpool . Qpool^T on the matrix
 // core: lane n holds query cell n and, for g = 0..3, the four cells of key
 // block 2g + (lane / 32), so the key-cell log-sum-exp is lane-local and the
-// query-cell one spans four adjacent lanes.
+// query-cell one spans four adjacent lanes. The grid covers the query blocks
+// [qb0, qb0 + qslab) (qb0 a multiple of 32, so the cell tiles stay inside the
+// padded pool); scores are written slab-relative, [head][qslab][blocks].
 __global__ __launch_bounds__(256) void sb_score(const uint16_t *qpool, const uint16_t *kpool, float *scores,
-                                                unsigned seq, unsigned cells, unsigned blocks, unsigned *fault) {
+                                                unsigned seq, unsigned cells, unsigned blocks, unsigned qb0,
+                                                unsigned qslab, unsigned *fault) {
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64, n = lane % 32, hf = lane / 32;
     const unsigned head = blockIdx.z;
-    const unsigned qt = blockIdx.x * (CELL_TILE / 32) + wave;          // 32-cell query tile
+    const unsigned qt = blockIdx.x * (CELL_TILE / 32) + wave;          // 32-cell query tile in the slab
     const unsigned valid = (seq + 15) / 16;                            // cells holding rows
-    const unsigned qcell = qt * 32 + n, qblock = qcell / 4, a = qcell % 4;
-    if (qt * 8 >= blocks) return;
+    const unsigned qcell = qb0 * 4 + qt * 32 + n, qblock = qcell / 4, a = qcell % 4;
+    const unsigned qend = min(blocks, qb0 + qslab);
+    if (qt * 8 >= qslab) return;
     const uint16_t *qh = qpool + (size_t)head * cells * D;
     const uint16_t *kh = kpool + (size_t)head * cells * D;
     bf16x8 qf[8];
@@ -121,10 +125,10 @@ __global__ __launch_bounds__(256) void sb_score(const uint16_t *qpool, const uin
             // Query-cell log-sum-exp over the block's four lanes.
             const float top = quad_max(lse);
             const float total = quad_sum(q_valid && nk ? __builtin_amdgcn_exp2f(lse - top) : 0.f);
-            if (a == 0 && qblock < blocks && kblock < blocks) {
+            if (a == 0 && qblock < qend && kblock < blocks) {
                 const float score = (top + __builtin_amdgcn_logf(total)) * 0.6931471805599453f;
                 bad |= !finite_f32(score);
-                scores[((size_t)head * blocks + qblock) * blocks + kblock] = score;
+                scores[((size_t)head * qslab + (qblock - qb0)) * blocks + kblock] = score;
             }
         }
     }
@@ -138,7 +142,8 @@ __device__ inline uint32_t score_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// One workgroup per (query block, head). Route rule and counters of the
+// One workgroup per (query block of the slab [qb0, qb0 + qslab), head); rows
+// of scores, routes, lists and counts are slab-relative. Route rule and counters of the
 // reference's selection (cuda_subblock.cu:300-324): with
 // rank(k) = #{j : s_j > s_k} + #{j < k : s_j == s_k}, key block k is kept
 // when rank < keep, when it is protected, when the query block is protected
@@ -150,15 +155,15 @@ __device__ inline uint32_t score_key(float f) {
 // added_blocks[row] the protected key blocks kept beyond the top.
 __global__ __launch_bounds__(256) void sb_select(const float *scores, uint8_t *routes, const uint8_t *q_protect,
                                                  const uint8_t *k_protect, unsigned blocks, unsigned padded,
-                                                 unsigned keep, int force_all, uint32_t *lists, uint32_t *counts,
-                                                 uint32_t *added_blocks) {
+                                                 unsigned keep, int force_all, unsigned qb0, unsigned qslab,
+                                                 uint32_t *lists, uint32_t *counts, uint32_t *added_blocks) {
     extern __shared__ unsigned long long sortbuf[];   // [padded], then top flags [blocks]
     uint8_t *top_flag = reinterpret_cast<uint8_t *>(sortbuf + padded);
     __shared__ unsigned wave_total[4];
     __shared__ unsigned red[4];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned qb = blockIdx.x, head = blockIdx.y;
-    const size_t row = (size_t)head * blocks + qb;
+    const unsigned qb = qb0 + blockIdx.x, head = blockIdx.y;
+    const size_t row = (size_t)head * qslab + blockIdx.x;
     const float *src = scores + row * blocks;
     for (unsigned i = tid; i < padded; i += 256)
         sortbuf[i] = i < blocks ? ((unsigned long long)score_key(src[i]) << 32) | (0xffffffffu - i) : 0ull;
@@ -264,39 +269,89 @@ int h3_subblock_bind(h3_gpu *g, h3_subblock_router *r, const h3_sol_layout *layo
     return 1;
 }
 
+namespace {
+// Byte layout of one chunk's router workspace; offsets into r when r is set.
+size_t router_layout(uint32_t blocks, uint32_t cells, uint32_t group, uint32_t qslab, h3_subblock_router *r) {
+    size_t off = 0, o[7];
+    o[0] = off; off = align256(off + (size_t)group * cells * D * 2);           // Q pool
+    o[1] = off; off = align256(off + (size_t)group * cells * D * 2);           // K pool
+    o[2] = off; off = align256(off + (size_t)group * qslab * blocks * 4);      // scores
+    o[3] = off; off = align256(off + (size_t)group * qslab * blocks);          // routes
+    o[4] = off; off = align256(off + (size_t)group * qslab * blocks * 4);      // lists
+    o[5] = off; off = align256(off + (size_t)group * qslab * 4);               // counts
+    o[6] = off; off = align256(off + (size_t)group * qslab * 4);               // protected added
+    if (r) {
+        r->off_qpool = o[0]; r->off_kpool = o[1]; r->off_scores = o[2]; r->off_routes = o[3];
+        r->off_list = o[4]; r->off_count = o[5]; r->off_added = o[6];
+    }
+    return off;
+}
+uint32_t cells_of(uint32_t blocks) { return (blocks * 4 + CELL_TILE - 1) / CELL_TILE * CELL_TILE; }
+}  // namespace
+
+int h3_subblock_plan(h3_gpu *g, const h3_subblock_router *r, uint32_t seq, uint32_t heads, h3_subblock_chunking *out) {
+    if (!r->bound) return h3_set_error(g, "SubBlock attention needs a bound layout (h3_gpu_dit_sol_layout)");
+    if (seq != r->seq) return h3_set_error(g, "SubBlock layout was bound for sequence %u, not %u", r->seq, seq);
+    const uint32_t blocks = (seq + 63) / 64, cells = cells_of(blocks);
+    for (uint32_t group = heads;; group = std::max(1u, group / 2)) {
+        const uint32_t g_eff = std::min(group, heads);
+        uint32_t slab = blocks;
+        for (;;) {
+            const size_t router = router_layout(blocks, cells, g_eff, slab, nullptr);
+            const size_t vt = h3_attention_bf16_workspace(seq, g_eff);
+            if (router + vt <= r->cap) {
+                out->group = g_eff; out->slab = slab;
+                out->router_bytes = router; out->vt_bytes = vt; out->bytes = router + vt;
+                return 1;
+            }
+            // Next slab: the largest multiple of 32 below the current one, halving.
+            uint32_t next = slab == blocks ? (blocks - 1) / 32 * 32 : slab / 2 / 32 * 32;
+            if (next < 32 || next >= slab) break;
+            slab = next;
+        }
+        if (group == 1) break;
+    }
+    return h3_set_error(g, "SubBlock: S=%u H=%u workspace plan exceeds its fixed budget of %zu bytes", seq, heads,
+                        r->cap);
+}
+
 int h3_subblock_route(h3_gpu *g, h3_subblock_router *r, const uint16_t *q, const uint16_t *k, uint32_t seq,
-                      uint32_t heads, float scale, unsigned keep, bool force_all) {
+                      uint32_t heads, uint32_t head0, uint32_t group, uint32_t qb0, uint32_t qslab, float scale,
+                      unsigned keep, bool force_all, bool pool) {
     if (!r->bound) return h3_set_error(g, "SubBlock attention needs a bound layout (h3_gpu_dit_sol_layout)");
     if (seq != r->seq) return h3_set_error(g, "SubBlock layout was bound for sequence %u, not %u", r->seq, seq);
     if (!keep || keep > r->blocks) return h3_set_error(g, "SubBlock: invalid budget %u of %u blocks", keep, r->blocks);
     const uint32_t blocks = r->blocks;
+    if (!group || head0 + group > heads || qb0 % 32 || !qslab || qb0 + qslab > blocks)
+        return h3_set_error(g, "SubBlock: invalid chunk (heads %u+%u of %u, blocks %u+%u of %u)", head0, group, heads,
+                            qb0, qslab, blocks);
     // Cells padded to whole score workgroups (128 cells); pad cells pool to 0.
-    const uint32_t cells = (blocks * 4 + CELL_TILE - 1) / CELL_TILE * CELL_TILE;
-    size_t off = 0;
-    r->off_qpool = off; off = align256(off + (size_t)heads * cells * D * 2);
-    r->off_kpool = off; off = align256(off + (size_t)heads * cells * D * 2);
-    r->off_scores = off; off = align256(off + (size_t)heads * blocks * blocks * 4);
-    r->off_routes = off; off = align256(off + (size_t)heads * blocks * blocks);
-    r->off_list = off; off = align256(off + (size_t)heads * blocks * blocks * 4);
-    r->off_count = off; off = align256(off + (size_t)heads * blocks * 4);
-    r->off_added = off; off = align256(off + (size_t)heads * blocks * 4);
-    r->off_counters = off; off = align256(off + 4 * 8);
-    const bool fresh = r->ws.bytes < off;
-    if (!h3_buffer_reserve(g, &r->ws, off, "SubBlock workspace")) return 0;
+    const uint32_t cells = cells_of(blocks);
+    const size_t bytes = router_layout(blocks, cells, group, qslab, r);
+    if (!pool && (r->group != group || r->head0 != head0 || r->ws.bytes < bytes))
+        return h3_set_error(g, "SubBlock: chunk without pooled cells of its head group");
+    if (!h3_buffer_reserve(g, &r->ws, bytes, "SubBlock workspace")) return 0;
+    if (!r->counters.ptr) {
+        if (!h3_buffer_reserve(g, &r->counters, 4 * 8, "SubBlock counters") ||
+            !h3_hip_check(g, hipMemsetAsync(r->counters.ptr, 0, 4 * 8, g->compute), "SubBlock counters"))
+            return 0;
+    }
     auto *base = (uint8_t *)r->ws.ptr;
-    auto *counters = (unsigned long long *)(base + r->off_counters);
-    if (fresh && !h3_hip_check(g, hipMemsetAsync(counters, 0, 4 * 8, g->compute), "SubBlock counters")) return 0;
-    r->heads = heads; r->cells = cells;
+    auto *counters = (unsigned long long *)r->counters.ptr;
+    r->heads = heads; r->cells = cells; r->group = group; r->head0 = head0; r->qb0 = qb0; r->qslab = qslab;
     auto *qpool = (uint16_t *)(base + r->off_qpool), *kpool = (uint16_t *)(base + r->off_kpool);
     auto *scores = (float *)(base + r->off_scores);
     const auto *meta = (const uint8_t *)r->meta.ptr;
 
-    hipLaunchKernelGGL(sb_pool, dim3(cells / 16, heads, 2), dim3(256), 0, g->compute, q, k, qpool, kpool, seq, heads,
-                       cells, scale * 1.4426950408889634f, g->fault);
-    if (!h3_launch_status(g, "SubBlock pool")) return 0;
+    if (pool) {
+        hipLaunchKernelGGL(sb_pool, dim3(cells / 16, group, 2), dim3(256), 0, g->compute, q + (size_t)head0 * D,
+                           k + (size_t)head0 * D, qpool, kpool, seq, heads, cells, scale * 1.4426950408889634f,
+                           g->fault);
+        if (!h3_launch_status(g, "SubBlock pool")) return 0;
+    }
     const unsigned ktiles = cells / 32;
-    hipLaunchKernelGGL(sb_score, dim3(cells / CELL_TILE, (ktiles + KEY_SPLIT - 1) / KEY_SPLIT, heads), dim3(256), 0,
-                       g->compute, qpool, kpool, scores, seq, cells, blocks, g->fault);
+    hipLaunchKernelGGL(sb_score, dim3((qslab * 4 + CELL_TILE - 1) / CELL_TILE, (ktiles + KEY_SPLIT - 1) / KEY_SPLIT, group),
+                       dim3(256), 0, g->compute, qpool, kpool, scores, seq, cells, blocks, qb0, qslab, g->fault);
     if (!h3_launch_status(g, "SubBlock score")) return 0;
     unsigned padded = 1;
     while (padded < blocks) padded <<= 1;
@@ -308,16 +363,16 @@ int h3_subblock_route(h3_gpu *g, h3_subblock_router *r, const uint16_t *q, const
             return 0;
         configured = true;
     }
-    hipLaunchKernelGGL(sb_select, dim3(blocks, heads), dim3(256), shared, g->compute, scores, base + r->off_routes,
-                       meta, meta + blocks, blocks, padded, keep, force_all ? 1 : 0, (uint32_t *)(base + r->off_list),
-                       (uint32_t *)(base + r->off_count), (uint32_t *)(base + r->off_added));
+    hipLaunchKernelGGL(sb_select, dim3(qslab, group), dim3(256), shared, g->compute, scores, base + r->off_routes,
+                       meta, meta + blocks, blocks, padded, keep, force_all ? 1 : 0, qb0, qslab,
+                       (uint32_t *)(base + r->off_list), (uint32_t *)(base + r->off_count),
+                       (uint32_t *)(base + r->off_added));
     if (!h3_launch_status(g, "SubBlock select")) return 0;
     hipLaunchKernelGGL(sb_count, dim3(1), dim3(1024), 0, g->compute, (const uint32_t *)(base + r->off_count),
-                       (const uint32_t *)(base + r->off_added), (size_t)heads * blocks, counters);
+                       (const uint32_t *)(base + r->off_added), (size_t)group * qslab, counters);
     if (!h3_launch_status(g, "SubBlock counters")) return 0;
-    r->possible += (uint64_t)heads * blocks * blocks;
+    r->possible += (uint64_t)group * qslab * blocks;
     r->counters_pending = true;
-    g->stats.subblock_router_calls++;
     return 1;
 }
 
@@ -331,7 +386,7 @@ const uint32_t *h3_subblock_counts(const h3_subblock_router *r) {
 void h3_subblock_collect(h3_gpu *g, h3_subblock_router *r) {
     if (!r->counters_pending) return;
     unsigned long long c[4] = {0, 0, 0, 0};
-    void *counters = (uint8_t *)r->ws.ptr + r->off_counters;
+    void *counters = r->counters.ptr;
     if (hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost) != hipSuccess) return;
     if (hipMemset(counters, 0, sizeof(c)) != hipSuccess) return;
     g->stats.subblock_selected += c[0];
@@ -342,6 +397,7 @@ void h3_subblock_collect(h3_gpu *g, h3_subblock_router *r) {
 
 void h3_subblock_free(h3_subblock_router *r) {
     h3_buffer_free(&r->ws);
+    h3_buffer_free(&r->counters);
     h3_buffer_free(&r->meta);
     r->bound = false;
 }
@@ -355,6 +411,7 @@ extern "C" int h3_hip_subblock_routes(h3_gpu *g, uint8_t *routes, float *scores,
     if (!g) return 0;
     auto *r = h3_attention_router(g);
     if (!r || !r->heads) return h3_set_error(g, "SubBlock routes: no routed call yet");
+    if (r->chunked) return h3_set_error(g, "SubBlock routes: the last call ran in chunks; only whole calls are kept");
     const size_t nr = (size_t)r->heads * r->blocks * r->blocks, cells = (size_t)r->blocks * 4;
     if ((routes || scores) && route_count != nr) return h3_set_error(g, "SubBlock routes: expected %zu routes", nr);
     if ((q_pool || k_pool) && pool_count != r->heads * cells * D)

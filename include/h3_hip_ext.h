@@ -95,6 +95,19 @@ int h3_hip_dit_subblock_policy(h3_gpu *gpu, float sparsity, int warmup);
 int h3_hip_subblock_routes(h3_gpu *gpu, uint8_t *routes, float *scores, size_t route_count,
                            uint16_t *q_pool, uint16_t *k_pool, size_t pool_count);
 
+/* SubBlock routed calls keep their device workspace (router buffers plus the
+ * transposed V of one head group) under a fixed budget, the reference's
+ * attention workspace cap of 512 MiB (src/denoise/attention.h:12, plan order of
+ * h3_subblock_plan_make, src/denoise/subblock.c:18-42): heads run in groups
+ * (all, then halved) and 64-query blocks in slabs (all, then multiples of 32)
+ * until the chunk fits. h3_hip_subblock_workspace_cap sets this context's
+ * budget (0 restores 512 MiB), e.g. to force chunking in tests; a shape that
+ * fits no chunk fails. h3_hip_subblock_plan_info reports the last routed
+ * call's head group, query slab and workspace bytes. A chunked call keeps no
+ * routes for h3_hip_subblock_routes. */
+int h3_hip_subblock_workspace_cap(h3_gpu *gpu, size_t bytes);
+int h3_hip_subblock_plan_info(h3_gpu *gpu, uint32_t *group, uint32_t *slab, size_t *bytes);
+
 /* SOL (mode 3) route capture, the counterpart of the reference's
  * h3_cuda_sol_routes (src/cuda/cuda_sol.cu:418-423): after a routed SOL call,
  * copies its routes u8 [heads][QB][KB] (QB = ceil(seq / q_block), KB =

@@ -122,6 +122,71 @@ def test_router_and_output(seq, heads, kind):
         g.close()
 
 
+def plan_info(g):
+    grp, slab, nbytes = C.c_uint32(), C.c_uint32(), C.c_size_t()
+    g.check(g.lib.h3_hip_subblock_plan_info(g.handle, C.byref(grp), C.byref(slab), C.byref(nbytes)), "plan")
+    return grp.value, slab.value, nbytes.value
+
+
+def test_chunked_workspace_matches_whole_call():
+    """Bounded workspace (plan order of the reference's h3_subblock_plan_make,
+    src/denoise/subblock.c:18-42, under the 512 MiB cap of
+    src/denoise/attention.h:12). Lowering this context's budget splits the call
+    into head groups, then query slabs; every split gives the whole call's
+    output bit for bit (row- and head-major) and the same route counters, the
+    planned bytes stay within the budget, and a budget no chunk fits fails."""
+    seq, heads = 5000, 3
+    blocks = (seq + 63) // 64
+    print(f"[subblock] chunked seq={seq} heads={heads}", flush=True)
+    q, k, v = subblock_case_inputs(seq, heads, 4)
+    prot = protect_ends(seq)
+    g = make_router(seq, prot, prot)
+    try:
+        whole = sdpa(g, q, k, v, seq, heads, scale=SCALE, step=STEP, block=BLOCK)
+        whole_hm = sdpa(g, q, k, v, seq, heads, scale=SCALE, step=STEP, block=BLOCK, head_major=True)
+        assert np.array_equal(whole_hm, whole)
+        grp, slab, nbytes = plan_info(g)
+        assert (grp, slab) == (heads, blocks) and nbytes <= 512 << 20
+        routes = capture(g, seq, heads)[0]
+        per_call = int(routes.sum())
+        selected = stats(g).subblock_selected
+        assert selected == 2 * per_call
+        seen_group = seen_slab = failed = False
+        for _ in range(20):
+            # A budget one byte below the last plan forces the next smaller one.
+            cap = nbytes - 1
+            g.check(g.lib.h3_hip_subblock_workspace_cap(g.handle, cap), "cap")
+            try:
+                out = sdpa(g, q, k, v, seq, heads, scale=SCALE, step=STEP, block=BLOCK)
+            except RuntimeError as e:
+                assert "fixed budget" in str(e), str(e)
+                failed = True
+                break
+            grp, slab, nbytes = plan_info(g)
+            print(f"  cap={cap} -> head group {grp}, slab {slab}, {nbytes} bytes", flush=True)
+            assert nbytes <= cap and grp <= heads and slab <= blocks
+            assert slab == blocks or slab % 32 == 0
+            assert np.array_equal(out, whole), (grp, slab)
+            s = stats(g).subblock_selected
+            assert s - selected == per_call, (grp, slab)
+            selected = s
+            if slab < blocks:
+                hm = sdpa(g, q, k, v, seq, heads, scale=SCALE, step=STEP, block=BLOCK, head_major=True)
+                assert np.array_equal(hm, whole)
+                selected = stats(g).subblock_selected
+                # A chunked call keeps no whole-call routes.
+                assert not g.lib.h3_hip_subblock_routes(g.handle, None, None, 0, None, None, 0)
+            seen_group |= grp < heads
+            seen_slab |= slab < blocks
+        assert seen_group and seen_slab and failed
+        # The default budget again: one chunk.
+        g.check(g.lib.h3_hip_subblock_workspace_cap(g.handle, 0), "cap")
+        assert np.array_equal(sdpa(g, q, k, v, seq, heads, scale=SCALE, step=STEP, block=BLOCK), whole)
+        assert plan_info(g)[:2] == (heads, blocks)
+    finally:
+        g.close()
+
+
 def test_constant_value_and_ties():
     """Zero Q and K: all scores tie, so each query block keeps the first
     `keep` key blocks; V = 0.5 gives exactly 0.5 (subblock_oracle.py:95)."""
@@ -198,5 +263,45 @@ def test_layout_rules():
         q2, k2, v2 = synth.attention_inputs(seq + 64, 1, seed=2)
         with pytest.raises(RuntimeError):
             sdpa(g, q2, k2, v2, seq + 64, 1, step=STEP, block=BLOCK)
+    finally:
+        g.close()
+
+
+def test_real_h3_shape_under_cap():
+    """The real H3 video shape (S = 109078, H = 56): the whole call would need
+    about 3 GB of router buffers and transposed V; under the default 512 MiB
+    budget it runs in head groups and its output equals the whole call's (a
+    budget large enough for one chunk) bit for bit. Inputs are 0.5 N(0,1) from
+    the device generator; the first and last 64-row blocks are protected."""
+    seq, heads = 109078, 56
+    blocks = (seq + 63) // 64
+    n = seq * heads * 128
+    print(f"[subblock] real shape seq={seq} heads={heads}", flush=True)
+    prot = protect_ends(seq)
+    g = make_router(seq, prot, prot)
+    try:
+        lib = g.lib
+        q, k, v, out = (g.empty(n) for _ in range(4))
+        g.begin()
+        for i, t in enumerate((q, k, v)):
+            g.check(lib.h3_hip_fill_normal_bf16(g.handle, t.handle, 77 * 16 + i, 0.5, n), "fill")
+        g.submit()
+
+        def run():
+            g.begin()
+            g.check(lib.h3_gpu_dit_sdpa_bf16(g.handle, out.handle, q.handle, k.handle, v.handle, seq, heads, 128,
+                                             C.c_float(SCALE), 0, BLOCK, STEP), "routed attention")
+            g.submit()
+            return out.read()
+
+        chunked = run()
+        grp, slab, nbytes = plan_info(g)
+        print(f"  default budget: head group {grp}, slab {slab}, {nbytes} bytes", flush=True)
+        assert nbytes <= 512 << 20 and grp < heads
+        assert np.all(np.isfinite(bf16(chunked[:: 997])))
+        g.check(lib.h3_hip_subblock_workspace_cap(g.handle, 8 << 30), "cap")
+        whole = run()
+        assert plan_info(g)[:2] == (heads, blocks)
+        assert np.array_equal(chunked, whole)
     finally:
         g.close()
