@@ -660,256 +660,6 @@ void attn_bf16_wide(Args a) {
     if (a.lse && hf == 0 && q < qrows) a.lse[(size_t)head * qrows + q] = (m + log2f(total)) * 0.6931471805599453f;
 }
 
-// Paired query blocks: each wave owns two 32-query blocks (64 queries) of one
-// head, so every K and V^T fragment read from LDS feeds two MFMAs (half the
-// LDS reads per FLOP of the 32-query wave). One wave per SIMD, four per
-// workgroup (256 queries): a wave may use all 512 registers, the accumulators
-// of both blocks sit in AGPRs, and the exponentials of one block are issued
-// between the other block's MFMAs within the wave. Running max and overflow
-// handling as the NOMAX wide kernel; the retry bytes keep its layout (byte
-// 2 * wave + block of the workgroup's eight), so the same per-tile-max launch
-// recomputes flagged rows.
-template <int KT>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
-void attn_bf16_pair(Args a) {
-    constexpr int WAVES = 4;
-    constexpr int BM = 256;
-    constexpr int STAGE = KT * (K_BYTES + V_BYTES);
-    constexpr int LOADS = (K_BYTES / 1024) / WAVES;
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-
-    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned n = lane % 32, hf = lane / 32;
-    const unsigned qrows = a.qrows ? a.qrows : a.seq;
-    const unsigned nqb = (qrows + BM - 1) / BM;
-    const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
-    const unsigned head = id / nqb, qb = id % nqb;
-    const unsigned q0 = qb * BM;
-    uint8_t *const retry = a.retry + ((size_t)head * nqb + qb) * 8;
-    const size_t stride = (size_t)a.heads * D;
-    const uint16_t *qh = a.q + (size_t)head * D;
-    const uint16_t *kh = a.k + (size_t)head * D;
-    const uint16_t *vth = a.vt + (size_t)head * D * a.padded;
-    const float c = a.scale_log2;
-    const unsigned count = (a.seq + BN - 1) / BN;
-    const unsigned groups = (count + KT - 1) / KT;
-
-    bf16x8 qf[2][8];
-    {
-        bool bad = false;
-#pragma unroll
-        for (int qa = 0; qa < 2; qa++) {
-            unsigned row = q0 + wave * 64 + qa * 32 + n;
-            row = row < qrows ? row : qrows - 1;
-            const uint16_t *p = qh + (size_t)row * stride + hf * 8;
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                qf[qa][ks] = *reinterpret_cast<const bf16x8 *>(p + ks * 16);
-                bad |= bf16_vec_nonfinite(qf[qa][ks]);
-            }
-        }
-        if (bad) a.fault[0] = 1u;
-    }
-
-    uint32_t koff, voff;
-    {
-        const unsigned key = 4 * wave + lane / 16, d = 8 * wave + lane / 8;
-        koff = (key * (uint32_t)stride + k_chunk(key, lane % 16) * 8) * 2;
-        voff = (d * a.padded + v_chunk(d, lane % 8) * 8) * 2;
-    }
-    auto load_group = [&](unsigned g, int stage) {
-        uint8_t *base = smem + stage * STAGE;
-#pragma unroll
-        for (int j = 0; j < KT; j++) {
-            const unsigned tile = min(g * KT + j, count - 1);
-            const unsigned key0 = tile * BN;
-            uint8_t *ks = base + j * K_BYTES;
-            uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
-            if (key0 + BN <= a.seq) {
-#pragma unroll
-                for (int t = 0; t < LOADS; t++) {
-                    const __attribute__((address_space(1))) char *kt =
-                        (const __attribute__((address_space(1))) char *)(kh + ((size_t)key0 + 4 * WAVES * t) * stride);
-                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(kt + koff),
-                                                     (__attribute__((address_space(3))) void *)(ks + (wave + WAVES * t) * 1024),
-                                                     16, 0, 0);
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < LOADS; t++) {
-                    const unsigned b = wave + WAVES * t;
-                    const unsigned key = 4 * b + lane / 16;
-                    const unsigned row = min(key0 + key, a.seq - 1);
-                    const uint16_t *src = kh + (size_t)row * stride + k_chunk(key, lane % 16) * 8;
-                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                                     (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < LOADS; t++) {
-                const __attribute__((address_space(1))) char *vt = (const __attribute__((address_space(1))) char *)(
-                    vth + (size_t)8 * WAVES * t * a.padded + min(key0, a.padded - BN));
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(vt + voff),
-                                                 (__attribute__((address_space(3))) void *)(vs + (wave + WAVES * t) * 1024),
-                                                 16, 0, 0);
-            }
-        }
-    };
-
-    f32x16 o[2][4];
-#pragma unroll
-    for (int qa = 0; qa < 2; qa++)
-#pragma unroll
-        for (int md = 0; md < 4; md++) o[qa][md] = f32x16{};
-    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
-    bool failed[2] = {false, false};
-
-    if (groups) load_group(0, 0);
-    wait_vm_loads();
-    __syncthreads();
-    for (unsigned g = 0; g < groups; g++) {
-        const int cur = g & 1;
-        if (g + 1 < groups) load_group(g + 1, cur ^ 1);
-        const uint8_t *base = smem + cur * STAGE;
-        f32x16 s[KT][2][2];   // [sub-tile][query block][32-key half]
-#pragma unroll
-        for (int j = 0; j < KT; j++) {
-            const uint8_t *ks = base + j * K_BYTES;
-            bf16x8 kfr[16];
-#pragma unroll
-            for (int x = 0; x < 16; x++) {
-                const unsigned key = (x % 2) * 32 + n;
-                kfr[x] = *reinterpret_cast<const bf16x8 *>(ks + key * 256 + k_chunk(key, (x / 2) * 2 + hf) * 16);
-            }
-#pragma unroll
-            for (int qa = 0; qa < 2; qa++)
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++) s[j][qa][mb] = f32x16{};
-#pragma unroll
-            for (int kstep = 0; kstep < 8; kstep++)
-#pragma unroll
-                for (int qa = 0; qa < 2; qa++)
-#pragma unroll
-                    for (int mb = 0; mb < 2; mb++)
-                        s[j][qa][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[kstep * 2 + mb], qf[qa][kstep],
-                                                                               s[j][qa][mb], 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < KT; j++) {
-            const unsigned tile = g * KT + j;
-            if (tile >= count || tile * BN + BN > a.seq) {
-#pragma unroll
-                for (int qa = 0; qa < 2; qa++)
-#pragma unroll
-                    for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
-                            if (tile >= count || key >= a.seq) s[j][qa][mb][r] = -INFINITY;
-                        }
-            }
-        }
-        if (g == 0) {
-            // The first group sets the running max; later groups raise it
-            // from the row sums only.
-#pragma unroll
-            for (int qa = 0; qa < 2; qa++) {
-                float mx = -INFINITY;
-#pragma unroll
-                for (int j = 0; j < KT; j++)
-#pragma unroll
-                    for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[j][qa][mb][r]);
-                m[qa] = fmaxf(m[qa], half_max_swap(mx) * c);
-            }
-        }
-        int raise[2] = {0, 0};
-#pragma unroll
-        for (int j = 0; j < KT; j++) {
-            const uint8_t *vs = base + KT * K_BYTES + j * V_BYTES;
-            bf16x8 vfr[16];
-#pragma unroll
-            for (int x = 0; x < 16; x++) {
-                const unsigned d = (x % 4) * 32 + n;
-                vfr[x] = *reinterpret_cast<const bf16x8 *>(vs + d * 128 + v_chunk(d, (x / 4) * 2 + hf) * 16);
-            }
-#pragma unroll
-            for (int qa = 0; qa < 2; qa++) {
-                const float neg = -m[qa];
-                bf16x8 pb[4];
-                float psum = 0.f;
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2) {
-                        float p0 = exp2f_fast(fmaf(s[j][qa][mb][r], c, neg));
-                        float p1 = exp2f_fast(fmaf(s[j][qa][mb][r + 1], c, neg));
-                        psum += p0 + p1;
-                        pb[mb * 2 + r / 8][r % 8] = (__bf16)p0;
-                        pb[mb * 2 + r / 8][r % 8 + 1] = (__bf16)p1;
-                    }
-                // A partial sum outside [0, 2^20] raises m by its exponent
-                // after this group (branch-free); from 2^RETRY_EXP, or not
-                // finite, the rows go to the recomputation launch.
-                if (!(psum <= PSUM_LIMIT))
-                    raise[qa] = max(raise[qa], (int)((__builtin_bit_cast(uint32_t, psum) >> 23) & 0xFF) - 127);
-                l[qa] += psum;
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-                    for (int md = 0; md < 4; md++)
-                        o[qa][md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[kk * 4 + md], pb[kk], o[qa][md], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int qa = 0; qa < 2; qa++) {
-            if (__builtin_amdgcn_ballot_w64(raise[qa] != 0)) {
-                int r = (int)half_max_swap((float)raise[qa]);
-                failed[qa] |= r >= RETRY_EXP;
-                if (r >= RETRY_EXP) r = 0;
-                const float alpha = ldexpf(1.f, -r);
-                m[qa] += (float)r;
-                l[qa] *= alpha;
-#pragma unroll
-                for (int md = 0; md < 4; md++) o[qa][md] *= alpha;
-            }
-        }
-        wait_vm_loads();
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int qa = 0; qa < 2; qa++) {
-        const float total = half_sum_swap(l[qa]);
-        const float inv = total > 0.f ? 1.f / total : 0.f;
-        const unsigned q = q0 + wave * 64 + qa * 32 + n;
-        bool bad = false;
-        if (q < qrows) {
-            uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
-#pragma unroll
-            for (int md = 0; md < 4; md++)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    u16x4 w;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        float x = o[qa][md][g4 * 4 + i] * inv;
-                        bad |= !finite_f32(x);
-                        w[i] = f32_to_bf16(x);
-                    }
-                    *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
-                }
-        }
-        // Non-finite output with no flagged sum: P below 2^RETRY_EXP times a
-        // large |V| (or a non-finite input); the recomputation decides.
-        const bool any = __builtin_amdgcn_ballot_w64(failed[qa] || bad) != 0;
-        if (lane == 0) retry[2 * wave + qa] = any ? 1 : 0;
-        if (!any && a.lse && hf == 0 && q < qrows)
-            a.lse[(size_t)head * qrows + q] = (m[qa] + log2f(total)) * 0.6931471805599453f;
-    }
-}
-
 template <int KT, bool SPARSE, bool MSUM, bool NOMAX, int WAVES = 8>
 int configure_wide(h3_gpu *g) {
     static bool configured = false;
@@ -1206,28 +956,6 @@ int launch_pingpong(h3_gpu *g, const Args &a, unsigned groups) {
     h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "BF16 attention");
 }
-
-template <int KT>
-int launch_pair(h3_gpu *g, const Args &a, unsigned groups) {
-    constexpr size_t shared = 2 * KT * STAGE_BYTES;
-    static bool configured = false;
-    if (!configured) {
-        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)attn_bf16_pair<KT>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shared),
-                          "attention shared memory"))
-            return 0;
-        configured = true;
-    }
-    if (!configure_wide<2, false, false, false>(g)) return 0;
-    hipEvent_t timing = h3_kernel_timing_begin(g);
-    hipLaunchKernelGGL(attn_bf16_pair<KT>, dim3(groups), dim3(256), shared, g->compute, a);
-    if (!h3_launch_status(g, "BF16 attention")) return 0;
-    hipLaunchKernelGGL((attn_bf16_wide<2, false, false, false>), dim3(groups), dim3(512), 2 * 2 * STAGE_BYTES,
-                       g->compute, a);
-    h3_kernel_timing_end(g, timing);
-    return h3_launch_status(g, "BF16 attention");
-}
-
 
 // Listed sparse attention: one workgroup of QW waves per (32 * QW-query block,
 // head) walks that block's own list of kept 64-key tiles (ascending tile ids,
@@ -1585,16 +1313,13 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     if (kv_list) return launch<4, 1, 2, true, true>(g, a, (seq + 127) / 128 * heads);
     if (g->attention_variant == 1) return launch<8, 1, 2, false, true>(g, a, (seq + 255) / 256 * heads);
     if (g->attention_variant == 2) return launch<12, 1, 3, false, false>(g, a, (seq + 383) / 384 * heads);
-    if (g->attention_variant == 5) return launch<4, 2, 1, false, false>(g, a, (seq + 255) / 256 * heads);
     // Variant 3: a tile max every 128 keys instead of the row-sum test.
     if (g->attention_variant == 3) return launch_wide<2, false, false, false>(g, a, (seq + 255) / 256 * heads);
     a.retry = (uint8_t *)workspace + retry_offset(seq, heads);
     // Variant 4: four waves (128 queries) per workgroup and two workgroups per
     // CU, whose barriers are independent, 64 keys per interval (6% slower).
     if (g->attention_variant == 4) return launch_wide<1, false, false, true, 4>(g, a, (seq + 127) / 128 * heads);
-    if (g->attention_variant == 6) return launch_pair<2>(g, a, (seq + 255) / 256 * heads);
-    if (g->attention_variant == 7) return launch_pair<1>(g, a, (seq + 255) / 256 * heads);
-    if (g->attention_variant == 8) return launch_pingpong<2>(g, a, (seq + 255) / 256 * heads);
+    // Variant 9: ping-pong wave groups (22.8 ms against 18.5 at S = 32400, H = 40).
     if (g->attention_variant == 9) return launch_pingpong<1>(g, a, (seq + 255) / 256 * heads);
     return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
 }

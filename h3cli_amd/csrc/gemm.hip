@@ -75,17 +75,13 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // registers sit in AGPRs, and each fragment read from LDS feeds four MFMAs
 // instead of two or four). CHANNEL: one scale per output row (group == K),
 // loaded once. EPI bit 0: bias, bit 1: GELU, bit 2: alpha (before the bias).
-template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4, int XST = 2>
+template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * WM * WN, 64 * WM * WN),
                           amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_kernel(GemmArgs a) {
     constexpr int T = 64 * WM * WN;            // threads
     constexpr int NBM = TM / WM / 32, NBN = TN / WN / 32;
     constexpr int WCH = 1024 / T;              // weight chunks per thread
-    // XST = 3 (q8 only): three X stages and two BF16 weight stages in LDS
-    // (160 KB), X and int8 W loads issued two k-steps ahead.
-    static_assert(XST == 2 || (XST == 3 && Q8), "three X stages need register-staged weights");
-    constexpr int VM_PER_STEP = 32 / (WM * WN) + WCH + (CHANNEL ? 0 : WCH);
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
     const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
@@ -106,28 +102,27 @@ void gemm_kernel(GemmArgs a) {
         for (int j = 0; j < NBM; j++) acc[i][j] = f32x16{};
 
     // Weight staging (q8): 256 rows x 64 int8 = 1024 16-byte chunks, WCH per thread.
-    i32x4 wq[WCH], wq2[WCH];
-    float wscale[WCH], wscale2[WCH];
+    i32x4 wq[WCH];
+    float wscale[WCH];
     if constexpr (Q8 && CHANNEL) {
 #pragma unroll
-        for (int j = 0; j < WCH; j++) wscale2[j] = wscale[j] = a.scales[n0 + w_row(tid + T * j)];
+        for (int j = 0; j < WCH; j++) wscale[j] = a.scales[n0 + w_row(tid + T * j)];
     }
-    auto load_w_into = [&](unsigned kt, i32x4 *dq, float *ds) {
+    auto load_w = [&](unsigned kt) {
         if constexpr (Q8) {
             const int8_t *w8 = reinterpret_cast<const int8_t *>(a.w);
 #pragma unroll
             for (int j = 0; j < WCH; j++) {
                 unsigned c = tid + T * j, row = w_row(c), part = w_part(c);
-                dq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
+                wq[j] = *reinterpret_cast<const i32x4 *>(w8 + (size_t)(n0 + row) * a.k + kt * TK + part * 16);
                 if constexpr (!CHANNEL)
-                    ds[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
+                    wscale[j] = a.scales[(size_t)(n0 + row) * a.groups + (kt * TK + part * 16) / a.group];
             }
         }
     };
-    auto load_w = [&](unsigned kt) { load_w_into(kt, wq, wscale); };
-    auto x_stage = [&](int stage) { return lds + stage * (XST == 3 ? TILE_BYTES : STAGE); };
-    auto w_stage = [&](int stage) { return XST == 3 ? lds + (3 + stage) * TILE_BYTES : lds + stage * STAGE + TILE_BYTES; };
-    auto store_w_from = [&](int stage, const i32x4 *wq, const float *wscale) {
+    auto x_stage = [&](int stage) { return lds + stage * STAGE; };
+    auto w_stage = [&](int stage) { return lds + stage * STAGE + TILE_BYTES; };
+    auto store_w = [&](int stage) {
         if constexpr (Q8) {
             uint8_t *ws = w_stage(stage);
 #pragma unroll
@@ -148,7 +143,6 @@ void gemm_kernel(GemmArgs a) {
             }
         }
     };
-    auto store_w = [&](int stage) { store_w_from(stage, wq, wscale); };
     // Direct global -> LDS loads: X rows (clamped at M) and, for BF16 weights, W rows.
     auto load_direct = [&](unsigned kt, int stage) {
         uint8_t *xs = x_stage(stage);
@@ -179,49 +173,7 @@ void gemm_kernel(GemmArgs a) {
         }
     };
 
-    if constexpr (XST == 3) {
-        // Step kt: issue X(kt+2) and W(kt+2) (indices clamped, so the loads are
-        // unconditional; past the end they refill stages no step reads again),
-        // run the MFMAs of stage kt, then dequantize W(kt+1) into its LDS stage.
-        // The two register sets alternate roles by call site, so no loaded
-        // register is copied (a copy would wait for its load).
-        auto step = [&](unsigned kt, i32x4 *held, float *held_s, i32x4 *next, float *next_s) {
-            const unsigned k2 = min(kt + 2, ksteps - 1);
-            load_direct(k2, (kt + 2) % 3);
-            load_w_into(k2, next, next_s);
-            const uint8_t *xs = x_stage(kt % 3);
-            const uint8_t *ws = w_stage(kt & 1);
-            bf16x8 wf[2][NBN], xf[2][NBM];
-            frags(xs, ws, 0, wf[0], xf[0]);
-#pragma unroll
-            for (int ks = 0; ks < TK / 16; ks++) {
-                if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
-#pragma unroll
-                for (int i = 0; i < NBN; i++)
-#pragma unroll
-                    for (int j = 0; j < NBM; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
-            }
-            store_w_from((kt + 1) & 1, held, held_s);
-            // X(kt+1) has landed; the loads of step kt+2 stay in flight.
-            __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STEP);
-            __syncthreads();
-        };
-        load_direct(0, 0);
-        load_w_into(0, wq2, wscale2);
-        load_direct(min(1u, ksteps - 1), 1);
-        load_w_into(min(1u, ksteps - 1), wq, wscale);
-        store_w_from(0, wq2, wscale2);
-        __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STEP);
-        __syncthreads();
-        unsigned kt = 0;
-        for (; kt + 1 < ksteps; kt += 2) {
-            step(kt, wq, wscale, wq2, wscale2);
-            step(kt + 1, wq2, wscale2, wq, wscale);
-        }
-        if (kt < ksteps) step(kt, wq, wscale, wq2, wscale2);
-        wait_vm_loads();
-    } else {
+    {
     load_direct(0, 0);
     load_w(0);
     store_w(0);
@@ -306,11 +258,11 @@ __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
     a.y[idx] = b;
 }
 
-template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4, int XST = 2>
+template <bool Q8, bool CHANNEL, int EPI, int WM = 2, int WN = 4>
 int launch_tiled(h3_gpu *g, const GemmArgs &a) {
-    constexpr size_t shared = XST == 3 ? 5 * TILE_BYTES : 2 * STAGE;
+    constexpr size_t shared = 2 * STAGE;
     static bool configured = false;
-    auto kernel = gemm_kernel<Q8, CHANNEL, EPI, WM, WN, XST>;
+    auto kernel = gemm_kernel<Q8, CHANNEL, EPI, WM, WN>;
     if (!configured) {
         if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)shared), "GEMM shared memory"))
@@ -327,16 +279,7 @@ int launch_tiled(h3_gpu *g, const GemmArgs &a) {
 template <bool Q8, bool CHANNEL>
 int launch_epi(h3_gpu *g, const GemmArgs &a) {
     const int epi = (a.bias ? 1 : 0) | (a.gelu ? 2 : 0);
-    if constexpr (Q8) {
-        if (g->gemm_variant == 2) {
-            switch (epi) {
-            case 0: return launch_tiled<Q8, CHANNEL, 0, 2, 4, 3>(g, a);
-            case 1: return launch_tiled<Q8, CHANNEL, 1, 2, 4, 3>(g, a);
-            case 2: return launch_tiled<Q8, CHANNEL, 2, 2, 4, 3>(g, a);
-            default: return launch_tiled<Q8, CHANNEL, 3, 2, 4, 3>(g, a);
-            }
-        }
-    }
+    // Variant 1: 2 x 2 waves of 128 x 128 (one wave per SIMD), about 10% slower.
     if (g->gemm_variant == 1) {
         switch (epi) {
         case 0: return launch_tiled<Q8, CHANNEL, 0, 2, 2>(g, a);
