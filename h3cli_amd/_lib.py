@@ -148,6 +148,8 @@ _SIGNATURES.update({
     "h3_hip_subblock_routes": (_i, [_p, _p, _p, C.c_size_t, _p, _p, C.c_size_t]),
     "h3_hip_subblock_workspace_cap": (_i, [_p, _sz]),
     "h3_hip_subblock_plan_info": (_i, [_p, _p, _p, _p]),
+    "h3_hip_sol_workspace_cap": (_i, [_p, _sz]),
+    "h3_hip_sol_plan_info": (_i, [_p, _p, _p]),
     "h3_hip_sol_routes": (_i, [_p, _p, C.c_size_t, _p, C.c_size_t, _p, _p, C.c_size_t]),
     "h3_hip_dit_sol_force_exact": (_i, [_p, _i]),
     "h3_hip_sol_counters": (_i, [_p, _p, C.c_size_t]),

@@ -294,15 +294,25 @@ extern "C" int h3_gpu_dit_sdpa_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_
             return dispatch(g, out, q, k, v, seq, heads, round_scale_bf16(scale), head_major != 0, MODE_DEFAULT, false);
         }
         const float rounded = round_scale_bf16(scale);
-        if (!h3_sol_route(g, &s->sol, (const uint16_t *)q->data, (const uint16_t *)k->data, (const uint16_t *)v->data,
-                          seq, heads, rounded))
+        // Centroids of all heads, then routes, lists and attention per head
+        // group under the fixed workspace budget.
+        uint32_t group = 0;
+        size_t bytes = 0;
+        if (!h3_sol_plan(g, &s->sol, seq, heads, &group, &bytes) ||
+            !h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, group), "attention workspace") ||
+            !h3_sol_prepare(g, &s->sol, (const uint16_t *)q->data, (const uint16_t *)k->data,
+                            (const uint16_t *)v->data, seq, heads, group))
             return 0;
-        const h3_sol_lists lists = h3_sol_lists_of(&s->sol);
-        if (!h3_buffer_reserve(g, &s->bf16_ws, h3_attention_bf16_workspace(seq, heads), "attention workspace") ||
-            !h3_launch_attention_sol(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data,
-                                     (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads, rounded,
-                                     head_major != 0, (uint32_t)s->sol.options.q_block, &lists))
-            return 0;
+        for (uint32_t h0 = 0; h0 < heads; h0 += group) {
+            const uint32_t gh = std::min(group, heads - h0);
+            if (!h3_sol_route(g, &s->sol, seq, heads, h0, gh, rounded)) return 0;
+            const h3_sol_lists lists = h3_sol_lists_of(&s->sol);
+            if (!h3_launch_attention_sol(g, s->bf16_ws.ptr, (uint16_t *)out->data, (const uint16_t *)q->data,
+                                         (const uint16_t *)k->data, (const uint16_t *)v->data, seq, heads, rounded,
+                                         head_major != 0, (uint32_t)s->sol.options.q_block, &lists, h0, gh))
+                return 0;
+        }
+        s->sol.plan_bytes = bytes;
         g->stats.attention_dispatches++;
         return 1;
     }
@@ -416,5 +426,22 @@ extern "C" int h3_hip_subblock_plan_info(h3_gpu *g, uint32_t *group, uint32_t *s
     if (group) *group = p.group;
     if (slab) *slab = p.slab;
     if (bytes) *bytes = p.bytes;
+    return 1;
+}
+
+// Workspace budget of SOL routed calls on this context (0 restores 512 MiB)
+// and the head group and bytes of the last routed call.
+extern "C" int h3_hip_sol_workspace_cap(h3_gpu *g, size_t bytes) {
+    if (!g || !g->attention) return 0;
+    g->attention->sol.cap = bytes ? bytes : (size_t)512 << 20;
+    return 1;
+}
+
+extern "C" int h3_hip_sol_plan_info(h3_gpu *g, uint32_t *group, size_t *bytes) {
+    if (!g || !g->attention) return 0;
+    const auto &r = g->attention->sol;
+    if (!r.group) return h3_set_error(g, "SOL plan: no routed call yet");
+    if (group) *group = r.group;
+    if (bytes) *bytes = r.plan_bytes;
     return 1;
 }

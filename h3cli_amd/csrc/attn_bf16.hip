@@ -1375,20 +1375,24 @@ int h3_launch_attention_routed(h3_gpu *g, void *workspace, uint16_t *out, const 
 
 int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                             const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                            uint32_t q_block, const h3_sol_lists *lists) {
+                            uint32_t q_block, const h3_sol_lists *lists, uint32_t head0, uint32_t group) {
+    // Heads [head0, head0 + group): Q, K, output and the centroid arrays move
+    // to the group's first head (strides stay those of all heads); the lists
+    // and the transposed V hold the group's heads only.
     Args a{};
-    a.out = out; a.q = q; a.k = k; a.vt = (const uint16_t *)workspace;
+    a.out = out + (head_major ? (size_t)head0 * seq * D : (size_t)head0 * D);
+    a.q = q + (size_t)head0 * D; a.k = k + (size_t)head0 * D; a.vt = (const uint16_t *)workspace;
     a.seq = seq; a.heads = heads; a.padded = (seq + 63) / 64 * 64;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = lists->exact; a.kv_count = lists->exact_count; a.list_stride = lists->exact_stride;
     a.cent_list = lists->cent; a.cent_count = lists->cent_count; a.cent_mask = lists->cent_mask;
     a.cent_stride = lists->cent_stride; a.key_blocks = lists->key_blocks; a.kc_padded = lists->kc_padded;
-    a.kc = lists->kc; a.vct = lists->vct;
+    a.kc = lists->kc + (size_t)head0 * D; a.vct = lists->vct + (size_t)head0 * D * lists->kc_padded;
     a.fault = g->fault;
-    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
-                       seq, heads, a.padded, g->fault);
+    hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, group), dim3(256), 0, g->compute, v + (size_t)head0 * D, a.k,
+                       (uint16_t *)workspace, seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
     (void)q_block;   // 32-row blocks come paired in the lists: one 64-query workgroup either way
-    return launch_listed<true, 2, 2, true>(g, a, (seq + 63) / 64 * heads);
+    return launch_listed<true, 2, 2, true>(g, a, (seq + 63) / 64 * group);
 }

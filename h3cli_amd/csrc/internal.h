@@ -43,9 +43,11 @@ struct h3_sol_lists {
     uint32_t cent_stride, key_blocks, kc_padded;
     const uint16_t *kc, *vct;
 };
+// SOL attention of heads [head0, head0 + group): lists hold the group's heads,
+// kc / vct all heads; workspace receives the group's transposed V.
 int h3_launch_attention_sol(h3_gpu *g, void *workspace, uint16_t *out, const uint16_t *q, const uint16_t *k,
                             const uint16_t *v, uint32_t seq, uint32_t heads, float scale, bool head_major,
-                            uint32_t q_block, const h3_sol_lists *lists);
+                            uint32_t q_block, const h3_sol_lists *lists, uint32_t head0, uint32_t group);
 
 // Grow-only device buffer; growing waits for queued work that may read the old one.
 // FP8 projections (quant.hip): y = FP8 GEMM of x with a packed weight; teardown.

@@ -116,13 +116,15 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                                                  uint32_t *cent_list, uint32_t *cent_count, uint64_t *cent_mask,
                                                  unsigned heads, unsigned qblocks, unsigned kblocks, unsigned tiles,
                                                  unsigned units, unsigned radius, unsigned minimum, float scale,
-                                                 float tau, int force_exact, uint32_t *row_counts) {
+                                                 float tau, int force_exact, uint32_t *row_counts, unsigned head0) {
     __shared__ float q[UPW][PAIR][D];
     __shared__ float limit[UPW][PAIR];
     __shared__ unsigned wave_total[1][4][2];
     __shared__ uint32_t wave_tally[4][7];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const unsigned h = blockIdx.y, u0 = blockIdx.x * UPW, nu = min(UPW, units - u0);
+    // Head h of all heads (centroids, moments); outputs are indexed by the
+    // head's place hl in the routed group [head0, head0 + gridDim.y).
+    const unsigned h = head0 + blockIdx.y, hl = blockIdx.y, u0 = blockIdx.x * UPW, nu = min(UPW, units - u0);
     const float a = __fmul_rn(scale, 1.4426950408889634f);
     for (unsigned i = tid; i < UPW * PAIR * D; i += 256) {
         const unsigned u = i / (PAIR * D), qb = (u0 + u) * PAIR + (i / D) % PAIR;
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
                                        km.first_frame <= qm.last_frame + (int)radius;
                     const bool recovery = !finite_f32(di) || !finite_f32(t);
                     exact[i] = force_exact || protect || local || floor_ || recovery || tail || di > t;
-                    routes[((size_t)h * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
+                    routes[((size_t)hl * qblocks + qb0 + i) * kblocks + b] = (uint8_t)exact[i];
                     tally[exact[i] ? 0 : 1]++;
                     tally[2] += protect;
                     tally[3] += local && !protect;
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
             const unsigned long long m1 = PAIR == 1 ? m0 : __ballot(valid && present > 1 && !exact[1]);
             if (lane == 0) { wave_total[0][wave][0] = __popcll(ex); wave_total[0][wave][1] = (m0 | m1) != 0; }
             __syncthreads();
-            const size_t row = (size_t)h * units + u0 + u;
+            const size_t row = (size_t)hl * units + u0 + u;
             unsigned pos = lengths[u][0] + __popcll(ex & ((1ull << lane) - 1ull)), cpos = lengths[u][1];
             unsigned add_exact = 0, add_cent = 0;
             for (unsigned w = 0; w < 4; w++) {
@@ -227,8 +229,8 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
     }
     __syncthreads();
     if (tid < nu) {
-        exact_count[(size_t)h * units + u0 + tid] = lengths[tid][0];
-        cent_count[(size_t)h * units + u0 + tid] = lengths[tid][1];
+        exact_count[(size_t)hl * units + u0 + tid] = lengths[tid][0];
+        cent_count[(size_t)hl * units + u0 + tid] = lengths[tid][1];
     }
 #pragma unroll
     for (int j = 0; j < 7; j++) {
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(256) void sol_route(const uint16_t *qc, const uint1
     }
     __syncthreads();
     if (tid < 8) {
-        const size_t row = (size_t)h * units + u0;
+        const size_t row = (size_t)hl * units + u0;
         // The workgroup's counts land in its first unit's row; the others hold zeros.
         for (unsigned u = 0; u < nu; u++)
             row_counts[(row + u) * 8 + tid] =
@@ -302,33 +304,56 @@ int h3_sol_bind(h3_gpu *g, h3_sol_router *r, const h3_sol_layout *layout, const 
     return 1;
 }
 
-int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint32_t seq,
-                 uint32_t heads, float scale) {
+namespace {
+// Workspace of a SOL call: the centroids and moments of all heads, then the
+// routes and lists of one head group. Offsets into r when r is set.
+size_t sol_layout(uint32_t seq, uint32_t heads, uint32_t group, uint32_t QB, uint32_t KB, h3_sol_router *r) {
+    const uint32_t kpad = (KB + 63) / 64 * 64, tiles = kpad / 64, units = (seq + 63) / 64;
+    size_t off = 0, o[11];
+    o[0] = off; off = align256(off + (size_t)heads * QB * D * 2);          // qc
+    o[1] = off; off = align256(off + (size_t)KB * heads * D * 2);          // kc
+    o[2] = off; off = align256(off + (size_t)heads * D * kpad * 2);        // vct
+    o[3] = off; off = align256(off + (size_t)heads * 256 * 4);             // moments
+    o[4] = off; off = align256(off + (size_t)group * QB * KB);             // routes
+    o[5] = off; off = align256(off + (size_t)group * units * KB * 4);      // exact lists
+    o[6] = off; off = align256(off + (size_t)group * units * 4);
+    o[7] = off; off = align256(off + (size_t)group * units * tiles * 4);   // centroid lists
+    o[8] = off; off = align256(off + (size_t)group * units * 4);
+    o[9] = off; off = align256(off + (size_t)group * units * tiles * 16);  // approximate masks
+    o[10] = off; off = align256(off + (size_t)group * units * 8 * 4);      // pair counts
+    if (r) {
+        r->off_qc = o[0]; r->off_kc = o[1]; r->off_vct = o[2]; r->off_moments = o[3]; r->off_routes = o[4];
+        r->off_exact = o[5]; r->off_exact_count = o[6]; r->off_cent = o[7]; r->off_cent_count = o[8];
+        r->off_cent_mask = o[9]; r->off_row_counts = o[10];
+        r->kpad = kpad; r->tiles = tiles;
+    }
+    return off;
+}
+}  // namespace
+
+int h3_sol_plan(h3_gpu *g, const h3_sol_router *r, uint32_t seq, uint32_t heads, uint32_t *group, size_t *bytes) {
     if (!r->bound) return h3_set_error(g, "SOL attention needs a bound layout (h3_gpu_dit_sol_layout)");
     if (seq != r->seq) return h3_set_error(g, "SOL layout was bound for sequence %u, not %u", r->seq, seq);
-    const uint32_t QB = r->qblocks, KB = r->kblocks, kpad = (KB + 63) / 64 * 64, tiles = kpad / 64;
-    size_t off = 0;
-    r->off_qc = off; off = align256(off + (size_t)heads * QB * D * 2);
-    r->off_kc = off; off = align256(off + (size_t)KB * heads * D * 2);
-    r->off_vct = off; off = align256(off + (size_t)heads * D * kpad * 2);
-    r->off_moments = off; off = align256(off + (size_t)heads * 256 * 4);
-    r->off_routes = off; off = align256(off + (size_t)heads * QB * KB);
-    const uint32_t units = (seq + 63) / 64;     // lists are per 64-query unit
-    r->off_exact = off; off = align256(off + (size_t)heads * units * KB * 4);
-    r->off_exact_count = off; off = align256(off + (size_t)heads * units * 4);
-    r->off_cent = off; off = align256(off + (size_t)heads * units * tiles * 4);
-    r->off_cent_count = off; off = align256(off + (size_t)heads * units * 4);
-    r->off_cent_mask = off; off = align256(off + (size_t)heads * units * tiles * 16);
-    r->off_row_counts = off; off = align256(off + (size_t)heads * units * 8 * 4);
-    if (!h3_buffer_reserve(g, &r->ws, off, "SOL workspace")) return 0;
-    r->heads = heads; r->kpad = kpad; r->tiles = tiles;
+    for (uint32_t gr = heads;; gr = std::max(1u, gr / 2)) {
+        const size_t need = sol_layout(seq, heads, gr, r->qblocks, r->kblocks, nullptr) +
+                            h3_attention_bf16_workspace(seq, gr);
+        if (need <= r->cap) { *group = gr; *bytes = need; return 1; }
+        if (gr == 1) break;
+    }
+    return h3_set_error(g, "SOL: S=%u H=%u workspace plan exceeds its fixed budget of %zu bytes", seq, heads, r->cap);
+}
+
+int h3_sol_prepare(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint32_t seq,
+                   uint32_t heads, uint32_t group) {
+    const uint32_t QB = r->qblocks, KB = r->kblocks;
+    const size_t bytes = sol_layout(seq, heads, group, QB, KB, r);
+    if (!h3_buffer_reserve(g, &r->ws, bytes, "SOL workspace")) return 0;
+    r->heads = heads; r->group = group;
     auto *base = (uint8_t *)r->ws.ptr;
     auto *qc = (uint16_t *)(base + r->off_qc), *kc = (uint16_t *)(base + r->off_kc);
     auto *vct = (uint16_t *)(base + r->off_vct);
     auto *moments = (float *)(base + r->off_moments);
-    const auto *qmeta = (const h3_sol_block *)r->meta.ptr;
-    const auto *kmeta = qmeta + QB;
-    const uint32_t qblock = (uint32_t)r->options.q_block;
+    const uint32_t qblock = (uint32_t)r->options.q_block, kpad = r->kpad;
     const unsigned head_groups = (heads + 15) / 16;
     hipLaunchKernelGGL(sol_summary<SUM_Q>, dim3(QB, head_groups), dim3(256), 0, g->compute, q, qc, seq, heads, qblock, QB,
                        kpad, g->fault);
@@ -338,21 +363,34 @@ int h3_sol_route(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_t 
                        kpad, g->fault);
     hipLaunchKernelGGL(sol_moments, dim3(heads), dim3(128), 0, g->compute, kc, moments, heads, KB);
     if (!h3_launch_status(g, "SOL summaries")) return 0;
+    r->calls++;
+    return 1;
+}
+
+int h3_sol_route(h3_gpu *g, h3_sol_router *r, uint32_t seq, uint32_t heads, uint32_t head0, uint32_t group,
+                 float scale) {
+    if (group != r->group || head0 + group > heads) return h3_set_error(g, "SOL: invalid head group");
+    const uint32_t QB = r->qblocks, KB = r->kblocks, tiles = r->tiles;
+    auto *base = (uint8_t *)r->ws.ptr;
+    const auto *qc = (const uint16_t *)(base + r->off_qc), *kc = (const uint16_t *)(base + r->off_kc);
+    const auto *moments = (const float *)(base + r->off_moments);
+    const auto *qmeta = (const h3_sol_block *)r->meta.ptr;
+    const auto *kmeta = qmeta + QB;
+    const uint32_t qblock = (uint32_t)r->options.q_block;
     const unsigned minimum = (unsigned)std::ceil((double)r->options.min_exact * KB);
+    const uint32_t units = (seq + 63) / 64;     // lists are per 64-query unit
     // Lists per 64-query unit: pairs of 32-row blocks, or single 64-row blocks.
     auto route = qblock == 32 ? sol_route<2> : sol_route<1>;
-    hipLaunchKernelGGL(route, dim3((units + UPW - 1) / UPW, heads), dim3(256), 0, g->compute, qc, kc, moments, qmeta,
+    hipLaunchKernelGGL(route, dim3((units + UPW - 1) / UPW, group), dim3(256), 0, g->compute, qc, kc, moments, qmeta,
                        kmeta, base + r->off_routes, (uint32_t *)(base + r->off_exact),
                        (uint32_t *)(base + r->off_exact_count), (uint32_t *)(base + r->off_cent),
                        (uint32_t *)(base + r->off_cent_count), (uint64_t *)(base + r->off_cent_mask), heads, QB, KB,
                        tiles, units, (unsigned)r->options.local_radius, minimum, scale, r->options.tau,
-                       r->force_exact ? 1 : 0,
-                       (uint32_t *)(base + r->off_row_counts));
+                       r->force_exact ? 1 : 0, (uint32_t *)(base + r->off_row_counts), head0);
     if (!h3_launch_status(g, "SOL route")) return 0;
     hipLaunchKernelGGL(sol_count, dim3(1), dim3(1024), 0, g->compute, (const uint32_t *)(base + r->off_row_counts),
-                       (size_t)heads * units, (unsigned long long *)r->counters.ptr);
+                       (size_t)group * units, (unsigned long long *)r->counters.ptr);
     if (!h3_launch_status(g, "SOL counters")) return 0;
-    r->calls++;
     r->pending = true;
     return 1;
 }
@@ -400,6 +438,7 @@ extern "C" int h3_hip_sol_routes(h3_gpu *g, uint8_t *routes, size_t route_count,
     if (!g) return 0;
     auto *r = h3_attention_sol(g);
     if (!r || !r->heads) return h3_set_error(g, "SOL routes: no routed call yet");
+    if (r->group != r->heads) return h3_set_error(g, "SOL routes: the last call ran in head groups; only whole calls are kept");
     const size_t H = r->heads, QB = r->qblocks, KB = r->kblocks;
     if (routes && route_count != H * QB * KB) return h3_set_error(g, "SOL routes: expected %zu routes", H * QB * KB);
     if (qc && qc_count != H * QB * D) return h3_set_error(g, "SOL routes: expected %zu query centroids", H * QB * D);

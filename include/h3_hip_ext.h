@@ -108,6 +108,16 @@ int h3_hip_subblock_routes(h3_gpu *gpu, uint8_t *routes, float *scores, size_t r
 int h3_hip_subblock_workspace_cap(h3_gpu *gpu, size_t bytes);
 int h3_hip_subblock_plan_info(h3_gpu *gpu, uint32_t *group, uint32_t *slab, size_t *bytes);
 
+/* SOL (mode 3) routed calls under the same fixed 512 MiB budget (the
+ * reference's h3_cuda_sol_plan_make, src/cuda/cuda_sol_policy.c): the centroids
+ * of all heads, then routes, lists and the transposed V one head group at a
+ * time (all heads, halved until the group fits). h3_hip_sol_workspace_cap sets
+ * this context's budget (0 restores 512 MiB); h3_hip_sol_plan_info reports the
+ * last routed call's head group and workspace bytes. A call that ran in head
+ * groups keeps no routes for h3_hip_sol_routes. */
+int h3_hip_sol_workspace_cap(h3_gpu *gpu, size_t bytes);
+int h3_hip_sol_plan_info(h3_gpu *gpu, uint32_t *group, size_t *bytes);
+
 /* SOL (mode 3) route capture, the counterpart of the reference's
  * h3_cuda_sol_routes (src/cuda/cuda_sol.cu:418-423): after a routed SOL call,
  * copies its routes u8 [heads][QB][KB] (QB = ceil(seq / q_block), KB =

@@ -182,3 +182,109 @@ def test_dense_bypass_and_layout_rules():
         assert not g.lib.h3_gpu_dit_sol_layout(g.handle, good.ptr)                    # already configured
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("q", [32, 64])
+def test_head_groups_match_whole_call(q):
+    """Fixed workspace budget (the reference's h3_cuda_sol_plan_make,
+    src/cuda/cuda_sol_policy.c:47-69): centroids of all heads, then routes,
+    lists and attention per head group. Each budget one byte below the last
+    plan halves the group; every split gives the whole call's output bit for
+    bit and the same pair counters, and a budget no group fits fails."""
+    seq, heads = 4103, 4
+    print(f"[sol] head groups seq={seq} heads={heads} q={q}", flush=True)
+    qx, kx, vx = sol_inputs(seq, heads, seed=9)
+    meta = sol_layout(seq, q)
+    g = make_sol(seq, meta, q)
+    try:
+        def counters():
+            c = np.zeros(9, np.uint64)
+            g.check(g.lib.h3_hip_sol_counters(g.handle, c.ctypes.data, 9), "counters")
+            return c
+
+        def plan():
+            grp, nbytes = C.c_uint32(), C.c_size_t()
+            g.check(g.lib.h3_hip_sol_plan_info(g.handle, C.byref(grp), C.byref(nbytes)), "plan")
+            return grp.value, nbytes.value
+
+        whole = sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK)
+        grp, nbytes = plan()
+        assert grp == heads and nbytes <= 512 << 20
+        base = counters()
+        per_call = base[2:].copy()
+        groups = []
+        while True:
+            g.check(g.lib.h3_hip_sol_workspace_cap(g.handle, nbytes - 1), "cap")
+            try:
+                out = sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK)
+            except RuntimeError as e:
+                assert "fixed budget" in str(e), str(e)
+                break
+            grp, new_bytes = plan()
+            assert new_bytes < nbytes and grp < (groups[-1] if groups else heads)
+            nbytes = new_bytes
+            groups.append(grp)
+            assert np.array_equal(out, whole), grp
+            now = counters()
+            assert np.array_equal(now[2:] - base[2:], per_call), grp
+            base = now
+            hm = sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK, head_major=True)
+            assert np.array_equal(hm, whole), grp
+            base = counters()
+            assert not g.lib.h3_hip_sol_routes(g.handle, None, 0, None, 0, None, None, 0)
+        assert groups == [2, 1], groups
+        g.check(g.lib.h3_hip_sol_workspace_cap(g.handle, 0), "cap")
+        assert np.array_equal(sdpa(g, qx, kx, vx, seq, heads, step=STEP, block=BLOCK), whole)
+        assert plan()[0] == heads
+    finally:
+        g.close()
+
+
+def test_real_h3_shape_under_cap():
+    """S = 109078, H = 56 with 64-row query blocks: the whole call needs about
+    2.4 GB (routes, lists and the transposed V of every head); under the
+    default 512 MiB budget it runs in head groups, and its output equals the
+    whole call's (a budget large enough for one group) bit for bit. Inputs are
+    0.5 N(0,1) from the device generator; no frame metadata, no protection."""
+    seq, heads, q = 109078, 56, 64
+    n = seq * heads * 128
+    print(f"[sol] real shape seq={seq} heads={heads}", flush=True)
+    meta = []
+    for block in (q, 64):
+        blocks = (seq + block - 1) // block
+        m = np.zeros((blocks, 4), np.int32)
+        m[:, 1:3] = -1
+        m[:, 3] = np.minimum(block, seq - block * np.arange(blocks))
+        meta.append(m)
+    g = make_sol(seq, meta, q)
+    try:
+        lib = g.lib
+        tq, tk, tv, out = (g.empty(n) for _ in range(4))
+        g.begin()
+        for i, t in enumerate((tq, tk, tv)):
+            g.check(lib.h3_hip_fill_normal_bf16(g.handle, t.handle, 78 * 16 + i, 0.5, n), "fill")
+        g.submit()
+
+        def run():
+            g.begin()
+            g.check(lib.h3_gpu_dit_sdpa_bf16(g.handle, out.handle, tq.handle, tk.handle, tv.handle, seq, heads, 128,
+                                             C.c_float(SCALE), 0, BLOCK, STEP), "SOL attention")
+            g.submit()
+            return out.read()
+
+        def plan():
+            grp, nbytes = C.c_uint32(), C.c_size_t()
+            g.check(lib.h3_hip_sol_plan_info(g.handle, C.byref(grp), C.byref(nbytes)), "plan")
+            return grp.value, nbytes.value
+
+        grouped = run()
+        grp, nbytes = plan()
+        print(f"  default budget: head group {grp}, {nbytes} bytes", flush=True)
+        assert nbytes <= 512 << 20 and grp < heads
+        assert np.all(np.isfinite(bf16(grouped[:: 997])))
+        g.check(lib.h3_hip_sol_workspace_cap(g.handle, 8 << 30), "cap")
+        whole = run()
+        assert plan()[0] == heads
+        assert np.array_equal(grouped, whole)
+    finally:
+        g.close()
