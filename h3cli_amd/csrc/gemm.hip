@@ -19,7 +19,10 @@
 //    dequantized in registers (w = bf16(code * scale)) and written to LDS as BF16,
 //    so each weight is converted once per workgroup, not per wave;
 //  * tile ids are XCD-remapped and grouped along M so that the workgroups an XCD
-//    runs together share weight columns in its L2.
+//    runs together share weight columns in its L2;
+//  * per-channel q8 (group == K) runs gemm_q8_staged: the int8 tile two steps
+//    ahead goes straight to LDS, and the next step's dequantization shares a
+//    basic block with this step's MFMAs, so its VALU work issues between them.
 #include "common.h"
 #include "internal.h"
 #include <cmath>
@@ -233,6 +236,191 @@ void gemm_kernel(GemmArgs a) {
     }
 }
 
+// W8A16 with the int8 weight tile staged in LDS: 8 waves (2 x 4, 128 x 64
+// per wave, two per SIMD) as gemm_kernel, but the int8 tile of step kt + 2 is
+// fetched straight into LDS (buffer_load ... lds) during step kt, and the
+// dequantization of step kt + 1 (LDS int8 -> registers -> BF16 LDS tile) runs
+// in the same basic block as step kt's MFMAs, so its VALU work can issue
+// between them instead of after them. No register is held across a step for
+// the weights. LDS: two stages of X and BF16 W (128 KB) plus two int8 stages
+// (32 KB). X and W8 rows past the matrices read as zeros (buffer range).
+constexpr int W8_BYTES = 256 * TK;                  // 16 KB int8 tile
+// Per-output-channel scales (group == K) only: they are loaded once.
+template <int EPI>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+void gemm_q8_staged(GemmArgs a) {
+    constexpr int WM = 2, WN = 4, T = 512;
+    constexpr int NBM = TM / WM / 32, NBN = TN / WN / 32;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    uint8_t *const w8s = lds + 2 * STAGE;
+    // wave is read as a uniform value, so LDS destinations and buffer offsets
+    // stay scalar (no waterfall loop around the buffer loads).
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+    const unsigned n32 = lane % 32, hf = lane / 32;
+    const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
+    const unsigned pid = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned band = pid / (GROUP_M * tiles_n), first_m = band * GROUP_M;
+    const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)GROUP_M);
+    const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
+    const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(tm * TM), n0 = __builtin_amdgcn_readfirstlane(tn * TN);
+    const unsigned wm = wave / WN, wn = wave % WN;
+    const unsigned ksteps = a.k / TK;
+
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, (int)((size_t)a.m * a.k * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.w, (short)0, (int)((size_t)a.n * a.k), 0x00020000);
+    // X block b = wave + 8 t: rows 8 b + lane / 8, 16-byte chunk lane % 8
+    // (swizzled); the swizzle does not depend on t, so one lane offset serves
+    // all four loads.
+    const uint32_t xoff = ((8 * wave + lane / 8) * a.k + swz(8 * wave + lane / 8, lane % 8) * 8) * 2;
+    // Weight chunks c = tid + 512 j: row w_row(c) = w_row(tid) + 128 j, part w_part(tid).
+    const unsigned wrow = w_row(tid), wpart = w_part(tid);
+    const uint32_t woff = wrow * a.k + wpart * 16;
+
+    f32x16 acc[NBN][NBM];
+#pragma unroll
+    for (int i = 0; i < NBN; i++)
+#pragma unroll
+        for (int j = 0; j < NBM; j++) acc[i][j] = f32x16{};
+
+    float wscale[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) wscale[j] = a.scales[n0 + wrow + 128 * j];
+    // Loads of step kt's data into the stages of step `at` (the step numbers
+    // of the stages are unclamped, so a clamped reload never lands in a stage
+    // that the current step reads).
+    auto load_x = [&](unsigned kt, unsigned at) {
+        uint8_t *xs = lds + (at & 1) * STAGE;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(xs + (wave + 8 * t) * 1024), 16, xoff,
+                (uint32_t)(((size_t)m0 + 64 * t) * a.k * 2 + kt * TK * 2), 0, 0);
+    };
+    auto load_w8 = [&](unsigned kt, unsigned at) {
+        uint8_t *ws8 = w8s + (at & 1) * W8_BYTES;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wr, (__attribute__((address_space(3))) void *)(ws8 + (wave + 8 * j) * 1024), 16, woff,
+                (uint32_t)(((size_t)n0 + 128 * j) * a.k + kt * TK), 0, 0);
+    };
+    // int8 chunks of stage `at` (this thread's own two) -> BF16 W stage at & 1.
+    auto dequant = [&](unsigned at) {
+        const uint8_t *ws8 = w8s + (at & 1) * W8_BYTES;
+        uint8_t *ws = lds + (at & 1) * STAGE + TILE_BYTES;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const i32x4 q = *reinterpret_cast<const i32x4 *>(ws8 + (tid + T * j) * 16);
+            const unsigned row = wrow + 128 * j;
+            bf16x8 half[2];
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                int word = q[e / 4];
+                f32x2 f = {(float)(int8_t)(word >> (8 * (e % 4))) * wscale[j],
+                           (float)(int8_t)(word >> (8 * (e % 4 + 1))) * wscale[j]};
+                bf16x2 b = __builtin_convertvector(f, bf16x2);
+                half[e / 8][e % 8] = b[0];
+                half[e / 8][e % 8 + 1] = b[1];
+            }
+            *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, wpart * 2) * 16) = half[0];
+            *reinterpret_cast<bf16x8 *>(ws + row * ROW_BYTES + swz(row, wpart * 2 + 1) * 16) = half[1];
+        }
+    };
+    auto frags = [&](const uint8_t *xs, const uint8_t *ws, int ks, bf16x8 *wf, bf16x8 *xf) {
+#pragma unroll
+        for (int i = 0; i < NBN; i++) {
+            unsigned wr_ = wn * 32 * NBN + i * 32 + n32;
+            wf[i] = *reinterpret_cast<const bf16x8 *>(ws + wr_ * ROW_BYTES + swz(wr_, ks * 2 + hf) * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < NBM; j++) {
+            unsigned xr_ = wm * 32 * NBM + j * 32 + n32;
+            xf[j] = *reinterpret_cast<const bf16x8 *>(xs + xr_ * ROW_BYTES + swz(xr_, ks * 2 + hf) * 16);
+        }
+    };
+
+    // Prologue: X(0), W8(0), W8(1); W(0) dequantized.
+    load_x(0, 0);
+    load_w8(0, 0);
+    load_w8(min(1u, ksteps - 1), 1);
+    wait_vm_loads();
+    __syncthreads();
+    dequant(0);
+    __syncthreads();
+
+    for (unsigned kt = 0; kt < ksteps; kt++) {
+        // Step indices past the end are clamped: those loads and the last
+        // dequantization refill stages no later step reads.
+        const unsigned k1 = min(kt + 1, ksteps - 1), k2 = min(kt + 2, ksteps - 1);
+        load_x(k1, kt + 1);
+        load_w8(k2, kt + 2);
+        const uint8_t *xs = lds + (kt & 1) * STAGE;
+        const uint8_t *ws = xs + TILE_BYTES;
+        bf16x8 wf[2][NBN], xf[2][NBM];
+        frags(xs, ws, 0, wf[0], xf[0]);
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ks++) {
+            if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < NBN; i++)
+#pragma unroll
+                for (int j = 0; j < NBM; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
+            // Branch-free, so the scheduler can interleave it with the MFMAs;
+            // on the last step it fills a stage no step reads.
+            if (ks == 0) dequant(kt + 1);
+        }
+        wait_vm_loads();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < NBM; j++) {
+        const unsigned row = m0 + wm * 32 * NBM + j * 32 + n32;
+        if (row >= a.m) continue;
+        uint16_t *dst = a.y + (size_t)row * a.n;
+#pragma unroll
+        for (int i = 0; i < NBN; i++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const unsigned col = n0 + wn * 32 * NBN + i * 32 + g4 * 8 + hf * 4;
+                u16x4 out;
+                u16x4 bias4 = {};
+                if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float v = acc[i][j][g4 * 4 + e];
+                    if constexpr (EPI & 1) v += bf16_to_f32(bias4[e]);
+                    uint16_t b = f32_to_bf16(v);
+                    if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
+                    out[e] = b;
+                }
+                *reinterpret_cast<u16x4 *>(dst + col) = out;
+            }
+    }
+}
+
+template <int EPI>
+int launch_staged(h3_gpu *g, const GemmArgs &a) {
+    constexpr size_t shared = 2 * STAGE + 2 * W8_BYTES;
+    static bool configured = false;
+    auto kernel = gemm_q8_staged<EPI>;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)shared), "GEMM shared memory"))
+            return 0;
+        configured = true;
+    }
+    unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
+    hipEvent_t timing = h3_kernel_timing_begin(g);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(512), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "W8A16 GEMM");
+}
+
 // Any-shape fallback (small or unaligned projections): one thread per output,
 // FP32 accumulation in k order. Same weight reconstruction as the tiled kernel.
 __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
@@ -279,6 +467,19 @@ int launch_tiled(h3_gpu *g, const GemmArgs &a) {
 template <bool Q8, bool CHANNEL>
 int launch_epi(h3_gpu *g, const GemmArgs &a) {
     const int epi = (a.bias ? 1 : 0) | (a.gelu ? 2 : 0);
+    if constexpr (Q8 && CHANNEL) {
+        // Per-channel W8A16 (the synthetic DiT): int8 tiles
+        // staged in LDS (buffer offsets are 32-bit). Variant 2 keeps the
+        // register-staged weights of gemm_kernel (3-4% slower on config 4).
+        if (g->gemm_variant != 2 && (size_t)a.m * a.k * 2 < (1ull << 31) && (size_t)a.n * a.k < (1ull << 31)) {
+            switch (epi) {
+            case 0: return launch_staged<0>(g, a);
+            case 1: return launch_staged<1>(g, a);
+            case 2: return launch_staged<2>(g, a);
+            default: return launch_staged<3>(g, a);
+            }
+        }
+    }
     // Variant 1: 2 x 2 waves of 128 x 128 (one wave per SIMD), about 10% slower.
     if (g->gemm_variant == 1) {
         switch (epi) {
