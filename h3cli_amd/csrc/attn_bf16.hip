@@ -712,13 +712,15 @@ void attn_bf16_pingpong(Args a) {
     constexpr int LOADS = (K_BYTES / 1024) / WAVES;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
-    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    // wave and head are read as uniform values so that LDS destinations and
+    // buffer offsets stay scalar (no waterfall loops around the loads).
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
     const int grp = (int)__builtin_amdgcn_readfirstlane(wave / 4);
     const unsigned qrows = a.qrows ? a.qrows : a.seq;
     const unsigned nqb = (qrows + BM - 1) / BM;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
-    const unsigned head = id / nqb, qb = id % nqb;
+    const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
     const unsigned q0 = qb * BM;
     uint8_t *const retry = a.retry + ((size_t)head * nqb + qb) * 8;
     const size_t stride = (size_t)a.heads * D;
@@ -1319,7 +1321,7 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     // Variant 4: four waves (128 queries) per workgroup and two workgroups per
     // CU, whose barriers are independent, 64 keys per interval (6% slower).
     if (g->attention_variant == 4) return launch_wide<1, false, false, true, 4>(g, a, (seq + 127) / 128 * heads);
-    // Variant 9: ping-pong wave groups (22.8 ms against 18.5 at S = 32400, H = 40).
+    // Variant 9: ping-pong wave groups (21.7 ms against 18.3 at S = 32400, H = 40).
     if (g->attention_variant == 9) return launch_pingpong<1>(g, a, (seq + 255) / 256 * heads);
     return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
 }
