@@ -303,6 +303,9 @@ void sage_attn_kernel(SArgs a) {
     };
 
     auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile) {
+        // Dense kernel: keep the fp8 ones in registers (hipcc otherwise
+        // rebuilds them with 7 moves per tile); the sparse kernel has no room.
+        if constexpr (!SPARSE) asm volatile("" : "+v"(ones));
         i32x16 si[2];
         si[0] = i32x16{}; si[1] = i32x16{};
 #pragma unroll
@@ -353,7 +356,9 @@ void sage_attn_kernel(SArgs a) {
                 const int idx = 4 * w + i;
                 p[i] = exp2f_fast(fmaf((float)si[idx / 16][idx % 16], c, bias));
             }
-            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false);
+            // The first pack's other word is overwritten by the second, so
+            // its old value may be any dead register (p[0]'s own: no copy).
+            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], __builtin_bit_cast(int, p[0]), false);
             pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], packed, true);
         }
         // O^T[md] += V^T[md] P^T (fp8, K = 64 keys); row sums from ones . P^T.
