@@ -82,7 +82,16 @@ struct Args {
     // Listed kernel only: a slab of query blocks [qb0, qb0 + qslab) (lists
     // indexed slab-relative, [head][qslab]); qslab 0 covers the sequence.
     unsigned qb0, qslab;
+    // K and V^T fit 32-bit buffer offsets (below 4 GiB each): the dense
+    // kernels then load tiles with buffer loads.
+    int buffered;
 };
+
+// Whether K [seq, heads, 128] and V^T [heads, 128, padded] both fit 32-bit
+// buffer offsets.
+static int fits_buffer(const Args &a) {
+    return (size_t)a.seq * a.heads * D * 2 < (1ull << 32) && (size_t)a.heads * D * a.padded * 2 < (1ull << 32);
+}
 
 // Position of key j (0..63) inside a transposed V row: keys are grouped by 16
 // and, inside a group, ordered the way a lane half holds them in the S^T
@@ -389,12 +398,14 @@ void attn_bf16_wide(Args a) {
     constexpr int STAGE = KT * (K_BYTES + V_BYTES);
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
-    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    // wave and head are read as uniform values so that LDS destinations and
+    // buffer offsets stay scalar.
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
     const unsigned n = lane % 32, hf = lane / 32;
     const unsigned qrows = a.qrows ? a.qrows : a.seq;
     const unsigned nqb = (qrows + BM - 1) / BM;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
-    const unsigned head = id / nqb, qb = id % nqb;
+    const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
     const unsigned q0 = qb * BM;
     uint8_t *const retry = a.retry ? a.retry + ((size_t)head * nqb + qb) * WAVES : nullptr;
     // The recomputation launch runs only the workgroups the fast kernel flagged.
@@ -450,8 +461,34 @@ void attn_bf16_wide(Args a) {
         voff = (d * a.padded + v_chunk(d, lane % 8) * 8) * 2;
     }
 
+    // Dense: buffer loads straight to LDS, a uniform byte offset per load plus
+    // the lane's koff / voff (no per-load address arithmetic); keys at or
+    // past seq lie past the end of K's buffer and read as zeros (their scores
+    // are masked), and group ids past the end are clamped.
+    const __amdgpu_buffer_rsrc_t krsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.k, (short)0, (int)(uint32_t)((size_t)a.seq * stride * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.vt, (short)0, (int)(uint32_t)((size_t)a.heads * D * a.padded * 2),
+                                          0x00020000);
     auto load_group = [&](unsigned g, int stage) {
         uint8_t *base = smem + stage * STAGE;
+        if (!SPARSE && a.buffered) {
+#pragma unroll
+            for (int j = 0; j < KT; j++) {
+                const unsigned key0 = min(g * KT + j, count - 1) * BN;
+#pragma unroll
+                for (int t = 0; t < LOADS; t++) {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        krsrc, (__attribute__((address_space(3))) void *)(base + j * K_BYTES + (wave + WAVES * t) * 1024),
+                        16, koff, (unsigned)(((size_t)head * D + ((size_t)key0 + 4 * WAVES * t) * stride) * 2), 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        vrsrc,
+                        (__attribute__((address_space(3))) void *)(base + KT * K_BYTES + j * V_BYTES + (wave + WAVES * t) * 1024),
+                        16, voff, (unsigned)(((size_t)head * D * a.padded + (size_t)8 * WAVES * t * a.padded + key0) * 2), 0, 0);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < KT; j++) {
             const unsigned tile = sub_at(g * KT + j);
@@ -1306,6 +1343,8 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride;
     a.fault = g->fault;
+    // Variant 13: the global-load path that tensors of 4 GiB and more take.
+    a.buffered = fits_buffer(a) && g->attention_variant != 13;
     hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;
@@ -1322,7 +1361,7 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     // CU, whose barriers are independent, 64 keys per interval (6% slower).
     if (g->attention_variant == 4) return launch_wide<1, false, false, true, 4>(g, a, (seq + 127) / 128 * heads);
     // Variant 9: ping-pong wave groups (21.7 ms against 18.3 at S = 32400, H = 40).
-    if (g->attention_variant == 9) return launch_pingpong<1>(g, a, (seq + 255) / 256 * heads);
+    if (g->attention_variant == 9 && a.buffered) return launch_pingpong<1>(g, a, (seq + 255) / 256 * heads);
     return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
 }
 
@@ -1340,6 +1379,7 @@ int h3_launch_attention_flash(h3_gpu *g, void *workspace, uint16_t *out, const u
     a.head_major = head_major ? 1 : 0;
     a.lse = lse;
     a.fault = g->fault;
+    a.buffered = fits_buffer(a);
     hipLaunchKernelGGL(transpose_v, dim3(a.padded / BN, heads), dim3(256), 0, g->compute, v, k, (uint16_t *)workspace,
                        seq, heads, a.padded, g->fault);
     if (!h3_launch_status(g, "V transpose")) return 0;

@@ -115,6 +115,23 @@ def test_recomputation_launch_matches_tile_max_kernel(gpu, monkeypatch):
         g3.close()
 
 
+@pytest.mark.parametrize("seq,heads", [(4200, 2), (65, 3), (1, 1)])
+def test_global_load_path_matches_buffer_path(gpu, monkeypatch, seq, heads):
+    """K and V^T below 4 GiB load their tiles with buffer loads (keys past the
+    sequence read as zeros); larger tensors take the global-load path (rows
+    clamped to the last key), forced here with attention variant 13. Both
+    mask the same keys, so the outputs agree bit for bit, ragged tails
+    included."""
+    q, k, v = synth.attention_inputs(seq, heads, seed=31, scale=0.5)
+    buffered = sdpa(gpu, q, k, v, seq, heads)
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", "13")
+    g13 = Gpu()
+    try:
+        assert np.array_equal(sdpa(g13, q, k, v, seq, heads), buffered)
+    finally:
+        g13.close()
+
+
 def test_large_values_after_score_jump(gpu):
     """A 41-log2-unit score jump with |V| near 1e26: P that large must not
     reach O unscaled (it would overflow FP32). The rows go to the
