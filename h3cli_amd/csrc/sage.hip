@@ -230,6 +230,7 @@ struct SArgs {
     const uint32_t *kv_list, *kv_count;
     unsigned list_stride;
     unsigned *fault;
+    int buffered;                           // k8 and v8 below 4 GiB: buffer loads with 32-bit offsets
 };
 
 constexpr int Q8_TILE = BN * D;             // K8 tile bytes: 64 rows x 128 B
@@ -251,10 +252,14 @@ void sage_attn_kernel(SArgs a) {
     static_assert(Q8_TILE == V8_TILE, "tile split");
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
-    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, n = lane % 32, hf = lane / 32;
+    // wave and head are read as uniform values so that LDS destinations and
+    // buffer offsets stay scalar.
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+    const unsigned n = lane % 32, hf = lane / 32;
     const unsigned nqb = (a.seq + BM - 1) / BM;
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
-    const unsigned head = id / nqb, qb = id % nqb, q0 = qb * BM;
+    const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
+    const unsigned q0 = qb * BM;
     const unsigned ntiles = a.padded / BN;
     const int8_t *qh = a.q8 + (size_t)head * a.padded * D;
     const int8_t *kh = a.k8 + (size_t)head * a.padded * D;
@@ -285,10 +290,33 @@ void sage_attn_kernel(SArgs a) {
     for (int i = 0; i < 8; i++) ones[i] = 0x38383838;
 
     // Direct global->LDS tile loads, one contiguous KB per wave instruction.
+    // Buffered: a uniform byte offset per load plus one lane offset each for
+    // K and V (block wave + WAVES i sits 8 WAVES i keys / 16 WAVES i channels
+    // further on, with the same swizzle).
+    const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.k8, (short)0, (int)(uint32_t)((size_t)a.heads * a.padded * D), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.v8, (short)0, (int)(uint32_t)((size_t)a.heads * D * a.padded), 0x00020000);
+    const uint32_t koff = (8 * wave + lane / 8) * D + k8_chunk(8 * wave + lane / 8, lane % 8) * 16;
+    const uint32_t voff = (16 * wave + lane / 4) * a.padded + v8_chunk(16 * wave + lane / 4, lane % 4) * 16;
     auto load_tile = [&](unsigned tile, int stage) {
         const unsigned t = min(tile, ntiles - 1);
         uint8_t *ks = lds + stage * SAGE_TILE;
         uint8_t *vs = ks + Q8_TILE;
+        if (a.buffered) {
+#pragma unroll
+            for (unsigned i = 0; i < (BLOCKS + WAVES - 1) / WAVES; i++) {
+                const unsigned b = wave + WAVES * i;
+                if (b >= BLOCKS) break;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    krsrc, (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, koff,
+                    (unsigned)(((size_t)head * a.padded + (size_t)t * BN + 8 * WAVES * i) * D), 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    vrsrc, (__attribute__((address_space(3))) void *)(vs + b * 1024), 16, voff,
+                    (unsigned)(((size_t)head * D + 16 * WAVES * i) * a.padded + (size_t)t * BN), 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (unsigned b = wave; b < BLOCKS; b += WAVES) {
             unsigned key = 8 * b + lane / 8, ph = lane % 8;
@@ -452,6 +480,8 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride; a.fault = g->fault;
+    // Variant 13: the global-load path that operands of 4 GiB and more take.
+    a.buffered = (size_t)heads * L.padded * D < (1ull << 32) && g->attention_variant != 13;
     // Block-sparse lists are per 128-query block: 4 waves, three workgroups per CU.
     if (kv_list) return launch_sage<4, 3, true>(g, a, (seq + 127) / 128 * heads);
     // 12 waves x 32 queries: three waves per SIMD (166 VGPRs each).

@@ -107,3 +107,19 @@ def test_sage_dispatch_counted_and_nonfinite(gpu):
     gpu.cancel()
     stats = (C.c_uint64 * 128)()
     assert lib.h3_gpu_get_stats(gpu.handle, stats)
+
+
+@pytest.mark.parametrize("seq,heads", [(2500, 2), (65, 1)])
+def test_global_load_path_matches_buffer_path(gpu, monkeypatch, seq, heads):
+    """Quantized operands below 4 GiB load their tiles with buffer loads;
+    larger ones take the global-load path, forced here with attention variant
+    13. The tiles are the same bytes, so the outputs agree bit for bit."""
+    q, k, v = sage_inputs(seq, heads, seed=17)
+    buffered = sdpa(gpu, q, k, v, seq, heads)
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", "13")
+    g13 = Gpu()
+    try:
+        g13.check(g13.lib.h3_gpu_dit_attention_configure(g13.handle, 1), "configure sage2++")
+        assert np.array_equal(sdpa(g13, q, k, v, seq, heads), buffered)
+    finally:
+        g13.close()

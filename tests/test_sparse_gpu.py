@@ -68,6 +68,25 @@ def test_masked_sage():
         g.close()
 
 
+def test_masked_sage_global_load_path(monkeypatch):
+    """The block-sparse Sage kernel's buffer-load path and its global-load path
+    (attention variant 13, what operands of 4 GiB and more take) agree bit for
+    bit."""
+    seq, video, heads = 1500, 1200, 2
+    mask = oracle.block_mask(seq, video, 128, 0.25, seed=3)
+    q, k, v = sage_inputs(seq, heads, seed=13)
+    outs = []
+    for variant in ("0", "13"):
+        monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", variant)
+        g = make_gpu(1)
+        try:
+            bind_mask(g, mask)
+            outs.append(sdpa(g, q, k, v, seq, heads))
+        finally:
+            g.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_subblock_requires_mask_and_step():
     g = make_gpu(4)
     try:
