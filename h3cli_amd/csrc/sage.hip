@@ -482,11 +482,16 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride; a.fault = g->fault;
     // Variant 13: the global-load path that operands of 4 GiB and more take.
     a.buffered = (size_t)heads * L.padded * D < (1ull << 32) && g->attention_variant != 13;
-    // Block-sparse lists are per 128-query block: 4 waves, three workgroups per CU.
+    // 4 waves x 32 queries per workgroup, three workgroups per CU (three
+    // waves per SIMD, 166 VGPRs each); block-sparse lists are per 128-query
+    // block, the same shape. The workgroups' barriers are independent, so the
+    // waves that share a SIMD drift into different phases of their tiles (one
+    // 12-wave workgroup per CU keeps all twelve in step: 6% slower, variant 2;
+    // 8 waves at two per SIMD: variant 1).
     if (kv_list) return launch_sage<4, 3, true>(g, a, (seq + 127) / 128 * heads);
-    // 12 waves x 32 queries: three waves per SIMD (166 VGPRs each).
     if (g->attention_variant == 1) return launch_sage<8, 2, false>(g, a, (seq + 255) / 256 * heads);
-    return launch_sage<12, 3, false>(g, a, (seq + 383) / 384 * heads);
+    if (g->attention_variant == 2) return launch_sage<12, 3, false>(g, a, (seq + 383) / 384 * heads);
+    return launch_sage<4, 3, false>(g, a, (seq + 127) / 128 * heads);
 }
 
 extern "C" unsigned h3_hip_sage_v_position(unsigned j) { return sage_v_position(j & 63); }
