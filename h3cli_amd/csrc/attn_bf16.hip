@@ -462,9 +462,9 @@ void attn_bf16_wide(Args a) {
     }
 
     // Dense: buffer loads straight to LDS, a uniform byte offset per load plus
-    // the lane's koff / voff (no per-load address arithmetic); keys at or
-    // past seq lie past the end of K's buffer and read as zeros (their scores
-    // are masked), and group ids past the end are clamped.
+    // the lane's koff / voff (no per-load address arithmetic). In the last
+    // tile, lanes whose key is at or past seq take BUFFER_OOB and load zeros
+    // (their scores are masked); group ids past the end are clamped.
     const __amdgpu_buffer_rsrc_t krsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.k, (short)0, (int)(uint32_t)((size_t)a.seq * stride * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t vrsrc =
@@ -476,11 +476,17 @@ void attn_bf16_wide(Args a) {
 #pragma unroll
             for (int j = 0; j < KT; j++) {
                 const unsigned key0 = min(g * KT + j, count - 1) * BN;
+                const bool tail = key0 + BN > a.seq;
 #pragma unroll
                 for (int t = 0; t < LOADS; t++) {
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        krsrc, (__attribute__((address_space(3))) void *)(base + j * K_BYTES + (wave + WAVES * t) * 1024),
-                        16, koff, (unsigned)(((size_t)head * D + ((size_t)key0 + 4 * WAVES * t) * stride) * 2), 0, 0);
+                    const unsigned so = (unsigned)(((size_t)head * D + ((size_t)key0 + 4 * WAVES * t) * stride) * 2);
+                    auto *dst = (__attribute__((address_space(3))) void *)(base + j * K_BYTES + (wave + WAVES * t) * 1024);
+                    if (tail) {
+                        const unsigned key = key0 + 4 * WAVES * t + 4 * wave + lane / 16;
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, dst, 16, key < a.seq ? koff : BUFFER_OOB, so, 0, 0);
+                    } else {
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, dst, 16, koff, so, 0, 0);
+                    }
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
                         vrsrc,
                         (__attribute__((address_space(3))) void *)(base + KT * K_BYTES + j * V_BYTES + (wave + WAVES * t) * 1024),
@@ -789,9 +795,10 @@ void attn_bf16_pingpong(Args a) {
     }
     // Group g's K tiles into K slot g % 2, V^T tiles into V slot g % 2, with
     // buffer loads straight to LDS: a uniform byte offset per load plus one
-    // per-lane offset (koff / voff). Keys at or past seq lie past the end of
-    // K's buffer and read as zeros (their scores are masked); tile ids past
-    // the end are clamped (such loads refill a slot no step reads).
+    // per-lane offset (koff / voff). In the last tile, lanes whose key is at
+    // or past seq take BUFFER_OOB and load zeros (their scores are masked);
+    // tile ids past the end are clamped (such loads refill a slot no step
+    // reads).
     const __amdgpu_buffer_rsrc_t krsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.k, (short)0, (int)((size_t)a.seq * stride * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t vrsrc =
@@ -801,12 +808,17 @@ void attn_bf16_pingpong(Args a) {
 #pragma unroll
         for (int j = 0; j < KT; j++) {
             const unsigned key0 = min(g * KT + j, count - 1) * BN;
+            const bool tail = key0 + BN > a.seq;
 #pragma unroll
             for (int t = 0; t < LOADS; t++) {
                 const unsigned so = (unsigned)(((size_t)head * D + ((size_t)key0 + 4 * WAVES * t) * stride) * 2);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    krsrc, (__attribute__((address_space(3))) void *)(base + j * K_BYTES + (wave + WAVES * t) * 1024), 16,
-                    koff, so, 0, 0);
+                auto *dst = (__attribute__((address_space(3))) void *)(base + j * K_BYTES + (wave + WAVES * t) * 1024);
+                if (tail) {
+                    const unsigned key = key0 + 4 * WAVES * t + 4 * wave + lane / 16;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, dst, 16, key < a.seq ? koff : BUFFER_OOB, so, 0, 0);
+                } else {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, dst, 16, koff, so, 0, 0);
+                }
             }
         }
     };

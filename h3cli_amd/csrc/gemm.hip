@@ -243,7 +243,8 @@ void gemm_kernel(GemmArgs a) {
 // in the same basic block as step kt's MFMAs, so its VALU work can issue
 // between them instead of after them. No register is held across a step for
 // the weights. LDS: two stages of X and BF16 W (128 KB) plus two int8 stages
-// (32 KB). X and W8 rows past the matrices read as zeros (buffer range).
+// (32 KB). X rows past M load zeros (BUFFER_OOB lane offsets); W8 rows never
+// pass N, a multiple of 256.
 constexpr int W8_BYTES = 256 * TK;                  // 16 KB int8 tile
 // Per-output-channel scales (group == K) only: they are loaded once.
 template <int EPI>
@@ -291,13 +292,22 @@ void gemm_q8_staged(GemmArgs a) {
     // Loads of step kt's data into the stages of step `at` (the step numbers
     // of the stages are unclamped, so a clamped reload never lands in a stage
     // that the current step reads).
+    // In the last row tile, lanes whose row is at or past M take BUFFER_OOB
+    // and load zeros (those output rows are not stored).
+    const bool m_tail = m0 + TM > a.m;
     auto load_x = [&](unsigned kt, unsigned at) {
         uint8_t *xs = lds + (at & 1) * STAGE;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void *)(xs + (wave + 8 * t) * 1024), 16, xoff,
-                (uint32_t)(((size_t)m0 + 64 * t) * a.k * 2 + kt * TK * 2), 0, 0);
+        for (int t = 0; t < 4; t++) {
+            auto *dst = (__attribute__((address_space(3))) void *)(xs + (wave + 8 * t) * 1024);
+            const uint32_t so = (uint32_t)(((size_t)m0 + 64 * t) * a.k * 2 + kt * TK * 2);
+            if (m_tail) {
+                const unsigned row = m0 + 64 * t + 8 * wave + lane / 8;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, row < a.m ? xoff : BUFFER_OOB, so, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, xoff, so, 0, 0);
+            }
+        }
     };
     auto load_w8 = [&](unsigned kt, unsigned at) {
         uint8_t *ws8 = w8s + (at & 1) * W8_BYTES;
