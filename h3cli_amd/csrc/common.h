@@ -76,12 +76,12 @@ __device__ inline bool bf16_vec_nonfinite(const V &v) {
 // Wait for this wave's outstanding vector-memory loads, including direct
 // global->LDS loads, before a barrier publishes their LDS contents.
 __device__ inline void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-// Raw buffer loads bounds-check the per-lane (VGPR) offset against the
-// descriptor's size and return zeros past it; the uniform (SGPR) offset is
-// added to the base, so a row past a tensor's end that is reached through the
-// SGPR offset must be masked with this VGPR offset instead (it is past every
-// size below 4 GiB, and as a 32-bit sum with any SGPR offset it stays inside
-// the same 4 GiB window).
+// Raw buffer loads return zeros for a per-lane (VGPR) offset past the
+// descriptor's size. The kernels rely on that check only, not on one covering
+// the uniform (SGPR) offset: a row past a tensor's end that the SGPR offset
+// reaches is masked with this VGPR offset instead. It is past every size below
+// 4 GiB, and even as a 32-bit sum with an SGPR offset it addresses no byte
+// outside the tensor's own 4 GiB window.
 constexpr uint32_t BUFFER_OOB = 0xFFFFFFF0u;
 
 // ---------------------------------------------------------------- objects
