@@ -470,9 +470,12 @@ void attn_bf16_wide(Args a) {
     const __amdgpu_buffer_rsrc_t vrsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.vt, (short)0, (int)(uint32_t)((size_t)a.heads * D * a.padded * 2),
                                           0x00020000);
-    auto load_group = [&](unsigned g, int stage) {
+    // BUF_ONLY: the caller has checked a.buffered (the global-load path is
+    // then not compiled into that caller).
+    auto load_group = [&](unsigned g, int stage, auto buf_only_tag) {
+        constexpr bool BUF_ONLY = decltype(buf_only_tag)::value;
         uint8_t *base = smem + stage * STAGE;
-        if (!SPARSE && a.buffered) {
+        if (!SPARSE && (BUF_ONLY || a.buffered)) {
 #pragma unroll
             for (int j = 0; j < KT; j++) {
                 const unsigned key0 = min(g * KT + j, count - 1) * BN;
@@ -542,12 +545,20 @@ void attn_bf16_wide(Args a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.0f;
 
-    if (groups) load_group(0, 0);
+    if (groups) load_group(0, 0, std::false_type{});
     wait_vm_loads();
     __syncthreads();
-    for (unsigned g = 0; g < groups; g++) {
+    // One group of KT sub-tiles. FULL: a group past the first whose keys are
+    // all below seq (dense, NOMAX, buffer loads): no masking, no group max
+    // and no global-load path are compiled in. Those groups run in a loop of
+    // their own, with the first group and the tail peeled off it, so the loop
+    // holds one compact path (1.5-1.9% faster than one loop over all groups,
+    // whose cold branches sit between the hot code). Same arithmetic either
+    // way.
+    auto group = [&](unsigned g, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
         const int cur = g & 1;
-        if (g + 1 < groups) load_group(g + 1, cur ^ 1);
+        if (g + 1 < groups) load_group(g + 1, cur ^ 1, full_tag);
         const uint8_t *base = smem + cur * STAGE;
         f32x16 s[KT][2];
 #pragma unroll
@@ -568,6 +579,7 @@ void attn_bf16_wide(Args a) {
                     s[j][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[kstep * 2 + mb], qf[kstep], s[j][mb], 0, 0, 0);
         }
         // Mask keys past the sequence end and sub-tiles past the list end.
+        if constexpr (!FULL)
 #pragma unroll
         for (int j = 0; j < KT; j++) {
             const unsigned idx = g * KT + j;
@@ -582,7 +594,7 @@ void attn_bf16_wide(Args a) {
                     }
             }
         }
-        if (!NOMAX || g == 0) {
+        if (!FULL && (!NOMAX || g == 0)) {
         float mx0 = -INFINITY, mx1 = -INFINITY;
 #pragma unroll
         for (int j = 0; j < KT; j++)
@@ -666,7 +678,17 @@ void attn_bf16_wide(Args a) {
         }
         wait_vm_loads();
         __syncthreads();
+    };
+    unsigned g0 = 0;
+    if constexpr (NOMAX && !SPARSE) {
+        if (a.buffered) {
+            const unsigned full = a.seq / (KT * BN);
+            if (groups) group(0u, std::false_type{});
+            for (g0 = 1; g0 < full; g0++) group(g0, std::true_type{});
+            g0 = max(g0, 1u);
+        }
     }
+    for (unsigned g = g0; g < groups; g++) group(g, std::false_type{});
 
     const float total = MSUM ? lsum[0] : half_sum_swap(l);
     const float inv = total > 0.f ? 1.f / total : 0.f;
