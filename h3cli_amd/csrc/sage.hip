@@ -299,11 +299,12 @@ void sage_attn_kernel(SArgs a) {
         (void *)a.v8, (short)0, (int)(uint32_t)((size_t)a.heads * D * a.padded), 0x00020000);
     const uint32_t koff = (8 * wave + lane / 8) * D + k8_chunk(8 * wave + lane / 8, lane % 8) * 16;
     const uint32_t voff = (16 * wave + lane / 4) * a.padded + v8_chunk(16 * wave + lane / 4, lane % 4) * 16;
-    auto load_tile = [&](unsigned tile, int stage) {
+    auto load_tile = [&](unsigned tile, int stage, auto buf_only_tag) {
+        constexpr bool BUF_ONLY = decltype(buf_only_tag)::value;   // caller checked a.buffered
         const unsigned t = min(tile, ntiles - 1);
         uint8_t *ks = lds + stage * SAGE_TILE;
         uint8_t *vs = ks + Q8_TILE;
-        if (a.buffered) {
+        if (BUF_ONLY || a.buffered) {
 #pragma unroll
             for (unsigned i = 0; i < (BLOCKS + WAVES - 1) / WAVES; i++) {
                 const unsigned b = wave + WAVES * i;
@@ -330,7 +331,8 @@ void sage_attn_kernel(SArgs a) {
         }
     };
 
-    auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile) {
+    auto process = [&](const uint8_t *ks, const uint8_t *vs, unsigned tile, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;   // every key of the tile < seq
         // Dense kernel: keep the fp8 ones in registers (hipcc otherwise
         // rebuilds them with 7 moves per tile); the sparse kernel has no room.
         if constexpr (!SPARSE) asm volatile("" : "+v"(ones));
@@ -346,7 +348,7 @@ void sage_attn_kernel(SArgs a) {
             }
         }
         const float c = qs * a.k_scale[head * a.blocks + min(tile, a.blocks - 1)];
-        const bool masked = tile * BN + BN > a.seq;
+        const bool masked = !FULL && tile * BN + BN > a.seq;
         if (masked) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
@@ -408,21 +410,30 @@ void sage_attn_kernel(SArgs a) {
         if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
         if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
     }
-    if (count) load_tile(tile, 0);
+    if (count) load_tile(tile, 0, std::false_type{});
     wait_vm_loads();
     __syncthreads();
-    for (unsigned it = 0; it < count; it++) {
+    // One tile step. FULL (dense, buffer loads): every key of the tile is
+    // below seq, and no masking or global-load code is compiled in; those
+    // tiles run in a loop of their own so that its code stays compact.
+    auto step = [&](unsigned it, auto full_tag) {
         const int cur = it & 1;
-        if (it + 1 < count) load_tile(next, cur ^ 1);
+        if (it + 1 < count) load_tile(next, cur ^ 1, full_tag);
         uint32_t later = it + 2;
         if constexpr (SPARSE) later = it + 2 < count ? list[it + 2] : 0u;
         const uint8_t *ks = lds + cur * SAGE_TILE;
-        process(ks, ks + Q8_TILE, tile);
+        process(ks, ks + Q8_TILE, tile, full_tag);
         wait_vm_loads();
         __syncthreads();
         tile = next;
         next = SPARSE ? __builtin_amdgcn_readfirstlane(later) : later;
+    };
+    unsigned it0 = 0;
+    if constexpr (!SPARSE) {
+        if (a.buffered)
+            for (const unsigned full = a.seq / BN; it0 < full; it0++) step(it0, std::true_type{});
     }
+    for (unsigned it = it0; it < count; it++) step(it, std::false_type{});
 
     bool bad = false;
     const float *vsc = a.v_scale + head * D;
