@@ -1135,11 +1135,13 @@ void attn_bf16_listed(Args a) {
         const unsigned d = 8 * wave + 8 * QW * t + lane / 8;
         vl[t] = ((8 * wave + lane / 8) * a.padded + v_chunk(d, lane % 8) * 8) * 2;
     }
-    auto load_k = [&](uint32_t e, uint8_t *ks) {
-        const bool cent = CENT && (e & CENT_BIT);
+    // FULL (key tiles only, every key < seq): no tail or centroid code.
+    auto load_k = [&](uint32_t e, uint8_t *ks, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        const bool cent = !FULL && CENT && (e & CENT_BIT);
         const unsigned key0 = (CENT ? e & TILE_BITS : e) * BN, limit = cent ? a.key_blocks : a.seq;
         const uint16_t *base = cent ? kch : kh;
-        if (a.buffered && !cent && key0 + BN <= limit) {
+        if (a.buffered && !cent && (FULL || key0 + BN <= limit)) {
 #pragma unroll
             for (int t = 0; t < LOADS; t++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -1147,7 +1149,7 @@ void attn_bf16_listed(Args a) {
                     (unsigned)(((size_t)head * D + ((size_t)key0 + 4 * QW * t) * stride) * 2), 0, 0);
             return;
         }
-        if (!cent && key0 + BN <= limit) {
+        if (FULL || (!cent && key0 + BN <= limit)) {
             const __attribute__((address_space(1))) char *tile =
                 (const __attribute__((address_space(1))) char *)(base + (size_t)key0 * stride);
 #pragma unroll
@@ -1166,8 +1168,9 @@ void attn_bf16_listed(Args a) {
                                              (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
         }
     };
-    auto load_v = [&](uint32_t e, uint8_t *vs) {
-        const bool cent = CENT && (e & CENT_BIT);
+    auto load_v = [&](uint32_t e, uint8_t *vs, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        const bool cent = !FULL && CENT && (e & CENT_BIT);
         const unsigned padded = cent ? a.kc_padded : a.padded;
         const unsigned col = min((CENT ? e & TILE_BITS : e) * BN, padded - BN);
         const uint16_t *base = cent ? vcth : vth;
@@ -1212,14 +1215,15 @@ void attn_bf16_listed(Args a) {
     // Online softmax of the tile and O^T += V^T P^T. bits: for a centroid
     // tile, bit mb * 16 + r says whether the key of accumulator element
     // s[mb][r] takes part; the bias is added in log2 units.
-    auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, uint32_t e, uint32_t bits) {
-        const bool cent = CENT && (e & CENT_BIT);
+    auto softmax_pv = [&](f32x16 (&s)[2], const uint8_t *vs, uint32_t e, uint32_t bits, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        const bool cent = !FULL && CENT && (e & CENT_BIT);
         const unsigned tile = CENT ? e & TILE_BITS : e;
         const float bias = cent ? 6.0f : 0.0f;      // log2(64)
         // A centroid tile is masked in the P domain below (its max may then
         // include excluded centroids: an upper bound, harmless to the softmax);
         // a key tile crossing the sequence end masks keys >= seq here.
-        if (!cent && tile * BN + BN > a.seq) {
+        if (!FULL && !cent && tile * BN + BN > a.seq) {
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
 #pragma unroll
@@ -1302,28 +1306,37 @@ void attn_bf16_listed(Args a) {
     if (CENT) mask = uniform64(mask_at(0));
     if constexpr (SPLIT) {
         uint8_t *ks = smem, *vs = smem + K_BYTES;
-        if (total) { load_k(tile, ks); load_v(tile, vs); }
+        if (total) { load_k(tile, ks, std::false_type{}); load_v(tile, vs, std::false_type{}); }
         wait_vm_loads();
         __syncthreads();
-        for (unsigned it = 0; it < total; it++) {
+        auto step = [&](unsigned it, auto full_tag) {
             const bool has_next = it + 1 < total;
             f32x16 s[2];
             if (!CENT || (tile & half_bit)) scores(ks, s);
             wait_vm_loads();               // this tile's V^T (own share)
             __syncthreads();               // K free; every share of V^T landed
-            if (has_next) load_k(next, ks);
+            if (has_next) load_k(next, ks, full_tag);
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
             const uint64_t mask_after = mask_at(it + 1);
-            if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT ? lane_bits(mask) : 0u);
+            if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT ? lane_bits(mask) : 0u, full_tag);
             wait_vm_loads();               // next K, the id after it and the next mask (own share)
             __syncthreads();               // V^T free; every share of the next K landed
-            if (has_next) load_v(next, vs);
+            if (has_next) load_v(next, vs, full_tag);
             tile = next;
             next = __builtin_amdgcn_readfirstlane(later);
             if (CENT) mask = uniform64(mask_after);
+        };
+        // Key tiles only: a list is ascending, so only its last entry can
+        // cross the sequence end, and a step loads the entry after its own.
+        // Steps whose own and next entries are not the last run in a loop of
+        // their own with no tail code (a compact loop).
+        unsigned it0 = 0;
+        if constexpr (!CENT) {
+            for (; it0 + 2 < total; it0++) step(it0, std::true_type{});
         }
+        for (unsigned it = it0; it < total; it++) step(it, std::false_type{});
     } else {
-        if (total) { load_k(tile, smem); load_v(tile, smem + K_BYTES); }
+        if (total) { load_k(tile, smem, std::false_type{}); load_v(tile, smem + K_BYTES, std::false_type{}); }
         wait_vm_loads();
         __syncthreads();
         for (unsigned it = 0; it < total; it++) {
@@ -1331,15 +1344,15 @@ void attn_bf16_listed(Args a) {
             uint8_t *ks = smem + cur * STAGE_BYTES;
             if (it + 1 < total) {
                 uint8_t *nk = smem + (cur ^ 1) * STAGE_BYTES;
-                load_k(next, nk);
-                load_v(next, nk + K_BYTES);
+                load_k(next, nk, std::false_type{});
+                load_v(next, nk + K_BYTES, std::false_type{});
             }
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
             const uint64_t mask_after = mask_at(it + 1);
             if (!CENT || (tile & half_bit)) {
                 f32x16 s[2];
                 scores(ks, s);
-                softmax_pv(s, ks + K_BYTES, tile, CENT ? lane_bits(mask) : 0u);
+                softmax_pv(s, ks + K_BYTES, tile, CENT ? lane_bits(mask) : 0u, std::false_type{});
             }
             wait_vm_loads();
             __syncthreads();
