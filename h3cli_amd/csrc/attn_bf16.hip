@@ -1137,13 +1137,15 @@ void attn_bf16_listed(Args a) {
         const unsigned d = 8 * wave + 8 * QW * t + lane / 8;
         vl[t] = ((8 * wave + lane / 8) * a.padded + v_chunk(d, lane % 8) * 8) * 2;
     }
-    // FULL (key tiles only, every key < seq): no tail or centroid code.
-    auto load_k = [&](uint32_t e, uint8_t *ks, auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
+    // FULL (key tiles only, every key < seq): no tail or centroid code, and
+    // with a load mode fixed by the caller (BUF: buffer loads, else global
+    // loads), only that mode's code.
+    auto load_k = [&](uint32_t e, uint8_t *ks, auto full_tag, auto buf_tag) {
+        constexpr bool FULL = decltype(full_tag)::value, BUF = decltype(buf_tag)::value;
         const bool cent = !FULL && CENT && (e & CENT_BIT);
         const unsigned key0 = (CENT ? e & TILE_BITS : e) * BN, limit = cent ? a.key_blocks : a.seq;
         const uint16_t *base = cent ? kch : kh;
-        if (a.buffered && !cent && (FULL || key0 + BN <= limit)) {
+        if ((FULL ? BUF : a.buffered) && !cent && (FULL || key0 + BN <= limit)) {
 #pragma unroll
             for (int t = 0; t < LOADS; t++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -1170,13 +1172,13 @@ void attn_bf16_listed(Args a) {
                                              (__attribute__((address_space(3))) void *)(ks + b * 1024), 16, 0, 0);
         }
     };
-    auto load_v = [&](uint32_t e, uint8_t *vs, auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
+    auto load_v = [&](uint32_t e, uint8_t *vs, auto full_tag, auto buf_tag) {
+        constexpr bool FULL = decltype(full_tag)::value, BUF = decltype(buf_tag)::value;
         const bool cent = !FULL && CENT && (e & CENT_BIT);
         const unsigned padded = cent ? a.kc_padded : a.padded;
         const unsigned col = min((CENT ? e & TILE_BITS : e) * BN, padded - BN);
         const uint16_t *base = cent ? vcth : vth;
-        if (a.buffered && !cent) {
+        if ((FULL ? BUF : a.buffered) && !cent) {
 #pragma unroll
             for (int t = 0; t < LOADS; t++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -1308,22 +1310,22 @@ void attn_bf16_listed(Args a) {
     if (CENT) mask = uniform64(mask_at(0));
     if constexpr (SPLIT) {
         uint8_t *ks = smem, *vs = smem + K_BYTES;
-        if (total) { load_k(tile, ks, std::false_type{}); load_v(tile, vs, std::false_type{}); }
+        if (total) { load_k(tile, ks, std::false_type{}, std::false_type{}); load_v(tile, vs, std::false_type{}, std::false_type{}); }
         wait_vm_loads();
         __syncthreads();
-        auto step = [&](unsigned it, auto full_tag) {
+        auto step = [&](unsigned it, auto full_tag, auto buf_tag) {
             const bool has_next = it + 1 < total;
             f32x16 s[2];
             if (!CENT || (tile & half_bit)) scores(ks, s);
             wait_vm_loads();               // this tile's V^T (own share)
             __syncthreads();               // K free; every share of V^T landed
-            if (has_next) load_k(next, ks, full_tag);
+            if (has_next) load_k(next, ks, full_tag, buf_tag);
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
             const uint64_t mask_after = mask_at(it + 1);
             if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT ? lane_bits(mask) : 0u, full_tag);
             wait_vm_loads();               // next K, the id after it and the next mask (own share)
             __syncthreads();               // V^T free; every share of the next K landed
-            if (has_next) load_v(next, vs, full_tag);
+            if (has_next) load_v(next, vs, full_tag, buf_tag);
             tile = next;
             next = __builtin_amdgcn_readfirstlane(later);
             if (CENT) mask = uniform64(mask_after);
@@ -1334,11 +1336,17 @@ void attn_bf16_listed(Args a) {
         // their own with no tail code (a compact loop).
         unsigned it0 = 0;
         if constexpr (!CENT) {
-            for (; it0 + 2 < total; it0++) step(it0, std::true_type{});
+            if (a.buffered)
+                for (; it0 + 2 < total; it0++) step(it0, std::true_type{}, std::true_type{});
+            else
+                for (; it0 + 2 < total; it0++) step(it0, std::true_type{}, std::false_type{});
         }
-        for (unsigned it = it0; it < total; it++) step(it, std::false_type{});
+        for (unsigned it = it0; it < total; it++) step(it, std::false_type{}, std::false_type{});
     } else {
-        if (total) { load_k(tile, smem, std::false_type{}); load_v(tile, smem + K_BYTES, std::false_type{}); }
+        if (total) {
+            load_k(tile, smem, std::false_type{}, std::false_type{});
+            load_v(tile, smem + K_BYTES, std::false_type{}, std::false_type{});
+        }
         wait_vm_loads();
         __syncthreads();
         for (unsigned it = 0; it < total; it++) {
@@ -1346,8 +1354,8 @@ void attn_bf16_listed(Args a) {
             uint8_t *ks = smem + cur * STAGE_BYTES;
             if (it + 1 < total) {
                 uint8_t *nk = smem + (cur ^ 1) * STAGE_BYTES;
-                load_k(next, nk, std::false_type{});
-                load_v(next, nk + K_BYTES, std::false_type{});
+                load_k(next, nk, std::false_type{}, std::false_type{});
+                load_v(next, nk + K_BYTES, std::false_type{}, std::false_type{});
             }
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
             const uint64_t mask_after = mask_at(it + 1);
