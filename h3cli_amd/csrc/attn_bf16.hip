@@ -1314,6 +1314,7 @@ void attn_bf16_listed(Args a) {
         wait_vm_loads();
         __syncthreads();
         auto step = [&](unsigned it, auto full_tag, auto buf_tag) {
+            constexpr bool FULL = decltype(full_tag)::value;   // this and the next entry: full exact tiles
             const bool has_next = it + 1 < total;
             f32x16 s[2];
             if (!CENT || (tile & half_bit)) scores(ks, s);
@@ -1321,26 +1322,26 @@ void attn_bf16_listed(Args a) {
             __syncthreads();               // K free; every share of V^T landed
             if (has_next) load_k(next, ks, full_tag, buf_tag);
             const uint32_t later = it + 2 < total ? entry_at(it + 2) : 0u;
-            const uint64_t mask_after = mask_at(it + 1);
-            if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT ? lane_bits(mask) : 0u, full_tag);
+            const uint64_t mask_after = FULL ? 0ull : mask_at(it + 1);
+            if (!CENT || (tile & half_bit)) softmax_pv(s, vs, tile, CENT && !FULL ? lane_bits(mask) : 0u, full_tag);
             wait_vm_loads();               // next K, the id after it and the next mask (own share)
             __syncthreads();               // V^T free; every share of the next K landed
             if (has_next) load_v(next, vs, full_tag, buf_tag);
             tile = next;
             next = __builtin_amdgcn_readfirstlane(later);
-            if (CENT) mask = uniform64(mask_after);
+            if (CENT && !FULL) mask = uniform64(mask_after);
         };
-        // Key tiles only: a list is ascending, so only its last entry can
-        // cross the sequence end, and a step loads the entry after its own.
-        // Steps whose own and next entries are not the last run in a loop of
-        // their own with no tail code (a compact loop).
+        // Exact tiles come first and ascending, so only the last exact entry
+        // can cross the sequence end (centroid entries follow), and a step
+        // loads the entry after its own. Steps whose own and next entries are
+        // exact and not the last exact one run in a loop of their own with no
+        // tail or centroid code (a compact loop).
         unsigned it0 = 0;
-        if constexpr (!CENT) {
-            if (a.buffered)
-                for (; it0 + 2 < total; it0++) step(it0, std::true_type{}, std::true_type{});
-            else
-                for (; it0 + 2 < total; it0++) step(it0, std::true_type{}, std::false_type{});
-        }
+        const unsigned exact = CENT ? count : total;
+        if (a.buffered)
+            for (; it0 + 2 < exact; it0++) step(it0, std::true_type{}, std::true_type{});
+        else
+            for (; it0 + 2 < exact; it0++) step(it0, std::true_type{}, std::false_type{});
         for (unsigned it = it0; it < total; it++) step(it, std::false_type{}, std::false_type{});
     } else {
         if (total) {
