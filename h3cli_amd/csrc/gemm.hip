@@ -295,13 +295,15 @@ void gemm_q8_staged(GemmArgs a) {
     // In the last row tile, lanes whose row is at or past M take BUFFER_OOB
     // and load zeros (those output rows are not stored).
     const bool m_tail = m0 + TM > a.m;
-    auto load_x = [&](unsigned kt, unsigned at) {
+    // TAIL: compiled in only for the last row tile's loop.
+    auto load_x = [&](unsigned kt, unsigned at, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
         uint8_t *xs = lds + (at & 1) * STAGE;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             auto *dst = (__attribute__((address_space(3))) void *)(xs + (wave + 8 * t) * 1024);
             const uint32_t so = (uint32_t)(((size_t)m0 + 64 * t) * a.k * 2 + kt * TK * 2);
-            if (m_tail) {
+            if constexpr (TAIL) {
                 const unsigned row = m0 + 64 * t + 8 * wave + lane / 8;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, row < a.m ? xoff : BUFFER_OOB, so, 0, 0);
             } else {
@@ -353,7 +355,8 @@ void gemm_q8_staged(GemmArgs a) {
     };
 
     // Prologue: X(0), W8(0), W8(1); W(0) dequantized.
-    load_x(0, 0);
+    if (m_tail) load_x(0, 0, std::true_type{});
+    else load_x(0, 0, std::false_type{});
     load_w8(0, 0);
     load_w8(min(1u, ksteps - 1), 1);
     wait_vm_loads();
@@ -361,11 +364,13 @@ void gemm_q8_staged(GemmArgs a) {
     dequant(0);
     __syncthreads();
 
+    // The K loop, instantiated for the last row tile and for the others.
+    auto kloop = [&](auto tail_tag) {
     for (unsigned kt = 0; kt < ksteps; kt++) {
         // Step indices past the end are clamped: those loads and the last
         // dequantization refill stages no later step reads.
         const unsigned k1 = min(kt + 1, ksteps - 1), k2 = min(kt + 2, ksteps - 1);
-        load_x(k1, kt + 1);
+        load_x(k1, kt + 1, tail_tag);
         load_w8(k2, kt + 2);
         const uint8_t *xs = lds + (kt & 1) * STAGE;
         const uint8_t *ws = xs + TILE_BYTES;
@@ -386,6 +391,9 @@ void gemm_q8_staged(GemmArgs a) {
         wait_vm_loads();
         __syncthreads();
     }
+    };
+    if (m_tail) kloop(std::true_type{});
+    else kloop(std::false_type{});
 
 #pragma unroll
     for (int j = 0; j < NBM; j++) {
