@@ -36,9 +36,9 @@ PEAK_HBM = 8000.0       # MI355X HBM3E, GB/s
 # WRITE_SIZE passes over `python3 bench.py --probe`, each scaled by the same
 # counter's reading for a device copy of known size (probe's calibration copy);
 # the summary with the commands and raw readings is
-# profiles/attn_bf16_wide_s32400_h40_traffic.md: fetched 2.0 x 1718464 KiB +
-# written 1.0 x 325302 KiB per launch.
-TRAFFIC = 3.853e9
+# profiles/attn_bf16_wide_s32400_h40_traffic.md: fetched 2.0 x 1744248 KiB +
+# written 1.0 x 437091 KiB per launch.
+TRAFFIC = 4.020e9
 
 
 def attention_flops(seq, heads, dim=DIM, density=1.0):
