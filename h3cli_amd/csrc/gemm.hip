@@ -27,6 +27,7 @@
 #include "internal.h"
 #include <cmath>
 
+
 namespace {
 
 constexpr int TM = 256, TN = 256, TK = 64;
@@ -365,31 +366,38 @@ void gemm_q8_staged(GemmArgs a) {
     __syncthreads();
 
     // The K loop, instantiated for the last row tile and for the others.
+    // Fragments are read one sub-step ahead of their MFMAs; in the last
+    // sub-step the barrier comes first and the next tile's first fragments are
+    // read before this sub-step's MFMAs, so their LDS latency sits under them
+    // (after the last tile those reads land in registers nobody uses). The
+    // sched_barrier keeps hipcc from sinking the reads below the MFMAs.
     auto kloop = [&](auto tail_tag) {
+    bf16x8 wf[2][NBN], xf[2][NBM];
+    frags(lds, lds + TILE_BYTES, 0, wf[0], xf[0]);
     for (unsigned kt = 0; kt < ksteps; kt++) {
-        // Step indices past the end are clamped: those loads and the last
-        // dequantization refill stages no later step reads.
         const unsigned k1 = min(kt + 1, ksteps - 1), k2 = min(kt + 2, ksteps - 1);
         load_x(k1, kt + 1, tail_tag);
         load_w8(k2, kt + 2);
         const uint8_t *xs = lds + (kt & 1) * STAGE;
         const uint8_t *ws = xs + TILE_BYTES;
-        bf16x8 wf[2][NBN], xf[2][NBM];
-        frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ks++) {
-            if (ks + 1 < TK / 16) frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
+            if (ks + 1 < TK / 16) {
+                frags(xs, ws, ks + 1, wf[(ks + 1) & 1], xf[(ks + 1) & 1]);
+            } else {
+                wait_vm_loads();
+                __syncthreads();
+                const uint8_t *nx = lds + ((kt + 1) & 1) * STAGE;
+                frags(nx, nx + TILE_BYTES, 0, wf[0], xf[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < NBN; i++)
 #pragma unroll
                 for (int j = 0; j < NBM; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][i], xf[ks & 1][j], acc[i][j], 0, 0, 0);
-            // Branch-free, so the scheduler can interleave it with the MFMAs;
-            // on the last step it fills a stage no step reads.
             if (ks == 0) dequant(kt + 1);
         }
-        wait_vm_loads();
-        __syncthreads();
     }
     };
     if (m_tail) kloop(std::true_type{});
