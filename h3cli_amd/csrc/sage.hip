@@ -12,7 +12,8 @@
 //    per-row scale, and P is rounded to fp8 e4m3;
 //  * V is fp8 e4m3 with one scale per (head, channel) = max|v| / 448, and P.V
 //    runs on v_mfma_f32_32x32x64_f8f6f4 with fp32 accumulation;
-//  * out = (P.V) * v_scale / sum(P), BF16.
+//  * out = (P.V) * v_scale / sum(P), BF16, with sum(P) over the fp8 P that
+//    enter P.V (a 16x16x128 fp8 MFMA against a lane-selecting ones matrix).
 // The quantizers are deterministic: every integer code and scale is bit-exact
 // against the CPU restatement in oracle/ (which follows the same operation order).
 #include "common.h"
@@ -237,6 +238,13 @@ constexpr int Q8_TILE = BN * D;             // K8 tile bytes: 64 rows x 128 B
 constexpr int V8_TILE = D * BN;             // V8 tile bytes: 128 rows x 64 B
 constexpr int SAGE_TILE = Q8_TILE + V8_TILE;
 constexpr float P_SLACK = 2.0f;             // log2 units the running max may lag (P <= 448)
+// QK^T accumulators start at the bits of the float 1.5 * 2^23: an integer
+// dot product s (|s| <= 128 * 127 * 127 < 2^22) added to them leaves the
+// exponent alone, so the accumulator read as a float is exactly 1.5 * 2^23 + s
+// and needs no int-to-float conversion.
+constexpr int MAGIC_BITS = 0x4B400000;
+constexpr float MAGIC_F = 12582912.0f;
+constexpr int MASKED_BITS = (int)0xFF000000u;   // float -1.7e38: a key past seq
 
 // 16-byte chunk swizzles of the LDS tiles: each 16-lane group of a
 // ds_read_b128 hits 16 distinct 4-bank groups.
@@ -283,11 +291,16 @@ void sage_attn_kernel(SArgs a) {
     f32x16 o[4];
 #pragma unroll
     for (int md = 0; md < 4; md++) o[md] = f32x16{};
-    f32x16 lsum = f32x16{};                 // every element holds the query's running sum of P
+    // Row sums on a 16x16x128 MFMA: lane l's B operand (its P^T fragment)
+    // counts as keys 32 (l / 16) .. + 31 of column l % 16, which is query
+    // l % 32 = 16 ((l / 16) % 2) + l % 16. The ones matrix keeps, for output
+    // rows 4b .. 4b + 3, the key groups g with b + g even, so every lane's
+    // four results hold the full sum of its own query.
+    f32x4 lsum = f32x4{};
     float m = -1e30f;
-    i32x8 ones;                              // fp8 e4m3 1.0 = 0x38
+    i32x8 ones;                              // fp8 e4m3 1.0 = 0x38, or 0 where not kept
 #pragma unroll
-    for (int i = 0; i < 8; i++) ones[i] = 0x38383838;
+    for (int i = 0; i < 8; i++) ones[i] = (((lane % 16) / 4 + lane / 16) & 1) ? 0 : 0x38383838;
 
     // Direct global->LDS tile loads, one contiguous KB per wave instruction.
     // Buffered: a uniform byte offset per load plus one lane offset each for
@@ -337,7 +350,12 @@ void sage_attn_kernel(SArgs a) {
         // rebuilds them with 7 moves per tile); the sparse kernel has no room.
         if constexpr (!SPARSE) asm volatile("" : "+v"(ones));
         i32x16 si[2];
-        si[0] = i32x16{}; si[1] = i32x16{};
+        {
+            i32x16 mg;
+#pragma unroll
+            for (int r = 0; r < 16; r++) mg[r] = MAGIC_BITS;
+            si[0] = mg; si[1] = mg;
+        }
 #pragma unroll
         for (int kstep = 0; kstep < 4; kstep++) {
 #pragma unroll
@@ -355,18 +373,23 @@ void sage_attn_kernel(SArgs a) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     unsigned key = tile * BN + mb * 32 + (r / 4) * 8 + hf * 4 + (r % 4);
-                    if (key >= a.seq) si[mb][r] = INT32_MIN / 2;
+                    if (key >= a.seq) si[mb][r] = MASKED_BITS;
                 }
         }
-        // Integer row max (3-input), then one scale.
+        // Integer row max (3-input; the biased accumulators order as the
+        // scores do), then one scale.
         int mi0 = max(si[0][0], si[0][1]), mi1 = max(si[1][0], si[1][1]);
 #pragma unroll
         for (int r = 2; r < 16; r += 2) {
             mi0 = max(max(mi0, si[0][r]), si[0][r + 1]);
             mi1 = max(max(mi1, si[1][r]), si[1][r + 1]);
         }
-        const float mx = half_max_swap((float)max(mi0, mi1)) * c;
-        if (__builtin_amdgcn_ballot_w64(mx > m + P_SLACK)) {
+        const float mx = (half_max_swap(__builtin_bit_cast(float, max(mi0, mi1))) - MAGIC_F) * c;
+        // The exponent below carries the magnitude 1.5 * 2^23 c + |m| and rounds
+        // by up to 2^-24 of it; P stays <= 448 (fp8 e4m3 encodes 464 and above
+        // as NaN) if the max lags by less than the slack minus twice that.
+        const float lag_max = P_SLACK - fmaf(MAGIC_F, c, fmaf(2.f, fabsf(m), 16.f)) * 0x1p-23f;
+        if (__builtin_amdgcn_ballot_w64(mx > m + lag_max)) {
             const float mnew = fmaxf(m, mx);
             const float alpha = exp2f_fast(m - mnew);
             m = mnew;
@@ -376,7 +399,9 @@ void sage_attn_kernel(SArgs a) {
         }
         // P = 2^(s - m + log2 448 - slack) <= 448, rounded to fp8 e4m3. Masked
         // keys (huge negative score) give exactly 0.
-        const float bias = LOG2_448 - P_SLACK - m;
+        // (1.5 * 2^23 + s) c + bias = s c + log2 448 - slack - m, rounded by at
+        // most 2^-24 |bias| (far below the int8 quantization error of s c).
+        const float bias = fmaf(-MAGIC_F, c, LOG2_448 - P_SLACK - m);
         i32x8 pf;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
@@ -384,7 +409,10 @@ void sage_attn_kernel(SArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int idx = 4 * w + i;
-                p[i] = exp2f_fast(fmaf((float)si[idx / 16][idx % 16], c, bias));
+                // Copied to a scalar first: hipcc's bit cast of a vector
+                // element lvalue reads element 0.
+                const int bits = si[idx / 16][idx % 16];
+                p[i] = exp2f_fast(fmaf(__builtin_bit_cast(float, bits), c, bias));
             }
             // The first pack's other word is overwritten by the second, so
             // its old value may be any dead register (p[0]'s own: no copy).
@@ -400,7 +428,7 @@ void sage_attn_kernel(SArgs a) {
             i32x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             o[md] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[md], 0, 0, 0, 0, 0, 0);
         }
-        lsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, lsum, 0, 0, 0, 0, 0, 0);
+        lsum = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lsum, 0, 0, 0, 0, 0, 0);
     };
 
     // Sparse tile ids are wave-uniform and read one iteration ahead (see the

@@ -94,6 +94,29 @@ def test_attention_tolerance(gpu, seq, heads):
     assert mq["cosine"] >= 0.9995 and mq["max_abs"] <= ATTN_MAX_ABS, mq
 
 
+@pytest.mark.parametrize("gain", [30.0, 60.0])
+def test_large_logit_scale(gpu, gain):
+    """Q and K scaled up so that the per-tile logit scale c = q_scale k_scale
+    scale log2(e) reaches 0.1-0.7. The kernel's exponent then carries the
+    offset 1.5 * 2^23 c of its biased accumulators (up to ~8e6, rounding by up
+    to 0.25 log2 units) and its running max rises early by twice that bound, so
+    P stays within fp8 e4m3 (464 and above encode as NaN). Output finite and
+    within tolerance of attention over the same quantized operands. (The full
+    config-5 step in test_dit_block_gpu.py reaches the boundary case itself.)"""
+    seq, heads = 1000, 2
+    print(f"[sage large logits] gain={gain}", flush=True)
+    q, k, v = sage_inputs(seq, heads, seed=11)
+    q = synth.f32_to_bf16(bf16(q) * gain)
+    k = synth.f32_to_bf16(bf16(k) * gain)
+    scale = scale_bf16(1 / math.sqrt(128))
+    pack = oracle.sage_pack(q, k, v, seq, heads)
+    assert float(pack["q_scale"].max() * pack["k_scale"].max()) * scale * math.log2(math.e) > 0.1
+    out = bf16(sdpa(gpu, q, k, v, seq, heads))
+    assert np.all(np.isfinite(out))
+    mq = metrics(out, oracle.sage_attention(pack, seq, heads, scale))
+    assert mq["cosine"] >= 0.999, mq
+
+
 def test_sage_dispatch_counted_and_nonfinite(gpu):
     lib = gpu.lib
     seq, heads = 128, 2
