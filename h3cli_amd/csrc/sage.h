@@ -12,7 +12,7 @@ void h3_sage_workspace_free(h3_sage_workspace *w);
 // Layout of the packed operands inside a workspace (byte offsets).
 struct h3_sage_layout {
     unsigned seq, heads, padded, blocks, partials;
-    size_t q8, k8, v8, q_scale, k_scale, v_scale, v_recip, k_mean, sums, maxima, total;
+    size_t q8, k8, v8, q_scale, k_scale, v_scale, v_recip, k_mean, sums, maxima, retry, total;
 };
 h3_sage_layout h3_sage_plan(unsigned seq, unsigned heads);
 

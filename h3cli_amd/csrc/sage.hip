@@ -48,6 +48,9 @@ h3_sage_layout h3_sage_plan(unsigned seq, unsigned heads) {
     L.k_mean = take((size_t)heads * D * 2);
     L.sums = take((size_t)heads * L.partials * D * 4);
     L.maxima = take((size_t)heads * L.partials * D * 4);
+    // One byte per (head, 32-query wave), for every launch shape (up to 12
+    // waves per workgroup): the attention kernel's recomputation flags.
+    L.retry = take((size_t)heads * ((seq + 383) / 384) * 12);
     L.total = align256(c) + 256;
     return L;
 }
@@ -232,6 +235,7 @@ struct SArgs {
     unsigned list_stride;
     unsigned *fault;
     int buffered;                           // k8 and v8 below 4 GiB: buffer loads with 32-bit offsets
+    uint8_t *retry;                         // per (head, wave): rows the exact launch recomputes
 };
 
 constexpr int Q8_TILE = BN * D;             // K8 tile bytes: 64 rows x 128 B
@@ -245,6 +249,9 @@ constexpr float P_SLACK = 2.0f;             // log2 units the running max may la
 constexpr int MAGIC_BITS = 0x4B400000;
 constexpr float MAGIC_F = 12582912.0f;
 constexpr int MASKED_BITS = (int)0xFF000000u;   // float -1.7e38: a key past seq
+// Largest logit scale c of the fast exponent (1.5 * 2^23 c <= 2^23): its
+// rounding bound then stays below 0.7 log2 units.
+constexpr float MAGIC_C_MAX = 2.0f / 3.0f;
 
 // 16-byte chunk swizzles of the LDS tiles: each 16-lane group of a
 // ds_read_b128 hits 16 distinct 4-bank groups.
@@ -252,7 +259,10 @@ __device__ inline unsigned k8_chunk(unsigned key, unsigned ch) { return ch ^ ((k
 __device__ inline unsigned v8_chunk(unsigned d, unsigned ch) { return ch ^ ((d >> 2) & 3); }
 
 // WAVES wavefronts of 32 queries; OCC waves per SIMD overlap softmax with MFMA.
-template <int WAVES, int OCC, bool SPARSE>
+// EXACT: the recomputation launch. It runs only workgroups with a flagged
+// wave, computes P's exponent without the biased-accumulator shortcut and
+// writes the flagged waves' rows.
+template <int WAVES, int OCC, bool SPARSE, bool EXACT = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * WAVES, 64 * WAVES), amdgpu_waves_per_eu(OCC, OCC)))
 void sage_attn_kernel(SArgs a) {
     constexpr int BM = 32 * WAVES;
@@ -269,6 +279,16 @@ void sage_attn_kernel(SArgs a) {
     const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
     const unsigned q0 = qb * BM;
     const unsigned ntiles = a.padded / BN;
+    uint8_t *const retry = a.retry + ((size_t)head * nqb + qb) * WAVES;
+    bool redo = true;                      // EXACT: this wave's rows are recomputed
+    if constexpr (EXACT) {
+        bool any = false;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) any |= __builtin_amdgcn_readfirstlane(retry[w]) != 0;
+        if (!any) return;                  // uniform, before any barrier
+        redo = __builtin_amdgcn_readfirstlane(retry[wave]) != 0;
+    }
+    bool failed = false;                   // fast launch: c can exceed MAGIC_C_MAX
     const int8_t *qh = a.q8 + (size_t)head * a.padded * D;
     const int8_t *kh = a.k8 + (size_t)head * a.padded * D;
     const uint8_t *vh = a.v8 + (size_t)head * D * a.padded;
@@ -287,6 +307,15 @@ void sage_attn_kernel(SArgs a) {
     for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const i32x4 *>(qh + (size_t)qrow * D + ks * 32 + hf * 16);
     const unsigned qblk = min((q0 + wave * 32) / 64, a.blocks - 1);
     const float qs = a.q_scale[head * a.blocks + qblk] * a.scale_log2;
+    if constexpr (!EXACT) {
+        // The largest c this wave's tiles can have: qs times the head's
+        // largest key-block scale.
+        float kmax = 0.f;
+        for (unsigned b = lane; b < a.blocks; b += 64) kmax = fmaxf(kmax, a.k_scale[head * a.blocks + b]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, off, 64));
+        failed = __builtin_amdgcn_readfirstlane(qs * kmax > MAGIC_C_MAX ? 1 : 0) != 0;
+    }
 
     f32x16 o[4];
 #pragma unroll
@@ -385,10 +414,14 @@ void sage_attn_kernel(SArgs a) {
             mi1 = max(max(mi1, si[1][r]), si[1][r + 1]);
         }
         const float mx = (half_max_swap(__builtin_bit_cast(float, max(mi0, mi1))) - MAGIC_F) * c;
-        // The exponent below carries the magnitude 1.5 * 2^23 c + |m| and rounds
-        // by up to 2^-24 of it; P stays <= 448 (fp8 e4m3 encodes 464 and above
-        // as NaN) if the max lags by less than the slack minus twice that.
-        const float lag_max = P_SLACK - fmaf(MAGIC_F, c, fmaf(2.f, fabsf(m), 16.f)) * 0x1p-23f;
+        // Fast launch: the exponent below carries the magnitude 1.5 * 2^23 c +
+        // |m| and rounds by up to 2^-24 of it; P stays <= 448 (fp8 e4m3 encodes
+        // 464 and above as NaN) if the max lags by less than the slack minus
+        // twice that. A wave whose c can exceed MAGIC_C_MAX on some tile
+        // (scores spread over 10^5 log2 units and more) was flagged for the
+        // exact launch at the start.
+        float lag_max = P_SLACK;
+        if constexpr (!EXACT) lag_max = P_SLACK - fmaf(MAGIC_F, c, fmaf(2.f, fabsf(m), 16.f)) * 0x1p-23f;
         if (__builtin_amdgcn_ballot_w64(mx > m + lag_max)) {
             const float mnew = fmaxf(m, mx);
             const float alpha = exp2f_fast(m - mnew);
@@ -400,8 +433,9 @@ void sage_attn_kernel(SArgs a) {
         // P = 2^(s - m + log2 448 - slack) <= 448, rounded to fp8 e4m3. Masked
         // keys (huge negative score) give exactly 0.
         // (1.5 * 2^23 + s) c + bias = s c + log2 448 - slack - m, rounded by at
-        // most 2^-24 |bias| (far below the int8 quantization error of s c).
-        const float bias = fmaf(-MAGIC_F, c, LOG2_448 - P_SLACK - m);
+        // most 2^-24 |bias| (far below the int8 quantization error of s c);
+        // exact launch: (F - 1.5 * 2^23) c + log2 448 - slack - m.
+        const float bias = EXACT ? LOG2_448 - P_SLACK - m : fmaf(-MAGIC_F, c, LOG2_448 - P_SLACK - m);
         i32x8 pf;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
@@ -412,7 +446,8 @@ void sage_attn_kernel(SArgs a) {
                 // Copied to a scalar first: hipcc's bit cast of a vector
                 // element lvalue reads element 0.
                 const int bits = si[idx / 16][idx % 16];
-                p[i] = exp2f_fast(fmaf(__builtin_bit_cast(float, bits), c, bias));
+                const float f = __builtin_bit_cast(float, bits);
+                p[i] = exp2f_fast(fmaf(EXACT ? f - MAGIC_F : f, c, bias));
             }
             // The first pack's other word is overwritten by the second, so
             // its old value may be any dead register (p[0]'s own: no copy).
@@ -463,6 +498,12 @@ void sage_attn_kernel(SArgs a) {
     }
     for (unsigned it = it0; it < count; it++) step(it, std::false_type{});
 
+    if constexpr (!EXACT) {
+        if (lane == 0) retry[wave] = failed ? 1 : 0;
+        if (failed) return;                // after the last barrier
+    } else if (!redo) {
+        return;
+    }
     bool bad = false;
     const float *vsc = a.v_scale + head * D;
     const float total = lsum[0];
@@ -488,12 +529,16 @@ void sage_attn_kernel(SArgs a) {
     if (bad) a.fault[0] = 1u;
 }
 
+// The fast launch, then the recomputation launch, whose workgroups return at
+// once unless one of their waves was flagged.
 template <int WAVES, int OCC, bool SPARSE>
 int launch_sage(h3_gpu *g, const SArgs &a, unsigned groups) {
     constexpr size_t shared = 2 * SAGE_TILE;
     hipEvent_t timing = h3_kernel_timing_begin(g);
     hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE>), dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
     h3_kernel_timing_end(g, timing);
+    hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE, true>), dim3(groups), dim3(64 * WAVES), shared,
+                       g->compute, a);
     return h3_launch_status(g, "Sage attention");
 }
 }  // namespace
@@ -519,6 +564,7 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     a.scale_log2 = scale * 1.4426950408889634f;
     a.head_major = head_major ? 1 : 0;
     a.kv_list = kv_list; a.kv_count = kv_count; a.list_stride = list_stride; a.fault = g->fault;
+    a.retry = (uint8_t *)(ws + L.retry);
     // Variant 13: the global-load path that operands of 4 GiB and more take.
     a.buffered = (size_t)heads * L.padded * D < (1ull << 32) && g->attention_variant != 13;
     // 4 waves x 32 queries per workgroup, three workgroups per CU (three

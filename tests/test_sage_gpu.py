@@ -94,13 +94,14 @@ def test_attention_tolerance(gpu, seq, heads):
     assert mq["cosine"] >= 0.9995 and mq["max_abs"] <= ATTN_MAX_ABS, mq
 
 
-@pytest.mark.parametrize("gain", [30.0, 60.0])
+@pytest.mark.parametrize("gain", [30.0, 60.0, 400.0])
 def test_large_logit_scale(gpu, gain):
     """Q and K scaled up so that the per-tile logit scale c = q_scale k_scale
-    scale log2(e) reaches 0.1-0.7. The kernel's exponent then carries the
-    offset 1.5 * 2^23 c of its biased accumulators (up to ~8e6, rounding by up
-    to 0.25 log2 units) and its running max rises early by twice that bound, so
-    P stays within fp8 e4m3 (464 and above encode as NaN). Output finite and
+    scale log2(e) reaches 0.1-0.7 (gain 30, 60) or ~30 (gain 400). The
+    kernel's exponent then carries the offset 1.5 * 2^23 c of its biased
+    accumulators, rounding by up to 0.75 c log2 units; its running max rises
+    early by twice that bound, and past the slack P are lowered by the excess,
+    so P stays within fp8 e4m3 (464 and above encode as NaN). Output finite and
     within tolerance of attention over the same quantized operands. (The full
     config-5 step in test_dit_block_gpu.py reaches the boundary case itself.)"""
     seq, heads = 1000, 2
@@ -114,7 +115,9 @@ def test_large_logit_scale(gpu, gain):
     out = bf16(sdpa(gpu, q, k, v, seq, heads))
     assert np.all(np.isfinite(out))
     mq = metrics(out, oracle.sage_attention(pack, seq, heads, scale))
-    assert mq["cosine"] >= 0.999, mq
+    # At gain 400 (c up to ~30) the softmax is an argmax over int8 scores, and
+    # ties between near-equal quantized scores decide rows either way.
+    assert mq["cosine"] >= (0.999 if gain < 100 else 0.99), mq
 
 
 def test_sage_dispatch_counted_and_nonfinite(gpu):
