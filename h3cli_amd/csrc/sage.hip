@@ -48,9 +48,10 @@ h3_sage_layout h3_sage_plan(unsigned seq, unsigned heads) {
     L.k_mean = take((size_t)heads * D * 2);
     L.sums = take((size_t)heads * L.partials * D * 4);
     L.maxima = take((size_t)heads * L.partials * D * 4);
-    // One byte per (head, 32-query wave), for every launch shape (up to 12
-    // waves per workgroup): the attention kernel's recomputation flags.
-    L.retry = take((size_t)heads * ((seq + 383) / 384) * 12);
+    // One byte per (head, 32-query wave) of the attention launch, whatever its
+    // workgroup shape: W waves per workgroup pad a head to
+    // ceil(seq / 32W) W <= ceil(seq / 32) + W - 1 waves, W <= 12.
+    L.retry = take((size_t)heads * ((seq + 31) / 32 + 11));
     L.total = align256(c) + 256;
     return L;
 }
