@@ -149,3 +149,27 @@ def test_global_load_path_matches_buffer_path(gpu, monkeypatch, seq, heads):
         assert np.array_equal(sdpa(g13, q, k, v, seq, heads), buffered)
     finally:
         g13.close()
+
+
+@pytest.mark.parametrize("variant", ["1", "2"])
+def test_launch_shapes_match(gpu, monkeypatch, variant):
+    """Attention variants 1 and 2 launch the Sage kernel as 8 and 12 waves per
+    workgroup instead of 4. Every 32-query wave walks the same tiles with the
+    same arithmetic, so the outputs are bit-identical, also on an input whose
+    logit scale sends every wave through the exact recomputation launch
+    (S = 300, where the retry bytes of the three shapes are laid out
+    differently)."""
+    seq, heads = 300, 3
+    q, k, v = sage_inputs(seq, heads, seed=23)
+    qb = synth.f32_to_bf16(bf16(q) * 400.0)
+    kb = synth.f32_to_bf16(bf16(k) * 400.0)
+    ref = [sdpa(gpu, q, k, v, seq, heads), sdpa(gpu, qb, kb, v, seq, heads)]
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", variant)
+    gv = Gpu()
+    try:
+        gv.check(gv.lib.h3_gpu_dit_attention_configure(gv.handle, 1), "configure sage2++")
+        print(f"[sage shapes] variant={variant}", flush=True)
+        assert np.array_equal(sdpa(gv, q, k, v, seq, heads), ref[0])
+        assert np.array_equal(sdpa(gv, qb, kb, v, seq, heads), ref[1])
+    finally:
+        gv.close()
