@@ -68,6 +68,30 @@ def test_masked_sage():
         g.close()
 
 
+def test_masked_sage_large_logit_scale():
+    """Block-sparse Sage with Q and K at 400x (logit scale c ~ 30): every wave
+    of the fast launch is flagged and the exact launch recomputes its rows
+    over the same tile lists. Finite and within tolerance of the masked
+    quantized-operand oracle."""
+    seq, video, heads = 1500, 1200, 2
+    print(f"[sparse sage large logits] seq={seq}", flush=True)
+    g = make_gpu(1)
+    try:
+        mask = oracle.block_mask(seq, video, 128, 0.25, seed=3)
+        bind_mask(g, mask)
+        q, k, v = sage_inputs(seq, heads, seed=13)
+        q = synth.f32_to_bf16(bf16(q) * 400.0)
+        k = synth.f32_to_bf16(bf16(k) * 400.0)
+        out = bf16(sdpa(g, q, k, v, seq, heads))
+        assert np.all(np.isfinite(out))
+        scale = scale_bf16(1 / math.sqrt(128))
+        pack = oracle.sage_pack(q, k, v, seq, heads)
+        mq = metrics(out, oracle.sage_attention(pack, seq, heads, scale, mask=mask, block=128))
+        assert mq["cosine"] >= 0.99, mq
+    finally:
+        g.close()
+
+
 def test_masked_sage_global_load_path(monkeypatch):
     """The block-sparse Sage kernel's buffer-load path and its global-load path
     (attention variant 13, what operands of 4 GiB and more take) agree bit for
