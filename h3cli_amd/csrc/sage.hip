@@ -386,6 +386,11 @@ void sage_attn_kernel(SArgs a) {
             for (int r = 0; r < 16; r++) mg[r] = MAGIC_BITS;
             si[0] = mg; si[1] = mg;
         }
+        // The QK^T MFMAs issue at raised wave priority: with three waves per
+        // SIMD in independent workgroups, the one starting its scores gets
+        // them into the matrix pipe ahead of the others' softmax VALU work
+        // (1.3% faster; the same around P.V, or in the BF16 kernel, is not).
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kstep = 0; kstep < 4; kstep++) {
 #pragma unroll
@@ -395,6 +400,7 @@ void sage_attn_kernel(SArgs a) {
                 si[mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kstep], si[mb], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         const float c = qs * a.k_scale[head * a.blocks + min(tile, a.blocks - 1)];
         const bool masked = !FULL && tile * BN + BN > a.seq;
         if (masked) {
