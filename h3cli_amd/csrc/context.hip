@@ -11,6 +11,10 @@
 #include <new>
 #include <unistd.h>
 #include <chrono>
+#include <condition_variable>
+#include <memory>
+#include <mutex>
+#include <thread>
 
 #ifndef H3HIP_VERSION
 #define H3HIP_VERSION "0.1"
@@ -339,41 +343,59 @@ extern "C" int h3_hip_event_elapsed_ms(h3_gpu *g, h3_gpu_event *a, h3_gpu_event 
 }
 
 // ------------------------------------------------------------------ weight streaming
-// Two pinned bounce buffers feed asynchronous H2D copies on the copy stream
-// (reference src/cuda/gpu_cuda.cu:761-840). Each destination tensor carries a
+// File → device fills (the reference's h3_gpu_tensor_read/stream_file_bf16,
+// src/gpu.h:225-236; behaviour of src/cuda/gpu_cuda.cu:761-840) go through a
+// ring of pinned staging slots. A reader thread pulls the file into the slots
+// while the calling thread queues each filled slot's H2D copy on the copy
+// stream and records that slot's "drained" event behind it; the reader waits on
+// that event before it reuses the slot. Each destination tensor also carries a
 // "ready" event (recorded on the copy stream after its last chunk; kernels that
 // read the tensor wait on it) and a "released" event (recorded on the compute
 // stream after the last kernel that read it; the next fill waits on it).
+namespace {
+constexpr unsigned kStagingSlots = 4;
+constexpr size_t kStagingSlotBytes = 8u << 20;
+
+struct StagingSlot {
+    void *host = nullptr;
+    hipEvent_t drained = nullptr;
+    bool armed = false;  // drained has been recorded at least once
+};
+}  // namespace
+
 struct h3_stream_state {
-    void *bounce[2] = {nullptr, nullptr};
-    hipEvent_t bounce_free[2] = {nullptr, nullptr};
-    bool bounce_used[2] = {false, false};
-    size_t bounce_bytes = 16u << 20;
+    StagingSlot slots[kStagingSlots];
 };
 
 void h3_streaming_destroy(h3_gpu *g) {
-    auto *s = g->streaming;
-    if (!s) return;
-    for (int i = 0; i < 2; i++) {
-        if (s->bounce_free[i]) hipEventDestroy(s->bounce_free[i]);
-        if (s->bounce[i]) hipHostFree(s->bounce[i]);
+    h3_stream_state *ring = g->streaming;
+    if (!ring) return;
+    for (StagingSlot &s : ring->slots) {
+        if (s.armed) hipEventSynchronize(s.drained);
+        if (s.drained) hipEventDestroy(s.drained);
+        if (s.host) hipHostFree(s.host);
     }
-    delete s; g->streaming = nullptr;
+    delete ring;
+    g->streaming = nullptr;
 }
 
-static int streaming_init(h3_gpu *g) {
-    if (g->streaming) return 1;
-    auto *s = new (std::nothrow) h3_stream_state();
-    if (!s) return h3_set_error(g, "streaming: out of host memory");
-    g->streaming = s;
-    for (int i = 0; i < 2; i++) {
-        if (!h3_hip_check(g, hipHostMalloc(&s->bounce[i], s->bounce_bytes, hipHostMallocDefault), "pinned bounce buffer") ||
-            !h3_hip_check(g, hipEventCreateWithFlags(&s->bounce_free[i], hipEventDisableTiming), "bounce event"))
-            return 0;
+static h3_stream_state *staging_ring(h3_gpu *g) {
+    if (g->streaming) return g->streaming;
+    std::unique_ptr<h3_stream_state> ring(new (std::nothrow) h3_stream_state());
+    if (!ring) { h3_set_error(g, "streaming: out of host memory"); return nullptr; }
+    for (StagingSlot &s : ring->slots) {
+        bool ok = h3_hip_check(g, hipHostMalloc(&s.host, kStagingSlotBytes, hipHostMallocDefault), "pinned staging slot") &&
+                  h3_hip_check(g, hipEventCreateWithFlags(&s.drained, hipEventDisableTiming), "staging slot event");
+        if (!ok) {
+            g->streaming = ring.release();
+            h3_streaming_destroy(g);
+            return nullptr;
+        }
     }
-    g->stats.pinned_bytes += 2 * s->bounce_bytes;
+    g->stats.pinned_bytes += kStagingSlots * kStagingSlotBytes;
     g->stats.peak_pinned_bytes = std::max(g->stats.peak_pinned_bytes, g->stats.pinned_bytes);
-    return 1;
+    g->streaming = ring.release();
+    return g->streaming;
 }
 
 int h3_tensor_events(h3_gpu *g, h3_gpu_tensor *t) {
@@ -412,41 +434,144 @@ static int fill_end(h3_gpu *g, h3_gpu_tensor *t) {
     return 1;
 }
 
+namespace {
+// One file range → device tensor transfer. Chunk c of the range lands in slot
+// c % kStagingSlots. The reader thread owns the file and the slots' contents;
+// the calling thread owns every HIP call that queues work. They meet on two
+// counters under one mutex: `staged` (chunks read) and `queued` (chunks whose
+// copy and drained event are on the copy stream).
+class FileFill {
+public:
+    FileFill(h3_gpu *g, h3_stream_state *ring, int fd, uint64_t offset, size_t bytes)
+        : g_(g), ring_(ring), fd_(fd), offset_(offset), bytes_(bytes),
+          chunks_((bytes + kStagingSlotBytes - 1) / kStagingSlotBytes) {}
+
+    // Runs the transfer into dst; returns 1, or 0 with g->error set.
+    int run(char *dst, const char *path) {
+        if (!chunks_) return 1;
+        std::thread reader([this] { read_all(); });
+        int ok = 1;
+        for (size_t c = 0; c < chunks_ && ok; c++) {
+            std::unique_lock<std::mutex> lock(mutex_);
+            changed_.wait(lock, [&] { return staged_ > c || read_failed_; });
+            if (staged_ <= c) {  // the reader stopped at chunk c
+                ok = read_failed_hip_
+                         ? h3_set_error(g_, "%s", hip_error_)
+                         : h3_set_error(g_, "read weight %s at %llu: %s", path, (unsigned long long)failed_at_,
+                                        read_errno_ ? strerror(read_errno_) : "unexpected EOF");
+                break;
+            }
+            lock.unlock();
+            StagingSlot &s = ring_->slots[c % kStagingSlots];
+            const size_t at = c * kStagingSlotBytes, n = std::min(kStagingSlotBytes, bytes_ - at);
+            ok = h3_hip_check(g_, hipMemcpyAsync(dst + at, s.host, n, hipMemcpyHostToDevice, g_->copy), "weight H2D") &&
+                 h3_hip_check(g_, hipEventRecord(s.drained, g_->copy), "staging slot release");
+            lock.lock();
+            if (ok) { s.armed = true; queued_ = c + 1; }
+            else stop_ = true;
+            changed_.notify_all();
+        }
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            stop_ = true;
+            changed_.notify_all();
+        }
+        reader.join();
+        return ok;
+    }
+
+private:
+    void read_all() {
+        for (size_t c = 0; c < chunks_; c++) {
+            StagingSlot &s = ring_->slots[c % kStagingSlots];
+            {
+                // The slot's previous chunk of this transfer must be queued
+                // before its drained event says anything about it.
+                std::unique_lock<std::mutex> lock(mutex_);
+                changed_.wait(lock, [&] { return stop_ || c < kStagingSlots || queued_ + kStagingSlots > c; });
+                if (stop_) return;
+            }
+            if (s.armed) {
+                if (hipEventQuery(s.drained) == hipErrorNotReady) stalls_++;
+                hipError_t e = hipEventSynchronize(s.drained);
+                if (e != hipSuccess) { fail(0, e, 0); return; }
+            }
+            const size_t at = c * kStagingSlotBytes, n = std::min(kStagingSlotBytes, bytes_ - at);
+            size_t got = 0;
+            while (got < n) {
+                const ssize_t r = pread(fd_, (char *)s.host + got, n - got, (off_t)(offset_ + at + got));
+                if (r > 0) { got += (size_t)r; continue; }
+                if (r < 0 && errno == EINTR) continue;
+                fail(r < 0 ? errno : 0, hipSuccess, offset_ + at + got);
+                return;
+            }
+            std::lock_guard<std::mutex> lock(mutex_);
+            staged_ = c + 1;
+            changed_.notify_all();
+        }
+    }
+
+    void fail(int err, hipError_t e, uint64_t where) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        read_failed_ = true;
+        read_errno_ = err;
+        failed_at_ = where;
+        if (e != hipSuccess) {
+            read_failed_hip_ = true;
+            snprintf(hip_error_, sizeof(hip_error_), "staging slot reuse: %s", hipGetErrorString(e));
+        }
+        changed_.notify_all();
+    }
+
+public:
+    uint64_t stalls_ = 0;
+
+private:
+    h3_gpu *g_;
+    h3_stream_state *ring_;
+    int fd_;
+    uint64_t offset_;
+    size_t bytes_, chunks_;
+    std::mutex mutex_;
+    std::condition_variable changed_;
+    size_t staged_ = 0, queued_ = 0;
+    bool stop_ = false, read_failed_ = false, read_failed_hip_ = false;
+    int read_errno_ = 0;
+    uint64_t failed_at_ = 0;
+    char hip_error_[160] = {};
+};
+}  // namespace
+
+// Fills the first n elements of t from path at offset. On failure the message
+// is left in g->error and copied to error[error_size] when that is another buffer.
 static int file_into(h3_gpu_tensor *t, const char *path, uint64_t offset, size_t n, h3_gpu_dtype dtype,
                      bool streaming, char *error, size_t error_size) {
     if (!t || !path || t->dtype != dtype || t->q8 || n > t->elements) return 0;
     h3_gpu *g = t->owner;
-    int ok = 1;
-    int fd = open(path, O_RDONLY | O_CLOEXEC);
-    if (fd < 0) { if (error && error_size) snprintf(error, error_size, "%s: %s", path, strerror(errno)); return 0; }
-    std::lock_guard<std::mutex> lock(g->copy_mutex);
-    double started = now_seconds();
-    size_t bytes = n * item_size(dtype);
-    ok = streaming_init(g) && fill_begin(g, t);
-    auto *s = g->streaming;
-    unsigned slot = 0;
-    for (size_t done = 0; ok && done < bytes;) {
-        if (s->bounce_used[slot]) {
-            if (hipEventQuery(s->bounce_free[slot]) == hipErrorNotReady) g->stats.stream_stalls++;
-            if (!h3_hip_check(g, hipEventSynchronize(s->bounce_free[slot]), "bounce buffer reuse")) { ok = 0; break; }
-        }
-        size_t want = std::min(s->bounce_bytes, bytes - done), got = 0;
-        while (got < want) {
-            ssize_t r = pread(fd, (char *)s->bounce[slot] + got, want - got, (off_t)(offset + done + got));
-            if (r < 0 && errno == EINTR) continue;
-            if (r <= 0) { ok = h3_set_error(g, "read weight %s: %s", path, r ? strerror(errno) : "unexpected EOF"); break; }
-            got += (size_t)r;
-        }
-        if (ok)
-            ok = h3_hip_check(g, hipMemcpyAsync((char *)t->data + done, s->bounce[slot], want, hipMemcpyHostToDevice, g->copy), "weight H2D") &&
-                 h3_hip_check(g, hipEventRecord(s->bounce_free[slot], g->copy), "bounce release");
-        s->bounce_used[slot] = true; slot ^= 1; done += want;
+    const size_t bytes = n * item_size(dtype);
+    if (offset > (uint64_t)INT64_MAX - bytes) return h3_set_error(g, "read weight %s: range overflows", path);
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        if (error && error_size) snprintf(error, error_size, "%s: %s", path, strerror(errno));
+        return 0;
     }
-    if (ok) ok = fill_end(g, t);
+    const double started = now_seconds();
+    int ok;
+    {
+        std::lock_guard<std::mutex> lock(g->copy_mutex);
+        h3_stream_state *ring = staging_ring(g);
+        ok = ring && fill_begin(g, t);
+        if (ok) {
+            FileFill fill(g, ring, fd, offset, bytes);
+            ok = fill.run((char *)t->data, path);
+            g->stats.stream_stalls += fill.stalls_;
+        }
+        if (ok) ok = fill_end(g, t);
+        g->stats.h2d_bytes += bytes;
+        if (streaming) g->stats.streamed_bytes += bytes;
+        g->stats.transfer_seconds += now_seconds() - started;
+    }
     close(fd);
-    g->stats.h2d_bytes += bytes;
-    if (streaming) g->stats.streamed_bytes += bytes;
-    g->stats.transfer_seconds += now_seconds() - started;
     if (!ok && error && error_size && error != g->error) snprintf(error, error_size, "%s", g->error);
     return ok;
 }
@@ -486,9 +611,12 @@ static int copy_tensor(h3_gpu *g, h3_gpu_tensor *d, size_t dst, const h3_gpu_ten
     if (!n) return 1;
     size_t z = item_size(dtype);
     g->stats.d2d_bytes += n * z;
-    return h3_hip_check(g, hipMemcpyAsync((char *)d->data + dst * z, (const char *)s->data + src * z, n * z,
+    // Either side may be a streamed slot: wait for its fill, and make the
+    // next fill of it wait for this copy.
+    return h3_tensor_acquire(g, s) && h3_tensor_acquire(g, d) &&
+           h3_hip_check(g, hipMemcpyAsync((char *)d->data + dst * z, (const char *)s->data + src * z, n * z,
                                           hipMemcpyDeviceToDevice, g->compute), "tensor D2D") &&
-           h3_launch_status(g, "tensor D2D");
+           h3_launch_status(g, "tensor D2D") && h3_tensor_release(g, s) && h3_tensor_release(g, d);
 }
 extern "C" int h3_gpu_copy_bf16(h3_gpu *g, h3_gpu_tensor *d, size_t dst, const h3_gpu_tensor *s, size_t src, size_t n) {
     return copy_tensor(g, d, dst, s, src, n, H3_GPU_BF16);

@@ -7,9 +7,12 @@
 // Both entries run the dense BF16 kernel of h3_gpu_sdpa_bf16 (sequence-major
 // Q/K/V [seq, heads, 128], non-causal) and also write lse [batch, heads,
 // query rows] = log sum_j exp(scale q.k_j) in FP32, FlashAttention's layout.
-// The kernel needs a workspace (V transposed, retry bytes); it is taken from
-// the stream-ordered allocator (hipMallocAsync / hipFreeAsync on the caller's
-// stream), whose pool hands the same memory back to later calls.
+// The kernel needs a workspace (V transposed, retry bytes). Each device keeps
+// one, grown only when a call needs more (the only allocation, after the last
+// use of the old buffer has finished), and reused by every later call: a call
+// first makes its stream wait for the previous call's last use of the buffer
+// and records its own after its launches, so calls on different streams take
+// the workspace in turn instead of racing on it.
 //
 // Taken: BF16, head dimension 128, heads == kv_heads, non-causal. The
 // reference's other cases (causal text attention, the head-dimension-72
@@ -19,6 +22,7 @@
 #include "internal.h"
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 
 namespace {
 
@@ -27,26 +31,59 @@ int refuse(char *error, size_t size, const char *what) {
     return 0;
 }
 
-// One call: workspace from the stream's pool, the launches, workspace back.
+constexpr int MAX_DEVICES = 16;
+
+// A device's reusable workspace and the event recorded after its last use.
+struct DeviceWorkspace {
+    std::mutex lock;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t last_use = nullptr;
+};
+DeviceWorkspace workspaces[MAX_DEVICES];
+
+int fail(char *error, size_t size, const char *what, hipError_t e) {
+    if (error && size) snprintf(error, size, "%s: %s", what, hipGetErrorString(e));
+    return -1;
+}
+
+// One call on the device's workspace, under its lock: wait for the last use,
+// grow if needed, launch, record this use.
 int run(void *out, const void *q, const void *k, const void *v, float *lse, unsigned seq, unsigned qrows,
         unsigned heads, float scale, bool head_major, hipStream_t stream, char *error, size_t size) {
     h3_gpu g{};
-    hipGetDevice(&g.device);
+    hipError_t e = hipGetDevice(&g.device);
+    if (e != hipSuccess) return fail(error, size, "FlashAttention device", e);
+    if (g.device < 0 || g.device >= MAX_DEVICES) return refuse(error, size, "FlashAttention: device ordinal out of range");
     g.compute = stream;
-    const size_t bytes = h3_attention_bf16_workspace(seq, heads);
-    void *ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, bytes + 256, stream);
-    if (e != hipSuccess) {
-        if (error && size) snprintf(error, size, "FlashAttention workspace: %s", hipGetErrorString(e));
-        return -1;
+    DeviceWorkspace &w = workspaces[g.device];
+    std::lock_guard<std::mutex> guard(w.lock);
+    if (!w.last_use && (e = hipEventCreateWithFlags(&w.last_use, hipEventDisableTiming)) != hipSuccess) {
+        w.last_use = nullptr;
+        return fail(error, size, "FlashAttention workspace event", e);
     }
-    // The kernels' non-finite flag goes to the last bytes of the workspace:
+    // The kernels' non-finite flag goes to the 256 bytes after the workspace:
     // this interface reports no deferred faults, as the reference's does not.
-    g.fault = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(ws) + bytes);
-    const int ok = h3_launch_attention_flash(&g, ws, static_cast<uint16_t *>(out), static_cast<const uint16_t *>(q),
+    const size_t bytes = h3_attention_bf16_workspace(seq, heads) + 256;
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            if ((e = hipEventSynchronize(w.last_use)) != hipSuccess) return fail(error, size, "FlashAttention workspace", e);
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        if ((e = hipMalloc(&w.ptr, bytes)) != hipSuccess) {
+            w.ptr = nullptr;
+            return fail(error, size, "FlashAttention workspace", e);
+        }
+        w.bytes = bytes;
+    }
+    if ((e = hipStreamWaitEvent(stream, w.last_use, 0)) != hipSuccess) return fail(error, size, "FlashAttention workspace", e);
+    g.fault = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(w.ptr) + bytes - 256);
+    const int ok = h3_launch_attention_flash(&g, w.ptr, static_cast<uint16_t *>(out), static_cast<const uint16_t *>(q),
                                              static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), lse,
                                              seq, qrows, heads, scale, head_major);
-    hipFreeAsync(ws, stream);
+    if ((e = hipEventRecord(w.last_use, stream)) != hipSuccess) return fail(error, size, "FlashAttention workspace", e);
     if (!ok) {
         if (error && size) snprintf(error, size, "FlashAttention launch: %s", g.error);
         return -1;

@@ -28,6 +28,8 @@
 #include "../../include/h3_gpu_surface.h"
 #include "../host/sha256.h"
 #include <algorithm>
+#include <atomic>
+#include <memory>
 #include <cerrno>
 #include <cmath>
 #include <cstdio>
@@ -383,13 +385,6 @@ int launch_gemm(h3_gpu *g, const Fp8Args &a) {
 }
 
 // ---------------------------------------------------------------- host helpers
-std::string hex32(const unsigned char d[32]) {
-    static const char digits[] = "0123456789abcdef";
-    std::string s(64, '0');
-    for (int i = 0; i < 32; i++) { s[2 * i] = digits[d[i] >> 4]; s[2 * i + 1] = digits[d[i] & 15]; }
-    return s;
-}
-
 void sha256_of(const void *data, size_t bytes, unsigned char out[32]) {
     h3hip_sha256 s;
     h3hip_sha256_init(&s);
@@ -397,58 +392,238 @@ void sha256_of(const void *data, size_t bytes, unsigned char out[32]) {
     h3hip_sha256_final(&s, out);
 }
 
-void put_le(unsigned char *p, uint64_t v, unsigned n) { for (unsigned i = 0; i < n; i++) p[i] = (unsigned char)(v >> (8 * i)); }
-uint64_t get_le(const unsigned char *p, unsigned n) {
-    uint64_t v = 0;
-    for (unsigned i = 0; i < n; i++) v |= (uint64_t)p[i] << (8 * i);
-    return v;
-}
+// Little-endian field cursors over a fixed header image.
+class HeaderWriter {
+public:
+    explicit HeaderWriter(unsigned char *p) : p_(p) {}
+    HeaderWriter &raw(const void *v, size_t n) { memcpy(p_ + at_, v, n); at_ += n; return *this; }
+    HeaderWriter &u32(uint32_t v) { return le(v, 4); }
+    HeaderWriter &u64(uint64_t v) { return le(v, 8); }
+private:
+    HeaderWriter &le(uint64_t v, unsigned n) {
+        for (unsigned b = 0; b < n; b++) p_[at_ + b] = (unsigned char)(v >> (8 * b));
+        at_ += n;
+        return *this;
+    }
+    unsigned char *p_;
+    size_t at_ = 0;
+};
+class HeaderReader {
+public:
+    explicit HeaderReader(const unsigned char *p) : p_(p) {}
+    HeaderReader &raw(void *v, size_t n) { memcpy(v, p_ + at_, n); at_ += n; return *this; }
+    HeaderReader &u32(uint32_t &v) { v = (uint32_t)le(4); return *this; }
+    HeaderReader &u64(uint64_t &v) { v = le(8); return *this; }
+private:
+    uint64_t le(unsigned n) {
+        uint64_t v = 0;
+        for (unsigned b = n; b-- > 0;) v = v << 8 | p_[at_ + b];
+        at_ += n;
+        return v;
+    }
+    const unsigned char *p_;
+    size_t at_ = 0;
+};
 
-bool file_io(int fd, void *data, size_t bytes, bool writing) {
-    auto *p = (unsigned char *)data;
-    while (bytes) {
-        ssize_t n = writing ? ::write(fd, p, bytes) : ::read(fd, p, bytes);
-        if (n < 0 && errno == EINTR) continue;
-        if (n <= 0) return false;
-        p += n; bytes -= (size_t)n;
+// The H3QWT001 artifact header (the reference's strict format,
+// cuda_quant.cuh:169-248): 128 bytes, "H3QWT001", recipe u32, mode u32, n u32,
+// k u32, payload bytes u64, scale offset u64, global offset u64, SHA-256 of the
+// BF16 source, SHA-256 of the payload, 16 zero bytes.
+struct ArtifactHeader {
+    static constexpr size_t kSize = 128;
+    static constexpr char kMagic[9] = "H3QWT001";
+    uint32_t recipe = 0, mode = 0, n = 0, k = 0;
+    uint64_t bytes = 0, scale = 0, global = 0;
+    unsigned char source_sha[32] = {}, payload_sha[32] = {};
+
+    void encode(unsigned char out[kSize]) const {
+        memset(out, 0, kSize);
+        HeaderWriter(out).raw(kMagic, 8).u32(recipe).u32(mode).u32(n).u32(k).u64(bytes).u64(scale).u64(global)
+            .raw(source_sha, 32).raw(payload_sha, 32);
+    }
+    // False when the magic or the reserved tail is wrong.
+    bool decode(const unsigned char in[kSize]) {
+        char magic[8];
+        HeaderReader(in).raw(magic, 8).u32(recipe).u32(mode).u32(n).u32(k).u64(bytes).u64(scale).u64(global)
+            .raw(source_sha, 32).raw(payload_sha, 32);
+        static const unsigned char zero[16] = {};
+        return memcmp(magic, kMagic, 8) == 0 && memcmp(in + 112, zero, 16) == 0;
+    }
+    // Same weight, same packing: every field but the payload digest.
+    bool describes_same(const ArtifactHeader &o) const {
+        return recipe == o.recipe && mode == o.mode && n == o.n && k == o.k && bytes == o.bytes &&
+               scale == o.scale && global == o.global && memcmp(source_sha, o.source_sha, 32) == 0;
+    }
+};
+constexpr char ArtifactHeader::kMagic[9];
+
+// What identifies a source file's contents without reading them: a file whose
+// identity differs from an earlier one may have changed since.
+struct FileIdentity {
+    dev_t dev = 0;
+    ino_t ino = 0;
+    off_t size = 0;
+    struct timespec mtime = {}, ctime = {};
+
+    static FileIdentity of(const struct stat &st) {
+        FileIdentity id;
+        id.dev = st.st_dev; id.ino = st.st_ino; id.size = st.st_size;
+        id.mtime = st.st_mtim; id.ctime = st.st_ctim;
+        return id;
+    }
+    bool still_matches(const char *path) const {
+        struct stat st;
+        if (stat(path, &st) != 0) return false;
+        const FileIdentity now = of(st);
+        auto same = [](const timespec &a, const timespec &b) { return a.tv_sec == b.tv_sec && a.tv_nsec == b.tv_nsec; };
+        return now.dev == dev && now.ino == ino && now.size == size && same(now.mtime, mtime) && same(now.ctime, ctime);
+    }
+};
+
+// A read-only mapping of the n x k BF16 source of one packed weight, with the
+// identity the file had when it was opened.
+class SourceWeight {
+public:
+    ~SourceWeight() { if (base_ != MAP_FAILED) munmap(base_, length_); }
+
+    bool open(h3_gpu *g, const char *path, uint64_t offset, size_t bytes) {
+        const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+        struct stat st;
+        const bool in_range = fd >= 0 && fstat(fd, &st) == 0 && offset <= (uint64_t)st.st_size &&
+                              bytes <= (uint64_t)st.st_size - offset;
+        if (!in_range) {
+            if (fd >= 0) close(fd);
+            return h3_set_error(g, "invalid quantized source range: %s", path);
+        }
+        identity_ = FileIdentity::of(st);
+        const size_t page = (size_t)sysconf(_SC_PAGESIZE);
+        skip_ = (size_t)(offset % page);
+        length_ = bytes + skip_;
+        base_ = mmap(nullptr, length_, PROT_READ, MAP_PRIVATE, fd, (off_t)(offset - skip_));
+        const int map_errno = errno;
+        close(fd);
+        if (base_ == MAP_FAILED) return h3_set_error(g, "cannot map quantized source: %s", strerror(map_errno));
+        bytes_ = bytes;
+        return true;
+    }
+    const uint16_t *values() const { return (const uint16_t *)((const char *)base_ + skip_); }
+    void digest(unsigned char out[32]) const { sha256_of(values(), bytes_, out); }
+    const FileIdentity &identity() const { return identity_; }
+
+private:
+    void *base_ = MAP_FAILED;
+    size_t length_ = 0, skip_ = 0, bytes_ = 0;
+    FileIdentity identity_;
+};
+
+// An exclusive advisory lock on <artifact>.lock, held for one lookup/publish.
+class ArtifactLock {
+public:
+    ~ArtifactLock() { if (fd_ >= 0) { flock(fd_, LOCK_UN); close(fd_); } }
+    bool take(const std::string &artifact) {
+        fd_ = ::open((artifact + ".lock").c_str(), O_CREAT | O_RDWR | O_CLOEXEC, 0600);
+        if (fd_ < 0) return false;
+        if (flock(fd_, LOCK_EX) == 0) return true;
+        const int e = errno;
+        close(fd_);
+        fd_ = -1;
+        errno = e;
+        return false;
+    }
+private:
+    int fd_ = -1;
+};
+
+// All of [p, p + n) read from, or written to, fd.
+bool read_all(int fd, void *p, size_t n) {
+    for (auto *c = (unsigned char *)p; n;) {
+        const ssize_t r = read(fd, c, n);
+        if (r > 0) { c += r; n -= (size_t)r; }
+        else if (r == 0 || errno != EINTR) return false;
+    }
+    return true;
+}
+bool write_all(int fd, const void *p, size_t n) {
+    for (auto *c = (const unsigned char *)p; n;) {
+        const ssize_t r = write(fd, c, n);
+        if (r > 0) { c += r; n -= (size_t)r; }
+        else if (r == 0 || errno != EINTR) return false;
     }
     return true;
 }
 
-bool same_source(const char *path, const struct stat &before) {
-    struct stat now;
-    return stat(path, &now) == 0 && before.st_dev == now.st_dev && before.st_ino == now.st_ino &&
-           before.st_size == now.st_size && before.st_mtim.tv_sec == now.st_mtim.tv_sec &&
-           before.st_mtim.tv_nsec == now.st_mtim.tv_nsec && before.st_ctim.tv_sec == now.st_ctim.tv_sec &&
-           before.st_ctim.tv_nsec == now.st_ctim.tv_nsec;
-}
+// The artifact directory: <cache>/v<recipe>-<mode>-<n>x<k>-<sha256(source) hex>.h3q.
+class ArtifactStore {
+public:
+    enum class Lookup { Absent, Hit, Corrupt, Unreadable };
 
-int make_dirs(const std::string &path) {
-    if (path.empty()) return 0;
-    for (size_t i = 1; i <= path.size(); i++)
-        if (i == path.size() || path[i] == '/') {
-            const std::string part = path.substr(0, i);
-            if (mkdir(part.c_str(), 0755) != 0 && errno != EEXIST) return 0;
-            struct stat st;
-            if (stat(part.c_str(), &st) != 0 || !S_ISDIR(st.st_mode)) return 0;
-        }
-    return 1;
-}
+    explicit ArtifactStore(std::string dir) : dir_(std::move(dir)) {}
 
-// A read-only mapping of [offset, offset + bytes) of a file.
-struct Mapping {
-    void *base = MAP_FAILED;
-    size_t length = 0, delta = 0;
-    const uint16_t *data() const { return (const uint16_t *)((const char *)base + delta); }
-    ~Mapping() { if (base != MAP_FAILED) munmap(base, length); }
-    bool map(int fd, uint64_t offset, size_t bytes) {
-        const size_t page = (size_t)sysconf(_SC_PAGESIZE);
-        delta = offset % page;
-        length = bytes + delta;
-        base = mmap(nullptr, length, PROT_READ, MAP_PRIVATE, fd, (off_t)(offset - delta));
-        return base != MAP_FAILED;
+    std::string path_for(const ArtifactHeader &h) const {
+        char hex[65];
+        for (int i = 0; i < 32; i++) snprintf(hex + 2 * i, 3, "%02x", h.source_sha[i]);
+        return dir_ + "/v" + std::to_string(h.recipe) + "-" + mode_name((int)h.mode) + "-" + std::to_string(h.n) + "x" +
+               std::to_string(h.k) + "-" + hex + ".h3q";
     }
+
+    // Reads the artifact at path into payload (payload.size() bytes) when it
+    // holds exactly the weight `want` describes and its payload digest checks.
+    Lookup fetch(const std::string &path, const ArtifactHeader &want, std::vector<unsigned char> &payload) const {
+        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd < 0) return errno == ENOENT ? Lookup::Absent : Lookup::Unreadable;
+        unsigned char image[ArtifactHeader::kSize];
+        ArtifactHeader found;
+        struct stat st;
+        bool good = fstat(fd, &st) == 0 && (uint64_t)st.st_size == ArtifactHeader::kSize + payload.size() &&
+                    read_all(fd, image, sizeof(image)) && found.decode(image) && found.describes_same(want) &&
+                    read_all(fd, payload.data(), payload.size());
+        close(fd);
+        if (good) {
+            unsigned char digest[32];
+            sha256_of(payload.data(), payload.size(), digest);
+            good = memcmp(digest, found.payload_sha, 32) == 0;
+        }
+        return good ? Lookup::Hit : Lookup::Corrupt;
+    }
+
+    // Writes header + payload to a private file beside path, flushes it, and
+    // renames it over path, so readers see a whole artifact or none.
+    bool publish(const std::string &path, const ArtifactHeader &h, const std::vector<unsigned char> &payload) const {
+        unsigned char image[ArtifactHeader::kSize];
+        h.encode(image);
+        static std::atomic<unsigned> serial{0};
+        const std::string part = path + ".part-" + std::to_string((long)getpid()) + "-" + std::to_string(serial++);
+        const int fd = ::open(part.c_str(), O_CREAT | O_EXCL | O_WRONLY | O_CLOEXEC, 0644);
+        if (fd < 0) return false;
+        bool ok = write_all(fd, image, sizeof(image)) && write_all(fd, payload.data(), payload.size()) && fsync(fd) == 0;
+        ok = close(fd) == 0 && ok;
+        ok = ok && rename(part.c_str(), path.c_str()) == 0;
+        if (!ok) {
+            const int e = errno;
+            unlink(part.c_str());
+            errno = e;
+        }
+        return ok;
+    }
+
+private:
+    std::string dir_;
 };
+
+// Creates dir and its missing parents (mode 0755); true if it is a directory.
+bool ensure_directory(const std::string &dir) {
+    if (dir.empty()) return false;
+    struct stat st;
+    if (stat(dir.c_str(), &st) == 0) {
+        if (S_ISDIR(st.st_mode)) return true;
+        errno = ENOTDIR;
+        return false;
+    }
+    const size_t cut = dir.find_last_of('/');
+    if (cut != std::string::npos && cut > 0 && !ensure_directory(dir.substr(0, cut))) return false;
+    if (mkdir(dir.c_str(), 0755) == 0 || errno == EEXIST) return stat(dir.c_str(), &st) == 0 && S_ISDIR(st.st_mode);
+    return false;
+}
 
 // Packs n x k BF16 weights (host) into the descriptor layout on the device and
 // copies it back: packed receives `bytes` bytes.
@@ -495,143 +670,122 @@ int nvfp4_resident_dequant(h3_gpu *g, h3_gpu_tensor *t) {
     return h3_launch_status(g, "NVFP4 dequantization") && h3_hip_check(g, hipStreamSynchronize(g->compute), "NVFP4 dequantization");
 }
 
-h3_gpu_tensor *finish_weight(h3_gpu *g, std::vector<unsigned char> &packed, uint32_t n, uint32_t k, size_t scale,
-                             size_t global, bool hit) {
-    const int mode = g->quant_mode;
-    float gs;
-    memcpy(&gs, packed.data() + global, 4);
-    if (!std::isfinite(gs) || gs <= 0) { h3_set_error(g, "invalid quantized weight global scale"); return nullptr; }
+// Why a packed payload cannot be used, or nullptr. FP8: the global slot and
+// the scale agree, positive and finite, and no code is an E4M3 NaN (0x7f, 0xff);
+// NVFP4: a positive finite global scale and every UE4M3 block scale in 1..126.
+const char *payload_defect(int mode, const std::vector<unsigned char> &p, const ArtifactHeader &h) {
+    float global_scale;
+    memcpy(&global_scale, p.data() + h.global, 4);
+    if (!(global_scale > 0.f) || !std::isfinite(global_scale)) return "invalid quantized weight global scale";
     if (mode == H3_QUANT_FP8) {
-        float ss;
-        memcpy(&ss, packed.data() + scale, 4);
-        if (ss != gs) { h3_set_error(g, "invalid FP8 weight scale"); return nullptr; }
-        for (size_t i = 0; i < (size_t)n * k; i++)
-            if ((packed[i] & 0x7f) == 0x7f) { h3_set_error(g, "nonfinite FP8 weight"); return nullptr; }
-    } else {
-        const size_t plane = (size_t)(n + 127) / 128 * 128 * ((k / 16 + 3) / 4 * 4);
-        for (size_t i = 0; i < plane; i++)
-            if (!packed[scale + i] || packed[scale + i] >= 127) {
-                h3_set_error(g, "invalid NVFP4 weight block scale");
-                return nullptr;
-            }
+        float weight_scale;
+        memcpy(&weight_scale, p.data() + h.scale, 4);
+        if (weight_scale != global_scale) return "invalid FP8 weight scale";
+        const unsigned char *codes = p.data();
+        const unsigned char *end = codes + (size_t)h.n * h.k;
+        return std::any_of(codes, end, [](unsigned char c) { return (c | 0x80) == 0xff; }) ? "nonfinite FP8 weight"
+                                                                                           : nullptr;
     }
+    const size_t plane = (size_t)(h.n + 127) / 128 * 128 * ((h.k / 16 + 3) / 4 * 4);
+    const unsigned char *sf = p.data() + h.scale;
+    return std::all_of(sf, sf + plane, [](unsigned char s) { return s >= 1 && s <= 126; })
+               ? nullptr
+               : "invalid NVFP4 weight block scale";
+}
+
+// A packed weight tensor from a checked payload: device-resident, or kept in
+// pinned host memory when the context streams its packed weights.
+h3_gpu_tensor *packed_tensor(h3_gpu *g, const std::vector<unsigned char> &payload, const ArtifactHeader &h) {
     const h3_gpu_storage storage = g->quant->streaming ? H3_GPU_HOST_PINNED : H3_GPU_DEVICE_ONLY;
-    h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, packed.size(), H3_GPU_I8, storage);
+    h3_gpu_tensor *t = h3_gpu_tensor_alloc(g, payload.size(), H3_GPU_I8, storage);
     if (!t) return nullptr;
-    bool ok;
-    if (storage == H3_GPU_DEVICE_ONLY) {
-        ok = h3_hip_check(g, hipMemcpy(t->data, packed.data(), packed.size(), hipMemcpyHostToDevice), "packed weight upload");
-        g->stats.h2d_bytes += packed.size();
+    if (storage == H3_GPU_HOST_PINNED) {
+        memcpy(t->data, payload.data(), payload.size());
+    } else if (!h3_hip_check(g, hipMemcpy(t->data, payload.data(), payload.size(), hipMemcpyHostToDevice),
+                             "packed weight upload")) {
+        h3_gpu_tensor_free(t);
+        return nullptr;
     } else {
-        memcpy(t->data, packed.data(), packed.size());
-        ok = true;
+        g->stats.h2d_bytes += payload.size();
     }
-    if (!ok) { h3_gpu_tensor_free(t); return nullptr; }
-    t->elements = (size_t)n * k;
-    t->quant_mode = mode; t->quant_n = n; t->quant_k = k; t->quant_scale = scale; t->quant_global = global;
-    if (mode == H3_QUANT_NVFP4 && storage == H3_GPU_DEVICE_ONLY && !nvfp4_resident_dequant(g, t)) {
+    t->elements = (size_t)h.n * h.k;
+    t->quant_mode = (int)h.mode; t->quant_n = h.n; t->quant_k = h.k;
+    t->quant_scale = h.scale; t->quant_global = h.global;
+    if (t->quant_mode == H3_QUANT_NVFP4 && storage == H3_GPU_DEVICE_ONLY && !nvfp4_resident_dequant(g, t)) {
         h3_gpu_tensor_free(t);
         return nullptr;
     }
-    if (hit) g->stats.quant_cache_hits++; else g->stats.quant_cache_misses++;
     return t;
 }
 
-// Content-hashed artifacts, the reference's strict format (cuda_quant.cuh:169-248,
-// which the reference selects with H3_QUANT_VERIFY=1; this backend uses it for
-// every load, and does not write the host's metadata-keyed cache):
-// <cache>/v<recipe>-<mode>-<n>x<k>-<sha256(source)>.h3q with a
-// 128-byte H3QWT001 header: recipe u32 @8, mode u32 @12, n u32 @16, k u32 @20,
-// bytes u64 @24, scale @32, global @40, source SHA-256 @48, payload SHA-256 @80,
-// zero @112-127.
-h3_gpu_tensor *load_artifact(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k, size_t bytes,
-                           size_t scale, size_t global) {
-    const size_t source_bytes = (size_t)n * k * 2;
-    int fd = open(path, O_RDONLY);
-    struct stat st;
-    if (fd < 0 || fstat(fd, &st) != 0 || offset > (uint64_t)st.st_size || source_bytes > (uint64_t)st.st_size - offset) {
-        if (fd >= 0) close(fd);
-        h3_set_error(g, "invalid quantized source range: %s", path);
-        return nullptr;
-    }
-    const struct stat source_status = st;
-    Mapping map;
-    const bool mapped = map.map(fd, offset, source_bytes);
-    close(fd);
-    if (!mapped) { h3_set_error(g, "cannot map quantized source: %s", strerror(errno)); return nullptr; }
-    unsigned char source_hash[32];
-    sha256_of(map.data(), source_bytes, source_hash);
-    const std::string artifact = g->quant->cache + "/v" + std::to_string(H3_QUANT_VERSION) + "-" +
-                                 mode_name(g->quant_mode) + "-" + std::to_string(n) + "x" + std::to_string(k) + "-" +
-                                 hex32(source_hash) + ".h3q";
-    int lock = open((artifact + ".lock").c_str(), O_CREAT | O_RDWR, 0600);
-    if (lock < 0 || flock(lock, LOCK_EX) != 0) {
-        if (lock >= 0) close(lock);
-        h3_set_error(g, "cannot lock quantization artifact: %s", strerror(errno));
-        return nullptr;
-    }
-    std::vector<unsigned char> packed(bytes);
-    unsigned char header[128];
-    bool ok = true, hit = false;
-    fd = open(artifact.c_str(), O_RDONLY);
-    if (fd >= 0) {
-        ok = fstat(fd, &st) == 0 && (uint64_t)st.st_size == 128 + bytes && file_io(fd, header, 128, false) &&
-             memcmp(header, "H3QWT001", 8) == 0 && get_le(header + 8, 4) == H3_QUANT_VERSION &&
-             get_le(header + 12, 4) == (unsigned)g->quant_mode && get_le(header + 16, 4) == n && get_le(header + 20, 4) == k &&
-             get_le(header + 24, 8) == bytes && get_le(header + 32, 8) == scale && get_le(header + 40, 8) == global &&
-             memcmp(header + 48, source_hash, 32) == 0 && file_io(fd, packed.data(), bytes, false);
-        close(fd);
-        if (ok) {
-            unsigned char digest[32];
-            sha256_of(packed.data(), bytes, digest);
-            ok = memcmp(header + 80, digest, 32) == 0;
+// One packed weight through the content-hashed artifact cache. Every load
+// hashes its source; the artifact is reused when its header names the same
+// source digest and packing and its payload digest checks, and otherwise
+// packed on the GPU and published. A corrupt artifact is an error, never
+// silently replaced. The source must not change while it is packed or checked.
+h3_gpu_tensor *load_through_artifact(h3_gpu *g, const char *path, uint64_t offset, const ArtifactHeader &shape) {
+    SourceWeight source;
+    if (!source.open(g, path, offset, (size_t)shape.n * shape.k * 2)) return nullptr;
+    ArtifactHeader want = shape;
+    source.digest(want.source_sha);
+    const ArtifactStore store(g->quant->cache);
+    const std::string artifact = store.path_for(want);
+    std::vector<unsigned char> payload(want.bytes);
+    bool hit = false;
+    {
+        ArtifactLock lock;
+        if (!lock.take(artifact)) {
+            h3_set_error(g, "cannot lock quantization artifact: %s", strerror(errno));
+            return nullptr;
         }
-        for (unsigned i = 112; ok && i < 128; i++) ok = header[i] == 0;
-        if (!ok) h3_set_error(g, "corrupt/incompatible quantization artifact %s; remove it and prepare again", artifact.c_str());
-        hit = ok;
-    } else if (errno != ENOENT) {
-        ok = false;
-        h3_set_error(g, "cannot read quantization artifact: %s", strerror(errno));
-    }
-    if (ok && !hit) {
-        ok = prepare_packed(g, map.data(), n, k, bytes, scale, global, packed.data());
-        if (ok && !same_source(path, source_status)) {
-            ok = false;
-            h3_set_error(g, "source weight changed during quantization; retry with immutable model files");
-        }
-        if (ok) {
-            memset(header, 0, sizeof(header));
-            memcpy(header, "H3QWT001", 8);
-            put_le(header + 8, H3_QUANT_VERSION, 4); put_le(header + 12, (unsigned)g->quant_mode, 4);
-            put_le(header + 16, n, 4); put_le(header + 20, k, 4);
-            put_le(header + 24, bytes, 8); put_le(header + 32, scale, 8); put_le(header + 40, global, 8);
-            memcpy(header + 48, source_hash, 32);
-            sha256_of(packed.data(), bytes, header + 80);
-            std::string staging = artifact + ".tmp.XXXXXX";
-            std::vector<char> name(staging.begin(), staging.end());
-            name.push_back(0);
-            fd = mkstemp(name.data());
-            ok = fd >= 0;
-            if (ok) {
-                ok = file_io(fd, header, 128, true) && file_io(fd, packed.data(), bytes, true) && fsync(fd) == 0;
-                if (close(fd) != 0) ok = false;
+        switch (store.fetch(artifact, want, payload)) {
+        case ArtifactStore::Lookup::Hit:
+            hit = true;
+            break;
+        case ArtifactStore::Lookup::Corrupt:
+            h3_set_error(g, "corrupt/incompatible quantization artifact %s; remove it and prepare again", artifact.c_str());
+            return nullptr;
+        case ArtifactStore::Lookup::Unreadable:
+            h3_set_error(g, "cannot read quantization artifact: %s", strerror(errno));
+            return nullptr;
+        case ArtifactStore::Lookup::Absent: {
+            if (!prepare_packed(g, source.values(), want.n, want.k, want.bytes, want.scale, want.global, payload.data()))
+                return nullptr;
+            if (!source.identity().still_matches(path)) {
+                h3_set_error(g, "source weight changed during quantization; retry with immutable model files");
+                return nullptr;
             }
-            if (ok) ok = rename(name.data(), artifact.c_str()) == 0;
-            if (!ok) {
-                unlink(name.data());
+            ArtifactHeader done = want;
+            sha256_of(payload.data(), payload.size(), done.payload_sha);
+            if (!store.publish(artifact, done, payload)) {
                 h3_set_error(g, "cannot commit quantization artifact: %s", strerror(errno));
+                return nullptr;
             }
+            break;
+        }
         }
     }
-    flock(lock, LOCK_UN);
-    close(lock);
-    if (!ok) return nullptr;
-    if (!same_source(path, source_status)) {
+    if (!source.identity().still_matches(path)) {
         h3_set_error(g, "source weight changed during artifact verification; retry with immutable model files");
         return nullptr;
     }
-    return finish_weight(g, packed, n, k, scale, global, hit);
+    if (const char *defect = payload_defect((int)want.mode, payload, want)) {
+        h3_set_error(g, "%s", defect);
+        return nullptr;
+    }
+    h3_gpu_tensor *t = packed_tensor(g, payload, want);
+    if (t) (hit ? g->stats.quant_cache_hits : g->stats.quant_cache_misses)++;
+    return t;
 }
+
+// The four projections of one H3 DiT block, as admission counts them
+// (qkv 3 x 7168 x 5376, out 5376 x 7168, fc1 2 x 14336 x 5376, fc2 5376 x 14336).
+struct ProjectionShape { uint32_t n, k; };
+constexpr ProjectionShape kH3BlockProjections[4] = {{3 * 7168, 5376}, {5376, 7168}, {2 * 14336, 5376}, {5376, 14336}};
+// Admission headroom beyond the packed weights and activations: the largest
+// conversion operand plus the packed stream buffer, and the activation/output
+// scratch (the reference's figures, cuda_quant.cuh:150-151).
+constexpr uint64_t kWeightHeadroom = 1ull << 30, kActivationHeadroom = 2ull << 30;
 
 }  // namespace
 
@@ -663,43 +817,50 @@ extern "C" int h3_quant_preflight(int mode, char *error, size_t size) {
     return 1;
 }
 
-// gpu.h:44-45 (reference cuda_quant.cuh:120-162).
+// gpu.h:44-45 (behaviour of the reference's cuda_quant.cuh:120-162). Admission
+// counts whole H3 blocks: `weights` must be a multiple of one block's BF16
+// projection bytes, and the packed equivalent plus headroom goes to the
+// residency planner, whose answer decides whether packed weights stream.
 extern "C" int h3_gpu_quant_configure(h3_gpu *g, int mode, const char *cache, uint64_t weights, uint64_t activations,
                                       int force_stream) {
     if (!g || !h3_quant_preflight(mode, g->error, sizeof(g->error))) return 0;
     if (!mode) return 1;      // BF16 projections never touch packed-weight caches
     if (g->quant_mode) return h3_set_error(g, "quantized GPU context already configured");
-    const char *home = getenv("HOME");
-    std::string dir = cache ? cache : std::string(home ? home : ".") + "/.cache/h3/denoise-quant";
-    if (!make_dirs(dir)) return h3_set_error(g, "cannot create quantization cache %s: %s", dir.c_str(), strerror(errno));
-    // Admission counts whole H3 blocks: the BF16 bytes of the four projections
-    // (qkv 3 x 7168 x 5376, out 5376 x 7168, fc1 2 x 14336 x 5376, fc2 5376 x 14336).
-    const uint64_t bf16_block = 2ull * (4ull * 7168 * 5376 + 3ull * 14336 * 5376);
-    if (weights % bf16_block) return h3_set_error(g, "invalid packed DiT core geometry");
-    const uint32_t shapes[4][2] = {{3 * 7168, 5376}, {5376, 7168}, {2 * 14336, 5376}, {5376, 14336}};
-    uint64_t packed_block = 0;
-    for (auto &s : shapes) {
-        uint64_t sc, gl, by;
-        h3_weight_packed_size(s[0], s[1], mode, &sc, &gl, &by);
-        packed_block += by;
+    std::string dir;
+    if (cache) {
+        dir = cache;
+    } else {
+        const char *home = getenv("HOME");
+        dir = std::string(home ? home : ".") + "/.cache/h3/denoise-quant";
     }
-    const uint64_t packed = weights / bf16_block * packed_block;
+    if (!ensure_directory(dir)) return h3_set_error(g, "cannot create quantization cache %s: %s", dir.c_str(), strerror(errno));
+    uint64_t source_per_block = 0, packed_per_block = 0;
+    for (const ProjectionShape &p : kH3BlockProjections) {
+        uint64_t scale, global, bytes;
+        h3_weight_packed_size(p.n, p.k, mode, &scale, &global, &bytes);
+        source_per_block += 2ull * p.n * p.k;
+        packed_per_block += bytes;
+    }
+    if (weights % source_per_block) return h3_set_error(g, "invalid packed DiT core geometry");
     h3_weight_options o;
     if (!h3_weight_options_read(&o, 0, g->error, sizeof(g->error))) return 0;
     if (force_stream && o.mode == H3_WEIGHTS_RESIDENT)
         return h3_set_error(g, "--ssd-streaming conflicts with CUDA resident weight mode");
-    const int stream = h3_gpu_plan_weights(g, packed + (1ull << 30), activations + (2ull << 30));
-    if (stream < 0) return 0;
-    g->quant = new (std::nothrow) h3_quant_state();
-    if (!g->quant) return h3_set_error(g, "quantization: out of host memory");
-    g->quant->cache = dir;
-    g->quant->streaming = stream != 0 || force_stream;
+    const uint64_t packed_total = weights / source_per_block * packed_per_block;
+    const int planned = h3_gpu_plan_weights(g, packed_total + kWeightHeadroom, activations + kActivationHeadroom);
+    if (planned < 0) return 0;
+    std::unique_ptr<h3_quant_state> state(new (std::nothrow) h3_quant_state());
+    if (!state) return h3_set_error(g, "quantization: out of host memory");
+    state->cache = std::move(dir);
+    state->streaming = planned != 0 || force_stream;
+    g->quant = state.release();
     g->quant_mode = mode;
     return 1;
 }
 
-// gpu.h:46-47 (reference cuda_quant.cuh:249-330): a packed FP8 weight from
-// rows x columns BF16 values at offset of a file, through the artifact cache.
+// gpu.h:46-47 (behaviour of the reference's cuda_quant.cuh:249-330): a packed
+// weight of the configured mode from rows x columns BF16 values at offset of a
+// file, through the artifact cache.
 extern "C" h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *g, const char *path, uint64_t offset, uint32_t n, uint32_t k) {
     if (!g) return nullptr;
     if (!g->quant_mode || !n || !k || n % 128 || k % 128 || (uint64_t)n * k > UINT32_MAX) {
@@ -707,9 +868,13 @@ extern "C" h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *g, const char *path, uint64_
         return nullptr;
     }
     if (!path) { h3_set_error(g, "invalid quantized source range: (null)"); return nullptr; }
-    uint64_t scale, global, bytes;
-    h3_weight_packed_size(n, k, g->quant_mode, &scale, &global, &bytes);
-    return load_artifact(g, path, offset, n, k, bytes, scale, global);
+    ArtifactHeader shape;
+    shape.recipe = H3_QUANT_VERSION;
+    shape.mode = (uint32_t)g->quant_mode;
+    shape.n = n;
+    shape.k = k;
+    h3_weight_packed_size(n, k, g->quant_mode, &shape.scale, &shape.global, &shape.bytes);
+    return load_through_artifact(g, path, offset, shape);
 }
 
 // y[rows, n] = FP8 projection of x[rows, k] with a packed weight (reference

@@ -543,10 +543,15 @@ int launch_sage(h3_gpu *g, const SArgs &a, unsigned groups) {
     constexpr size_t shared = 2 * SAGE_TILE;
     hipEvent_t timing = h3_kernel_timing_begin(g);
     hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE>), dim3(groups), dim3(64 * WAVES), shared, g->compute, a);
-    h3_kernel_timing_end(g, timing);
+    if (!h3_launch_status(g, "Sage attention")) {
+        h3_kernel_timing_end(g, timing);
+        return 0;
+    }
     hipLaunchKernelGGL((sage_attn_kernel<WAVES, OCC, SPARSE, true>), dim3(groups), dim3(64 * WAVES), shared,
                        g->compute, a);
-    return h3_launch_status(g, "Sage attention");
+    // Both launches inside one timing window, as the BF16 path times them.
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "Sage exact recomputation");
 }
 }  // namespace
 

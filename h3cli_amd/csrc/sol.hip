@@ -369,7 +369,10 @@ int h3_sol_prepare(h3_gpu *g, h3_sol_router *r, const uint16_t *q, const uint16_
 
 int h3_sol_route(h3_gpu *g, h3_sol_router *r, uint32_t seq, uint32_t heads, uint32_t head0, uint32_t group,
                  float scale) {
-    if (group != r->group || head0 + group > heads) return h3_set_error(g, "SOL: invalid head group");
+    // The workspace is laid out for r->group heads; the last group of a split
+    // may hold fewer (the reference runs min(head_group, heads - first),
+    // cuda_sol.cu:388-389).
+    if (!group || group > r->group || head0 + group > heads) return h3_set_error(g, "SOL: invalid head group");
     const uint32_t QB = r->qblocks, KB = r->kblocks, tiles = r->tiles;
     auto *base = (uint8_t *)r->ws.ptr;
     const auto *qc = (const uint16_t *)(base + r->off_qc), *kc = (const uint16_t *)(base + r->off_kc);

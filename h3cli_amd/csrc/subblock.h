@@ -42,8 +42,15 @@ struct h3_subblock_router {
 // block rows min(64, seq - 64 b) (reference cuda_subblock.cu:352-361).
 int h3_subblock_bind(h3_gpu *g, h3_subblock_router *r, const h3_sol_layout *layout);
 // Largest head group (heads, halved down to 1), then largest query slab (all
-// blocks, else multiples of 32 blocks halving), whose workspace fits r->cap
-// (the reference's plan order, src/denoise/subblock.c:18-42).
+// blocks, else multiples of 32 blocks halving), whose chunk workspace fits
+// r->cap. The loop shape is the reference's (src/denoise/subblock.c:18-42:
+// head group outer, query slab inner), the slab sequence is not: the reference
+// tries slabs 128, 64, ..., 1 and clamps the cap to 512 MiB, while the routed
+// kernels here take slabs of whole 32-block rows and the cap is whatever
+// h3_hip_subblock_workspace_cap set (512 MiB by default). The budget covers
+// one chunk's router buffers and transposed V only; buffers the context
+// already holds from earlier calls (its grow-only BF16 workspace) are not
+// counted. Outputs do not depend on the split.
 int h3_subblock_plan(h3_gpu *g, const h3_subblock_router *r, uint32_t seq, uint32_t heads, h3_subblock_chunking *out);
 // One chunk: with pool set, pools Q and K of heads [head0, head0 + group)
 // (q, k point at head 0; strides are those of `heads`); then scores the query

@@ -50,7 +50,13 @@ struct h3_hip_dit_synth {
     h3_gpu_tensor *cos_t, *sin_t, *row_map;
     uint64_t kept, total;
     h3_gpu_tensor *trace[TRACE_COUNT]; /* copies of the traced block's stages */
+    /* With trace_block set: the modulation chain's inputs and intermediates
+     * (time features, both time projections, SiLU input, shared projection,
+     * the traced block's own table), kept for the parity tests. */
+    h3_gpu_tensor *mod_trace[6];
 };
+static const char *const MOD_TRACE_NAMES[6] = {"time.features", "time.w1", "time.w2", "time.t1", "time.shared",
+                                               "trace.mod_table"};
 
 static int fail(char *error, size_t size, const char *fmt, ...) {
     if (error && size) {
@@ -189,10 +195,16 @@ static int modulation(h3_hip_dit_synth *m, char *error, size_t size) {
         h3_gpu_tensor *table = normal_tensor(g, 2 * (size_t)SLOTS * H, sd + 100 + b, 0.05f, 0.f);
         m->mod[b] = h3_gpu_tensor_new_bf16(g, 2 * (size_t)SLOTS * H);
         ok = table && m->mod[b] && h3_gpu_add_bf16(g, m->mod[b], shared, table, 2 * SLOTS * H) && h3_gpu_synchronize(g);
-        h3_gpu_tensor_free(table);
+        if (ok && m->c.trace_block == b + 1) m->mod_trace[5] = table;
+        else h3_gpu_tensor_free(table);
     }
     m->head_mod = ok ? normal_tensor(g, 2 * 2 * (size_t)H, sd + 3, 0.05f, 0.f) : NULL;
     ok = ok && m->head_mod && h3_gpu_synchronize(g);
+    if (ok && m->c.trace_block) {
+        m->mod_trace[0] = tf; m->mod_trace[1] = w1; m->mod_trace[2] = w2;
+        m->mod_trace[3] = t1; m->mod_trace[4] = shared;
+        tf = w1 = w2 = t1 = shared = NULL;
+    }
     h3_gpu_tensor_free(tf); h3_gpu_tensor_free(w1); h3_gpu_tensor_free(w2);
     h3_gpu_tensor_free(t1); h3_gpu_tensor_free(t2); h3_gpu_tensor_free(shared);
     return ok ? 1 : fail(error, size, "modulation: %s", h3_gpu_error(g));
@@ -417,6 +429,7 @@ void h3_hip_dit_synth_free(h3_hip_dit_synth *m) {
                             m->row_map};
     for (size_t i = 0; i < sizeof(all) / sizeof(*all); i++) h3_gpu_tensor_free(all[i]);
     for (int i = 0; i < TRACE_COUNT; i++) h3_gpu_tensor_free(m->trace[i]);
+    for (int i = 0; i < 6; i++) h3_gpu_tensor_free(m->mod_trace[i]);
     free(m->proj); free(m->host); free(m->norm1); free(m->norm2); free(m->mod); free(m->qn); free(m->kn);
     free(m->layout_blocks);
     free(m);
@@ -576,6 +589,8 @@ h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *m, const char *name) {
     if (!strcmp(name, "rope_cos")) return m->cos_t;
     if (!strcmp(name, "rope_sin")) return m->sin_t;
     if (!strcmp(name, "row_map")) return m->row_map;
+    for (int i = 0; i < 6; i++)
+        if (!strcmp(name, MOD_TRACE_NAMES[i])) return m->mod_trace[i];
     if (!strncmp(name, "trace.", 6)) {
         for (int i = 0; i < TRACE_COUNT; i++)
             if (!strcmp(name + 6, TRACE_NAMES[i])) return m->trace[i];

@@ -107,7 +107,12 @@ int h3_hip_dit_synth_load(h3_hip_dit_synth *model, const char *path, char *error
  * trace_block the traced block's stages "trace.x0" (block input), "xn1"
  * (AdaLN), "qkv", "q", "k", "v", "attn", "o" (out projection), "x1" (gated
  * residual), "xn2" (second AdaLN), "h" (fc1, GELU applied when fused),
- * "act" (SwiGLU or separate GELU), "f" (fc2) and "x2" (block output). */
+ * "act" (SwiGLU or separate GELU), "f" (fc2) and "x2" (block output), and
+ * the modulation chain's tensors: "time.features" (BF16 [2, 256] timestep
+ * features), "time.w1" [hidden, 256], "time.t1" [2, hidden] (first
+ * projection, the SiLU input), "time.w2" [6 hidden, hidden], "time.shared"
+ * [2, 6, hidden] (second projection) and "trace.mod_table" [2, 6, hidden]
+ * (the traced block's own table, added to time.shared). */
 h3_gpu_tensor *h3_hip_dit_synth_tensor(h3_hip_dit_synth *model, const char *name);
 uint32_t h3_hip_dit_synth_rows(const h3_hip_dit_synth *model);
 /* Kept 128x128 blocks of the bound mask and the total (for FLOP accounting). */

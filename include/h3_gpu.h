@@ -148,9 +148,10 @@ void h3_gpu_event_free(h3_gpu_event *event);                    /* gpu.h:33 */
 int h3_gpu_quant_configure(h3_gpu *gpu, int mode, const char *cache,
                            uint64_t bf16_weights, uint64_t activations, int force_stream);
 /* gpu.h:46 (cuda_quant.cuh:249-330). rows x columns BF16 weights at offset
- * of a file (multiples of 128), packed to the FP8 descriptor through the
- * artifact cache (H3QMT002, or H3QWT001 with H3_QUANT_VERIFY=1). The result is
- * passed to h3_gpu_linear_bf16 like a BF16 weight (no bias). */
+ * of a file (multiples of 128), packed to the configured mode's descriptor
+ * through the content-hashed H3QWT001 artifact cache (every load hashes its
+ * source; the reference's H3_QUANT_VERIFY=1 behaviour). The result is passed
+ * to h3_gpu_linear_bf16 like a BF16 weight (no bias). */
 h3_gpu_tensor *h3_gpu_quant_load(h3_gpu *gpu, const char *path, uint64_t offset,
                                  uint32_t rows, uint32_t columns);
 /* gpu.h:74. rows x columns BF16 weights from a file packed as q8 (int8

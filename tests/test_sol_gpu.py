@@ -184,14 +184,15 @@ def test_dense_bypass_and_layout_rules():
         g.close()
 
 
-@pytest.mark.parametrize("q", [32, 64])
-def test_head_groups_match_whole_call(q):
+@pytest.mark.parametrize("q,heads", [(32, 4), (64, 4), (64, 5)])
+def test_head_groups_match_whole_call(q, heads):
     """Fixed workspace budget (the reference's h3_cuda_sol_plan_make,
     src/cuda/cuda_sol_policy.c:47-69): centroids of all heads, then routes,
     lists and attention per head group. Each budget one byte below the last
     plan halves the group; every split gives the whole call's output bit for
-    bit and the same pair counters, and a budget no group fits fails."""
-    seq, heads = 4103, 4
+    bit and the same pair counters, and a budget no group fits fails. With
+    H = 5 the group of 2 leaves a last group of 1 head (cuda_sol.cu:388-389)."""
+    seq = 4103
     print(f"[sol] head groups seq={seq} heads={heads} q={q}", flush=True)
     qx, kx, vx = sol_inputs(seq, heads, seed=9)
     meta = sol_layout(seq, q)
