@@ -139,6 +139,10 @@ struct h3_gpu {
     // event pairs on the compute stream, summed when read.
     bool kernel_timing;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> *kernel_events;
+    // gemm.hip: BF16 values of the W8A16 weight of the current projection
+    // (grow-only; reused by every projection on the compute stream).
+    void *gemm_weights;
+    size_t gemm_weights_bytes;
 };
 
 // ---------------------------------------------------------------- helpers

@@ -130,6 +130,7 @@ extern "C" void h3_gpu_free(h3_gpu *g) {
     kernel_events_clear(g);
     delete g->kernel_events;
     if (g->fault) hipFree(g->fault);
+    if (g->gemm_weights) hipFree(g->gemm_weights);
     if (g->compute) hipStreamDestroy(g->compute);
     if (g->copy) hipStreamDestroy(g->copy);
     delete g;

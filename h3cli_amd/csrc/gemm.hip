@@ -23,6 +23,14 @@
 //  * per-channel q8 (group == K) runs gemm_q8_staged: the int8 tile two steps
 //    ahead goes straight to LDS, and the next step's dequantization shares a
 //    basic block with this step's MFMAs, so its VALU work issues between them.
+// Shapes with K % 128 == 0 and N % 256 == 0 (every DiT projection) run
+// gemm_bf16_pipe instead: a hand-scheduled K loop at one wave per SIMD (see
+// its comment). For W8A16 weights a dequantization pass first writes
+// w = bf16(code * scale) for the whole weight into a BF16 buffer of the
+// context (in registers, 16 codes per thread: the same reconstruction as
+// above), which costs about 1% of the GEMM at M = 32400 and leaves the MFMA
+// loop free of VALU work. gemm_q8_staged and gemm_kernel remain for the other
+// shapes (and as H3_HIP_GEMM_VARIANT=3 for comparison).
 #include "common.h"
 #include "internal.h"
 #include <cmath>
@@ -447,6 +455,277 @@ int launch_staged(h3_gpu *g, const GemmArgs &a) {
     return h3_launch_status(g, "W8A16 GEMM");
 }
 
+// ------------------------------------------------------------ hand-scheduled BF16 GEMM
+// gemm_bf16_pipe: the same 256 x 256 output tile as gemm_kernel, computed by
+// four waves of 128 x 128 (one per SIMD, 2 x 2), each with 16 accumulator
+// blocks of 32 x 32 in AGPRs, so one fragment read from LDS feeds four MFMAs.
+// The whole K loop is one inline-asm block, because its value is the order of
+// the instructions; with one wave per SIMD nothing else hides a stall:
+//  * a K tile (64) is four substeps of 16 MFMAs (16 K each); fragments are
+//    read two substeps ahead into four register sets (one per substep), one
+//    ds_read_b128 after every second MFMA, so the LDS never sees a burst;
+//  * the 16 global -> LDS loads of a K tile (buffer_load ... lds, 1 KB each)
+//    are issued two tiles ahead, one after every second MFMA of the second
+//    half of a tile, into the stage that tile has finished reading;
+//  * one barrier per tile, between substeps 1 and 2: every wave has then
+//    read all fragments of this tile (the last ones were issued during
+//    substep 1) and its loads of the next tile (issued a tile earlier) have
+//    landed; the reads of the next tile start right after it.
+// LDS (128 KB): X stage 0 at 0, X stage 1 at 32 KB, W stage 0 at 64 KB,
+// W stage 1 at 96 KB; rows of 64 BF16 (128 B) with the 16-byte chunk swizzle
+// of swz(). Requirements: K % 128 == 0 (tiles come in stage pairs),
+// N % 256 == 0, M * K * 2 < 2^31 and N * K * 2 < 2^31 (32-bit offsets).
+constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
+
+#define PIPE_MFMA(S, I, J) "v_mfma_f32_32x32x16_bf16 %[c" #I #J "], %[" #S "w" #I "], %[" #S "x" #J "], %[c" #I #J "]\n"
+// Fragment f (0..3 W blocks, 4..7 X blocks) of substep KS from stage ST into set T.
+#define PIPE_RD(T, F, KS, ST) PIPE_RD_##F(T, KS, ST)
+#define PIPE_RD_0(T, KS, ST) "ds_read_b128 %[" #T "w0], %[pw" #KS "] offset:32768*" #ST "\n"
+#define PIPE_RD_1(T, KS, ST) "ds_read_b128 %[" #T "w1], %[pw" #KS "] offset:32768*" #ST "+4096\n"
+#define PIPE_RD_2(T, KS, ST) "ds_read_b128 %[" #T "w2], %[pw" #KS "] offset:32768*" #ST "+8192\n"
+#define PIPE_RD_3(T, KS, ST) "ds_read_b128 %[" #T "w3], %[pw" #KS "] offset:32768*" #ST "+12288\n"
+#define PIPE_RD_4(T, KS, ST) "ds_read_b128 %[" #T "x0], %[px" #KS "] offset:32768*" #ST "\n"
+#define PIPE_RD_5(T, KS, ST) "ds_read_b128 %[" #T "x1], %[px" #KS "] offset:32768*" #ST "+4096\n"
+#define PIPE_RD_6(T, KS, ST) "ds_read_b128 %[" #T "x2], %[px" #KS "] offset:32768*" #ST "+8192\n"
+#define PIPE_RD_7(T, KS, ST) "ds_read_b128 %[" #T "x3], %[px" #KS "] offset:32768*" #ST "+12288\n"
+// Load step t of a K tile into stage ST: 1 KB LDS block wave + 4 (t % 8) of X
+// (t < 8) or W (t >= 8). The lane offset of step t is the previous one plus
+// 32 rows (alternating temporaries, so no offset register is rewritten right
+// after the load that reads it); kc is the tile's K byte offset.
+#define PIPE_LD_X0(ST) "s_add_u32 m0, %[mb], 32768*" #ST "\n" "buffer_load_dwordx4 %[xo], %[sx], %[kc] offen lds\n"
+#define PIPE_LD_X(ST, T, DST, SRC) "s_add_u32 m0, %[mb], 32768*" #ST "+4096*" #T "\n"                        \
+    "v_add_u32 %[" #DST "], %[rs], %[" #SRC "]\n" "buffer_load_dwordx4 %[" #DST "], %[sx], %[kc] offen lds\n"
+#define PIPE_LD_W0(ST) "s_add_u32 m0, %[mb], 65536+32768*" #ST "\n" "buffer_load_dwordx4 %[wo], %[sw], %[kc] offen lds\n"
+#define PIPE_LD_W(ST, T, DST, SRC) "s_add_u32 m0, %[mb], 65536+32768*" #ST "+4096*" #T "\n"                  \
+    "v_add_u32 %[" #DST "], %[rs], %[" #SRC "]\n" "buffer_load_dwordx4 %[" #DST "], %[sw], %[kc] offen lds\n"
+#define PIPE_LOADS_X(ST) PIPE_LD_X0(ST) PIPE_LD_X(ST, 1, t0, xo) PIPE_LD_X(ST, 2, t1, t0) PIPE_LD_X(ST, 3, t0, t1) \
+    PIPE_LD_X(ST, 4, t1, t0) PIPE_LD_X(ST, 5, t0, t1) PIPE_LD_X(ST, 6, t1, t0) PIPE_LD_X(ST, 7, t0, t1)
+#define PIPE_LOADS_W(ST) PIPE_LD_W0(ST) PIPE_LD_W(ST, 1, t1, wo) PIPE_LD_W(ST, 2, t0, t1) PIPE_LD_W(ST, 3, t1, t0) \
+    PIPE_LD_W(ST, 4, t0, t1) PIPE_LD_W(ST, 5, t1, t0) PIPE_LD_W(ST, 6, t0, t1) PIPE_LD_W(ST, 7, t1, t0)
+
+// 16 MFMAs of set S (W block i x X block j, i major); O_k follows MFMA 2k,
+// the odd slot P_k follows MFMA 2k + 1.
+#define PIPE_SUB(S, O0, O1, O2, O3, O4, O5, O6, O7, P0, P1, P2, P3, P4, P5, P6, P7)                          \
+    PIPE_MFMA(S, 0, 0) O0 PIPE_MFMA(S, 0, 1) P0 PIPE_MFMA(S, 0, 2) O1 PIPE_MFMA(S, 0, 3) P1                    \
+    PIPE_MFMA(S, 1, 0) O2 PIPE_MFMA(S, 1, 1) P2 PIPE_MFMA(S, 1, 2) O3 PIPE_MFMA(S, 1, 3) P3                    \
+    PIPE_MFMA(S, 2, 0) O4 PIPE_MFMA(S, 2, 1) P4 PIPE_MFMA(S, 2, 2) O5 PIPE_MFMA(S, 2, 3) P5                    \
+    PIPE_MFMA(S, 3, 0) O6 PIPE_MFMA(S, 3, 1) P6 PIPE_MFMA(S, 3, 2) O7 PIPE_MFMA(S, 3, 3) P7
+// A substep on set S whose even slots read substep KS of stage ST into set T.
+#define PIPE_SUB_RD(S, T, KS, ST, P0, P1, P2, P3, P4, P5, P6, P7)                                            \
+    PIPE_SUB(S, PIPE_RD(T, 0, KS, ST), PIPE_RD(T, 1, KS, ST), PIPE_RD(T, 2, KS, ST), PIPE_RD(T, 3, KS, ST),    \
+             PIPE_RD(T, 4, KS, ST), PIPE_RD(T, 5, KS, ST), PIPE_RD(T, 6, KS, ST), PIPE_RD(T, 7, KS, ST),       \
+             P0, P1, P2, P3, P4, P5, P6, P7)
+// Expands its arguments before PIPE_SUB_RD counts them (PIPE_X8 / PIPE_W8
+// stand for eight arguments).
+#define PIPE_SUB_RD_EXP(...) PIPE_SUB_RD(__VA_ARGS__)
+#define PIPE_X8(ST) PIPE_LD_X0(ST), PIPE_LD_X(ST, 1, t0, xo), PIPE_LD_X(ST, 2, t1, t0), PIPE_LD_X(ST, 3, t0, t1), \
+    PIPE_LD_X(ST, 4, t1, t0), PIPE_LD_X(ST, 5, t0, t1), PIPE_LD_X(ST, 6, t1, t0), PIPE_LD_X(ST, 7, t0, t1)
+#define PIPE_W8(ST) PIPE_LD_W0(ST), PIPE_LD_W(ST, 1, t1, wo), PIPE_LD_W(ST, 2, t0, t1), PIPE_LD_W(ST, 3, t1, t0), \
+    PIPE_LD_W(ST, 4, t0, t1), PIPE_LD_W(ST, 5, t1, t0), PIPE_LD_W(ST, 6, t0, t1), PIPE_LD_W(ST, 7, t1, t0)
+
+// One K tile in stage ST (OT: the other stage). On entry set a holds
+// substep 0 and set b's reads (substep 1) may be in flight; on exit the
+// same holds for the next tile. kc is set to the K offset of the tile two
+// ahead (clamped to the last tile), which substeps 2 and 3 load into ST.
+#define PIPE_TILE(ST, OT)                                                                                     \
+    PIPE_SUB_RD(a, c, 2, ST, "", "", "", "", "", "", "", "")                                                  \
+    "s_waitcnt lgkmcnt(8)\n"                                                                                  \
+    PIPE_SUB_RD(b, d, 3, ST, "", "", "", "", "", "", "", "")                                                  \
+    "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                         \
+    "s_barrier\n"                                                                                             \
+    "s_min_u32 %[kc], %[kn], %[kmax]\n"                                                                       \
+    "s_add_u32 %[kn], %[kn], 128\n"                                                                           \
+    PIPE_SUB_RD_EXP(c, a, 0, OT, PIPE_X8(ST))                                                                 \
+    "s_waitcnt lgkmcnt(8)\n"                                                                                  \
+    PIPE_SUB_RD_EXP(d, b, 1, OT, PIPE_W8(ST))                                                                 \
+    "s_waitcnt lgkmcnt(8)\n"
+
+template <int EPI>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_pipe(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    const unsigned tid = threadIdx.x, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
+    const unsigned wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const unsigned wm = wave / 2, wn = wave % 2;
+    const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
+    const unsigned pid = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned band = pid / (GROUP_M * tiles_n), first_m = band * GROUP_M;
+    const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)GROUP_M);
+    const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
+    const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(tm * TM), n0 = __builtin_amdgcn_readfirstlane(tn * TN);
+    const unsigned ksteps = a.k / TK;
+
+    // Buffer descriptors based at the tile's first row: X rows at or past M
+    // lie past num_records (per-lane offsets carry the row) and load zeros.
+    const uint64_t xbase = (uint64_t)(a.x + (size_t)m0 * a.k);
+    const uint64_t wbase = (uint64_t)((const uint16_t *)a.w + (size_t)n0 * a.k);
+    const unsigned xrows = min(a.m - m0, (unsigned)TM);
+    const i32x4 sx = {(int)__builtin_amdgcn_readfirstlane((unsigned)xbase),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)(xbase >> 32)),
+                      (int)__builtin_amdgcn_readfirstlane(xrows * a.k * 2), 0x00020000};
+    const i32x4 sw = {(int)__builtin_amdgcn_readfirstlane((unsigned)wbase),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)(wbase >> 32)),
+                      (int)__builtin_amdgcn_readfirstlane(TN * a.k * 2), 0x00020000};
+    // Load lanes: LDS block wave + 4 t holds rows 8 (wave + 4 t) + lane / 8;
+    // physical chunk lane % 8 holds logical chunk (lane % 8) ^ swz term.
+    const unsigned lrow = 8 * wave + lane / 8;
+    const unsigned xo = lrow * a.k * 2 + swz(lrow, lane % 8) * 16, wo = xo;
+    const unsigned rs = __builtin_amdgcn_readfirstlane(32 * a.k * 2);
+    const unsigned mb = __builtin_amdgcn_readfirstlane(wave * 1024);
+    unsigned kn = 2 * TK * 2, kc = 0;
+    const unsigned kmax = __builtin_amdgcn_readfirstlane((ksteps - 1) * TK * 2);
+    unsigned pairs = __builtin_amdgcn_readfirstlane(ksteps / 2);
+    // Fragment bases of substep ks in stage 0 (stage 1: +32 KB, an immediate):
+    // row n32 of the wave's 128-row half, logical chunk 2 ks + hf.
+    unsigned bw0, bw1, bw2, bw3, bx0, bx1, bx2, bx3;
+    {
+        unsigned bw[4], bx[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const unsigned part = n32 * ROW_BYTES + swz(n32, 2 * ks + hf) * 16;
+            bw[ks] = 2 * TILE_BYTES + wn * 128 * ROW_BYTES + part;
+            bx[ks] = wm * 128 * ROW_BYTES + part;
+        }
+        bw0 = bw[0]; bw1 = bw[1]; bw2 = bw[2]; bw3 = bw[3];
+        bx0 = bx[0]; bx1 = bx[1]; bx2 = bx[2]; bx3 = bx[3];
+    }
+
+    f32x16 c00 = {}, c01 = {}, c02 = {}, c03 = {}, c10 = {}, c11 = {}, c12 = {}, c13 = {};
+    f32x16 c20 = {}, c21 = {}, c22 = {}, c23 = {}, c30 = {}, c31 = {}, c32 = {}, c33 = {};
+    bf16x8 aw0, aw1, aw2, aw3, ax0, ax1, ax2, ax3, bw0f, bw1f, bw2f, bw3f, bx0f, bx1f, bx2f, bx3f;
+    bf16x8 cw0, cw1, cw2, cw3, cx0, cx1, cx2, cx3, dw0, dw1, dw2, dw3, dx0, dx1, dx2, dx3;
+    unsigned t0, t1;
+    // Prologue: tiles 0 and 1 into stages 0 and 1, substeps 0 and 1 of tile 0
+    // into sets a and b. Then the tiles in stage pairs; the last pair's loads
+    // are clamped reloads of the last tile into a stage nobody reads again,
+    // and its closing reads land in registers nobody uses.
+    asm volatile(
+        "s_mov_b32 %[kc], 0\n" PIPE_LOADS_X(0) PIPE_LOADS_W(0)
+        "s_mov_b32 %[kc], 128\n" PIPE_LOADS_X(1) PIPE_LOADS_W(1)
+        "s_waitcnt vmcnt(0)\n"
+        "s_barrier\n"
+        PIPE_RD(a, 0, 0, 0) PIPE_RD(a, 1, 0, 0) PIPE_RD(a, 2, 0, 0) PIPE_RD(a, 3, 0, 0)
+        PIPE_RD(a, 4, 0, 0) PIPE_RD(a, 5, 0, 0) PIPE_RD(a, 6, 0, 0) PIPE_RD(a, 7, 0, 0)
+        PIPE_RD(b, 0, 1, 0) PIPE_RD(b, 1, 1, 0) PIPE_RD(b, 2, 1, 0) PIPE_RD(b, 3, 1, 0)
+        PIPE_RD(b, 4, 1, 0) PIPE_RD(b, 5, 1, 0) PIPE_RD(b, 6, 1, 0) PIPE_RD(b, 7, 1, 0)
+        "s_waitcnt lgkmcnt(8)\n"
+        "pipe_loop_%=:\n"
+        PIPE_TILE(0, 1)
+        PIPE_TILE(1, 0)
+        "s_sub_u32 %[pairs], %[pairs], 1\n"
+        "s_cmp_lg_u32 %[pairs], 0\n"
+        "s_cbranch_scc1 pipe_loop_%=\n"
+        "s_waitcnt vmcnt(0) lgkmcnt(0)\n"
+        // The last MFMAs' results are complete before the epilogue reads the
+        // accumulators (hipcc does not see the MFMAs inside this block).
+        "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
+        : [c00] "+a"(c00), [c01] "+a"(c01), [c02] "+a"(c02), [c03] "+a"(c03), [c10] "+a"(c10), [c11] "+a"(c11),
+          [c12] "+a"(c12), [c13] "+a"(c13), [c20] "+a"(c20), [c21] "+a"(c21), [c22] "+a"(c22), [c23] "+a"(c23),
+          [c30] "+a"(c30), [c31] "+a"(c31), [c32] "+a"(c32), [c33] "+a"(c33),
+          [aw0] "=&v"(aw0), [aw1] "=&v"(aw1), [aw2] "=&v"(aw2), [aw3] "=&v"(aw3),
+          [ax0] "=&v"(ax0), [ax1] "=&v"(ax1), [ax2] "=&v"(ax2), [ax3] "=&v"(ax3),
+          [bw0] "=&v"(bw0f), [bw1] "=&v"(bw1f), [bw2] "=&v"(bw2f), [bw3] "=&v"(bw3f),
+          [bx0] "=&v"(bx0f), [bx1] "=&v"(bx1f), [bx2] "=&v"(bx2f), [bx3] "=&v"(bx3f),
+          [cw0] "=&v"(cw0), [cw1] "=&v"(cw1), [cw2] "=&v"(cw2), [cw3] "=&v"(cw3),
+          [cx0] "=&v"(cx0), [cx1] "=&v"(cx1), [cx2] "=&v"(cx2), [cx3] "=&v"(cx3),
+          [dw0] "=&v"(dw0), [dw1] "=&v"(dw1), [dw2] "=&v"(dw2), [dw3] "=&v"(dw3),
+          [dx0] "=&v"(dx0), [dx1] "=&v"(dx1), [dx2] "=&v"(dx2), [dx3] "=&v"(dx3),
+          [t0] "=&v"(t0), [t1] "=&v"(t1), [kc] "+s"(kc), [kn] "+s"(kn), [pairs] "+s"(pairs)
+        : [sx] "s"(sx), [sw] "s"(sw), [xo] "v"(xo), [wo] "v"(wo), [rs] "s"(rs), [mb] "s"(mb), [kmax] "s"(kmax),
+          [pw0] "v"(bw0), [pw1] "v"(bw1), [pw2] "v"(bw2), [pw3] "v"(bw3),
+          [px0] "v"(bx0), [px1] "v"(bx1), [px2] "v"(bx2), [px3] "v"(bx3)
+        : "m0", "scc", "memory");
+
+    // Block (i, j): lane holds output row m0 + wm*128 + j*32 + n32 and columns
+    // n0 + wn*128 + i*32 + g*8 + hf*4 + 0..3 for register group g.
+    auto store = [&](const f32x16 &v, int i, int j) __attribute__((always_inline)) {
+        const unsigned row = m0 + wm * 128 + j * 32 + n32;
+        if (row >= a.m) return;
+        uint16_t *dst = a.y + (size_t)row * a.n;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            const unsigned col = n0 + wn * 128 + i * 32 + g4 * 8 + hf * 4;
+            u16x4 out;
+            u16x4 bias4 = {};
+            if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float x = v[g4 * 4 + e];
+                if constexpr (EPI & 4) x *= a.alpha[0];
+                if constexpr (EPI & 1) x += bf16_to_f32(bias4[e]);
+                uint16_t b = f32_to_bf16(x);
+                if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
+                out[e] = b;
+            }
+            *reinterpret_cast<u16x4 *>(dst + col) = out;
+        }
+    };
+    store(c00, 0, 0); store(c01, 0, 1); store(c02, 0, 2); store(c03, 0, 3);
+    store(c10, 1, 0); store(c11, 1, 1); store(c12, 1, 2); store(c13, 1, 3);
+    store(c20, 2, 0); store(c21, 2, 1); store(c22, 2, 2); store(c23, 2, 3);
+    store(c30, 3, 0); store(c31, 3, 1); store(c32, 3, 2); store(c33, 3, 3);
+}
+
+// timed: the launch is its own kernel-timing window (callers that time a
+// preceding pass together with it open the window themselves).
+template <int EPI>
+int launch_pipe(h3_gpu *g, const GemmArgs &a, bool timed = true) {
+    constexpr size_t shared = PIPE_LDS;
+    static bool configured = false;
+    auto kernel = gemm_bf16_pipe<EPI>;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)shared), "GEMM shared memory"))
+            return 0;
+        configured = true;
+    }
+    unsigned tiles = (a.m + TM - 1) / TM * (a.n / TN);
+    hipEvent_t timing = timed ? h3_kernel_timing_begin(g) : nullptr;
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(256), shared, g->compute, a);
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "BF16 GEMM");
+}
+bool pipe_fits(const GemmArgs &a) {
+    return a.n % TN == 0 && a.k % (2 * TK) == 0 && a.m >= 32 && (size_t)a.m * a.k * 2 < (1ull << 31) &&
+           (size_t)a.n * a.k * 2 < (1ull << 31);
+}
+int launch_pipe_epi(h3_gpu *g, const GemmArgs &a, int epi, bool timed = true) {
+    switch (epi) {
+    case 0: return launch_pipe<0>(g, a, timed);
+    case 1: return launch_pipe<1>(g, a, timed);
+    case 2: return launch_pipe<2>(g, a, timed);
+    case 3: return launch_pipe<3>(g, a, timed);
+    default: return launch_pipe<4>(g, a, timed);
+    }
+}
+
+// W8A16 weights -> BF16 values w = bf16(code * scale[row, k / group]), the
+// reconstruction of gemm_kernel and of the reference's Metal kernel
+// (shaders.metal:825-827), written once per projection call for
+// gemm_bf16_pipe. HBM-bound: each thread reads 16 codes (one 16-byte load)
+// and writes 32 bytes. group is a multiple of 16, so one scale covers them.
+__global__ __launch_bounds__(256) void q8_dequant_bf16(const int8_t *codes, const float *scales, uint16_t *out,
+                                                     unsigned k, unsigned group, unsigned groups, size_t chunks) {
+    const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const size_t first = c * 16;
+    const unsigned row = (unsigned)(first / k), col = (unsigned)(first % k);
+    const float s = scales[(size_t)row * groups + col / group];
+    const i32x4 q = *reinterpret_cast<const i32x4 *>(codes + first);
+    bf16x8 half[2];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+        const int word = q[e / 4];
+        f32x2 f = {(float)(int8_t)(word >> (8 * (e % 4))) * s, (float)(int8_t)(word >> (8 * (e % 4 + 1))) * s};
+        bf16x2 b = __builtin_convertvector(f, bf16x2);
+        half[e / 8][e % 8] = b[0];
+        half[e / 8][e % 8 + 1] = b[1];
+    }
+    *reinterpret_cast<bf16x8 *>(out + first) = half[0];
+    *reinterpret_cast<bf16x8 *>(out + first + 8) = half[1];
+}
+
 // Any-shape fallback (small or unaligned projections): one thread per output,
 // FP32 accumulation in k order. Same weight reconstruction as the tiled kernel.
 __global__ __launch_bounds__(256) void gemm_small(GemmArgs a, int q8) {
@@ -531,6 +810,7 @@ int h3_gemm_bf16_alpha(h3_gpu *g, uint16_t *y, const uint16_t *x, const uint16_t
                        uint32_t k, uint32_t n) {
     GemmArgs a{};
     a.y = y; a.x = x; a.w = w; a.alpha = alpha; a.m = m; a.n = n; a.k = k; a.group = 1; a.groups = 1;
+    if (pipe_fits(a) && g->gemm_variant != 3) return launch_pipe<4>(g, a);
     if (n % TN == 0 && k % TK == 0 && m >= 32) return launch_tiled<false, false, 4>(g, a);
     const size_t total = (size_t)m * n;
     hipLaunchKernelGGL(gemm_small, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g->compute, a, 0);
@@ -547,7 +827,38 @@ int h3_gemm(h3_gpu *g, uint16_t *y, const uint16_t *x, const h3_gpu_tensor *w, c
     if (!h3_tensor_acquire(g, w)) return 0;
     int ok;
     const bool tiled = n % TN == 0 && k % TK == 0 && m >= 32 && (!w->q8 || a.group % 16 == 0);
-    if (tiled) {
+    const int epi = (bias ? 1 : 0) | (gelu ? 2 : 0);
+    // Variant 3 keeps the earlier kernels (gemm_q8_staged, gemm_kernel) for A/B.
+    const bool pipe = tiled && pipe_fits(a) && g->gemm_variant != 3;
+    if (pipe && !w->q8) {
+        ok = launch_pipe_epi(g, a, epi);
+    } else if (pipe) {
+        // W8A16: a dequantization pass into the context's BF16 weight buffer
+        // (HBM-bound, ~1% of the GEMM at M = 32400), then the BF16 GEMM on it;
+        // both inside one kernel-timing window.
+        const size_t bytes = (size_t)n * k * 2;
+        if (g->gemm_weights_bytes < bytes) {
+            // An earlier projection may still read the old buffer.
+            if (g->gemm_weights && !h3_hip_check(g, hipStreamSynchronize(g->compute), "GEMM weight buffer")) return 0;
+            if (g->gemm_weights) hipFree(g->gemm_weights);
+            g->gemm_weights = nullptr;
+            g->gemm_weights_bytes = 0;
+            if (!h3_hip_check(g, hipMalloc(&g->gemm_weights, bytes), "GEMM weight buffer")) {
+                g->gemm_weights = nullptr;
+                return 0;
+            }
+            g->gemm_weights_bytes = bytes;
+        }
+        const size_t chunks = (size_t)n * k / 16;
+        hipEvent_t timing = h3_kernel_timing_begin(g);
+        hipLaunchKernelGGL(q8_dequant_bf16, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, g->compute,
+                           (const int8_t *)w->data, w->q8_scales, (uint16_t *)g->gemm_weights, k, a.group, a.groups,
+                           chunks);
+        GemmArgs b = a;
+        b.w = g->gemm_weights;
+        ok = h3_launch_status(g, "W8A16 dequantization") && launch_pipe_epi(g, b, epi, false);
+        h3_kernel_timing_end(g, timing);
+    } else if (tiled) {
         if (!w->q8) ok = launch_epi<false, false>(g, a);
         else if (a.group == k) ok = launch_epi<true, true>(g, a);
         else ok = launch_epi<true, false>(g, a);
