@@ -70,13 +70,13 @@ struct GemmArgs {
 };
 
 __device__ inline float gelu_tanh(float v) {
-    // Reference h3_gelu_bf16, approximate form (src/cuda/cuda_kernels.cuh:879-902);
-    // tanh(t) = 1 - 2 / (exp(2t) + 1) on the exp unit, |t| < 10 here.
-    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    if (inner <= -10.0f) return 0.0f;
-    if (inner >= 10.0f) return v;
-    float t = 1.0f - 2.0f / (__expf(2.0f * inner) + 1.0f);
-    return 0.5f * v * (1.0f + t);
+    // Reference h3_gelu_bf16, approximate form (src/cuda/cuda_kernels.cuh:879-902):
+    // 0.5 v (1 + tanh(c (v + 0.044715 v^3))), c = sqrt(2 / pi), written as
+    // v / (1 + exp(-2 c (v + 0.044715 v^3))) with the hardware exp and
+    // reciprocal (no IEEE division, no branches). Large |v| saturate through
+    // exp: to v (exp -> 0) or to a signed zero (exp -> inf, reciprocal 0).
+    const float u = v * (1.5957691216057308f + 0.071354816272192f * v * v);
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-u));
 }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -457,37 +457,27 @@ int launch_staged(h3_gpu *g, const GemmArgs &a) {
 
 // ------------------------------------------------------------ hand-scheduled BF16 GEMM
 // gemm_bf16_pipe: the same 256 x 256 output tile as gemm_kernel, computed by
-// four waves of 128 x 128 (one per SIMD, 2 x 2), each with 16 accumulator
-// blocks of 32 x 32 in AGPRs, so one fragment read from LDS feeds four MFMAs.
+// four waves of 128 x 128 (one per SIMD, 2 x 2) on v_mfma_f32_16x16x32_bf16,
+// each wave with 8 x 8 accumulator blocks of 16 x 16 in AGPRs, so one
+// fragment read from LDS feeds eight MFMAs. (The same loop on 32 x 32 x 16
+// MFMAs, 4 x 4 blocks of 16 AGPRs, measured 6% slower on the config-4 shapes.)
 // The whole K loop is one inline-asm block, because its value is the order of
 // the instructions; with one wave per SIMD nothing else hides a stall:
-//  * a K tile (64) is four substeps of 16 MFMAs (16 K each); fragments are
-//    read two substeps ahead into four register sets (one per substep), one
-//    ds_read_b128 after every second MFMA, so the LDS never sees a burst;
+//  * a K tile (64) is two substeps of 64 MFMAs (32 K each); the 16 fragments
+//    of the next substep are read during the first half of the current one,
+//    one ds_read_b128 after every second MFMA, into the other register set;
 //  * the 16 global -> LDS loads of a K tile (buffer_load ... lds, 1 KB each)
-//    are issued two tiles ahead, one after every second MFMA of the second
-//    half of a tile, into the stage that tile has finished reading;
-//  * one barrier per tile, between substeps 1 and 2: every wave has then
-//    read all fragments of this tile (the last ones were issued during
-//    substep 1) and its loads of the next tile (issued a tile earlier) have
-//    landed; the reads of the next tile start right after it.
+//    are issued two tiles ahead, two per eight MFMAs of the second substep,
+//    into the stage this tile has finished reading;
+//  * one barrier per tile, between the substeps: every wave has then read
+//    all fragments of this tile and its loads of the next tile (issued a
+//    tile earlier) have landed; the next tile's first reads follow it.
 // LDS (128 KB): X stage 0 at 0, X stage 1 at 32 KB, W stage 0 at 64 KB,
 // W stage 1 at 96 KB; rows of 64 BF16 (128 B) with the 16-byte chunk swizzle
 // of swz(). Requirements: K % 128 == 0 (tiles come in stage pairs),
 // N % 256 == 0, M * K * 2 < 2^31 and N * K * 2 < 2^31 (32-bit offsets).
 constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
 
-#define PIPE_MFMA(S, I, J) "v_mfma_f32_32x32x16_bf16 %[c" #I #J "], %[" #S "w" #I "], %[" #S "x" #J "], %[c" #I #J "]\n"
-// Fragment f (0..3 W blocks, 4..7 X blocks) of substep KS from stage ST into set T.
-#define PIPE_RD(T, F, KS, ST) PIPE_RD_##F(T, KS, ST)
-#define PIPE_RD_0(T, KS, ST) "ds_read_b128 %[" #T "w0], %[pw" #KS "] offset:32768*" #ST "\n"
-#define PIPE_RD_1(T, KS, ST) "ds_read_b128 %[" #T "w1], %[pw" #KS "] offset:32768*" #ST "+4096\n"
-#define PIPE_RD_2(T, KS, ST) "ds_read_b128 %[" #T "w2], %[pw" #KS "] offset:32768*" #ST "+8192\n"
-#define PIPE_RD_3(T, KS, ST) "ds_read_b128 %[" #T "w3], %[pw" #KS "] offset:32768*" #ST "+12288\n"
-#define PIPE_RD_4(T, KS, ST) "ds_read_b128 %[" #T "x0], %[px" #KS "] offset:32768*" #ST "\n"
-#define PIPE_RD_5(T, KS, ST) "ds_read_b128 %[" #T "x1], %[px" #KS "] offset:32768*" #ST "+4096\n"
-#define PIPE_RD_6(T, KS, ST) "ds_read_b128 %[" #T "x2], %[px" #KS "] offset:32768*" #ST "+8192\n"
-#define PIPE_RD_7(T, KS, ST) "ds_read_b128 %[" #T "x3], %[px" #KS "] offset:32768*" #ST "+12288\n"
 // Load step t of a K tile into stage ST: 1 KB LDS block wave + 4 (t % 8) of X
 // (t < 8) or W (t >= 8). The lane offset of step t is the previous one plus
 // 32 rows (alternating temporaries, so no offset register is rewritten right
@@ -503,48 +493,64 @@ constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
 #define PIPE_LOADS_W(ST) PIPE_LD_W0(ST) PIPE_LD_W(ST, 1, t1, wo) PIPE_LD_W(ST, 2, t0, t1) PIPE_LD_W(ST, 3, t1, t0) \
     PIPE_LD_W(ST, 4, t0, t1) PIPE_LD_W(ST, 5, t1, t0) PIPE_LD_W(ST, 6, t0, t1) PIPE_LD_W(ST, 7, t1, t0)
 
-// 16 MFMAs of set S (W block i x X block j, i major); O_k follows MFMA 2k,
-// the odd slot P_k follows MFMA 2k + 1.
-#define PIPE_SUB(S, O0, O1, O2, O3, O4, O5, O6, O7, P0, P1, P2, P3, P4, P5, P6, P7)                          \
-    PIPE_MFMA(S, 0, 0) O0 PIPE_MFMA(S, 0, 1) P0 PIPE_MFMA(S, 0, 2) O1 PIPE_MFMA(S, 0, 3) P1                    \
-    PIPE_MFMA(S, 1, 0) O2 PIPE_MFMA(S, 1, 1) P2 PIPE_MFMA(S, 1, 2) O3 PIPE_MFMA(S, 1, 3) P3                    \
-    PIPE_MFMA(S, 2, 0) O4 PIPE_MFMA(S, 2, 1) P4 PIPE_MFMA(S, 2, 2) O5 PIPE_MFMA(S, 2, 3) P5                    \
-    PIPE_MFMA(S, 3, 0) O6 PIPE_MFMA(S, 3, 1) P6 PIPE_MFMA(S, 3, 2) O7 PIPE_MFMA(S, 3, 3) P7
-// A substep on set S whose even slots read substep KS of stage ST into set T.
-#define PIPE_SUB_RD(S, T, KS, ST, P0, P1, P2, P3, P4, P5, P6, P7)                                            \
-    PIPE_SUB(S, PIPE_RD(T, 0, KS, ST), PIPE_RD(T, 1, KS, ST), PIPE_RD(T, 2, KS, ST), PIPE_RD(T, 3, KS, ST),    \
-             PIPE_RD(T, 4, KS, ST), PIPE_RD(T, 5, KS, ST), PIPE_RD(T, 6, KS, ST), PIPE_RD(T, 7, KS, ST),       \
-             P0, P1, P2, P3, P4, P5, P6, P7)
-// Expands its arguments before PIPE_SUB_RD counts them (PIPE_X8 / PIPE_W8
-// stand for eight arguments).
-#define PIPE_SUB_RD_EXP(...) PIPE_SUB_RD(__VA_ARGS__)
 #define PIPE_X8(ST) PIPE_LD_X0(ST), PIPE_LD_X(ST, 1, t0, xo), PIPE_LD_X(ST, 2, t1, t0), PIPE_LD_X(ST, 3, t0, t1), \
     PIPE_LD_X(ST, 4, t1, t0), PIPE_LD_X(ST, 5, t0, t1), PIPE_LD_X(ST, 6, t1, t0), PIPE_LD_X(ST, 7, t0, t1)
 #define PIPE_W8(ST) PIPE_LD_W0(ST), PIPE_LD_W(ST, 1, t1, wo), PIPE_LD_W(ST, 2, t0, t1), PIPE_LD_W(ST, 3, t1, t0), \
     PIPE_LD_W(ST, 4, t0, t1), PIPE_LD_W(ST, 5, t1, t0), PIPE_LD_W(ST, 6, t0, t1), PIPE_LD_W(ST, 7, t1, t0)
 
-// One K tile in stage ST (OT: the other stage). On entry set a holds
-// substep 0 and set b's reads (substep 1) may be in flight; on exit the
-// same holds for the next tile. kc is set to the K offset of the tile two
-// ahead (clamped to the last tile), which substeps 2 and 3 load into ST.
-#define PIPE_TILE(ST, OT)                                                                                     \
-    PIPE_SUB_RD(a, c, 2, ST, "", "", "", "", "", "", "", "")                                                  \
-    "s_waitcnt lgkmcnt(8)\n"                                                                                  \
-    PIPE_SUB_RD(b, d, 3, ST, "", "", "", "", "", "", "", "")                                                  \
+// MFMA (i, j) of set S: W block i (16 rows) x X block j.
+#define P16_MFMA(S, I, J) "v_mfma_f32_16x16x32_bf16 %[c" #I #J "], %[" #S "w" #I "], %[" #S "x" #J "], %[c" #I #J "]\n"
+#define P16_ROW(S, I, E0, E1, E2, E3, E4, E5, E6, E7)                                                        \
+    P16_MFMA(S, I, 0) E0 P16_MFMA(S, I, 1) E1 P16_MFMA(S, I, 2) E2 P16_MFMA(S, I, 3) E3                        \
+    P16_MFMA(S, I, 4) E4 P16_MFMA(S, I, 5) E5 P16_MFMA(S, I, 6) E6 P16_MFMA(S, I, 7) E7
+// Fragment reads of substep KS (0, 1) from stage ST into set T: W block F
+// (16 rows) at base pwKS + 2048 F, X block F at pxKS + 2048 F.
+#define P16_RW(T, F, KS, ST) "ds_read_b128 %[" #T "w" #F "], %[pw" #KS "] offset:32768*" #ST "+2048*" #F "\n"
+#define P16_RX(T, F, KS, ST) "ds_read_b128 %[" #T "x" #F "], %[px" #KS "] offset:32768*" #ST "+2048*" #F "\n"
+// A substep of set S; rows 0..3 read the 16 fragments of substep KS / stage
+// ST into set T at their even slots; L0..L15 go to the odd slots 1 and 5 of
+// rows 0..7.
+#define P16_SUB(S, T, KS, ST, L0, L1, L2, L3, L4, L5, L6, L7, L8, L9, L10, L11, L12, L13, L14, L15)            \
+    P16_ROW(S, 0, P16_RW(T, 0, KS, ST), L0, P16_RW(T, 1, KS, ST), "", P16_RW(T, 2, KS, ST), L1,                \
+            P16_RW(T, 3, KS, ST), "")                                                                        \
+    P16_ROW(S, 1, P16_RW(T, 4, KS, ST), L2, P16_RW(T, 5, KS, ST), "", P16_RW(T, 6, KS, ST), L3,                \
+            P16_RW(T, 7, KS, ST), "")                                                                        \
+    P16_ROW(S, 2, P16_RX(T, 0, KS, ST), L4, P16_RX(T, 1, KS, ST), "", P16_RX(T, 2, KS, ST), L5,                \
+            P16_RX(T, 3, KS, ST), "")                                                                        \
+    P16_ROW(S, 3, P16_RX(T, 4, KS, ST), L6, P16_RX(T, 5, KS, ST), "", P16_RX(T, 6, KS, ST), L7,                \
+            P16_RX(T, 7, KS, ST), "")                                                                        \
+    P16_ROW(S, 4, "", L8, "", "", "", L9, "", "")                                                             \
+    P16_ROW(S, 5, "", L10, "", "", "", L11, "", "")                                                           \
+    P16_ROW(S, 6, "", L12, "", "", "", L13, "", "")                                                           \
+    P16_ROW(S, 7, "", L14, "", "", "", L15, "", "")
+#define P16_SUB_EXP(...) P16_SUB(__VA_ARGS__)
+#define P16_NONE "", "", "", "", "", "", "", "", "", "", "", "", "", "", "", ""
+// One K tile in stage ST: substep 0 (set a) reads substep 1 of this tile
+// into set b; the barrier; substep 1 (set b) reads substep 0 of the next tile
+// (stage OT) into set a and loads the tile two ahead into ST.
+#define P16_TILE(ST, OT)                                                                                      \
+    P16_SUB_EXP(a, b, 1, ST, P16_NONE)                                                                        \
     "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                         \
     "s_barrier\n"                                                                                             \
     "s_min_u32 %[kc], %[kn], %[kmax]\n"                                                                       \
     "s_add_u32 %[kn], %[kn], 128\n"                                                                           \
-    PIPE_SUB_RD_EXP(c, a, 0, OT, PIPE_X8(ST))                                                                 \
-    "s_waitcnt lgkmcnt(8)\n"                                                                                  \
-    PIPE_SUB_RD_EXP(d, b, 1, OT, PIPE_W8(ST))                                                                 \
-    "s_waitcnt lgkmcnt(8)\n"
+    P16_SUB_EXP(b, a, 0, OT, PIPE_X8(ST), PIPE_W8(ST))                                                        \
+    "s_waitcnt lgkmcnt(0)\n"
+
+#define P16_ACC8(I) [c##I##0] "+a"(c[I][0]), [c##I##1] "+a"(c[I][1]), [c##I##2] "+a"(c[I][2]),               \
+    [c##I##3] "+a"(c[I][3]), [c##I##4] "+a"(c[I][4]), [c##I##5] "+a"(c[I][5]), [c##I##6] "+a"(c[I][6]),      \
+    [c##I##7] "+a"(c[I][7])
+#define P16_SET(S) [S##w0] "=&v"(S##f[0]), [S##w1] "=&v"(S##f[1]), [S##w2] "=&v"(S##f[2]),                    \
+    [S##w3] "=&v"(S##f[3]), [S##w4] "=&v"(S##f[4]), [S##w5] "=&v"(S##f[5]), [S##w6] "=&v"(S##f[6]),          \
+    [S##w7] "=&v"(S##f[7]), [S##x0] "=&v"(S##f[8]), [S##x1] "=&v"(S##f[9]), [S##x2] "=&v"(S##f[10]),          \
+    [S##x3] "=&v"(S##f[11]), [S##x4] "=&v"(S##f[12]), [S##x5] "=&v"(S##f[13]), [S##x6] "=&v"(S##f[14]),      \
+    [S##x7] "=&v"(S##f[15])
 
 template <int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_pipe(GemmArgs a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    const unsigned tid = threadIdx.x, lane = tid % 64, n32 = lane % 32, hf = lane / 32;
+    const unsigned tid = threadIdx.x, lane = tid % 64, n16 = lane % 16, q4 = lane / 16;
     const unsigned wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const unsigned wm = wave / 2, wn = wave % 2;
     const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
@@ -556,8 +562,6 @@ void gemm_bf16_pipe(GemmArgs a) {
     const unsigned m0 = __builtin_amdgcn_readfirstlane(tm * TM), n0 = __builtin_amdgcn_readfirstlane(tn * TN);
     const unsigned ksteps = a.k / TK;
 
-    // Buffer descriptors based at the tile's first row: X rows at or past M
-    // lie past num_records (per-lane offsets carry the row) and load zeros.
     const uint64_t xbase = (uint64_t)(a.x + (size_t)m0 * a.k);
     const uint64_t wbase = (uint64_t)((const uint16_t *)a.w + (size_t)n0 * a.k);
     const unsigned xrows = min(a.m - m0, (unsigned)TM);
@@ -567,8 +571,6 @@ void gemm_bf16_pipe(GemmArgs a) {
     const i32x4 sw = {(int)__builtin_amdgcn_readfirstlane((unsigned)wbase),
                       (int)__builtin_amdgcn_readfirstlane((unsigned)(wbase >> 32)),
                       (int)__builtin_amdgcn_readfirstlane(TN * a.k * 2), 0x00020000};
-    // Load lanes: LDS block wave + 4 t holds rows 8 (wave + 4 t) + lane / 8;
-    // physical chunk lane % 8 holds logical chunk (lane % 8) ^ swz term.
     const unsigned lrow = 8 * wave + lane / 8;
     const unsigned xo = lrow * a.k * 2 + swz(lrow, lane % 8) * 16, wo = xo;
     const unsigned rs = __builtin_amdgcn_readfirstlane(32 * a.k * 2);
@@ -576,82 +578,69 @@ void gemm_bf16_pipe(GemmArgs a) {
     unsigned kn = 2 * TK * 2, kc = 0;
     const unsigned kmax = __builtin_amdgcn_readfirstlane((ksteps - 1) * TK * 2);
     unsigned pairs = __builtin_amdgcn_readfirstlane(ksteps / 2);
-    // Fragment bases of substep ks in stage 0 (stage 1: +32 KB, an immediate):
-    // row n32 of the wave's 128-row half, logical chunk 2 ks + hf.
-    unsigned bw0, bw1, bw2, bw3, bx0, bx1, bx2, bx3;
-    {
-        unsigned bw[4], bx[4];
+    // Fragment bases of substep ks (32 K) in stage 0: row n16 of the wave's
+    // 128-row half, logical chunk 4 ks + q4.
+    unsigned pw[2], px[2];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const unsigned part = n32 * ROW_BYTES + swz(n32, 2 * ks + hf) * 16;
-            bw[ks] = 2 * TILE_BYTES + wn * 128 * ROW_BYTES + part;
-            bx[ks] = wm * 128 * ROW_BYTES + part;
-        }
-        bw0 = bw[0]; bw1 = bw[1]; bw2 = bw[2]; bw3 = bw[3];
-        bx0 = bx[0]; bx1 = bx[1]; bx2 = bx[2]; bx3 = bx[3];
+    for (int ks = 0; ks < 2; ks++) {
+        const unsigned part = n16 * ROW_BYTES + swz(n16, 4 * ks + q4) * 16;
+        pw[ks] = 2 * TILE_BYTES + wn * 128 * ROW_BYTES + part;
+        px[ks] = wm * 128 * ROW_BYTES + part;
     }
-
-    f32x16 c00 = {}, c01 = {}, c02 = {}, c03 = {}, c10 = {}, c11 = {}, c12 = {}, c13 = {};
-    f32x16 c20 = {}, c21 = {}, c22 = {}, c23 = {}, c30 = {}, c31 = {}, c32 = {}, c33 = {};
-    bf16x8 aw0, aw1, aw2, aw3, ax0, ax1, ax2, ax3, bw0f, bw1f, bw2f, bw3f, bx0f, bx1f, bx2f, bx3f;
-    bf16x8 cw0, cw1, cw2, cw3, cx0, cx1, cx2, cx3, dw0, dw1, dw2, dw3, dx0, dx1, dx2, dx3;
+    f32x4 c[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) c[i][j] = f32x4{};
+    bf16x8 af[16], bf[16];
     unsigned t0, t1;
-    // Prologue: tiles 0 and 1 into stages 0 and 1, substeps 0 and 1 of tile 0
-    // into sets a and b. Then the tiles in stage pairs; the last pair's loads
-    // are clamped reloads of the last tile into a stage nobody reads again,
-    // and its closing reads land in registers nobody uses.
+    // Prologue: tiles 0 and 1 into stages 0 and 1, substep 0 of tile 0 into
+    // set a. Then the tiles in stage pairs; the last pair's loads are clamped
+    // reloads of the last tile into a stage nobody reads again, and its
+    // closing reads land in registers nobody uses.
     asm volatile(
         "s_mov_b32 %[kc], 0\n" PIPE_LOADS_X(0) PIPE_LOADS_W(0)
         "s_mov_b32 %[kc], 128\n" PIPE_LOADS_X(1) PIPE_LOADS_W(1)
         "s_waitcnt vmcnt(0)\n"
         "s_barrier\n"
-        PIPE_RD(a, 0, 0, 0) PIPE_RD(a, 1, 0, 0) PIPE_RD(a, 2, 0, 0) PIPE_RD(a, 3, 0, 0)
-        PIPE_RD(a, 4, 0, 0) PIPE_RD(a, 5, 0, 0) PIPE_RD(a, 6, 0, 0) PIPE_RD(a, 7, 0, 0)
-        PIPE_RD(b, 0, 1, 0) PIPE_RD(b, 1, 1, 0) PIPE_RD(b, 2, 1, 0) PIPE_RD(b, 3, 1, 0)
-        PIPE_RD(b, 4, 1, 0) PIPE_RD(b, 5, 1, 0) PIPE_RD(b, 6, 1, 0) PIPE_RD(b, 7, 1, 0)
-        "s_waitcnt lgkmcnt(8)\n"
-        "pipe_loop_%=:\n"
-        PIPE_TILE(0, 1)
-        PIPE_TILE(1, 0)
+        P16_RW(a, 0, 0, 0) P16_RW(a, 1, 0, 0) P16_RW(a, 2, 0, 0) P16_RW(a, 3, 0, 0)
+        P16_RW(a, 4, 0, 0) P16_RW(a, 5, 0, 0) P16_RW(a, 6, 0, 0) P16_RW(a, 7, 0, 0)
+        P16_RX(a, 0, 0, 0) P16_RX(a, 1, 0, 0) P16_RX(a, 2, 0, 0) P16_RX(a, 3, 0, 0)
+        P16_RX(a, 4, 0, 0) P16_RX(a, 5, 0, 0) P16_RX(a, 6, 0, 0) P16_RX(a, 7, 0, 0)
+        "s_waitcnt lgkmcnt(0)\n"
+        "p16_loop_%=:\n"
+        P16_TILE(0, 1)
+        P16_TILE(1, 0)
         "s_sub_u32 %[pairs], %[pairs], 1\n"
         "s_cmp_lg_u32 %[pairs], 0\n"
-        "s_cbranch_scc1 pipe_loop_%=\n"
+        "s_cbranch_scc1 p16_loop_%=\n"
         "s_waitcnt vmcnt(0) lgkmcnt(0)\n"
         // The last MFMAs' results are complete before the epilogue reads the
         // accumulators (hipcc does not see the MFMAs inside this block).
         "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
-        : [c00] "+a"(c00), [c01] "+a"(c01), [c02] "+a"(c02), [c03] "+a"(c03), [c10] "+a"(c10), [c11] "+a"(c11),
-          [c12] "+a"(c12), [c13] "+a"(c13), [c20] "+a"(c20), [c21] "+a"(c21), [c22] "+a"(c22), [c23] "+a"(c23),
-          [c30] "+a"(c30), [c31] "+a"(c31), [c32] "+a"(c32), [c33] "+a"(c33),
-          [aw0] "=&v"(aw0), [aw1] "=&v"(aw1), [aw2] "=&v"(aw2), [aw3] "=&v"(aw3),
-          [ax0] "=&v"(ax0), [ax1] "=&v"(ax1), [ax2] "=&v"(ax2), [ax3] "=&v"(ax3),
-          [bw0] "=&v"(bw0f), [bw1] "=&v"(bw1f), [bw2] "=&v"(bw2f), [bw3] "=&v"(bw3f),
-          [bx0] "=&v"(bx0f), [bx1] "=&v"(bx1f), [bx2] "=&v"(bx2f), [bx3] "=&v"(bx3f),
-          [cw0] "=&v"(cw0), [cw1] "=&v"(cw1), [cw2] "=&v"(cw2), [cw3] "=&v"(cw3),
-          [cx0] "=&v"(cx0), [cx1] "=&v"(cx1), [cx2] "=&v"(cx2), [cx3] "=&v"(cx3),
-          [dw0] "=&v"(dw0), [dw1] "=&v"(dw1), [dw2] "=&v"(dw2), [dw3] "=&v"(dw3),
-          [dx0] "=&v"(dx0), [dx1] "=&v"(dx1), [dx2] "=&v"(dx2), [dx3] "=&v"(dx3),
+        : P16_ACC8(0), P16_ACC8(1), P16_ACC8(2), P16_ACC8(3), P16_ACC8(4), P16_ACC8(5), P16_ACC8(6), P16_ACC8(7),
+          P16_SET(a), P16_SET(b),
           [t0] "=&v"(t0), [t1] "=&v"(t1), [kc] "+s"(kc), [kn] "+s"(kn), [pairs] "+s"(pairs)
         : [sx] "s"(sx), [sw] "s"(sw), [xo] "v"(xo), [wo] "v"(wo), [rs] "s"(rs), [mb] "s"(mb), [kmax] "s"(kmax),
-          [pw0] "v"(bw0), [pw1] "v"(bw1), [pw2] "v"(bw2), [pw3] "v"(bw3),
-          [px0] "v"(bx0), [px1] "v"(bx1), [px2] "v"(bx2), [px3] "v"(bx3)
+          [pw0] "v"(pw[0]), [pw1] "v"(pw[1]), [px0] "v"(px[0]), [px1] "v"(px[1])
         : "m0", "scc", "memory");
 
-    // Block (i, j): lane holds output row m0 + wm*128 + j*32 + n32 and columns
-    // n0 + wn*128 + i*32 + g*8 + hf*4 + 0..3 for register group g.
-    auto store = [&](const f32x16 &v, int i, int j) __attribute__((always_inline)) {
-        const unsigned row = m0 + wm * 128 + j * 32 + n32;
-        if (row >= a.m) return;
+    // Block (i, j): lane holds output row m0 + wm*128 + j*16 + n16 and columns
+    // n0 + wn*128 + i*16 + 4*q4 + 0..3.
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const unsigned row = m0 + wm * 128 + j * 16 + n16;
+        if (row >= a.m) continue;
         uint16_t *dst = a.y + (size_t)row * a.n;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const unsigned col = n0 + wn * 128 + i * 32 + g4 * 8 + hf * 4;
+        for (int i = 0; i < 8; i++) {
+            const unsigned col = n0 + wn * 128 + i * 16 + 4 * q4;
             u16x4 out;
             u16x4 bias4 = {};
             if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                float x = v[g4 * 4 + e];
+                float x = c[i][j][e];
                 if constexpr (EPI & 4) x *= a.alpha[0];
                 if constexpr (EPI & 1) x += bf16_to_f32(bias4[e]);
                 uint16_t b = f32_to_bf16(x);
@@ -660,15 +649,9 @@ void gemm_bf16_pipe(GemmArgs a) {
             }
             *reinterpret_cast<u16x4 *>(dst + col) = out;
         }
-    };
-    store(c00, 0, 0); store(c01, 0, 1); store(c02, 0, 2); store(c03, 0, 3);
-    store(c10, 1, 0); store(c11, 1, 1); store(c12, 1, 2); store(c13, 1, 3);
-    store(c20, 2, 0); store(c21, 2, 1); store(c22, 2, 2); store(c23, 2, 3);
-    store(c30, 3, 0); store(c31, 3, 1); store(c32, 3, 2); store(c33, 3, 3);
+    }
 }
 
-// timed: the launch is its own kernel-timing window (callers that time a
-// preceding pass together with it open the window themselves).
 template <int EPI>
 int launch_pipe(h3_gpu *g, const GemmArgs &a, bool timed = true) {
     constexpr size_t shared = PIPE_LDS;
@@ -686,6 +669,7 @@ int launch_pipe(h3_gpu *g, const GemmArgs &a, bool timed = true) {
     h3_kernel_timing_end(g, timing);
     return h3_launch_status(g, "BF16 GEMM");
 }
+
 bool pipe_fits(const GemmArgs &a) {
     return a.n % TN == 0 && a.k % (2 * TK) == 0 && a.m >= 32 && (size_t)a.m * a.k * 2 < (1ull << 31) &&
            (size_t)a.n * a.k * 2 < (1ull << 31);
