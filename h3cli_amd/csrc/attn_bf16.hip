@@ -760,6 +760,488 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
     return h3_launch_status(g, "BF16 attention");
 }
 
+// ------------------------------------------------------------ hand-scheduled dense kernel
+// attn_bf16_pipe: the dense NOMAX kernel's arithmetic (same operations in the
+// same order, so its outputs equal attn_bf16_wide<2, false, false, true>'s
+// bit for bit) with half the LDS fragment traffic. Four waves of 64 queries
+// (two 32-query blocks b = 0, 1), one wave per SIMD: every K or V^T fragment
+// read from LDS feeds two MFMAs, one per block. With no second wave on the
+// SIMD, the key sweep is one inline-asm block whose instruction order does
+// the overlapping (hipcc's schedule for this shape left the exponentials
+// between their own MFMAs). Per 64-key sub-tile j the MFMA stream is
+//   S0(j) | PV1(j-1) | S1(j) | PV0(j)          (16 MFMAs each)
+// and block b's softmax of sub-tile j (32 exponentials per lane, the FP32 row
+// sum, P rounded to BF16 in place over its scores) runs under the two phases
+// that follow its scores, so its P.V is issued a phase after the last
+// exponential. V^T fragments of sub-tile j are read under S1(j), K fragments
+// of sub-tile j + 1 under PV0(j). Groups of 128 keys (two sub-tiles) share a
+// barrier, placed after the last V^T read of the group; the tiles two groups
+// ahead are loaded (buffer_load ... lds) right after it into the stage just
+// released. Running max, the row-sum test that raises it, the recomputation
+// bytes and the output follow the NOMAX wide kernel; the first group's max is
+// computed in C++ before the sweep, and the last group masks keys past S.
+//
+// Fixed registers inside the sweep:
+//   v[0:31]    scores / P of block 0 (v[0:15] keys 0-31, v[16:31] keys 32-63),
+//              v[32:63] block 1: clobbered;
+//   v[64:127]  O^T of block 0 (channel blocks of 16 registers), v[128:191]
+//              block 1: operands bound to these registers;
+//   a[0:63]    the 16 K fragments of a sub-tile, a[64:127] the 16 V^T
+//              fragments: clobbered;
+//   a[128:191] Q fragments (block 0, then block 1): operands.
+// LDS (128 KB): stage s at 64 KB s: K tiles j at 16 KB j, V^T tiles at
+// 32 KB + 16 KB j, in the wide kernel's swizzled layouts.
+constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
+
+#define AP_S(b, mb) "v[32*" #b "+16*" #mb ":32*" #b "+16*" #mb "+15]"
+#define AP_SR(b, mb, r) "v[32*" #b "+16*" #mb "+" #r "]"
+#define AP_P(b, kk) "v[32*" #b "+16*(" #kk "/2)+4*(" #kk "%%2):32*" #b "+16*(" #kk "/2)+4*(" #kk "%%2)+3]"
+#define AP_O(b, md) "v[64+64*" #b "+16*" #md ":64+64*" #b "+16*" #md "+15]"
+#define AP_K(x) "a[4*(" #x "):4*(" #x ")+3]"
+#define AP_V(x) "a[64+4*(" #x "):64+4*(" #x ")+3]"
+#define AP_Q(b, ks) "a[128+32*" #b "+4*" #ks ":128+32*" #b "+4*" #ks "+3]"
+
+// Scores of block b (keys x queries): kstep ks of key half mb.
+#define AP_SM(b, ks, mb) "v_mfma_f32_32x32x16_bf16 " AP_S(b, mb) ", " AP_K(2*ks+mb) ", " AP_Q(b, ks) ", " AP_S(b, mb) "\n"
+#define AP_SM0(b, mb) "v_mfma_f32_32x32x16_bf16 " AP_S(b, mb) ", " AP_K(mb) ", " AP_Q(b, 0) ", 0\n"
+// O^T of block b += V^T P^T: channel block md, 16-key chunk kk.
+#define AP_PV(b, kk, md) "v_mfma_f32_32x32x16_bf16 " AP_O(b, md) ", " AP_V(4*kk+md) ", " AP_P(b, kk) ", " AP_O(b, md) "\n"
+
+// 16 MFMAs M0..M15 with E_k after M_k.
+#define AP_PH(M0, M1, M2, M3, M4, M5, M6, M7, M8, M9, M10, M11, M12, M13, M14, M15, E0, E1, E2, E3, E4, E5, E6, E7, \
+              E8, E9, E10, E11, E12, E13, E14, E15)                                                              \
+    M0 E0 M1 E1 M2 E2 M3 E3 M4 E4 M5 E5 M6 E6 M7 E7 M8 E8 M9 E9 M10 E10 M11 E11 M12 E12 M13 E13 M14 E14 M15 E15
+#define AP_PH_EXP(...) AP_PH(__VA_ARGS__)
+#define AP_SMFMA(b) AP_SM0(b, 0), AP_SM0(b, 1), AP_SM(b, 1, 0), AP_SM(b, 1, 1), AP_SM(b, 2, 0), AP_SM(b, 2, 1),       \
+    AP_SM(b, 3, 0), AP_SM(b, 3, 1), AP_SM(b, 4, 0), AP_SM(b, 4, 1), AP_SM(b, 5, 0), AP_SM(b, 5, 1), AP_SM(b, 6, 0),    \
+    AP_SM(b, 6, 1), AP_SM(b, 7, 0), AP_SM(b, 7, 1)
+#define AP_PVMFMA(b) AP_PV(b, 0, 0), AP_PV(b, 0, 1), AP_PV(b, 0, 2), AP_PV(b, 0, 3), AP_PV(b, 1, 0), AP_PV(b, 1, 1),   \
+    AP_PV(b, 1, 2), AP_PV(b, 1, 3), AP_PV(b, 2, 0), AP_PV(b, 2, 1), AP_PV(b, 2, 2), AP_PV(b, 2, 3), AP_PV(b, 3, 0),    \
+    AP_PV(b, 3, 1), AP_PV(b, 3, 2), AP_PV(b, 3, 3)
+
+// Softmax of scores 8h + 2i, 8h + 2i + 1 of key half mb of block b, in two
+// parts: A computes p = exp2(fma(s, c, -m)) in place, B adds p0 + p1 to psum
+// and writes the BF16 pair over score 4h + i. At least one instruction must
+// separate a v_exp_f32 from the first VALU that reads its result (gfx950's
+// transcendental forwarding hazard: read right after, the result is stale in
+// part of the wave), so B always follows A after an MFMA or another A.
+#define AP_A(b, mb, h, i)                                                                                         \
+    "v_fma_f32 " AP_SR(b, mb, 8*h+2*i) ", " AP_SR(b, mb, 8*h+2*i) ", %[c], %[nm" #b "]\n"                          \
+    "v_fma_f32 " AP_SR(b, mb, 8*h+2*i+1) ", " AP_SR(b, mb, 8*h+2*i+1) ", %[c], %[nm" #b "]\n"                      \
+    "v_exp_f32 " AP_SR(b, mb, 8*h+2*i) ", " AP_SR(b, mb, 8*h+2*i) "\n"                                             \
+    "v_exp_f32 " AP_SR(b, mb, 8*h+2*i+1) ", " AP_SR(b, mb, 8*h+2*i+1) "\n"
+#define AP_B(b, mb, h, i)                                                                                         \
+    "v_add_f32 %[t" #b "], " AP_SR(b, mb, 8*h+2*i) ", " AP_SR(b, mb, 8*h+2*i+1) "\n"                                \
+    "v_add_f32 %[ps" #b "], %[ps" #b "], %[t" #b "]\n"                                                             \
+    "v_cvt_pk_bf16_f32 " AP_SR(b, mb, 4*h+i) ", " AP_SR(b, mb, 8*h+2*i) ", " AP_SR(b, mb, 8*h+2*i+1) "\n"
+// Last group: score r of half mb is key tile*64 + 32 mb + 8 (r / 4) + 4 hf + r % 4;
+// lim<J> = S - tile*64 - 4 hf, and keys at or past S score -inf.
+#define AP_KEEP(b, mb, r, J)                                                                                      \
+    "v_cmp_lt_i32 vcc, 32*" #mb "+8*((" #r ")/4)+((" #r ")%%4), %[lim" #J "]\n"                                       \
+    "v_cndmask_b32 " AP_SR(b, mb, r) ", %[ninf], " AP_SR(b, mb, r) ", vcc\n"
+// Part A unmasked (AP_UA) or masked with lim<J> (AP_MA).
+#define AP_UA(b, mb, h, i, J) AP_A(b, mb, h, i)
+#define AP_MA(b, mb, h, i, J) AP_KEEP(b, mb, 8*h+2*i, J) AP_KEEP(b, mb, 8*h+2*i+1, J) AP_A(b, mb, h, i)
+// A whole 16-key chunk (mb, h) with nothing to interleave: A0 A1 B0 A2 B1 A3 B2 (nop) B3.
+#define AP_CHUNK(b, mb, h, U, J)                                                                                  \
+    U(b, mb, h, 0, J) U(b, mb, h, 1, J) AP_B(b, mb, h, 0) U(b, mb, h, 2, J) AP_B(b, mb, h, 1) U(b, mb, h, 3, J)     \
+    AP_B(b, mb, h, 2) "s_nop 0\n" AP_B(b, mb, h, 3)
+
+// After a sub-tile of block b: l += psum; the row-sum test (psum not below
+// 2^20: raise = max(raise, exponent of psum)); psum = 0.
+#define AP_FIN(b)                                                                                                 \
+    "v_add_f32 %[l" #b "], %[l" #b "], %[ps" #b "]\n"                                                              \
+    "v_cmp_nge_f32 vcc, 0x49800000, %[ps" #b "]\n"                                                                \
+    "v_bfe_u32 %[t" #b "], %[ps" #b "], 23, 8\n"                                                                  \
+    "v_subrev_u32 %[t" #b "], 127, %[t" #b "]\n"                                                                  \
+    "v_max_i32 %[t" #b "], %[r" #b "], %[t" #b "]\n"                                                              \
+    "v_cndmask_b32 %[r" #b "], %[r" #b "], %[t" #b "], vcc\n"                                                    \
+    "v_mov_b32 %[ps" #b "], 0\n"
+
+#define AP_OMUL(b, md, e) "v_mul_f32 v[64+64*" #b "+16*" #md "+" #e "], v[64+64*" #b "+16*" #md "+" #e "], %[t" #b "]\n"
+#define AP_OMUL16(b, md) AP_OMUL(b, md, 0) AP_OMUL(b, md, 1) AP_OMUL(b, md, 2) AP_OMUL(b, md, 3) AP_OMUL(b, md, 4)     \
+    AP_OMUL(b, md, 5) AP_OMUL(b, md, 6) AP_OMUL(b, md, 7) AP_OMUL(b, md, 8) AP_OMUL(b, md, 9) AP_OMUL(b, md, 10)      \
+    AP_OMUL(b, md, 11) AP_OMUL(b, md, 12) AP_OMUL(b, md, 13) AP_OMUL(b, md, 14) AP_OMUL(b, md, 15)
+// End of a group for block b: when any lane's raise is set, both lanes of a
+// query take the larger; a raise of 32 or more marks the rows for the
+// recomputation launch (and is dropped); m rises by raise, l and O^T scale by
+// 2^-raise. The wait covers P.V MFMAs of the block still in flight. L: a
+// label unique within the asm block.
+#define AP_GEND(b, L)                                                                                             \
+    "v_cmp_ne_u32 vcc, 0, %[r" #b "]\n"                                                                           \
+    "s_cbranch_vccz ap_" #L "_%=\n"                                                                               \
+    "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"                             \
+    "v_cvt_f32_i32 %[t" #b "], %[r" #b "]\n"                                                                       \
+    "v_mov_b32 %[u" #b "], %[t" #b "]\n"                                                                           \
+    "s_nop 1\n"                                                                                                    \
+    "v_permlane32_swap_b32 %[t" #b "], %[u" #b "]\n"                                                               \
+    "v_max_f32 %[t" #b "], %[t" #b "], %[u" #b "]\n"                                                               \
+    "v_cvt_i32_f32 %[r" #b "], %[t" #b "]\n"                                                                       \
+    "v_cmp_le_i32 vcc, 32, %[r" #b "]\n"                                                                          \
+    "v_cndmask_b32_e64 %[f" #b "], %[f" #b "], 1, vcc\n"                                                          \
+    "v_cndmask_b32_e64 %[r" #b "], %[r" #b "], 0, vcc\n"                                                          \
+    "v_sub_u32 %[t" #b "], 0, %[r" #b "]\n"                                                                        \
+    "v_ldexp_f32 %[t" #b "], 1.0, %[t" #b "]\n"                                                                    \
+    "v_cvt_f32_i32 %[u" #b "], %[r" #b "]\n"                                                                       \
+    "v_sub_f32 %[nm" #b "], %[nm" #b "], %[u" #b "]\n"                                                             \
+    "v_mul_f32 %[l" #b "], %[l" #b "], %[t" #b "]\n"                                                               \
+    AP_OMUL16(b, 0) AP_OMUL16(b, 1) AP_OMUL16(b, 2) AP_OMUL16(b, 3)                                               \
+    "ap_" #L "_%=:\n"                                                                                             \
+    "v_mov_b32 %[r" #b "], 0\n"
+
+// Fragment reads: K fragment (ks, mb) of tile J from the current (SET c) or
+// the other (SET n) stage; V^T fragment (kk, md) of tile J, current stage.
+#define AP_RK(ks, mb, J, SET) "ds_read_b128 " AP_K(2*ks+mb) ", %[k" #SET #ks "] offset:" #mb "*8192+" #J "*16384\n"
+#define AP_RV(kk, md, J) "ds_read_b128 " AP_V(4*kk+md) ", %[vc" #kk "] offset:32768+" #md "*4096+" #J "*16384\n"
+
+// Loads of the tile lt (clamped to the last tile) into slot J of the
+// current stage: K rows 16 t + 4 wave + lane / 16 (lanes past S load zeros),
+// V^T channel rows 32 t + 8 wave + lane / 8.
+#define AP_LTILE                                                                                                  \
+    "s_min_u32 %[tt], %[lt], %[tmax]\n"                                                                           \
+    "s_mul_i32 %[sk], %[tt], %[k64]\n"                                                                            \
+    "s_add_u32 %[sk], %[sk], %[hk]\n"                                                                             \
+    "s_lshl_b32 %[sl], %[tt], 6\n"                                                                                \
+    "s_sub_i32 %[sl], %[seq], %[sl]\n"                                                                            \
+    "s_lshl_b32 %[sv], %[tt], 7\n"                                                                                \
+    "s_add_u32 %[sv], %[sv], %[hv]\n"                                                                             \
+    "s_add_u32 %[lt], %[lt], 1\n"
+#define AP_LK(J, T, TV)                                                                                           \
+    "s_add_u32 m0, %[mc], " #J "*16384+" #T "*4096\n"                                                              \
+    "v_cmp_gt_i32 vcc, %[sl], %[lk]\n"                                                                            \
+    "v_cndmask_b32 %[" #TV "], %[oob], %[ko], vcc\n"                                                              \
+    "buffer_load_dwordx4 %[" #TV "], %[kr], %[sk] offen lds\n"                                                     \
+    "s_add_u32 %[sk], %[sk], %[k16]\n"                                                                            \
+    "s_sub_i32 %[sl], %[sl], 16\n"
+#define AP_LV(J, T)                                                                                               \
+    "s_add_u32 m0, %[mc], 32768+" #J "*16384+" #T "*4096\n"                                                        \
+    "buffer_load_dwordx4 %[vo], %[vr], %[sv] offen lds\n"                                                         \
+    "s_add_u32 %[sv], %[sv], %[v32]\n"
+
+// Phase slot lists (16 extras each). Softmax pair i of a phase: part A in
+// slot 2i, part B in slot 2i + 1.
+// Phase 1: block 1's softmax of the previous sub-tile, key half 1 (U: AP_UA or AP_MA, J).
+#define AP_X1(U, J) U(1, 1, 0, 0, J), AP_B(1, 1, 0, 0), U(1, 1, 0, 1, J), AP_B(1, 1, 0, 1), U(1, 1, 0, 2, J),        \
+    AP_B(1, 1, 0, 2), U(1, 1, 0, 3, J), AP_B(1, 1, 0, 3), U(1, 1, 1, 0, J), AP_B(1, 1, 1, 0), U(1, 1, 1, 1, J),        \
+    AP_B(1, 1, 1, 1), U(1, 1, 1, 2, J), AP_B(1, 1, 1, 2), U(1, 1, 1, 3, J), AP_B(1, 1, 1, 3) AP_FIN(1)
+#define AP_X1_NONE "", "", "", "", "", "", "", "", "", "", "", "", "", "", "", ""
+// Phase 2: G (group end of block 0 or nothing), block 0's softmax, half 0.
+#define AP_X2(G, U, J) G U(0, 0, 0, 0, J), AP_B(0, 0, 0, 0), U(0, 0, 0, 1, J), AP_B(0, 0, 0, 1), U(0, 0, 0, 2, J),    \
+    AP_B(0, 0, 0, 2), U(0, 0, 0, 3, J), AP_B(0, 0, 0, 3), U(0, 0, 1, 0, J), AP_B(0, 0, 1, 0), U(0, 0, 1, 1, J),        \
+    AP_B(0, 0, 1, 1), U(0, 0, 1, 2, J), AP_B(0, 0, 1, 2), U(0, 0, 1, 3, J), AP_B(0, 0, 1, 3)
+// Phase 3: G (group end of block 1 or nothing), V^T reads of tile J, block
+// 0's softmax of half 1, its sub-tile end.
+#define AP_X3(G, U, J) G AP_RV(0, 0, J) AP_RV(0, 1, J) U(0, 1, 0, 0, J),                                             \
+    AP_RV(0, 2, J) AP_RV(0, 3, J) AP_B(0, 1, 0, 0), AP_RV(1, 0, J) U(0, 1, 0, 1, J),                                  \
+    AP_RV(1, 1, J) AP_RV(1, 2, J) AP_B(0, 1, 0, 1), AP_RV(1, 3, J) U(0, 1, 0, 2, J),                                  \
+    AP_RV(2, 0, J) AP_RV(2, 1, J) AP_B(0, 1, 0, 2), AP_RV(2, 2, J) U(0, 1, 0, 3, J),                                  \
+    AP_RV(2, 3, J) AP_RV(3, 0, J) AP_B(0, 1, 0, 3), AP_RV(3, 1, J) U(0, 1, 1, 0, J),                                  \
+    AP_RV(3, 2, J) AP_RV(3, 3, J) AP_B(0, 1, 1, 0), U(0, 1, 1, 1, J), AP_B(0, 1, 1, 1), U(0, 1, 1, 2, J),             \
+    AP_B(0, 1, 1, 2), U(0, 1, 1, 3, J), AP_B(0, 1, 1, 3) AP_FIN(0)
+// Phase 4: K reads (tile KJ of stage SET), block 1's softmax of half 0, and
+// (L = AP_L4 / AP_L4_NONE) the loads of the tiles two groups ahead.
+#define AP_X4(KJ, SET, U, J, L0, L1, L2, L3, L4, L5, L6, L7)                                                        \
+    AP_RK(0, 0, KJ, SET) AP_RK(0, 1, KJ, SET) U(1, 0, 0, 0, J), AP_RK(1, 0, KJ, SET) L0 AP_B(1, 0, 0, 0),            \
+    AP_RK(1, 1, KJ, SET) AP_RK(2, 0, KJ, SET) U(1, 0, 0, 1, J), AP_RK(2, 1, KJ, SET) L1 AP_B(1, 0, 0, 1),            \
+    AP_RK(3, 0, KJ, SET) AP_RK(3, 1, KJ, SET) U(1, 0, 0, 2, J), AP_RK(4, 0, KJ, SET) L2 AP_B(1, 0, 0, 2),            \
+    AP_RK(4, 1, KJ, SET) AP_RK(5, 0, KJ, SET) U(1, 0, 0, 3, J), AP_RK(5, 1, KJ, SET) L3 AP_B(1, 0, 0, 3),            \
+    AP_RK(6, 0, KJ, SET) AP_RK(6, 1, KJ, SET) U(1, 0, 1, 0, J), AP_RK(7, 0, KJ, SET) L4 AP_B(1, 0, 1, 0),            \
+    AP_RK(7, 1, KJ, SET) U(1, 0, 1, 1, J), L5 AP_B(1, 0, 1, 1), U(1, 0, 1, 2, J), L6 AP_B(1, 0, 1, 2),               \
+    U(1, 0, 1, 3, J), L7 AP_B(1, 0, 1, 3)
+#define AP_L4 AP_LTILE AP_LK(0, 0, tl0) AP_LV(0, 0), AP_LK(0, 1, tl1) AP_LV(0, 1), AP_LK(0, 2, tl0) AP_LV(0, 2),         \
+    AP_LK(0, 3, tl1) AP_LV(0, 3), AP_LTILE AP_LK(1, 0, tl0) AP_LV(1, 0), AP_LK(1, 1, tl1) AP_LV(1, 1),                  \
+    AP_LK(1, 2, tl0) AP_LV(1, 2), AP_LK(1, 3, tl1) AP_LV(1, 3)
+#define AP_L4_NONE "", "", "", "", "", "", "", ""
+#define AP_X4_EXP(...) AP_X4(__VA_ARGS__)
+
+#define AP_WAIT_LDS "s_waitcnt lgkmcnt(0)\n"
+#define AP_SWAP                                                                                                   \
+    "v_swap_b32 %[kc0], %[kn0]\n v_swap_b32 %[kc1], %[kn1]\n v_swap_b32 %[kc2], %[kn2]\n v_swap_b32 %[kc3], %[kn3]\n" \
+    "v_swap_b32 %[kc4], %[kn4]\n v_swap_b32 %[kc5], %[kn5]\n v_swap_b32 %[kc6], %[kn6]\n v_swap_b32 %[kc7], %[kn7]\n" \
+    "v_swap_b32 %[vc0], %[vn0]\n v_swap_b32 %[vc1], %[vn1]\n v_swap_b32 %[vc2], %[vn2]\n v_swap_b32 %[vc3], %[vn3]\n" \
+    "s_xor_b32 %[mc], %[mc], 0x10000\n"
+
+// One group (sub-tiles 0 and 1). FIRST: group 0 (nothing of a previous
+// sub-tile in flight). U0 / U1: the part-A macro for the softmax of sub-tiles
+// 0 and 1 (AP_MA masks with lim0 / lim1), UP: for block 1's previous sub-tile
+// in phase 1 of sub-tile 0 (the last sub-tile of the previous group).
+#define AP_GROUP(UP, JP, U0, U1, L)                                                                               \
+    AP_PH_EXP(AP_SMFMA(0), AP_X1(UP, JP))                                                                         \
+    AP_PH_EXP(AP_PVMFMA(1), AP_X2(AP_GEND(0, L##a), U0, 0))                                                       \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3(AP_GEND(1, L##b), U0, 0))                                                        \
+    AP_WAIT_LDS                                                                                                   \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, c, U0, 0, AP_L4_NONE))                                                   \
+    AP_WAIT_LDS                                                                                                   \
+    AP_PH_EXP(AP_SMFMA(0), AP_X1(U0, 0))                                                                          \
+    AP_PH_EXP(AP_PVMFMA(1), AP_X2("", U1, 1))                                                                     \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", U1, 1))                                                                      \
+    "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
+    "s_barrier\n"                                                                                                 \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, n, U1, 1, AP_L4))                                                        \
+    AP_WAIT_LDS                                                                                                   \
+    AP_SWAP
+#define AP_GROUP_FIRST                                                                                            \
+    AP_PH_EXP(AP_SMFMA(0), AP_X1_NONE)                                                                            \
+    "s_nop 7\n s_nop 7\n s_nop 7\n"                                                                               \
+    AP_CHUNK(0, 0, 0, AP_UA, 0) AP_CHUNK(0, 0, 1, AP_UA, 0)                                                       \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 0))                                                                   \
+    AP_WAIT_LDS                                                                                                   \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, c, AP_UA, 0, AP_L4_NONE))                                                \
+    AP_WAIT_LDS                                                                                                   \
+    AP_PH_EXP(AP_SMFMA(0), AP_X1(AP_UA, 0))                                                                       \
+    AP_PH_EXP(AP_PVMFMA(1), AP_X2("", AP_UA, 1))                                                                  \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 1))                                                                   \
+    "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
+    "s_barrier\n"                                                                                                 \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, n, AP_UA, 1, AP_L4))                                                     \
+    AP_WAIT_LDS                                                                                                   \
+    AP_SWAP
+// Last sub-tile of the last group: block 1's softmax (masked with lim1) and
+// P.V, both blocks' group ends, and a wait for every MFMA result before the
+// accumulators leave the asm block.
+#define AP_TAIL                                                                                                   \
+    AP_CHUNK(1, 1, 0, AP_MA, 1) AP_CHUNK(1, 1, 1, AP_MA, 1) AP_FIN(1)                                             \
+    AP_GEND(0, e0)                                                                                                \
+    AP_PH_EXP(AP_PVMFMA(1), AP_X1_NONE)                                                                           \
+    AP_GEND(1, e1)                                                                                                \
+    "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
+    "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
+
+#define AP_CL10(p, x) #p #x "0", #p #x "1", #p #x "2", #p #x "3", #p #x "4", #p #x "5", #p #x "6", #p #x "7",          \
+    #p #x "8", #p #x "9"
+#define AP_CLOBBERS                                                                                               \
+    "v0", "v1", "v2", "v3", "v4", "v5", "v6", "v7", "v8", "v9", AP_CL10(v, 1), AP_CL10(v, 2), AP_CL10(v, 3),           \
+    AP_CL10(v, 4), AP_CL10(v, 5), "v60", "v61", "v62", "v63",                                                      \
+    "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8", "a9", AP_CL10(a, 1), AP_CL10(a, 2), AP_CL10(a, 3),           \
+    AP_CL10(a, 4), AP_CL10(a, 5), AP_CL10(a, 6), AP_CL10(a, 7), AP_CL10(a, 8), AP_CL10(a, 9), AP_CL10(a, 10),          \
+    AP_CL10(a, 11), "a120", "a121", "a122", "a123", "a124", "a125", "a126", "a127",                               \
+    "m0", "vcc", "scc", "memory"
+
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void attn_bf16_pipe(Args a) {
+    constexpr int WAVES = 4, BM = 256;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const unsigned tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+    const unsigned n = lane % 32, hf = lane / 32;
+    const unsigned nqb = (a.seq + BM - 1) / BM;
+    const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
+    const unsigned q0 = qb * BM;
+    uint8_t *const retry = a.retry + ((size_t)head * nqb + qb) * 8;
+    const size_t stride = (size_t)a.heads * D;
+    const uint16_t *qh = a.q + (size_t)head * D;
+    const float c = a.scale_log2;
+    const unsigned count = (a.seq + BN - 1) / BN;        // 64-key tiles
+    const unsigned groups = (count + 1) / 2;             // the launcher ensures groups >= 3
+
+    // Q fragments of both blocks (rows past S repeat the last row).
+    bf16x8 qf[2][8];
+    {
+        bool bad = false;
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            unsigned row = q0 + wave * 64 + b * 32 + n;
+            row = row < a.seq ? row : a.seq - 1;
+            const uint16_t *p = qh + (size_t)row * stride + hf * 8;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                qf[b][ks] = *reinterpret_cast<const bf16x8 *>(p + ks * 16);
+                bad |= bf16_vec_nonfinite(qf[b][ks]);
+            }
+        }
+        if (bad) a.fault[0] = 1u;
+    }
+
+    // Tile loads (the layout of the wide kernel at four waves): K block
+    // wave + 4 t holds keys 16 t + 4 wave + lane / 16, V^T block wave + 4 t
+    // channels 32 t + 8 wave + lane / 8. Buffer offsets: K from the head's
+    // first channel, V^T from its first row; keys past S load zeros.
+    const unsigned kstride = (unsigned)(stride * 2);
+    const unsigned lk = 4 * wave + lane / 16, ld = 8 * wave + lane / 8;
+    const unsigned koff = lk * kstride + k_chunk(lk, lane % 16) * 16;
+    const unsigned voff = (ld * a.padded + v_chunk(ld, lane % 8) * 8) * 2;
+    const i32x4 kr = {(int)__builtin_amdgcn_readfirstlane((unsigned)(uint64_t)a.k),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)((uint64_t)a.k >> 32)),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)((size_t)a.seq * stride * 2)), 0x00020000};
+    const i32x4 vr = {(int)__builtin_amdgcn_readfirstlane((unsigned)(uint64_t)a.vt),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)((uint64_t)a.vt >> 32)),
+                      (int)__builtin_amdgcn_readfirstlane((unsigned)((size_t)a.heads * D * a.padded * 2)), 0x00020000};
+    const unsigned hk = __builtin_amdgcn_readfirstlane(head * D * 2);
+    const unsigned hv = __builtin_amdgcn_readfirstlane(head * D * a.padded * 2);
+    const unsigned k64 = __builtin_amdgcn_readfirstlane(64 * kstride), k16 = __builtin_amdgcn_readfirstlane(16 * kstride);
+    const unsigned v32 = __builtin_amdgcn_readfirstlane(32 * a.padded * 2);
+    const unsigned tmax = count - 1;
+    // Tiles 0..3 (groups 0 and 1) into stages 0 and 1.
+#pragma unroll
+    for (int t4 = 0; t4 < 4; t4++) {
+        const unsigned tile = min((unsigned)t4, tmax);
+        uint8_t *base = smem + (t4 / 2) * PIPE_STAGE + (t4 % 2) * K_BYTES;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const unsigned key = tile * BN + 16 * t + lk;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                *reinterpret_cast<const __amdgpu_buffer_rsrc_t *>(&kr),
+                (__attribute__((address_space(3))) void *)(base + (wave + 4 * t) * 1024), 16,
+                key < a.seq ? koff : BUFFER_OOB, hk + (tile * BN + 16 * t) * kstride, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                *reinterpret_cast<const __amdgpu_buffer_rsrc_t *>(&vr),
+                (__attribute__((address_space(3))) void *)(base + 2 * K_BYTES + (wave + 4 * t) * 1024), 16, voff,
+                hv + 32 * t * a.padded * 2 + tile * BN * 2, 0, 0);
+        }
+    }
+    wait_vm_loads();
+    __syncthreads();
+
+    // Fragment bases per stage: K fragment (ks, mb) at kb + 8 KB mb (+ 16 KB
+    // per tile), V^T fragment (kk, md) at vb + 32 KB + 4 KB md.
+    unsigned kc[8], kn[8], vc[4], vn[4];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        kc[ks] = n * 256 + k_chunk(n, 2 * ks + hf) * 16;
+        kn[ks] = kc[ks] + PIPE_STAGE;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        vc[kk] = n * 128 + v_chunk(n, 2 * kk + hf) * 16;
+        vn[kk] = vc[kk] + PIPE_STAGE;
+    }
+
+    // The running max of each block: the first group's score max (as the
+    // wide kernel's first group sets it from m = -1e30).
+    float nm[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        float mx0 = -INFINITY, mx1 = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(smem + j * K_BYTES + kc[ks]);
+                const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(smem + j * K_BYTES + kc[ks] + 8192);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qf[b][ks], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qf[b][ks], s1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                mx0 = fmaxf(fmaxf(mx0, s0[r]), s0[r + 1]);
+                mx1 = fmaxf(fmaxf(mx1, s1[r]), s1[r + 1]);
+            }
+        }
+        const float mx = half_max_swap(fmaxf(mx0, mx1)) * c;
+        nm[b] = -fmaxf(-1e30f, mx);
+    }
+
+    f32x16 o0[4], o1[4];
+#pragma unroll
+    for (int md = 0; md < 4; md++) { o0[md] = f32x16{}; o1[md] = f32x16{}; }
+    float l0 = 0.f, l1 = 0.f, ps0 = 0.f, ps1 = 0.f;
+    int r0 = 0, r1 = 0, f0 = 0, f1 = 0;
+    unsigned mc = __builtin_amdgcn_readfirstlane(wave * 1024);   // loads of group g + 2 go to stage g & 1
+    unsigned lt = 4, gl = groups - 2;
+    const unsigned last0 = 2 * (groups - 1) * BN;
+    const int lim0 = (int)a.seq - (int)last0 - 4 * (int)hf, lim1 = lim0 - BN;
+    const unsigned oob = BUFFER_OOB;
+    const float ninf = -INFINITY;
+    float t0, t1, u0, u1;
+    unsigned tl0, tl1, tt, sk, sl, sv;
+    asm volatile(
+        AP_RK(0, 0, 0, c) AP_RK(0, 1, 0, c) AP_RK(1, 0, 0, c) AP_RK(1, 1, 0, c) AP_RK(2, 0, 0, c) AP_RK(2, 1, 0, c)
+        AP_RK(3, 0, 0, c) AP_RK(3, 1, 0, c) AP_RK(4, 0, 0, c) AP_RK(4, 1, 0, c) AP_RK(5, 0, 0, c) AP_RK(5, 1, 0, c)
+        AP_RK(6, 0, 0, c) AP_RK(6, 1, 0, c) AP_RK(7, 0, 0, c) AP_RK(7, 1, 0, c)
+        AP_WAIT_LDS
+        AP_GROUP_FIRST
+        "s_cmp_eq_u32 %[gl], 0\n"
+        "s_cbranch_scc1 ap_loop_end_%=\n"
+        "ap_loop_%=:\n"
+        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gn)
+        "s_sub_u32 %[gl], %[gl], 1\n"
+        "s_cmp_lg_u32 %[gl], 0\n"
+        "s_cbranch_scc1 ap_loop_%=\n"
+        "ap_loop_end_%=:\n"
+        AP_GROUP(AP_UA, 0, AP_MA, AP_MA, gl)
+        AP_TAIL
+        : [o00] "+{v[64:79]}"(o0[0]), [o01] "+{v[80:95]}"(o0[1]), [o02] "+{v[96:111]}"(o0[2]),
+          [o03] "+{v[112:127]}"(o0[3]), [o10] "+{v[128:143]}"(o1[0]), [o11] "+{v[144:159]}"(o1[1]),
+          [o12] "+{v[160:175]}"(o1[2]), [o13] "+{v[176:191]}"(o1[3]),
+          [nm0] "+v"(nm[0]), [nm1] "+v"(nm[1]), [l0] "+v"(l0), [l1] "+v"(l1), [ps0] "+v"(ps0), [ps1] "+v"(ps1),
+          [r0] "+v"(r0), [r1] "+v"(r1), [f0] "+v"(f0), [f1] "+v"(f1),
+          [kc0] "+v"(kc[0]), [kc1] "+v"(kc[1]), [kc2] "+v"(kc[2]), [kc3] "+v"(kc[3]), [kc4] "+v"(kc[4]),
+          [kc5] "+v"(kc[5]), [kc6] "+v"(kc[6]), [kc7] "+v"(kc[7]), [kn0] "+v"(kn[0]), [kn1] "+v"(kn[1]),
+          [kn2] "+v"(kn[2]), [kn3] "+v"(kn[3]), [kn4] "+v"(kn[4]), [kn5] "+v"(kn[5]), [kn6] "+v"(kn[6]),
+          [kn7] "+v"(kn[7]), [vc0] "+v"(vc[0]), [vc1] "+v"(vc[1]), [vc2] "+v"(vc[2]), [vc3] "+v"(vc[3]),
+          [vn0] "+v"(vn[0]), [vn1] "+v"(vn[1]), [vn2] "+v"(vn[2]), [vn3] "+v"(vn[3]),
+          [mc] "+s"(mc), [lt] "+s"(lt), [gl] "+s"(gl),
+          [t0] "=&v"(t0), [t1] "=&v"(t1), [u0] "=&v"(u0), [u1] "=&v"(u1), [tl0] "=&v"(tl0), [tl1] "=&v"(tl1),
+          [tt] "=&s"(tt), [sk] "=&s"(sk), [sl] "=&s"(sl), [sv] "=&s"(sv)
+        : [q00] "{a[128:131]}"(qf[0][0]), [q01] "{a[132:135]}"(qf[0][1]), [q02] "{a[136:139]}"(qf[0][2]),
+          [q03] "{a[140:143]}"(qf[0][3]), [q04] "{a[144:147]}"(qf[0][4]), [q05] "{a[148:151]}"(qf[0][5]),
+          [q06] "{a[152:155]}"(qf[0][6]), [q07] "{a[156:159]}"(qf[0][7]), [q10] "{a[160:163]}"(qf[1][0]),
+          [q11] "{a[164:167]}"(qf[1][1]), [q12] "{a[168:171]}"(qf[1][2]), [q13] "{a[172:175]}"(qf[1][3]),
+          [q14] "{a[176:179]}"(qf[1][4]), [q15] "{a[180:183]}"(qf[1][5]), [q16] "{a[184:187]}"(qf[1][6]),
+          [q17] "{a[188:191]}"(qf[1][7]),
+          [c] "s"(c), [kr] "s"(kr), [vr] "s"(vr), [tmax] "s"(tmax), [k64] "s"(k64), [hk] "s"(hk),
+          [seq] "s"(a.seq), [hv] "s"(hv), [k16] "s"(k16), [v32] "s"(v32),
+          [lk] "v"(lk), [oob] "v"(oob), [ko] "v"(koff), [vo] "v"(voff), [ninf] "v"(ninf), [lim0] "v"(lim0),
+          [lim1] "v"(lim1)
+        : AP_CLOBBERS);
+
+    // Output: O^T / l for each block; rows whose row sum overflowed (or whose
+    // output is not finite) are left to the recomputation launch.
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const f32x16 *o = b ? o1 : o0;
+        const float total = half_sum_swap(b ? l1 : l0);
+        const float inv = total > 0.f ? 1.f / total : 0.f;
+        const unsigned q = q0 + wave * 64 + b * 32 + n;
+        bool bad = false;
+        if (q < a.seq) {
+            uint16_t *dst = a.out + (a.head_major ? ((size_t)head * a.seq + q) * D : ((size_t)q * a.heads + head) * D);
+#pragma unroll
+            for (int md = 0; md < 4; md++)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    u16x4 w;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float x = o[md][g4 * 4 + i] * inv;
+                        bad |= !finite_f32(x);
+                        w[i] = f32_to_bf16(x);
+                    }
+                    *reinterpret_cast<u16x4 *>(dst + md * 32 + g4 * 8 + hf * 4) = w;
+                }
+        }
+        const bool failed = (b ? f1 : f0) != 0 || bad;
+        const bool any = __builtin_amdgcn_ballot_w64(failed) != 0;
+        if (lane == 0) retry[2 * wave + b] = any ? 1 : 0;
+    }
+}
+
+int launch_pipe_attention(h3_gpu *g, const Args &a) {
+    constexpr size_t shared = 2 * PIPE_STAGE;
+    static bool configured = false;
+    if (!configured) {
+        if (!h3_hip_check(g, hipFuncSetAttribute((const void *)attn_bf16_pipe, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)shared), "attention shared memory"))
+            return 0;
+        configured = true;
+    }
+    if (!configure_wide<2, false, false, false, 8>(g)) return 0;
+    const unsigned groups = (a.seq + 255) / 256 * a.heads;
+    hipEvent_t timing = h3_kernel_timing_begin(g);
+    hipLaunchKernelGGL(attn_bf16_pipe, dim3(groups), dim3(256), shared, g->compute, a);
+    if (!h3_launch_status(g, "BF16 attention")) {
+        h3_kernel_timing_end(g, timing);
+        return 0;
+    }
+    // The recomputation launch: the wide kernel with a per-tile max over the
+    // 32-query blocks flagged above (same retry bytes, 256 queries per workgroup).
+    hipLaunchKernelGGL((attn_bf16_wide<2, false, false, false, 8>), dim3(groups), dim3(512), 2 * 2 * STAGE_BYTES,
+                       g->compute, a);
+    h3_kernel_timing_end(g, timing);
+    return h3_launch_status(g, "BF16 attention");
+}
+
 
 // Ping-pong: waves w and w + 4 of a workgroup share a SIMD, so the two wave
 // groups (0-3 and 4-7) run opposite phases of the key sweep. Each barrier
@@ -1453,6 +1935,9 @@ int h3_launch_attention_bf16(h3_gpu *g, void *workspace, uint16_t *out, const ui
     if (g->attention_variant == 4) return launch_wide<1, false, false, true, 4>(g, a, (seq + 127) / 128 * heads);
     // Variant 9: ping-pong wave groups (21.7 ms against 18.3 at S = 32400, H = 40).
     if (g->attention_variant == 9 && a.buffered) return launch_pingpong<1>(g, a, (seq + 255) / 256 * heads);
+    // The hand-scheduled kernel needs at least three 128-key groups; variant
+    // 14 keeps the wide kernel.
+    if (a.buffered && seq > 256 && g->attention_variant != 14) return launch_pipe_attention(g, a);
     return launch_wide<2, false, false, true>(g, a, (seq + 255) / 256 * heads);
 }
 
