@@ -36,9 +36,9 @@ PEAK_HBM = 8000.0       # MI355X HBM3E, GB/s
 # WRITE_SIZE passes over `python3 bench.py --probe`, each scaled by the same
 # counter's reading for a device copy of known size (probe's calibration copy);
 # the summary with the commands and raw readings is
-# profiles/attn_bf16_wide_s32400_h40_traffic.md: fetched 2.0 x 1744248 KiB +
-# written 1.0 x 437091 KiB per launch.
-TRAFFIC = 4.020e9
+# profiles/attn_bf16_pipe_s32400_h40_traffic.md: fetched 2.0 x 1718725 KiB +
+# written 1.0 x 324048 KiB per launch.
+TRAFFIC = 3.852e9
 
 
 def attention_flops(seq, heads, dim=DIM, density=1.0):
@@ -601,7 +601,7 @@ def main():
                        "heads": HEADS, "head_dim": DIM, "batch": 1, "flop_convention": "4*S^2*H*D"},
             "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3), "peak": PEAK_BF16,
                          "unit": "TFLOP/s", "frac": round(kernel_tflops / PEAK_BF16, 4), "traffic": TRAFFIC,
-                         "kernel": "attn_bf16_wide<2, false, false, true> + recomputation launch", "kernel_ms": round(kernel_ms, 4),
+                         "kernel": "attn_bf16_pipe + recomputation launch", "kernel_ms": round(kernel_ms, 4),
                          "kernel_launches": kernel_n, "traffic_unit": "HBM bytes per launch (rocprofv3, calibrated)",
                          "algorithmic": "4*S^2*H*D = 21.499 TFLOP per launch (one launch covers all 40 heads)"},
         })
