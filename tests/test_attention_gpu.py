@@ -132,6 +132,30 @@ def test_global_load_path_matches_buffer_path(gpu, monkeypatch, seq, heads):
         g13.close()
 
 
+@pytest.mark.parametrize("case", ["257x3", "300x40", "4200x2", "8191x2", "rise", "fall", "spike"])
+def test_scheduled_kernel_matches_wide_kernel(gpu, monkeypatch, case):
+    """Sequences above 256 keys run the hand-scheduled kernel (four waves of
+    64 queries); attention variant 14 forces the compiler-scheduled wide
+    kernel (eight waves of 32). Both compute the same products, sums and
+    lazily raised maxima in the same order, so they agree bit for bit: on
+    ragged tails, on many raises of the max, and when the recomputation
+    launch redoes every row."""
+    if case[0].isdigit():
+        seq, heads = map(int, case.split("x"))
+        q, k, v = synth.attention_inputs(seq, heads, seed=47, scale=0.5)
+    else:
+        seq, heads = 1500, 2
+        q, k, v = _growth_inputs(seq, heads, case)
+    print(f"[attention] scheduled vs wide {case}", flush=True)
+    pipe = sdpa(gpu, q, k, v, seq, heads)
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", "14")
+    g14 = Gpu()
+    try:
+        assert np.array_equal(sdpa(g14, q, k, v, seq, heads), pipe)
+    finally:
+        g14.close()
+
+
 def test_large_values_after_score_jump(gpu):
     """A 41-log2-unit score jump with |V| near 1e26: P that large must not
     reach O unscaled (it would overflow FP32). The rows go to the
