@@ -777,7 +777,10 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 // of sub-tile j + 1 under PV0(j). Groups of 128 keys (two sub-tiles) share a
 // barrier, placed after the last V^T read of the group; the tiles two groups
 // ahead are loaded (buffer_load ... lds) right after it into the stage just
-// released. Running max, the row-sum test that raises it, the recomputation
+// released. The loop body holds two groups, one per stage, so every LDS
+// address is a base register plus a constant; K rows past S are caught by
+// the buffer's bounds check on the per-lane offset (tile base + row), which
+// makes the loads the same for every group. Running max, the row-sum test that raises it, the recomputation
 // bytes and the output follow the NOMAX wide kernel; the first group's max is
 // computed in C++ before the sweep, and the last group masks keys past S.
 //
@@ -789,8 +792,9 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 //   a[0:63]    the 16 K fragments of a sub-tile, a[64:127] the 16 V^T
 //              fragments: clobbered;
 //   a[128:191] Q fragments (block 0, then block 1): operands.
-// LDS (128 KB): stage s at 64 KB s: K tiles j at 16 KB j, V^T tiles at
-// 32 KB + 16 KB j, in the wide kernel's swizzled layouts.
+// LDS (128 KB): K tile j of stage s at 32 KB s + 16 KB j, V^T tile j of
+// stage s at 64 KB + 32 KB s + 16 KB j, in the wide kernel's swizzled
+// layouts (every read offset then fits the 16-bit ds_read offset).
 constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
 
 #define AP_S(b, mb) "v[32*" #b "+16*" #mb ":32*" #b "+16*" #mb "+15]"
@@ -889,32 +893,27 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
     "ap_" #L "_%=:\n"                                                                                             \
     "v_mov_b32 %[r" #b "], 0\n"
 
-// Fragment reads: K fragment (ks, mb) of tile J from the current (SET c) or
-// the other (SET n) stage; V^T fragment (kk, md) of tile J, current stage.
-#define AP_RK(ks, mb, J, SET) "ds_read_b128 " AP_K(2*ks+mb) ", %[k" #SET #ks "] offset:" #mb "*8192+" #J "*16384\n"
-#define AP_RV(kk, md, J) "ds_read_b128 " AP_V(4*kk+md) ", %[vc" #kk "] offset:32768+" #md "*4096+" #J "*16384\n"
+// Fragment reads: K fragment (ks, mb) of tile J of stage ST; V^T fragment
+// (kk, md) of tile J of stage ST (the V^T bases include the 64 KB).
+#define AP_RK(ks, mb, J, ST) "ds_read_b128 " AP_K(2*ks+mb) ", %[kb" #ks "] offset:" #mb "*8192+" #J "*16384+" #ST "*32768\n"
+#define AP_RV(kk, md, J, ST) "ds_read_b128 " AP_V(4*kk+md) ", %[vb" #kk "] offset:" #md "*4096+" #J "*16384+" #ST "*32768\n"
 
-// Loads of the tile lt (clamped to the last tile) into slot J of the
-// current stage: K rows 16 t + 4 wave + lane / 16 (lanes past S load zeros),
-// V^T channel rows 32 t + 8 wave + lane / 8.
+// Loads of the tile lt (clamped to the last tile) into slot J of stage ST:
+// K rows 16 T + 4 wave + lane / 16 at per-lane offset ko<T> + tile base (rows
+// at or past S are out of the buffer's range and load zeros), V^T channel
+// rows 32 T + 8 wave + lane / 8.
 #define AP_LTILE                                                                                                  \
     "s_min_u32 %[tt], %[lt], %[tmax]\n"                                                                           \
     "s_mul_i32 %[sk], %[tt], %[k64]\n"                                                                            \
-    "s_add_u32 %[sk], %[sk], %[hk]\n"                                                                             \
-    "s_lshl_b32 %[sl], %[tt], 6\n"                                                                                \
-    "s_sub_i32 %[sl], %[seq], %[sl]\n"                                                                            \
     "s_lshl_b32 %[sv], %[tt], 7\n"                                                                                \
     "s_add_u32 %[sv], %[sv], %[hv]\n"                                                                             \
     "s_add_u32 %[lt], %[lt], 1\n"
-#define AP_LK(J, T, TV)                                                                                           \
-    "s_add_u32 m0, %[mc], " #J "*16384+" #T "*4096\n"                                                              \
-    "v_cmp_gt_i32 vcc, %[sl], %[lk]\n"                                                                            \
-    "v_cndmask_b32 %[" #TV "], %[oob], %[ko], vcc\n"                                                              \
-    "buffer_load_dwordx4 %[" #TV "], %[kr], %[sk] offen lds\n"                                                     \
-    "s_add_u32 %[sk], %[sk], %[k16]\n"                                                                            \
-    "s_sub_i32 %[sl], %[sl], 16\n"
-#define AP_LV(J, T)                                                                                               \
-    "s_add_u32 m0, %[mc], 32768+" #J "*16384+" #T "*4096\n"                                                        \
+#define AP_LK(ST, J, T, TV)                                                                                       \
+    "s_add_u32 m0, %[mc], " #ST "*32768+" #J "*16384+" #T "*4096\n"                                                \
+    "v_add_u32 %[" #TV "], %[sk], %[ko" #T "]\n"                                                                   \
+    "buffer_load_dwordx4 %[" #TV "], %[kr], %[hk] offen lds\n"
+#define AP_LV(ST, J, T)                                                                                           \
+    "s_add_u32 m0, %[mc], 65536+" #ST "*32768+" #J "*16384+" #T "*4096\n"                                          \
     "buffer_load_dwordx4 %[vo], %[vr], %[sv] offen lds\n"                                                         \
     "s_add_u32 %[sv], %[sv], %[v32]\n"
 
@@ -929,73 +928,76 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
 #define AP_X2(G, U, J) G U(0, 0, 0, 0, J), AP_B(0, 0, 0, 0), U(0, 0, 0, 1, J), AP_B(0, 0, 0, 1), U(0, 0, 0, 2, J),    \
     AP_B(0, 0, 0, 2), U(0, 0, 0, 3, J), AP_B(0, 0, 0, 3), U(0, 0, 1, 0, J), AP_B(0, 0, 1, 0), U(0, 0, 1, 1, J),        \
     AP_B(0, 0, 1, 1), U(0, 0, 1, 2, J), AP_B(0, 0, 1, 2), U(0, 0, 1, 3, J), AP_B(0, 0, 1, 3)
-// Phase 3: G (group end of block 1 or nothing), V^T reads of tile J, block
-// 0's softmax of half 1, its sub-tile end.
-#define AP_X3(G, U, J) G AP_RV(0, 0, J) AP_RV(0, 1, J) U(0, 1, 0, 0, J),                                             \
-    AP_RV(0, 2, J) AP_RV(0, 3, J) AP_B(0, 1, 0, 0), AP_RV(1, 0, J) U(0, 1, 0, 1, J),                                  \
-    AP_RV(1, 1, J) AP_RV(1, 2, J) AP_B(0, 1, 0, 1), AP_RV(1, 3, J) U(0, 1, 0, 2, J),                                  \
-    AP_RV(2, 0, J) AP_RV(2, 1, J) AP_B(0, 1, 0, 2), AP_RV(2, 2, J) U(0, 1, 0, 3, J),                                  \
-    AP_RV(2, 3, J) AP_RV(3, 0, J) AP_B(0, 1, 0, 3), AP_RV(3, 1, J) U(0, 1, 1, 0, J),                                  \
-    AP_RV(3, 2, J) AP_RV(3, 3, J) AP_B(0, 1, 1, 0), U(0, 1, 1, 1, J), AP_B(0, 1, 1, 1), U(0, 1, 1, 2, J),             \
+// Phase 3: G (group end of block 1 or nothing), V^T reads of tile J of stage
+// ST, block 0's softmax of half 1, its sub-tile end.
+#define AP_X3(G, U, J, ST) G AP_RV(0, 0, J, ST) AP_RV(0, 1, J, ST) U(0, 1, 0, 0, J),                                 \
+    AP_RV(0, 2, J, ST) AP_RV(0, 3, J, ST) AP_B(0, 1, 0, 0), AP_RV(1, 0, J, ST) U(0, 1, 0, 1, J),                      \
+    AP_RV(1, 1, J, ST) AP_RV(1, 2, J, ST) AP_B(0, 1, 0, 1), AP_RV(1, 3, J, ST) U(0, 1, 0, 2, J),                      \
+    AP_RV(2, 0, J, ST) AP_RV(2, 1, J, ST) AP_B(0, 1, 0, 2), AP_RV(2, 2, J, ST) U(0, 1, 0, 3, J),                      \
+    AP_RV(2, 3, J, ST) AP_RV(3, 0, J, ST) AP_B(0, 1, 0, 3), AP_RV(3, 1, J, ST) U(0, 1, 1, 0, J),                      \
+    AP_RV(3, 2, J, ST) AP_RV(3, 3, J, ST) AP_B(0, 1, 1, 0), U(0, 1, 1, 1, J), AP_B(0, 1, 1, 1), U(0, 1, 1, 2, J),     \
     AP_B(0, 1, 1, 2), U(0, 1, 1, 3, J), AP_B(0, 1, 1, 3) AP_FIN(0)
-// Phase 4: K reads (tile KJ of stage SET), block 1's softmax of half 0, and
-// (L = AP_L4 / AP_L4_NONE) the loads of the tiles two groups ahead.
-#define AP_X4(KJ, SET, U, J, L0, L1, L2, L3, L4, L5, L6, L7)                                                        \
-    AP_RK(0, 0, KJ, SET) AP_RK(0, 1, KJ, SET) U(1, 0, 0, 0, J), AP_RK(1, 0, KJ, SET) L0 AP_B(1, 0, 0, 0),            \
-    AP_RK(1, 1, KJ, SET) AP_RK(2, 0, KJ, SET) U(1, 0, 0, 1, J), AP_RK(2, 1, KJ, SET) L1 AP_B(1, 0, 0, 1),            \
-    AP_RK(3, 0, KJ, SET) AP_RK(3, 1, KJ, SET) U(1, 0, 0, 2, J), AP_RK(4, 0, KJ, SET) L2 AP_B(1, 0, 0, 2),            \
-    AP_RK(4, 1, KJ, SET) AP_RK(5, 0, KJ, SET) U(1, 0, 0, 3, J), AP_RK(5, 1, KJ, SET) L3 AP_B(1, 0, 0, 3),            \
-    AP_RK(6, 0, KJ, SET) AP_RK(6, 1, KJ, SET) U(1, 0, 1, 0, J), AP_RK(7, 0, KJ, SET) L4 AP_B(1, 0, 1, 0),            \
-    AP_RK(7, 1, KJ, SET) U(1, 0, 1, 1, J), L5 AP_B(1, 0, 1, 1), U(1, 0, 1, 2, J), L6 AP_B(1, 0, 1, 2),               \
+// Phase 4: K reads (tile KJ of stage KS), block 1's softmax of half 0, and
+// the loads of the tiles two groups ahead (AP_L4(ST) into stage ST, or
+// AP_LNONE(ST)).
+#define AP_X4(KJ, KS, U, J, L0, L1, L2, L3, L4, L5, L6, L7)                                                         \
+    AP_RK(0, 0, KJ, KS) AP_RK(0, 1, KJ, KS) U(1, 0, 0, 0, J), AP_RK(1, 0, KJ, KS) L0 AP_B(1, 0, 0, 0),                \
+    AP_RK(1, 1, KJ, KS) AP_RK(2, 0, KJ, KS) U(1, 0, 0, 1, J), AP_RK(2, 1, KJ, KS) L1 AP_B(1, 0, 0, 1),                \
+    AP_RK(3, 0, KJ, KS) AP_RK(3, 1, KJ, KS) U(1, 0, 0, 2, J), AP_RK(4, 0, KJ, KS) L2 AP_B(1, 0, 0, 2),                \
+    AP_RK(4, 1, KJ, KS) AP_RK(5, 0, KJ, KS) U(1, 0, 0, 3, J), AP_RK(5, 1, KJ, KS) L3 AP_B(1, 0, 0, 3),                \
+    AP_RK(6, 0, KJ, KS) AP_RK(6, 1, KJ, KS) U(1, 0, 1, 0, J), AP_RK(7, 0, KJ, KS) L4 AP_B(1, 0, 1, 0),                \
+    AP_RK(7, 1, KJ, KS) U(1, 0, 1, 1, J), L5 AP_B(1, 0, 1, 1), U(1, 0, 1, 2, J), L6 AP_B(1, 0, 1, 2),                 \
     U(1, 0, 1, 3, J), L7 AP_B(1, 0, 1, 3)
-#define AP_L4 AP_LTILE AP_LK(0, 0, tl0) AP_LV(0, 0), AP_LK(0, 1, tl1) AP_LV(0, 1), AP_LK(0, 2, tl0) AP_LV(0, 2),         \
-    AP_LK(0, 3, tl1) AP_LV(0, 3), AP_LTILE AP_LK(1, 0, tl0) AP_LV(1, 0), AP_LK(1, 1, tl1) AP_LV(1, 1),                  \
-    AP_LK(1, 2, tl0) AP_LV(1, 2), AP_LK(1, 3, tl1) AP_LV(1, 3)
+#define AP_L4(ST) AP_LTILE AP_LK(ST, 0, 0, tl0) AP_LV(ST, 0, 0), AP_LK(ST, 0, 1, tl1) AP_LV(ST, 0, 1),                   \
+    AP_LK(ST, 0, 2, tl0) AP_LV(ST, 0, 2), AP_LK(ST, 0, 3, tl1) AP_LV(ST, 0, 3),                                        \
+    AP_LTILE AP_LK(ST, 1, 0, tl0) AP_LV(ST, 1, 0), AP_LK(ST, 1, 1, tl1) AP_LV(ST, 1, 1),                               \
+    AP_LK(ST, 1, 2, tl0) AP_LV(ST, 1, 2), AP_LK(ST, 1, 3, tl1) AP_LV(ST, 1, 3)
 #define AP_L4_NONE "", "", "", "", "", "", "", ""
+#define AP_LNONE(ST) AP_L4_NONE
 #define AP_X4_EXP(...) AP_X4(__VA_ARGS__)
 
 #define AP_WAIT_LDS "s_waitcnt lgkmcnt(0)\n"
-#define AP_SWAP                                                                                                   \
-    "v_swap_b32 %[kc0], %[kn0]\n v_swap_b32 %[kc1], %[kn1]\n v_swap_b32 %[kc2], %[kn2]\n v_swap_b32 %[kc3], %[kn3]\n" \
-    "v_swap_b32 %[kc4], %[kn4]\n v_swap_b32 %[kc5], %[kn5]\n v_swap_b32 %[kc6], %[kn6]\n v_swap_b32 %[kc7], %[kn7]\n" \
-    "v_swap_b32 %[vc0], %[vn0]\n v_swap_b32 %[vc1], %[vn1]\n v_swap_b32 %[vc2], %[vn2]\n v_swap_b32 %[vc3], %[vn3]\n" \
-    "s_xor_b32 %[mc], %[mc], 0x10000\n"
 
-// One group (sub-tiles 0 and 1). FIRST: group 0 (nothing of a previous
-// sub-tile in flight). U0 / U1: the part-A macro for the softmax of sub-tiles
-// 0 and 1 (AP_MA masks with lim0 / lim1), UP: for block 1's previous sub-tile
-// in phase 1 of sub-tile 0 (the last sub-tile of the previous group).
-#define AP_GROUP(UP, JP, U0, U1, L)                                                                               \
+// One group (sub-tiles 0 and 1) in stage ST, the next group in stage OT. U0 /
+// U1: the part-A macro for the softmax of sub-tiles 0 and 1 (AP_MA masks with
+// lim0 / lim1), UP: for block 1's previous sub-tile in phase 1 of sub-tile 0
+// (the last sub-tile of the previous group); LD: AP_L4 or AP_LNONE.
+#define AP_GROUP(UP, JP, U0, U1, L, ST, OT, LD)                                                                   \
     AP_PH_EXP(AP_SMFMA(0), AP_X1(UP, JP))                                                                         \
     AP_PH_EXP(AP_PVMFMA(1), AP_X2(AP_GEND(0, L##a), U0, 0))                                                       \
-    AP_PH_EXP(AP_SMFMA(1), AP_X3(AP_GEND(1, L##b), U0, 0))                                                        \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3(AP_GEND(1, L##b), U0, 0, ST))                                                    \
     AP_WAIT_LDS                                                                                                   \
-    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, c, U0, 0, AP_L4_NONE))                                                   \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, ST, U0, 0, AP_L4_NONE))                                                  \
     AP_WAIT_LDS                                                                                                   \
     AP_PH_EXP(AP_SMFMA(0), AP_X1(U0, 0))                                                                          \
     AP_PH_EXP(AP_PVMFMA(1), AP_X2("", U1, 1))                                                                     \
-    AP_PH_EXP(AP_SMFMA(1), AP_X3("", U1, 1))                                                                      \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", U1, 1, ST))                                                                  \
     "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
     "s_barrier\n"                                                                                                 \
-    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, n, U1, 1, AP_L4))                                                        \
-    AP_WAIT_LDS                                                                                                   \
-    AP_SWAP
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, OT, U1, 1, LD(ST)))                                                      \
+    AP_WAIT_LDS
 #define AP_GROUP_FIRST                                                                                            \
     AP_PH_EXP(AP_SMFMA(0), AP_X1_NONE)                                                                            \
     "s_nop 7\n s_nop 7\n s_nop 7\n"                                                                               \
     AP_CHUNK(0, 0, 0, AP_UA, 0) AP_CHUNK(0, 0, 1, AP_UA, 0)                                                       \
-    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 0))                                                                   \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 0, 0))                                                                \
     AP_WAIT_LDS                                                                                                   \
-    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, c, AP_UA, 0, AP_L4_NONE))                                                \
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(1, 0, AP_UA, 0, AP_L4_NONE))                                                \
     AP_WAIT_LDS                                                                                                   \
     AP_PH_EXP(AP_SMFMA(0), AP_X1(AP_UA, 0))                                                                       \
     AP_PH_EXP(AP_PVMFMA(1), AP_X2("", AP_UA, 1))                                                                  \
-    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 1))                                                                   \
+    AP_PH_EXP(AP_SMFMA(1), AP_X3("", AP_UA, 1, 0))                                                                \
     "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
     "s_barrier\n"                                                                                                 \
-    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, n, AP_UA, 1, AP_L4))                                                     \
-    AP_WAIT_LDS                                                                                                   \
-    AP_SWAP
+    AP_PH_EXP(AP_PVMFMA(0), AP_X4_EXP(0, 1, AP_UA, 1, AP_L4(0)))                                                  \
+    AP_WAIT_LDS
+// Moves the fragment bases from stage 0 to stage 1, for a last group in
+// stage 1 (its code is written for stage 0).
+#define AP_BASE1 "v_add_u32 %[kb0], 0x8000, %[kb0]\n v_add_u32 %[kb1], 0x8000, %[kb1]\n"                              \
+    "v_add_u32 %[kb2], 0x8000, %[kb2]\n v_add_u32 %[kb3], 0x8000, %[kb3]\n v_add_u32 %[kb4], 0x8000, %[kb4]\n"         \
+    "v_add_u32 %[kb5], 0x8000, %[kb5]\n v_add_u32 %[kb6], 0x8000, %[kb6]\n v_add_u32 %[kb7], 0x8000, %[kb7]\n"         \
+    "v_add_u32 %[vb0], 0x8000, %[vb0]\n v_add_u32 %[vb1], 0x8000, %[vb1]\n v_add_u32 %[vb2], 0x8000, %[vb2]\n"         \
+    "v_add_u32 %[vb3], 0x8000, %[vb3]\n"
 // Last sub-tile of the last group: block 1's softmax (masked with lim1) and
 // P.V, both blocks' group ends, and a wait for every MFMA result before the
 // accumulators leave the asm block.
@@ -1059,6 +1061,7 @@ void attn_bf16_pipe(Args a) {
     const unsigned kstride = (unsigned)(stride * 2);
     const unsigned lk = 4 * wave + lane / 16, ld = 8 * wave + lane / 8;
     const unsigned koff = lk * kstride + k_chunk(lk, lane % 16) * 16;
+    const unsigned ko1 = koff + 16 * kstride, ko2 = koff + 32 * kstride, ko3 = koff + 48 * kstride;
     const unsigned voff = (ld * a.padded + v_chunk(ld, lane % 8) * 8) * 2;
     const i32x4 kr = {(int)__builtin_amdgcn_readfirstlane((unsigned)(uint64_t)a.k),
                       (int)__builtin_amdgcn_readfirstlane((unsigned)((uint64_t)a.k >> 32)),
@@ -1068,14 +1071,14 @@ void attn_bf16_pipe(Args a) {
                       (int)__builtin_amdgcn_readfirstlane((unsigned)((size_t)a.heads * D * a.padded * 2)), 0x00020000};
     const unsigned hk = __builtin_amdgcn_readfirstlane(head * D * 2);
     const unsigned hv = __builtin_amdgcn_readfirstlane(head * D * a.padded * 2);
-    const unsigned k64 = __builtin_amdgcn_readfirstlane(64 * kstride), k16 = __builtin_amdgcn_readfirstlane(16 * kstride);
+    const unsigned k64 = __builtin_amdgcn_readfirstlane(64 * kstride);
     const unsigned v32 = __builtin_amdgcn_readfirstlane(32 * a.padded * 2);
     const unsigned tmax = count - 1;
     // Tiles 0..3 (groups 0 and 1) into stages 0 and 1.
 #pragma unroll
     for (int t4 = 0; t4 < 4; t4++) {
         const unsigned tile = min((unsigned)t4, tmax);
-        uint8_t *base = smem + (t4 / 2) * PIPE_STAGE + (t4 % 2) * K_BYTES;
+        uint8_t *base = smem + (t4 / 2) * 2 * K_BYTES + (t4 % 2) * K_BYTES;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const unsigned key = tile * BN + 16 * t + lk;
@@ -1085,26 +1088,20 @@ void attn_bf16_pipe(Args a) {
                 key < a.seq ? koff : BUFFER_OOB, hk + (tile * BN + 16 * t) * kstride, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 *reinterpret_cast<const __amdgpu_buffer_rsrc_t *>(&vr),
-                (__attribute__((address_space(3))) void *)(base + 2 * K_BYTES + (wave + 4 * t) * 1024), 16, voff,
+                (__attribute__((address_space(3))) void *)(base + PIPE_STAGE + (wave + 4 * t) * 1024), 16, voff,
                 hv + 32 * t * a.padded * 2 + tile * BN * 2, 0, 0);
         }
     }
     wait_vm_loads();
     __syncthreads();
 
-    // Fragment bases per stage: K fragment (ks, mb) at kb + 8 KB mb (+ 16 KB
-    // per tile), V^T fragment (kk, md) at vb + 32 KB + 4 KB md.
-    unsigned kc[8], kn[8], vc[4], vn[4];
+    // Fragment bases (stage 0, tile 0): K fragment (ks, mb) at kb + 8 KB mb,
+    // V^T fragment (kk, md) at vb + 4 KB md.
+    unsigned kc[8], vc[4];
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-        kc[ks] = n * 256 + k_chunk(n, 2 * ks + hf) * 16;
-        kn[ks] = kc[ks] + PIPE_STAGE;
-    }
+    for (int ks = 0; ks < 8; ks++) kc[ks] = n * 256 + k_chunk(n, 2 * ks + hf) * 16;
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-        vc[kk] = n * 128 + v_chunk(n, 2 * kk + hf) * 16;
-        vn[kk] = vc[kk] + PIPE_STAGE;
-    }
+    for (int kk = 0; kk < 4; kk++) vc[kk] = PIPE_STAGE + n * 128 + v_chunk(n, 2 * kk + hf) * 16;
 
     // The running max of each block: the first group's score max (as the
     // wide kernel's first group sets it from m = -1e30).
@@ -1137,43 +1134,52 @@ void attn_bf16_pipe(Args a) {
     for (int md = 0; md < 4; md++) { o0[md] = f32x16{}; o1[md] = f32x16{}; }
     float l0 = 0.f, l1 = 0.f, ps0 = 0.f, ps1 = 0.f;
     int r0 = 0, r1 = 0, f0 = 0, f1 = 0;
-    unsigned mc = __builtin_amdgcn_readfirstlane(wave * 1024);   // loads of group g + 2 go to stage g & 1
-    unsigned lt = 4, gl = groups - 2;
+    const unsigned mc = __builtin_amdgcn_readfirstlane(wave * 1024);   // this wave's 1 KB load blocks
+    unsigned lt = 4, gl = groups - 2;                                    // gl: groups between the first and last
+    const unsigned last_stage = (groups - 1) & 1;
     const unsigned last0 = 2 * (groups - 1) * BN;
     const int lim0 = (int)a.seq - (int)last0 - 4 * (int)hf, lim1 = lim0 - BN;
-    const unsigned oob = BUFFER_OOB;
     const float ninf = -INFINITY;
     float t0, t1, u0, u1;
-    unsigned tl0, tl1, tt, sk, sl, sv;
+    unsigned tl0, tl1, tt, sk, sv;
+    // Group 0 in stage 0; the middle groups in a loop of two groups (stages
+    // 1, 0) left after its first half when their count is odd; the last group
+    // (no loads) in stage-0 code, its bases moved to stage 1 when it is there.
     asm volatile(
-        AP_RK(0, 0, 0, c) AP_RK(0, 1, 0, c) AP_RK(1, 0, 0, c) AP_RK(1, 1, 0, c) AP_RK(2, 0, 0, c) AP_RK(2, 1, 0, c)
-        AP_RK(3, 0, 0, c) AP_RK(3, 1, 0, c) AP_RK(4, 0, 0, c) AP_RK(4, 1, 0, c) AP_RK(5, 0, 0, c) AP_RK(5, 1, 0, c)
-        AP_RK(6, 0, 0, c) AP_RK(6, 1, 0, c) AP_RK(7, 0, 0, c) AP_RK(7, 1, 0, c)
+        AP_RK(0, 0, 0, 0) AP_RK(0, 1, 0, 0) AP_RK(1, 0, 0, 0) AP_RK(1, 1, 0, 0) AP_RK(2, 0, 0, 0) AP_RK(2, 1, 0, 0)
+        AP_RK(3, 0, 0, 0) AP_RK(3, 1, 0, 0) AP_RK(4, 0, 0, 0) AP_RK(4, 1, 0, 0) AP_RK(5, 0, 0, 0) AP_RK(5, 1, 0, 0)
+        AP_RK(6, 0, 0, 0) AP_RK(6, 1, 0, 0) AP_RK(7, 0, 0, 0) AP_RK(7, 1, 0, 0)
         AP_WAIT_LDS
         AP_GROUP_FIRST
         "s_cmp_eq_u32 %[gl], 0\n"
         "s_cbranch_scc1 ap_loop_end_%=\n"
         "ap_loop_%=:\n"
-        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gn)
+        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gp, 1, 0, AP_L4)
+        "s_sub_u32 %[gl], %[gl], 1\n"
+        "s_cmp_eq_u32 %[gl], 0\n"
+        "s_cbranch_scc1 ap_loop_end_%=\n"
+        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gq, 0, 1, AP_L4)
         "s_sub_u32 %[gl], %[gl], 1\n"
         "s_cmp_lg_u32 %[gl], 0\n"
         "s_cbranch_scc1 ap_loop_%=\n"
         "ap_loop_end_%=:\n"
-        AP_GROUP(AP_UA, 0, AP_MA, AP_MA, gl)
+        "s_cmp_eq_u32 %[ls], 0\n"
+        "s_cbranch_scc1 ap_last0_%=\n"
+        AP_BASE1
+        "ap_last0_%=:\n"
+        AP_GROUP(AP_UA, 0, AP_MA, AP_MA, gl, 0, 1, AP_LNONE)
         AP_TAIL
         : [o00] "+{v[64:79]}"(o0[0]), [o01] "+{v[80:95]}"(o0[1]), [o02] "+{v[96:111]}"(o0[2]),
           [o03] "+{v[112:127]}"(o0[3]), [o10] "+{v[128:143]}"(o1[0]), [o11] "+{v[144:159]}"(o1[1]),
           [o12] "+{v[160:175]}"(o1[2]), [o13] "+{v[176:191]}"(o1[3]),
           [nm0] "+v"(nm[0]), [nm1] "+v"(nm[1]), [l0] "+v"(l0), [l1] "+v"(l1), [ps0] "+v"(ps0), [ps1] "+v"(ps1),
           [r0] "+v"(r0), [r1] "+v"(r1), [f0] "+v"(f0), [f1] "+v"(f1),
-          [kc0] "+v"(kc[0]), [kc1] "+v"(kc[1]), [kc2] "+v"(kc[2]), [kc3] "+v"(kc[3]), [kc4] "+v"(kc[4]),
-          [kc5] "+v"(kc[5]), [kc6] "+v"(kc[6]), [kc7] "+v"(kc[7]), [kn0] "+v"(kn[0]), [kn1] "+v"(kn[1]),
-          [kn2] "+v"(kn[2]), [kn3] "+v"(kn[3]), [kn4] "+v"(kn[4]), [kn5] "+v"(kn[5]), [kn6] "+v"(kn[6]),
-          [kn7] "+v"(kn[7]), [vc0] "+v"(vc[0]), [vc1] "+v"(vc[1]), [vc2] "+v"(vc[2]), [vc3] "+v"(vc[3]),
-          [vn0] "+v"(vn[0]), [vn1] "+v"(vn[1]), [vn2] "+v"(vn[2]), [vn3] "+v"(vn[3]),
-          [mc] "+s"(mc), [lt] "+s"(lt), [gl] "+s"(gl),
+          [kb0] "+v"(kc[0]), [kb1] "+v"(kc[1]), [kb2] "+v"(kc[2]), [kb3] "+v"(kc[3]), [kb4] "+v"(kc[4]),
+          [kb5] "+v"(kc[5]), [kb6] "+v"(kc[6]), [kb7] "+v"(kc[7]), [vb0] "+v"(vc[0]), [vb1] "+v"(vc[1]),
+          [vb2] "+v"(vc[2]), [vb3] "+v"(vc[3]),
+          [lt] "+s"(lt), [gl] "+s"(gl),
           [t0] "=&v"(t0), [t1] "=&v"(t1), [u0] "=&v"(u0), [u1] "=&v"(u1), [tl0] "=&v"(tl0), [tl1] "=&v"(tl1),
-          [tt] "=&s"(tt), [sk] "=&s"(sk), [sl] "=&s"(sl), [sv] "=&s"(sv)
+          [tt] "=&s"(tt), [sk] "=&s"(sk), [sv] "=&s"(sv)
         : [q00] "{a[128:131]}"(qf[0][0]), [q01] "{a[132:135]}"(qf[0][1]), [q02] "{a[136:139]}"(qf[0][2]),
           [q03] "{a[140:143]}"(qf[0][3]), [q04] "{a[144:147]}"(qf[0][4]), [q05] "{a[148:151]}"(qf[0][5]),
           [q06] "{a[152:155]}"(qf[0][6]), [q07] "{a[156:159]}"(qf[0][7]), [q10] "{a[160:163]}"(qf[1][0]),
@@ -1181,9 +1187,9 @@ void attn_bf16_pipe(Args a) {
           [q14] "{a[176:179]}"(qf[1][4]), [q15] "{a[180:183]}"(qf[1][5]), [q16] "{a[184:187]}"(qf[1][6]),
           [q17] "{a[188:191]}"(qf[1][7]),
           [c] "s"(c), [kr] "s"(kr), [vr] "s"(vr), [tmax] "s"(tmax), [k64] "s"(k64), [hk] "s"(hk),
-          [seq] "s"(a.seq), [hv] "s"(hv), [k16] "s"(k16), [v32] "s"(v32),
-          [lk] "v"(lk), [oob] "v"(oob), [ko] "v"(koff), [vo] "v"(voff), [ninf] "v"(ninf), [lim0] "v"(lim0),
-          [lim1] "v"(lim1)
+          [hv] "s"(hv), [v32] "s"(v32), [mc] "s"(mc), [ls] "s"(last_stage),
+          [ko0] "v"(koff), [ko1] "v"(ko1), [ko2] "v"(ko2), [ko3] "v"(ko3), [vo] "v"(voff), [ninf] "v"(ninf),
+          [lim0] "v"(lim0), [lim1] "v"(lim1)
         : AP_CLOBBERS);
 
     // Output: O^T / l for each block; rows whose row sum overflowed (or whose
