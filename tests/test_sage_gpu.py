@@ -151,11 +151,12 @@ def test_global_load_path_matches_buffer_path(gpu, monkeypatch, seq, heads):
         g13.close()
 
 
-@pytest.mark.parametrize("variant", ["1", "2"])
+@pytest.mark.parametrize("variant", ["1", "2", "14"])
 def test_launch_shapes_match(gpu, monkeypatch, variant):
     """Attention variants 1 and 2 launch the Sage kernel as 8 and 12 waves per
-    workgroup instead of 4. Every 32-query wave walks the same tiles with the
-    same arithmetic, so the outputs are bit-identical, also on an input whose
+    workgroup, variant 14 as 4 waves of 32 queries, instead of the
+    hand-scheduled kernel (4 waves of 64 queries). Every 32-query block walks
+    the same tiles with the same arithmetic, so the outputs are bit-identical, also on an input whose
     logit scale sends every wave through the exact recomputation launch
     (S = 300, where the retry bytes of the three shapes are laid out
     differently)."""
@@ -173,3 +174,30 @@ def test_launch_shapes_match(gpu, monkeypatch, variant):
         assert np.array_equal(sdpa(gv, qb, kb, v, seq, heads), ref[1])
     finally:
         gv.close()
+
+
+@pytest.mark.parametrize("case", ["257x3", "1000x3", "2500x2", "4100x3", "gain30", "gain60", "gain400"])
+def test_scheduled_kernel_matches_four_wave_kernel(gpu, monkeypatch, case):
+    """Dense Sage above 256 keys runs the hand-scheduled kernel; variant 14
+    forces the compiler-scheduled 4-wave kernel. Same integer scores, maxima,
+    exponentials and fp8 packs in the same order: bit-identical outputs, on
+    ragged tails (an odd tile count ends in a fully masked tile), and at logit
+    scales that raise the running max often (gain 30, 60) or send every wave
+    to the exact recomputation launch (gain 400)."""
+    if case.startswith("gain"):
+        seq, heads, gain = 1000, 2, float(case[4:])
+        q, k, v = sage_inputs(seq, heads, seed=11)
+        q = synth.f32_to_bf16(bf16(q) * gain)
+        k = synth.f32_to_bf16(bf16(k) * gain)
+    else:
+        seq, heads = map(int, case.split("x"))
+        q, k, v = sage_inputs(seq, heads, seed=seq + 5)
+    print(f"[sage scheduled vs 4-wave] {case}", flush=True)
+    pipe = sdpa(gpu, q, k, v, seq, heads)
+    monkeypatch.setenv("H3_HIP_ATTENTION_VARIANT", "14")
+    g14 = Gpu()
+    try:
+        g14.check(g14.lib.h3_gpu_dit_attention_configure(g14.handle, 1), "configure sage2++")
+        assert np.array_equal(sdpa(g14, q, k, v, seq, heads), pipe)
+    finally:
+        g14.close()
