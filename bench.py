@@ -532,6 +532,44 @@ def probe():
     log("[probe] 2 attention launches (S=32400, H=40) + 1 GiB device copy done")
 
 
+def probe_gemm(which, m=32400, k=5120, n=15360):
+    """Launches for SQ counters on config 4's QKV shape, nothing timed: this
+    library's W8A16 projection twice (dequantization + GEMM), or, as the
+    calibration point, hipBLASLt's BF16 GEMM (torch.matmul on BF16 weights of
+    the same shape) twice. The hipBLASLt probe never loads this library (two
+    HIP runtimes in one process do not share the device)."""
+    if which == "hipblaslt":
+        import torch
+        x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        w = torch.randn(n, k, device="cuda", dtype=torch.bfloat16) * 0.02
+        for _ in range(2):
+            y = torch.matmul(x, w.t())
+        torch.cuda.synchronize()
+        log(f"[probe-gemm] hipBLASLt BF16 {m}x{k}x{n} twice, finite={bool(torch.isfinite(y).all())}")
+        return
+    from h3cli_amd.runtime import Gpu, Tensor
+    with Gpu() as gpu:
+        lib = gpu.lib
+        x = gpu.empty(m * k)
+        gpu.begin()
+        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, 64, 1.0, m * k), "fill")
+        gpu.submit()
+        rng = np.random.default_rng(4)
+        codes = rng.integers(-127, 128, size=n * k, dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+        h = lib.h3_hip_q8_from_packed(gpu.handle, codes.ctypes.data, scales.ctypes.data, n, k, k)
+        if not h:
+            raise RuntimeError(gpu.error())
+        w = Tensor(gpu, h, n * k, 2)
+        gpu.tensors.append(w)
+        y = gpu.empty(m * n)
+        gpu.begin()
+        for _ in range(2):
+            gpu.check(lib.h3_gpu_linear_bf16(gpu.handle, y.handle, x.handle, w.handle, None, m, k, n), "W8A16 GEMM")
+        gpu.submit()
+    log(f"[probe-gemm] W8A16 {m}x{k}x{n} twice")
+
+
 def profile_step():
     """One warmup and one timed config-5 step (blocks 20-39 streamed), nothing
     else: the program to run under `rocprofv3 --kernel-trace
@@ -556,6 +594,8 @@ def main():
     ap.add_argument("--probe", action="store_true",
                     help="counter probe for rocprofv3 --pmc: two attention launches and one 1 GiB device copy "
                          "(the calibration kernel), nothing timed")
+    ap.add_argument("--probe-gemm", choices=["h3", "hipblaslt"],
+                    help="counter probe: config 4's QKV projection twice, this library's or hipBLASLt's BF16 GEMM")
     ap.add_argument("--profile-step", action="store_true",
                     help="two config-5 steps with streamed weights and nothing else, for a rocprofv3 trace")
     args = ap.parse_args()
@@ -564,6 +604,9 @@ def main():
               "(multi-GPU sharding is a design note, not part of this build).", file=sys.stderr)
         sys.exit(2)
 
+    if args.probe_gemm:
+        probe_gemm(args.probe_gemm)
+        return
     from h3cli_amd.runtime import Gpu
     if args.probe:
         probe()
