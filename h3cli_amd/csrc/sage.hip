@@ -542,28 +542,34 @@ void sage_attn_kernel(SArgs a) {
 // four waves of 64 queries (two 32-query blocks b = 0, 1), so every K or V
 // fragment read from LDS feeds two MFMAs. The softmax VALU work of one block
 // (integer row max, the raise test, 32 exponentials and 16 fp8 packs per
-// lane) is as long as the MFMA work of both, so the key sweep is one
-// inline-asm block whose order overlaps them. Per 64-key tile j the MFMA
-// stream is
+// lane) is longer than the MFMA work of both, so the key sweep is one
+// inline-asm block ordered for the VALU: independent chains for the row max,
+// and the exponentials software-pipelined over groups of four scores (fmas
+// of group k, exponentials of group k - 1, packs of group k - 2), so that no
+// instruction waits on the one before it. Per 64-key tile j the MFMA stream is
 //   S0(j) | PV1(j-1) | S1(j) | PV0(j)
 // (S: 8 int8 MFMAs; PV: 4 fp8 MFMAs and the row-sum MFMA), and block b's
-// softmax of tile j runs under the two phases after its scores. V fragments
-// of tile j are read under S1(j), K fragments of tile j + 1 under PV0(j).
-// Groups of two tiles share a barrier, after the group's last V read; the
-// tiles two groups ahead are loaded right after it into the stage just
-// released. The loop body holds two groups, one per LDS stage.
+// softmax of tile j runs under the two phases after its scores. Fragment
+// registers are double-buffered by tile parity, so the V fragments of tile j
+// are read under S0(j) and the K fragments of tile j + 1 a phase or two
+// before their MFMAs. Groups of four tiles share a barrier (after phase 2 of
+// their last tile); the tiles two groups ahead are loaded in that tile's
+// phase 4 into the stage just released. Fragment bases carry the stage (bit
+// 15), flipped after every group, so the loop body is one group.
 //
 // Fixed registers inside the sweep:
 //   v[0:31]    scores / P of block 0 (P packed in v[0:7]), v[32:63] block 1;
 //   v[64:127]  O^T of block 0 (4 channel blocks of 16), v[128:191] block 1;
 //   v[192:207] the biased accumulator start (1.5 * 2^23 as float bits);
-//   v[208:215] the row-sum ones matrix; v[216:219], v[220:223] the row sums;
-//   a[0:31]    K fragments (k-step ks, key half mb) of a tile;
-//   a[32:63]   V fragments (channel block md: 8 registers);
-//   a[64:95]   Q fragments (block b, k-step ks).
-// LDS (64 KB): K tile j of stage s at 16 KB s + 8 KB j, V tile j of stage s
-// at 32 KB + 16 KB s + 8 KB j, in sage_attn_kernel's swizzled layouts.
-constexpr int SP_STAGE = 2 * Q8_TILE;   // 16 KB: the K (or V) tiles of one group
+//   v[216:219], v[220:223] the row sums of blocks 0 and 1;
+//   a[0:63]    K fragments of a tile (set s = tile parity at 32 s; k-step ks,
+//              key half mb at 8 ks + 4 mb);
+//   a[64:127]  V fragments (set s at 64 + 32 s; channel block md at 8 md);
+//   a[128:159] Q fragments (block b, k-step ks); a[160:167] the row-sum ones.
+// LDS (128 KB): K tile j of stage s at 32 KB s + 8 KB j, V tile j of stage s
+// at 64 KB + 32 KB s + 8 KB j, in sage_attn_kernel's swizzled layouts.
+constexpr int SP_GROUP_TILES = 4;
+constexpr int SP_STAGE = SP_GROUP_TILES * Q8_TILE;   // 32 KB: the K (or V) tiles of one group
 constexpr int SP_LDS = 4 * SP_STAGE;
 
 #define SP_S(b, mb) "v[32*" #b "+16*" #mb ":32*" #b "+16*" #mb "+15]"
@@ -573,66 +579,78 @@ constexpr int SP_LDS = 4 * SP_STAGE;
 #define SP_OR(b, md, e) "v[64+64*" #b "+16*" #md "+" #e "]"
 #define SP_L(b) "v[216+4*" #b ":219+4*" #b "]"
 #define SP_LR(b, e) "v[216+4*" #b "+" #e "]"
-#define SP_K(ks, mb) "a[8*" #ks "+4*" #mb ":8*" #ks "+4*" #mb "+3]"
-#define SP_V(md) "a[32+8*" #md ":39+8*" #md "]"
-#define SP_VH(md, h) "a[32+8*" #md "+4*" #h ":35+8*" #md "+4*" #h "]"
-#define SP_Q(b, ks) "a[64+16*" #b "+4*" #ks ":67+16*" #b "+4*" #ks "]"
+#define SP_K(ks, mb, s) "a[32*" #s "+8*" #ks "+4*" #mb ":32*" #s "+8*" #ks "+4*" #mb "+3]"
+#define SP_V(md, s) "a[64+32*" #s "+8*" #md ":71+32*" #s "+8*" #md "]"
+#define SP_VH(md, h, s) "a[64+32*" #s "+8*" #md "+4*" #h ":67+32*" #s "+8*" #md "+4*" #h "]"
+#define SP_Q(b, ks) "a[128+16*" #b "+4*" #ks ":131+16*" #b "+4*" #ks "]"
 
-// MFMAs. Scores start from the biased block (k-step 0) and accumulate.
-#define SP_SM(b, ks, mb) "v_mfma_i32_32x32x32_i8 " SP_S(b, mb) ", " SP_K(ks, mb) ", " SP_Q(b, ks) ", " SP_S(b, mb) "\n"
-#define SP_SM0(b, mb) "v_mfma_i32_32x32x32_i8 " SP_S(b, mb) ", " SP_K(0, mb) ", " SP_Q(b, 0) ", v[192:207]\n"
-#define SP_PVM(b, md) "v_mfma_f32_32x32x64_f8f6f4 " SP_O(b, md) ", " SP_V(md) ", " SP_P(b) ", " SP_O(b, md) "\n"
-#define SP_RSM(b) "v_mfma_f32_16x16x128_f8f6f4 " SP_L(b) ", v[208:215], " SP_P(b) ", " SP_L(b) "\n"
-#define SP_SMFMA(b) SP_SM0(b, 0), SP_SM0(b, 1), SP_SM(b, 1, 0), SP_SM(b, 1, 1), SP_SM(b, 2, 0), SP_SM(b, 2, 1),        \
-    SP_SM(b, 3, 0), SP_SM(b, 3, 1)
-#define SP_PVMFMA(b) SP_PVM(b, 0), SP_PVM(b, 1), SP_PVM(b, 2), SP_PVM(b, 3), SP_RSM(b)
+// MFMAs (s: the fragment set). Scores start from the biased block.
+#define SP_SM(b, ks, mb, s) "v_mfma_i32_32x32x32_i8 " SP_S(b, mb) ", " SP_K(ks, mb, s) ", " SP_Q(b, ks) ", " SP_S(b, mb) "\n"
+#define SP_SM0(b, mb, s) "v_mfma_i32_32x32x32_i8 " SP_S(b, mb) ", " SP_K(0, mb, s) ", " SP_Q(b, 0) ", v[192:207]\n"
+#define SP_PVM(b, md, s) "v_mfma_f32_32x32x64_f8f6f4 " SP_O(b, md) ", " SP_V(md, s) ", " SP_P(b) ", " SP_O(b, md) "\n"
+#define SP_RSM(b) "v_mfma_f32_16x16x128_f8f6f4 " SP_L(b) ", a[160:167], " SP_P(b) ", " SP_L(b) "\n"
+#define SP_SMFMA(b, s) SP_SM0(b, 0, s), SP_SM0(b, 1, s), SP_SM(b, 1, 0, s), SP_SM(b, 1, 1, s), SP_SM(b, 2, 0, s),   \
+    SP_SM(b, 2, 1, s), SP_SM(b, 3, 0, s), SP_SM(b, 3, 1, s)
+#define SP_PVMFMA(b, s) SP_PVM(b, 0, s), SP_PVM(b, 1, s), SP_PVM(b, 2, s), SP_PVM(b, 3, s), SP_RSM(b)
 #define SP_NOMFMA8 "", "", "", "", "", "", "", ""
 #define SP_NOMFMA5 "", "", "", "", ""
-// Phases: MFMA M_k, then extra E_k.
-#define SP_PH8(M0, M1, M2, M3, M4, M5, M6, M7, E0, E1, E2, E3, E4, E5, E6, E7)                                  \
-    M0 E0 M1 E1 M2 E2 M3 E3 M4 E4 M5 E5 M6 E6 M7 E7
-#define SP_PH5(M0, M1, M2, M3, M4, E0, E1, E2, E3, E4) M0 E0 M1 E1 M2 E2 M3 E3 M4 E4
+#define SP_NONE8 "", "", "", "", "", "", "", ""
+#define SP_NONE5 "", "", "", "", ""
+// Phases: MFMA M_k, then extra E_k (and a second extra list F_k).
+#define SP_PH8(M0, M1, M2, M3, M4, M5, M6, M7, E0, E1, E2, E3, E4, E5, E6, E7, F0, F1, F2, F3, F4, F5, F6, F7)  \
+    M0 E0 F0 M1 E1 F1 M2 E2 F2 M3 E3 F3 M4 E4 F4 M5 E5 F5 M6 E6 F6 M7 E7 F7
+#define SP_PH5(M0, M1, M2, M3, M4, E0, E1, E2, E3, E4, F0, F1, F2, F3, F4) M0 E0 F0 M1 E1 F1 M2 E2 F2 M3 E3 F3 M4 E4 F4
 #define SP_PH8_EXP(...) SP_PH8(__VA_ARGS__)
 #define SP_PH5_EXP(...) SP_PH5(__VA_ARGS__)
 
 // Keys at or past S (last group): score i of block b is key tile*64 + 32 (i / 16)
-// + 8 ((i % 16) / 4) + 4 hf + i % 4; lim<J> = S - tile*64 - 4 hf.
+// + 8 ((i % 16) / 4) + 4 hf + i % 4; lim<J> = S - tile*64 - 4 hf (tile J of
+// the group).
 #define SP_KEEP(b, i, J)                                                                                          \
     "v_cmp_lt_i32 vcc, 32*((" #i ")/16)+8*(((" #i ")%%16)/4)+((" #i ")%%4), %[lim" #J "]\n"                          \
     "v_cndmask_b32 " SP_R(b, i) ", %[masked], " SP_R(b, i) ", vcc\n"
 #define SP_KEEP8(b, i, J) SP_KEEP(b, i, J) SP_KEEP(b, i+1, J) SP_KEEP(b, i+2, J) SP_KEEP(b, i+3, J)               \
     SP_KEEP(b, i+4, J) SP_KEEP(b, i+5, J) SP_KEEP(b, i+6, J) SP_KEEP(b, i+7, J)
-#define SP_MASK(b, J) "s_nop 7\n s_nop 7\n s_nop 7\n" SP_KEEP8(b, 0, J) SP_KEEP8(b, 8, J) SP_KEEP8(b, 16, J) SP_KEEP8(b, 24, J)
+#define SP_MASK(b, J) "s_nop 7\n s_nop 7\n s_nop 7\n" SP_KEEP8(b, 0, J) SP_KEEP8(b, 8, J) SP_KEEP8(b, 16, J)         \
+    SP_KEEP8(b, 24, J)
 #define SP_NOMASK(b, J) ""
 
-// Softmax of block b, first part: c = qs k_scale(tile); the raise threshold
-// m + (2 - (1.5 * 2^23 c + 2 |m| + 16) 2^-23); the integer row max of the 32
-// biased scores (two chains).
-#define SP_MA(b)                                                                                                  \
-    "v_mul_f32 %[c" #b "], %[sks], %[qs]\n"                                                                       \
+// Softmax of block b, first part: c = k_scale(tile) qs (the tile's scale in
+// sks<J>); the raise threshold m + (2 - (1.5 * 2^23 c + 2 |m| + 16) 2^-23);
+// the integer row max of key half 0 as two chains (u: scores 0-7, x: 8-15).
+// The scale register of tile J of a group (tiles alternate sks0, sks1).
+#define SP_SKS_0 "sks0"
+#define SP_SKS_1 "sks1"
+#define SP_SKS_2 "sks0"
+#define SP_SKS_3 "sks1"
+#define SP_SKS(J) SP_SKS_##J
+#define SP_MA(b, J)                                                                                               \
+    "v_mul_f32 %[c" #b "], %[" SP_SKS(J) "], %[qs]\n"                                                                 \
     "v_fma_f32 %[t" #b "], |%[rm" #b "]|, 2.0, %[k16]\n"                                                          \
     "v_max_i32 %[u" #b "], " SP_R(b, 0) ", " SP_R(b, 1) "\n"                                                      \
+    "v_max_i32 %[x" #b "], " SP_R(b, 8) ", " SP_R(b, 9) "\n"                                                      \
     "v_fmac_f32 %[t" #b "], 0x4b400000, %[c" #b "]\n"                                                             \
     "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 2) ", " SP_R(b, 3) "\n"                                         \
+    "v_max3_i32 %[x" #b "], %[x" #b "], " SP_R(b, 10) ", " SP_R(b, 11) "\n"                                       \
     "v_fma_f32 %[t" #b "], %[t" #b "], %[nk23], 2.0\n"                                                            \
     "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 4) ", " SP_R(b, 5) "\n"                                         \
+    "v_max3_i32 %[x" #b "], %[x" #b "], " SP_R(b, 12) ", " SP_R(b, 13) "\n"                                       \
     "v_add_f32 %[t" #b "], %[rm" #b "], %[t" #b "]\n"                                                             \
     "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 6) ", " SP_R(b, 7) "\n"                                         \
-    "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 8) ", " SP_R(b, 9) "\n"                                         \
-    "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 10) ", " SP_R(b, 11) "\n"                                       \
-    "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 12) ", " SP_R(b, 13) "\n"                                       \
-    "v_max3_i32 %[u" #b "], %[u" #b "], " SP_R(b, 14) ", " SP_R(b, 15) "\n"
-// (key half 1, written by the phase's last MFMA, is read a slot later)
+    "v_max3_i32 %[x" #b "], %[x" #b "], " SP_R(b, 14) ", " SP_R(b, 15) "\n"
+// Key half 1 (written by the phase's last MFMA, read a slot later) as two
+// chains (w: 16-23, y: 24-31), then the four combined.
 #define SP_MB(b)                                                                                                  \
     "v_max_i32 %[w" #b "], " SP_R(b, 16) ", " SP_R(b, 17) "\n"                                                    \
+    "v_max_i32 %[y" #b "], " SP_R(b, 24) ", " SP_R(b, 25) "\n"                                                    \
     "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 18) ", " SP_R(b, 19) "\n"                                       \
+    "v_max3_i32 %[y" #b "], %[y" #b "], " SP_R(b, 26) ", " SP_R(b, 27) "\n"                                       \
     "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 20) ", " SP_R(b, 21) "\n"                                       \
+    "v_max3_i32 %[y" #b "], %[y" #b "], " SP_R(b, 28) ", " SP_R(b, 29) "\n"                                       \
     "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 22) ", " SP_R(b, 23) "\n"                                       \
-    "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 24) ", " SP_R(b, 25) "\n"                                       \
-    "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 26) ", " SP_R(b, 27) "\n"                                       \
-    "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 28) ", " SP_R(b, 29) "\n"                                       \
-    "v_max3_i32 %[w" #b "], %[w" #b "], " SP_R(b, 30) ", " SP_R(b, 31) "\n"                                       \
-    "v_max_i32 %[u" #b "], %[u" #b "], %[w" #b "]\n"
+    "v_max3_i32 %[y" #b "], %[y" #b "], " SP_R(b, 30) ", " SP_R(b, 31) "\n"                                       \
+    "v_max3_i32 %[u" #b "], %[u" #b "], %[x" #b "], %[w" #b "]\n"                                                 \
+    "v_max_i32 %[u" #b "], %[u" #b "], %[y" #b "]\n"
 // Second part: the max over both 32-lane halves, mx = (max - 1.5 * 2^23) c;
 // when some lane's mx passes the threshold (rare), m = max(m, mx) and l and
 // O^T scale by 2^(m_old - m) (after the block's P.V MFMAs in flight); then
@@ -647,10 +665,10 @@ constexpr int SP_LDS = 4 * SP_STAGE;
     "v_cmp_gt_f32 vcc, %[u" #b "], %[t" #b "]\n"                                                                  \
     "s_cbranch_vccz sp_" #L "_%=\n"                                                                               \
     "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"                             \
-    "v_max_f32 %[u" #b "], %[rm" #b "], %[u" #b "]\n"                                                              \
-    "v_sub_f32 %[w" #b "], %[rm" #b "], %[u" #b "]\n"                                                              \
+    "v_max_f32 %[u" #b "], %[rm" #b "], %[u" #b "]\n"                                                             \
+    "v_sub_f32 %[w" #b "], %[rm" #b "], %[u" #b "]\n"                                                             \
     "v_exp_f32 %[w" #b "], %[w" #b "]\n"                                                                          \
-    "v_mov_b32 %[rm" #b "], %[u" #b "]\n"                                                                          \
+    "v_mov_b32 %[rm" #b "], %[u" #b "]\n"                                                                         \
     "s_nop 1\n"                                                                                                   \
     "v_mul_f32 " SP_LR(b, 0) ", " SP_LR(b, 0) ", %[w" #b "]\n"                                                    \
     "v_mul_f32 " SP_LR(b, 1) ", " SP_LR(b, 1) ", %[w" #b "]\n"                                                    \
@@ -658,45 +676,55 @@ constexpr int SP_LDS = 4 * SP_STAGE;
     "v_mul_f32 " SP_LR(b, 3) ", " SP_LR(b, 3) ", %[w" #b "]\n"                                                    \
     SP_OMUL16(b, 0) SP_OMUL16(b, 1) SP_OMUL16(b, 2) SP_OMUL16(b, 3)                                               \
     "sp_" #L "_%=:\n"                                                                                             \
-    "v_sub_f32 %[t" #b "], 0x40d9d5da, %[rm" #b "]\n"                                                              \
+    "v_sub_f32 %[t" #b "], 0x40d9d5da, %[rm" #b "]\n"                                                             \
     "v_fmac_f32 %[t" #b "], 0xcb400000, %[c" #b "]\n"
 #define SP_OMUL(b, md, e) "v_mul_f32 " SP_OR(b, md, e) ", %[w" #b "], " SP_OR(b, md, e) "\n"
 #define SP_OMUL16(b, md) SP_OMUL(b, md, 0) SP_OMUL(b, md, 1) SP_OMUL(b, md, 2) SP_OMUL(b, md, 3) SP_OMUL(b, md, 4)   \
     SP_OMUL(b, md, 5) SP_OMUL(b, md, 6) SP_OMUL(b, md, 7) SP_OMUL(b, md, 8) SP_OMUL(b, md, 9) SP_OMUL(b, md, 10)      \
     SP_OMUL(b, md, 11) SP_OMUL(b, md, 12) SP_OMUL(b, md, 13) SP_OMUL(b, md, 14) SP_OMUL(b, md, 15)
 
-// P of scores 4w .. 4w + 3 of block b: x = fma(s, c, bias) in place, 2^x,
-// then two fp8 packs into register w (the scores of w were consumed by an
-// earlier unit, or by this one). Half A: the four fmas and two exponentials;
-// half B: two exponentials and the packs (at least one instruction between an
-// exponential and its first reader).
-#define SP_FMA(b, i) "v_fma_f32 " SP_R(b, i) ", " SP_R(b, i) ", %[c" #b "], %[t" #b "]\n"
-#define SP_EXP(b, i) "v_exp_f32 " SP_R(b, i) ", " SP_R(b, i) "\n"
-#define SP_UA(b, w) SP_FMA(b, 4*w) SP_FMA(b, 4*w+1) SP_FMA(b, 4*w+2) SP_FMA(b, 4*w+3) SP_EXP(b, 4*w) SP_EXP(b, 4*w+1)
-#define SP_UB(b, w) SP_EXP(b, 4*w+2) SP_EXP(b, 4*w+3)                                                             \
-    "v_cvt_pk_fp8_f32 " SP_R(b, w) ", " SP_R(b, 4*w) ", " SP_R(b, 4*w+1) "\n"                                     \
-    "v_cvt_pk_fp8_f32 " SP_R(b, w) ", " SP_R(b, 4*w+2) ", " SP_R(b, 4*w+3) " op_sel:[0,0,1]\n"
-#define SP_U(b, w) SP_UA(b, w) SP_UB(b, w)
+// P of score group g (scores 4g .. 4g + 3) of block b: x = fma(s, c, bias)
+// in place (F), 2^x in place (E), two fp8 packs into register g (C; the
+// scores of g were consumed by an earlier group, or by this one). Steps
+// interleave F of group k, E of group k - 1 and C of group k - 2.
+#define SP_F(b, g, i) "v_fma_f32 " SP_R(b, 4*g+i) ", " SP_R(b, 4*g+i) ", %[c" #b "], %[t" #b "]\n"
+#define SP_E(b, g, i) "v_exp_f32 " SP_R(b, 4*g+i) ", " SP_R(b, 4*g+i) "\n"
+#define SP_CL(b, g) "v_cvt_pk_fp8_f32 " SP_R(b, g) ", " SP_R(b, 4*g) ", " SP_R(b, 4*g+1) "\n"
+#define SP_CH(b, g) "v_cvt_pk_fp8_f32 " SP_R(b, g) ", " SP_R(b, 4*g+2) ", " SP_R(b, 4*g+3) " op_sel:[0,0,1]\n"
+#define SP_F4(b, g) SP_F(b, g, 0) SP_F(b, g, 1) SP_F(b, g, 2) SP_F(b, g, 3)
+#define SP_FE(b, f, e) SP_F(b, f, 0) SP_E(b, e, 0) SP_F(b, f, 1) SP_E(b, e, 1) SP_F(b, f, 2) SP_E(b, e, 2)           \
+    SP_F(b, f, 3) SP_E(b, e, 3)
+#define SP_FECA(b, f, e, c) SP_F(b, f, 0) SP_E(b, e, 0) SP_F(b, f, 1) SP_E(b, e, 1) SP_CL(b, c)
+#define SP_FECB(b, f, e, c) SP_F(b, f, 2) SP_E(b, e, 2) SP_F(b, f, 3) SP_E(b, e, 3) SP_CH(b, c)
+#define SP_FEC(b, f, e, c) SP_FECA(b, f, e, c) SP_FECB(b, f, e, c)
+#define SP_EC(b, e, c) SP_E(b, e, 0) SP_E(b, e, 1) SP_CL(b, c) SP_E(b, e, 2) SP_E(b, e, 3) SP_CH(b, c)
+#define SP_C(b, c) SP_CL(b, c) SP_CH(b, c)
 
-// Block b's softmax as 13 slot strings: 5 under a PV phase, then 8 under an
-// S phase (the P.V MFMAs that read P follow after two wait states). MSK: SP_MASK / SP_NOMASK with lim<J>; L: a label unique in the block.
-#define SP_SOFT_A(b, MSK, J, L) MSK(b, J) SP_MA(b), SP_MB(b) SP_MC(b, L), SP_U(b, 0), SP_U(b, 1), SP_U(b, 2)
-#define SP_SOFT_B(b) SP_U(b, 3), SP_UA(b, 4), SP_UB(b, 4), SP_UA(b, 5), SP_UB(b, 5), SP_UA(b, 6), SP_UB(b, 6),      \
-    SP_U(b, 7) "s_nop 1\n"
-#define SP_SOFT_NONE8 "", "", "", "", "", "", "", ""
+// Block b's softmax as 13 slot strings (tile J, its scale in sks<J>): 5 under
+// a PV phase, then 8 under an S phase; the P.V MFMAs that read P follow after
+// two wait states. MSK: SP_MASK / SP_NOMASK; L: a label unique in the block.
+#define SP_SOFT_A(b, MSK, J, L) MSK(b, J) SP_MA(b, J), SP_MB(b) SP_MC(b, L), SP_F4(b, 0) SP_FE(b, 1, 0),              \
+    SP_FEC(b, 2, 1, 0), SP_FEC(b, 3, 2, 1)
+#define SP_SOFT_B(b) SP_FECA(b, 4, 3, 2), SP_FECB(b, 4, 3, 2), SP_FECA(b, 5, 4, 3), SP_FECB(b, 5, 4, 3),              \
+    SP_FEC(b, 6, 5, 4), SP_FEC(b, 7, 6, 5), SP_EC(b, 7, 6), SP_C(b, 7) "s_nop 1\n"
 
-// Fragment reads: K (ks, mb) of tile J in stage ST; V channel block md (both
-// 16-byte halves) of tile J in stage ST.
-#define SP_RK(ks, mb, J, ST) "ds_read_b128 " SP_K(ks, mb) ", %[kb" #ks "] offset:" #mb "*4096+" #J "*8192+" #ST "*16384\n"
-#define SP_RV(md, J, ST)                                                                                          \
-    "ds_read_b128 " SP_VH(md, 0) ", %[vb0] offset:32768+" #md "*2048+" #J "*8192+" #ST "*16384\n"                  \
-    "ds_read_b128 " SP_VH(md, 1) ", %[vb1] offset:32768+" #md "*2048+" #J "*8192+" #ST "*16384\n"
-#define SP_RK8(J, ST) SP_RK(0, 0, J, ST) SP_RK(0, 1, J, ST) SP_RK(1, 0, J, ST) SP_RK(1, 1, J, ST)                    \
-    SP_RK(2, 0, J, ST) SP_RK(2, 1, J, ST) SP_RK(3, 0, J, ST) SP_RK(3, 1, J, ST)
+// Fragment reads into set s: K (ks, mb) of tile J; V channel block md (both
+// 16-byte halves) of tile J; K of the next group's tile 0 (bases kn<ks>). The
+// bases point into the current stage (the V bases include the 64 KB).
+#define SP_RK(ks, mb, J, s) "ds_read_b128 " SP_K(ks, mb, s) ", %[kb" #ks "] offset:" #mb "*4096+" #J "*8192\n"
+#define SP_RKN(ks, mb, s) "ds_read_b128 " SP_K(ks, mb, s) ", %[kn" #ks "] offset:" #mb "*4096\n"
+#define SP_RV(md, J, s)                                                                                           \
+    "ds_read_b128 " SP_VH(md, 0, s) ", %[vb0] offset:" #md "*2048+" #J "*8192\n"                                    \
+    "ds_read_b128 " SP_VH(md, 1, s) ", %[vb1] offset:" #md "*2048+" #J "*8192\n"
+// Slot lists: K reads, two per slot in the first four slots.
+#define SP_RK_SLOTS(J, s) SP_RK(0, 0, J, s) SP_RK(0, 1, J, s), SP_RK(1, 0, J, s) SP_RK(1, 1, J, s),                   \
+    SP_RK(2, 0, J, s) SP_RK(2, 1, J, s), SP_RK(3, 0, J, s) SP_RK(3, 1, J, s)
+#define SP_RKN_SLOTS(s) SP_RKN(0, 0, s) SP_RKN(0, 1, s), SP_RKN(1, 0, s) SP_RKN(1, 1, s),                             \
+    SP_RKN(2, 0, s) SP_RKN(2, 1, s), SP_RKN(3, 0, s) SP_RKN(3, 1, s)
 
-// Loads of tile lt (clamped to the last tile) into slot J of stage ST: this
-// wave's two 1 KB blocks of K (keys 8 wave + 32 i + lane / 8) and of V
-// (channels 16 wave + 64 i + lane / 4).
+// Loads of tile lt (clamped to the last tile) into slot J of the current
+// stage (m0 base mc): this wave's two 1 KB blocks of K (keys 8 wave + 32 i +
+// lane / 8) and of V (channels 16 wave + 64 i + lane / 4).
 #define SP_LTILE                                                                                                  \
     "s_min_u32 %[tt], %[lt], %[tmax]\n"                                                                           \
     "s_lshl_b32 %[sk], %[tt], 13\n"                                                                               \
@@ -704,79 +732,88 @@ constexpr int SP_LDS = 4 * SP_STAGE;
     "s_lshl_b32 %[sv], %[tt], 6\n"                                                                                \
     "s_add_u32 %[sv], %[sv], %[hv]\n"                                                                             \
     "s_add_u32 %[lt], %[lt], 1\n"
-#define SP_LD(ST, J)                                                                                              \
-    "s_add_u32 m0, %[mc], " #ST "*16384+" #J "*8192\n"                                                              \
+#define SP_LD(J)                                                                                                  \
+    "s_add_u32 m0, %[mc], " #J "*8192\n"                                                                             \
     "buffer_load_dwordx4 %[ko], %[kr], %[sk] offen lds\n"                                                         \
-    "s_add_u32 m0, %[mc], " #ST "*16384+" #J "*8192+4096\n"                                                         \
+    "s_add_u32 m0, %[mc], " #J "*8192+4096\n"                                                                        \
     "s_add_u32 %[sk], %[sk], 4096\n"                                                                              \
     "buffer_load_dwordx4 %[ko], %[kr], %[sk] offen lds\n"                                                         \
-    "s_add_u32 m0, %[mc], 32768+" #ST "*16384+" #J "*8192\n"                                                        \
+    "s_add_u32 m0, %[mc], 65536+" #J "*8192\n"                                                                       \
     "buffer_load_dwordx4 %[vo], %[vr], %[sv] offen lds\n"                                                         \
-    "s_add_u32 m0, %[mc], 32768+" #ST "*16384+" #J "*8192+4096\n"                                                   \
+    "s_add_u32 m0, %[mc], 65536+" #J "*8192+4096\n"                                                                  \
     "s_add_u32 %[sv], %[sv], %[v64]\n"                                                                            \
     "buffer_load_dwordx4 %[vo], %[vr], %[sv] offen lds\n"
-#define SP_LOADS(ST) SP_LTILE SP_LD(ST, 0) SP_LTILE SP_LD(ST, 1)
-#define SP_NOLOADS(ST) ""
-// The next tile's key scale: k_scale[head, min(tile, blocks - 1)].
-#define SP_KSCALE "s_min_u32 %[tk], %[st], %[bmax]\n s_lshl_b32 %[tk], %[tk], 2\n"                                  \
-    "s_load_dword %[sks], %[ksp], %[tk]\n s_add_u32 %[st], %[st], 1\n"
+#define SP_LOADS() "", SP_LTILE SP_LD(0), SP_LTILE SP_LD(1), SP_LTILE SP_LD(2), SP_LTILE SP_LD(3)
+#define SP_NOLOADS() SP_NONE5
+// The next tile's key scale k_scale[head, min(tile, blocks - 1)] into sks<N>.
+#define SP_KSCALE(N) "s_min_u32 %[tk], %[st], %[bmax]\n s_lshl_b32 %[tk], %[tk], 2\n"                             \
+    "s_load_dword %[sks" #N "], %[ksp], %[tk]\n s_add_u32 %[st], %[st], 1\n"
 
 #define SP_WAIT_LDS "s_waitcnt lgkmcnt(0)\n"
-
-// Phase 2 and 3 extras (block 0's softmax; V reads of tile J under S1).
-#define SP_X23(MSK, J, ST, L)                                                                                     \
-    SP_PH5_EXP(SP_PVMFMA(1), SP_SOFT_A(0, MSK, J, L))
-#define SP_X3(J, ST) SP_U(0, 3) SP_RV(0, J, ST), SP_UA(0, 4) SP_RV(1, J, ST), SP_UB(0, 4) SP_RV(2, J, ST),           \
-    SP_UA(0, 5) SP_RV(3, J, ST), SP_UB(0, 5), SP_UA(0, 6), SP_UB(0, 6), SP_U(0, 7) "s_nop 1\n"
-// Phase 4 extras: block 1's softmax (first part), the K reads of the next
-// tile (tile KJ of stage KS), the next key scale, and LD (loads or nothing).
-#define SP_X4(MSK, J, L, KJ, KS, LD)                                                                              \
-    MSK(1, J) SP_MA(1) SP_RK(0, 0, KJ, KS) SP_RK(0, 1, KJ, KS),                                                   \
-    SP_MB(1) SP_MC(1, L) SP_RK(1, 0, KJ, KS) SP_RK(1, 1, KJ, KS) SP_KSCALE,                                       \
-    SP_U(1, 0) SP_RK(2, 0, KJ, KS) SP_RK(2, 1, KJ, KS) LD,                                                        \
-    SP_U(1, 1) SP_RK(3, 0, KJ, KS) SP_RK(3, 1, KJ, KS),                                                           \
-    SP_U(1, 2)
-
-// One tile (J of stage ST; the next tile's K fragments come from tile KJ of
-// stage KS). PREV: block 1's softmax of the previous tile in phase 1
-// (SP_SOFT_B(1) or SP_SOFT_NONE8). BAR: the group barrier before phase 4.
-#define SP_TILE(PREV, MSK, J, ST, KJ, KS, L, BAR, LD)                                                             \
-    SP_PH8_EXP(SP_SMFMA(0), PREV)                                                                                 \
-    SP_PH5_EXP(SP_PVMFMA(1), SP_SOFT_A(0, MSK, J, L##a))                                                          \
-    SP_PH8_EXP(SP_SMFMA(1), SP_X3(J, ST))                                                                         \
-    BAR                                                                                                           \
-    SP_PH5_EXP(SP_PVMFMA(0), SP_X4(MSK, J, L##b, KJ, KS, LD(ST)))                                                 \
-    SP_WAIT_LDS
-#define SP_WAITV "s_waitcnt lgkmcnt(0)\n"
 #define SP_BARRIER "s_waitcnt vmcnt(0) lgkmcnt(0)\n s_barrier\n"
-// A group (tiles 0 and 1) in stage ST, the next group in stage OT.
-#define SP_GROUP(MSK, ST, OT, L, LD)                                                                              \
-    SP_TILE(SP_SOFT_B(1), MSK, 0, ST, 1, ST, L##0, SP_WAITV, SP_NOLOADS)                                          \
-    SP_TILE(SP_SOFT_B(1), MSK, 1, ST, 0, OT, L##1, SP_BARRIER, LD)
+
+// Tiles of a group. Even tile J (fragment set 0; PREV: block 1's softmax of
+// the previous tile, SP_SOFT_B(1) or SP_NONE8): V of tile J read in phase 1,
+// K of tile JN = J + 1 (set 1) in phase 2. Tile 1: K of tile 2 (set 0) in
+// phase 2. Tile 3: the barrier after phase 2, K of the next group's tile 0
+// (set 0, the other stage) in phase 3, the loads (LD) in phase 4, then the
+// stage flip.
+#define SP_TILE_E(PREV, MSK, J, JN, L)                                                                            \
+    SP_PH8_EXP(SP_SMFMA(0, 0), PREV, SP_KSCALE(1) SP_RV(0, J, 0), SP_RV(1, J, 0), SP_RV(2, J, 0), SP_RV(3, J, 0),   \
+               "", "", "", "")                                                                                     \
+    SP_PH5_EXP(SP_PVMFMA(1, 1), SP_SOFT_A(0, MSK, J, L##a), SP_RK_SLOTS(JN, 1), "")                               \
+    SP_PH8_EXP(SP_SMFMA(1, 0), SP_SOFT_B(0), SP_NONE8)                                                            \
+    SP_WAIT_LDS                                                                                                   \
+    SP_PH5_EXP(SP_PVMFMA(0, 0), SP_SOFT_A(1, MSK, J, L##b), SP_NONE5)                                             \
+    SP_WAIT_LDS
+#define SP_TILE_1(MSK, L)                                                                                         \
+    SP_PH8_EXP(SP_SMFMA(0, 1), SP_SOFT_B(1), SP_KSCALE(0) SP_RV(0, 1, 1), SP_RV(1, 1, 1), SP_RV(2, 1, 1),           \
+               SP_RV(3, 1, 1), "", "", "", "")                                                                     \
+    SP_PH5_EXP(SP_PVMFMA(1, 0), SP_SOFT_A(0, MSK, 1, L##a), SP_RK_SLOTS(2, 0), "")                                \
+    SP_PH8_EXP(SP_SMFMA(1, 1), SP_SOFT_B(0), SP_NONE8)                                                            \
+    SP_WAIT_LDS                                                                                                   \
+    SP_PH5_EXP(SP_PVMFMA(0, 1), SP_SOFT_A(1, MSK, 1, L##b), SP_NONE5)                                             \
+    SP_WAIT_LDS
+#define SP_TILE_3(MSK, L, LD)                                                                                     \
+    SP_PH8_EXP(SP_SMFMA(0, 1), SP_SOFT_B(1), SP_KSCALE(0) SP_RV(0, 3, 1), SP_RV(1, 3, 1), SP_RV(2, 3, 1),           \
+               SP_RV(3, 3, 1), "", "", "", "")                                                                     \
+    SP_PH5_EXP(SP_PVMFMA(1, 0), SP_SOFT_A(0, MSK, 3, L##a), SP_NONE5)                                             \
+    SP_BARRIER                                                                                                    \
+    SP_PH8_EXP(SP_SMFMA(1, 1), SP_SOFT_B(0), SP_RKN_SLOTS(0), "", "", "", "")                                     \
+    SP_WAIT_LDS                                                                                                   \
+    SP_PH5_EXP(SP_PVMFMA(0, 1), SP_SOFT_A(1, MSK, 3, L##b), LD())                                                   \
+    SP_WAIT_LDS                                                                                                   \
+    SP_FLIP
+// The next group's stage: fragment bases and the load base flip bit 15.
+#define SP_FLIP "v_xor_b32 %[kb0], 0x8000, %[kb0]\n v_xor_b32 %[kb1], 0x8000, %[kb1]\n"                             \
+    "v_xor_b32 %[kb2], 0x8000, %[kb2]\n v_xor_b32 %[kb3], 0x8000, %[kb3]\n"                                      \
+    "v_xor_b32 %[kn0], 0x8000, %[kn0]\n v_xor_b32 %[kn1], 0x8000, %[kn1]\n"                                      \
+    "v_xor_b32 %[kn2], 0x8000, %[kn2]\n v_xor_b32 %[kn3], 0x8000, %[kn3]\n"                                      \
+    "v_xor_b32 %[vb0], 0x8000, %[vb0]\n v_xor_b32 %[vb1], 0x8000, %[vb1]\n"                                      \
+    "s_xor_b32 %[mc], %[mc], 0x8000\n"
+// A group (tiles 0 to 3).
+#define SP_GROUP(MSK, L, LD) SP_TILE_E(SP_SOFT_B(1), MSK, 0, 1, L##0) SP_TILE_1(MSK, L##1)                          \
+    SP_TILE_E(SP_SOFT_B(1), MSK, 2, 3, L##2) SP_TILE_3(MSK, L##3, LD)
 // Group 0: no block-1 softmax before its first scores and no P.V of block 1
 // in its first phase 2 (the MFMA results of S0 are waited for instead).
 #define SP_GROUP_FIRST                                                                                            \
-    SP_PH8_EXP(SP_SMFMA(0), SP_SOFT_NONE8)                                                                        \
+    SP_PH8_EXP(SP_SMFMA(0, 0), SP_NONE8, SP_KSCALE(1) SP_RV(0, 0, 0), SP_RV(1, 0, 0), SP_RV(2, 0, 0),              \
+               SP_RV(3, 0, 0), "", "", "", "")                                                                     \
     "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"                                                           \
-    SP_PH5_EXP(SP_NOMFMA5, SP_SOFT_A(0, SP_NOMASK, 0, f0a))                                                       \
-    SP_PH8_EXP(SP_SMFMA(1), SP_X3(0, 0))                                                                          \
-    SP_WAITV                                                                                                      \
-    SP_PH5_EXP(SP_PVMFMA(0), SP_X4(SP_NOMASK, 0, f0b, 1, 0, SP_NOLOADS(0)))                                       \
+    SP_PH5_EXP(SP_NOMFMA5, SP_SOFT_A(0, SP_NOMASK, 0, f0a), SP_RK_SLOTS(1, 1), "")                                \
+    SP_PH8_EXP(SP_SMFMA(1, 0), SP_SOFT_B(0), SP_NONE8)                                                            \
     SP_WAIT_LDS                                                                                                   \
-    SP_TILE(SP_SOFT_B(1), SP_NOMASK, 1, 0, 0, 1, f1, SP_BARRIER, SP_LOADS)
-// After the last tile: block 1's softmax and P.V, and a wait for every MFMA
-// result before the accumulators leave the asm block.
+    SP_PH5_EXP(SP_PVMFMA(0, 0), SP_SOFT_A(1, SP_NOMASK, 0, f0b), SP_NONE5)                                        \
+    SP_WAIT_LDS                                                                                                   \
+    SP_TILE_1(SP_NOMASK, f1) SP_TILE_E(SP_SOFT_B(1), SP_NOMASK, 2, 3, f2) SP_TILE_3(SP_NOMASK, f3, SP_LOADS)
+// After the last tile (J = 3): block 1's softmax and P.V, and a wait for
+// every MFMA result before the accumulators leave the asm block.
 #define SP_TAIL                                                                                                   \
-    SP_PH8_EXP(SP_NOMFMA8, SP_SOFT_B(1))                                                                          \
+    SP_PH8_EXP(SP_NOMFMA8, SP_SOFT_B(1), SP_NONE8)                                                                \
     "s_nop 7\n"                                                                                                   \
-    SP_PH5_EXP(SP_PVMFMA(1), SP_NOMFMA5)                                                                          \
+    SP_PH5_EXP(SP_PVMFMA(1, 1), SP_NONE5, SP_NONE5)                                                               \
     "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                                             \
     "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
-// Moves the fragment bases from stage 0 to stage 1, for a last group in
-// stage 1 (its code is written for stage 0).
-#define SP_BASE1 "v_add_u32 %[kb0], 0x4000, %[kb0]\n v_add_u32 %[kb1], 0x4000, %[kb1]\n"                             \
-    "v_add_u32 %[kb2], 0x4000, %[kb2]\n v_add_u32 %[kb3], 0x4000, %[kb3]\n"                                      \
-    "v_add_u32 %[vb0], 0x4000, %[vb0]\n v_add_u32 %[vb1], 0x4000, %[vb1]\n"
 
 #define SP_CL10(p, x) #p #x "0", #p #x "1", #p #x "2", #p #x "3", #p #x "4", #p #x "5", #p #x "6", #p #x "7",          \
     #p #x "8", #p #x "9"
@@ -784,7 +821,8 @@ constexpr int SP_LDS = 4 * SP_STAGE;
     "v0", "v1", "v2", "v3", "v4", "v5", "v6", "v7", "v8", "v9", SP_CL10(v, 1), SP_CL10(v, 2), SP_CL10(v, 3),           \
     SP_CL10(v, 4), SP_CL10(v, 5), "v60", "v61", "v62", "v63",                                                      \
     "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8", "a9", SP_CL10(a, 1), SP_CL10(a, 2), SP_CL10(a, 3),           \
-    SP_CL10(a, 4), SP_CL10(a, 5), "a60", "a61", "a62", "a63", "m0", "vcc", "scc", "memory"
+    SP_CL10(a, 4), SP_CL10(a, 5), SP_CL10(a, 6), SP_CL10(a, 7), SP_CL10(a, 8), SP_CL10(a, 9), SP_CL10(a, 10),          \
+    SP_CL10(a, 11), "a120", "a121", "a122", "a123", "a124", "a125", "a126", "a127", "m0", "vcc", "scc", "memory"
 
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void sage_pipe(SArgs a) {
@@ -796,8 +834,8 @@ void sage_pipe(SArgs a) {
     const unsigned id = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned head = __builtin_amdgcn_readfirstlane(id / nqb), qb = __builtin_amdgcn_readfirstlane(id % nqb);
     const unsigned q0 = qb * BM;
-    const unsigned ntiles = a.padded / BN;               // the launcher ensures ntiles >= 5
-    const unsigned groups = (ntiles + 1) / 2;
+    const unsigned ntiles = a.padded / BN;               // the launcher ensures ntiles >= 9
+    const unsigned groups = (ntiles + SP_GROUP_TILES - 1) / SP_GROUP_TILES;
     const int8_t *qh = a.q8 + (size_t)head * a.padded * D;
 
     // Q fragments of both blocks (rows past the padding repeat the last row).
@@ -832,11 +870,11 @@ void sage_pipe(SArgs a) {
     const unsigned hv = __builtin_amdgcn_readfirstlane(head * D * a.padded);
     const unsigned v64 = __builtin_amdgcn_readfirstlane(64 * a.padded);
     const unsigned tmax = ntiles - 1;
-    // Tiles 0..3 (groups 0 and 1) into stages 0 and 1.
+    // Tiles 0..7 (groups 0 and 1) into stages 0 and 1.
 #pragma unroll
-    for (int t4 = 0; t4 < 4; t4++) {
-        const unsigned tile = min((unsigned)t4, tmax);
-        uint8_t *ks = lds + (t4 / 2) * SP_STAGE + (t4 % 2) * Q8_TILE;
+    for (int t8 = 0; t8 < 2 * SP_GROUP_TILES; t8++) {
+        const unsigned tile = min((unsigned)t8, tmax);
+        uint8_t *ks = lds + (t8 / SP_GROUP_TILES) * SP_STAGE + (t8 % SP_GROUP_TILES) * Q8_TILE;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -854,11 +892,14 @@ void sage_pipe(SArgs a) {
 
     // Fragment bases (stage 0, tile 0): K (ks, mb) at kb<ks> + 4 KB mb; V
     // channel block md at vb<h> + 2 KB md (h: the 16-byte half).
-    unsigned kb[4], vb[2];
+    unsigned kb[4], kn[4], vb[2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) kb[ks] = n * D + k8_chunk(n, 2 * ks + hf) * 16;
+    for (int ks = 0; ks < 4; ks++) {
+        kb[ks] = n * D + k8_chunk(n, 2 * ks + hf) * 16;
+        kn[ks] = kb[ks] + SP_STAGE;
+    }
 #pragma unroll
-    for (int h = 0; h < 2; h++) vb[h] = n * BN + v8_chunk(n, 2 * hf + h) * 16;
+    for (int h = 0; h < 2; h++) vb[h] = 2 * SP_STAGE + n * BN + v8_chunk(n, 2 * hf + h) * 16;
 
     f32x16 o0[4], o1[4];
 #pragma unroll
@@ -871,61 +912,50 @@ void sage_pipe(SArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (((lane % 16) / 4 + lane / 16) & 1) ? 0 : 0x38383838;
     float m0v = -1e30f, m1v = -1e30f;
-    const unsigned mc = __builtin_amdgcn_readfirstlane(wave * 1024);
-    unsigned lt = 4, gl = groups - 2, st = 1;
-    const unsigned last_stage = (groups - 1) & 1;
-    const unsigned last0 = 2 * (groups - 1) * BN;
-    const int lim0 = (int)a.seq - (int)last0 - 4 * (int)hf, lim1 = lim0 - BN;
+    unsigned mc = __builtin_amdgcn_readfirstlane(wave * 1024);
+    unsigned lt = 2 * SP_GROUP_TILES, gl = groups - 2, st = 1;
+    const unsigned last0 = SP_GROUP_TILES * (groups - 1) * BN;
+    const int lim0 = (int)a.seq - (int)last0 - 4 * (int)hf, lim1 = lim0 - BN, lim2 = lim1 - BN, lim3 = lim2 - BN;
     const uint64_t kspv = (uint64_t)(a.k_scale + head * a.blocks);
     // (readfirstlane returns int: widen through unsigned, not by sign extension)
     const uint64_t ksp = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(kspv >> 32)) << 32) |
                          (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)kspv);
-    float sks = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(            // tile 0's key scale
-        __builtin_bit_cast(unsigned, a.k_scale[head * a.blocks])));
+    float sks0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(           // tile 0's key scale
+        __builtin_bit_cast(unsigned, a.k_scale[head * a.blocks]))), sks1 = 0.f;
     const float k16 = 16.f, nk23 = -0x1p-23f;
     const int masked = MASKED_BITS;
-    float c0, c1, t0, t1, u0, u1, w0, w1;
+    float c0, c1, t0, t1, u0, u1, w0, w1, x0, x1, y0, y1;
     unsigned tt, tk, sk, sv;
     asm volatile(
-        SP_RK8(0, 0)
+        SP_RK(0, 0, 0, 0) SP_RK(0, 1, 0, 0) SP_RK(1, 0, 0, 0) SP_RK(1, 1, 0, 0)
+        SP_RK(2, 0, 0, 0) SP_RK(2, 1, 0, 0) SP_RK(3, 0, 0, 0) SP_RK(3, 1, 0, 0)
         SP_WAIT_LDS
         SP_GROUP_FIRST
-        "s_cmp_eq_u32 %[gl], 0\n"
-        "s_cbranch_scc1 sp_loop_end_%=\n"
         "sp_loop_%=:\n"
-        SP_GROUP(SP_NOMASK, 1, 0, gp, SP_LOADS)
-        "s_sub_u32 %[gl], %[gl], 1\n"
-        "s_cmp_eq_u32 %[gl], 0\n"
-        "s_cbranch_scc1 sp_loop_end_%=\n"
-        SP_GROUP(SP_NOMASK, 0, 1, gq, SP_LOADS)
+        SP_GROUP(SP_NOMASK, gp, SP_LOADS)
         "s_sub_u32 %[gl], %[gl], 1\n"
         "s_cmp_lg_u32 %[gl], 0\n"
         "s_cbranch_scc1 sp_loop_%=\n"
-        "sp_loop_end_%=:\n"
-        "s_cmp_eq_u32 %[ls], 0\n"
-        "s_cbranch_scc1 sp_last0_%=\n"
-        SP_BASE1
-        "sp_last0_%=:\n"
-        SP_TILE(SP_SOFT_B(1), SP_MASK, 0, 0, 1, 0, gl0, SP_WAITV, SP_NOLOADS)
-        SP_TILE(SP_SOFT_B(1), SP_MASK, 1, 0, 0, 1, gl1, SP_WAITV, SP_NOLOADS)
+        SP_GROUP(SP_MASK, gl, SP_NOLOADS)
         SP_TAIL
         : [o00] "+{v[64:79]}"(o0[0]), [o01] "+{v[80:95]}"(o0[1]), [o02] "+{v[96:111]}"(o0[2]),
           [o03] "+{v[112:127]}"(o0[3]), [o10] "+{v[128:143]}"(o1[0]), [o11] "+{v[144:159]}"(o1[1]),
           [o12] "+{v[160:175]}"(o1[2]), [o13] "+{v[176:191]}"(o1[3]), [l0] "+{v[216:219]}"(l0),
           [l1] "+{v[220:223]}"(l1),
           [rm0] "+v"(m0v), [rm1] "+v"(m1v), [kb0] "+v"(kb[0]), [kb1] "+v"(kb[1]), [kb2] "+v"(kb[2]),
-          [kb3] "+v"(kb[3]), [vb0] "+v"(vb[0]), [vb1] "+v"(vb[1]),
-          [lt] "+s"(lt), [gl] "+s"(gl), [st] "+s"(st), [sks] "+s"(sks),
+          [kb3] "+v"(kb[3]), [kn0] "+v"(kn[0]), [kn1] "+v"(kn[1]), [kn2] "+v"(kn[2]), [kn3] "+v"(kn[3]),
+          [vb0] "+v"(vb[0]), [vb1] "+v"(vb[1]), [mc] "+s"(mc),
+          [lt] "+s"(lt), [gl] "+s"(gl), [st] "+s"(st), [sks0] "+s"(sks0), [sks1] "+s"(sks1),
           [c0] "=&v"(c0), [c1] "=&v"(c1), [t0] "=&v"(t0), [t1] "=&v"(t1), [u0] "=&v"(u0), [u1] "=&v"(u1),
-          [w0] "=&v"(w0), [w1] "=&v"(w1), [tt] "=&s"(tt), [tk] "=&s"(tk), [sk] "=&s"(sk), [sv] "=&s"(sv)
-        : [q00] "{a[64:67]}"(qf[0][0]), [q01] "{a[68:71]}"(qf[0][1]), [q02] "{a[72:75]}"(qf[0][2]),
-          [q03] "{a[76:79]}"(qf[0][3]), [q10] "{a[80:83]}"(qf[1][0]), [q11] "{a[84:87]}"(qf[1][1]),
-          [q12] "{a[88:91]}"(qf[1][2]), [q13] "{a[92:95]}"(qf[1][3]),
-          [mg] "{v[192:207]}"(magic), [ones] "{v[208:215]}"(ones),
+          [w0] "=&v"(w0), [w1] "=&v"(w1), [x0] "=&v"(x0), [x1] "=&v"(x1), [y0] "=&v"(y0), [y1] "=&v"(y1), [tt] "=&s"(tt), [tk] "=&s"(tk), [sk] "=&s"(sk), [sv] "=&s"(sv)
+        : [q00] "{a[128:131]}"(qf[0][0]), [q01] "{a[132:135]}"(qf[0][1]), [q02] "{a[136:139]}"(qf[0][2]),
+          [q03] "{a[140:143]}"(qf[0][3]), [q10] "{a[144:147]}"(qf[1][0]), [q11] "{a[148:151]}"(qf[1][1]),
+          [q12] "{a[152:155]}"(qf[1][2]), [q13] "{a[156:159]}"(qf[1][3]),
+          [mg] "{v[192:207]}"(magic), [ones] "{a[160:167]}"(ones),
           [qs] "v"(qs), [k16] "s"(k16), [nk23] "s"(nk23), [masked] "v"(masked), [ksp] "s"(ksp),
           [bmax] "s"(a.blocks - 1), [kr] "s"(kr), [vr] "s"(vr), [tmax] "s"(tmax), [hk] "s"(hk), [hv] "s"(hv),
-          [v64] "s"(v64), [mc] "s"(mc), [ls] "s"(last_stage), [ko] "v"(koff), [vo] "v"(voff),
-          [lim0] "v"(lim0), [lim1] "v"(lim1)
+          [v64] "s"(v64), [ko] "v"(koff), [vo] "v"(voff),
+          [lim0] "v"(lim0), [lim1] "v"(lim1), [lim2] "v"(lim2), [lim3] "v"(lim3)
         : SP_CLOBBERS);
 
     // Output as sage_attn_kernel writes it; a wave whose logit scale can
@@ -1036,10 +1066,10 @@ int h3_sage_attention(h3_gpu *g, h3_sage_workspace *w, uint16_t *out, const uint
     if (kv_list) return launch_sage<4, 3, true>(g, a, (seq + 127) / 128 * heads);
     if (g->attention_variant == 1) return launch_sage<8, 2, false>(g, a, (seq + 255) / 256 * heads);
     if (g->attention_variant == 2) return launch_sage<12, 3, false>(g, a, (seq + 383) / 384 * heads);
-    // Dense, buffered, more than 256 keys: the hand-scheduled kernel (four
+    // Dense, buffered, more than 512 keys: the hand-scheduled kernel (four
     // waves of 64 queries, one per SIMD), bit-identical to the 4-wave kernel
     // that variant 14 forces.
-    if (a.buffered && seq > 256 && g->attention_variant != 14) return launch_sage_pipe(g, a);
+    if (a.buffered && seq > 512 && g->attention_variant != 14) return launch_sage_pipe(g, a);
     return launch_sage<4, 3, false>(g, a, (seq + 127) / 128 * heads);
 }
 

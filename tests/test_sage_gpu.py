@@ -176,7 +176,7 @@ def test_launch_shapes_match(gpu, monkeypatch, variant):
         gv.close()
 
 
-@pytest.mark.parametrize("case", ["257x3", "1000x3", "2500x2", "4100x3", "gain30", "gain60", "gain400"])
+@pytest.mark.parametrize("case", ["257x3", "513x2", "600x3", "1000x3", "2500x2", "4100x3", "gain30", "gain60", "gain400"])
 def test_scheduled_kernel_matches_four_wave_kernel(gpu, monkeypatch, case):
     """Dense Sage above 256 keys runs the hand-scheduled kernel; variant 14
     forces the compiler-scheduled 4-wave kernel. Same integer scores, maxima,
