@@ -479,24 +479,23 @@ int launch_staged(h3_gpu *g, const GemmArgs &a) {
 constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
 
 // Load step t of a K tile into stage ST: 1 KB LDS block wave + 4 (t % 8) of X
-// (t < 8) or W (t >= 8). The lane offset of step t is the previous one plus
-// 32 rows (alternating temporaries, so no offset register is rewritten right
-// after the load that reads it); kc is the tile's K byte offset.
-#define PIPE_LD_X0(ST) "s_add_u32 m0, %[mb], 32768*" #ST "\n" "buffer_load_dwordx4 %[xo], %[sx], %[kc] offen lds\n"
-#define PIPE_LD_X(ST, T, DST, SRC) "s_add_u32 m0, %[mb], 32768*" #ST "+4096*" #T "\n"                        \
-    "v_add_u32 %[" #DST "], %[rs], %[" #SRC "]\n" "buffer_load_dwordx4 %[" #DST "], %[sx], %[kc] offen lds\n"
-#define PIPE_LD_W0(ST) "s_add_u32 m0, %[mb], 65536+32768*" #ST "\n" "buffer_load_dwordx4 %[wo], %[sw], %[kc] offen lds\n"
-#define PIPE_LD_W(ST, T, DST, SRC) "s_add_u32 m0, %[mb], 65536+32768*" #ST "+4096*" #T "\n"                  \
-    "v_add_u32 %[" #DST "], %[rs], %[" #SRC "]\n" "buffer_load_dwordx4 %[" #DST "], %[sw], %[kc] offen lds\n"
-#define PIPE_LOADS_X(ST) PIPE_LD_X0(ST) PIPE_LD_X(ST, 1, t0, xo) PIPE_LD_X(ST, 2, t1, t0) PIPE_LD_X(ST, 3, t0, t1) \
-    PIPE_LD_X(ST, 4, t1, t0) PIPE_LD_X(ST, 5, t0, t1) PIPE_LD_X(ST, 6, t1, t0) PIPE_LD_X(ST, 7, t0, t1)
-#define PIPE_LOADS_W(ST) PIPE_LD_W0(ST) PIPE_LD_W(ST, 1, t1, wo) PIPE_LD_W(ST, 2, t0, t1) PIPE_LD_W(ST, 3, t1, t0) \
-    PIPE_LD_W(ST, 4, t0, t1) PIPE_LD_W(ST, 5, t1, t0) PIPE_LD_W(ST, 6, t0, t1) PIPE_LD_W(ST, 7, t1, t0)
+// (t < 8) or W (t >= 8), from the lane offset o<t % 8> (row 8 wave + lane / 8
+// + 32 (t % 8), precomputed: the loop holds no VALU instruction besides the
+// MFMAs, since with one wave per SIMD each one delays the next MFMA); kc is
+// the tile's K byte offset.
+#define PIPE_LD_X(ST, T) "s_add_u32 m0, %[mb], 32768*" #ST "+4096*" #T "\n"                                  \
+    "buffer_load_dwordx4 %[o" #T "], %[sx], %[kc] offen lds\n"
+#define PIPE_LD_W(ST, T) "s_add_u32 m0, %[mb], 65536+32768*" #ST "+4096*" #T "\n"                            \
+    "buffer_load_dwordx4 %[o" #T "], %[sw], %[kc] offen lds\n"
+#define PIPE_LOADS_X(ST) PIPE_LD_X(ST, 0) PIPE_LD_X(ST, 1) PIPE_LD_X(ST, 2) PIPE_LD_X(ST, 3)                      \
+    PIPE_LD_X(ST, 4) PIPE_LD_X(ST, 5) PIPE_LD_X(ST, 6) PIPE_LD_X(ST, 7)
+#define PIPE_LOADS_W(ST) PIPE_LD_W(ST, 0) PIPE_LD_W(ST, 1) PIPE_LD_W(ST, 2) PIPE_LD_W(ST, 3)                      \
+    PIPE_LD_W(ST, 4) PIPE_LD_W(ST, 5) PIPE_LD_W(ST, 6) PIPE_LD_W(ST, 7)
 
-#define PIPE_X8(ST) PIPE_LD_X0(ST), PIPE_LD_X(ST, 1, t0, xo), PIPE_LD_X(ST, 2, t1, t0), PIPE_LD_X(ST, 3, t0, t1), \
-    PIPE_LD_X(ST, 4, t1, t0), PIPE_LD_X(ST, 5, t0, t1), PIPE_LD_X(ST, 6, t1, t0), PIPE_LD_X(ST, 7, t0, t1)
-#define PIPE_W8(ST) PIPE_LD_W0(ST), PIPE_LD_W(ST, 1, t1, wo), PIPE_LD_W(ST, 2, t0, t1), PIPE_LD_W(ST, 3, t1, t0), \
-    PIPE_LD_W(ST, 4, t0, t1), PIPE_LD_W(ST, 5, t1, t0), PIPE_LD_W(ST, 6, t0, t1), PIPE_LD_W(ST, 7, t1, t0)
+#define PIPE_X8(ST) PIPE_LD_X(ST, 0), PIPE_LD_X(ST, 1), PIPE_LD_X(ST, 2), PIPE_LD_X(ST, 3), PIPE_LD_X(ST, 4),      \
+    PIPE_LD_X(ST, 5), PIPE_LD_X(ST, 6), PIPE_LD_X(ST, 7)
+#define PIPE_W8(ST) PIPE_LD_W(ST, 0), PIPE_LD_W(ST, 1), PIPE_LD_W(ST, 2), PIPE_LD_W(ST, 3), PIPE_LD_W(ST, 4),      \
+    PIPE_LD_W(ST, 5), PIPE_LD_W(ST, 6), PIPE_LD_W(ST, 7)
 
 // MFMA (i, j) of set S: W block i (16 rows) x X block j.
 #define P16_MFMA(S, I, J) "v_mfma_f32_16x16x32_bf16 %[c" #I #J "], %[" #S "w" #I "], %[" #S "x" #J "], %[c" #I #J "]\n"
@@ -572,8 +571,10 @@ void gemm_bf16_pipe(GemmArgs a) {
                       (int)__builtin_amdgcn_readfirstlane((unsigned)(wbase >> 32)),
                       (int)__builtin_amdgcn_readfirstlane(TN * a.k * 2), 0x00020000};
     const unsigned lrow = 8 * wave + lane / 8;
-    const unsigned xo = lrow * a.k * 2 + swz(lrow, lane % 8) * 16, wo = xo;
-    const unsigned rs = __builtin_amdgcn_readfirstlane(32 * a.k * 2);
+    // X and W tiles share the lane offsets: row lrow + 32 t, swizzled chunk.
+    unsigned o[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = (lrow + 32 * t) * a.k * 2 + swz(lrow, lane % 8) * 16;
     const unsigned mb = __builtin_amdgcn_readfirstlane(wave * 1024);
     unsigned kn = 2 * TK * 2, kc = 0;
     const unsigned kmax = __builtin_amdgcn_readfirstlane((ksteps - 1) * TK * 2);
@@ -593,7 +594,6 @@ void gemm_bf16_pipe(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; j++) c[i][j] = f32x4{};
     bf16x8 af[16], bf[16];
-    unsigned t0, t1;
     // Prologue: tiles 0 and 1 into stages 0 and 1, substep 0 of tile 0 into
     // set a. Then the tiles in stage pairs; the last pair's loads are clamped
     // reloads of the last tile into a stage nobody reads again, and its
@@ -620,8 +620,9 @@ void gemm_bf16_pipe(GemmArgs a) {
         "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
         : P16_ACC8(0), P16_ACC8(1), P16_ACC8(2), P16_ACC8(3), P16_ACC8(4), P16_ACC8(5), P16_ACC8(6), P16_ACC8(7),
           P16_SET(a), P16_SET(b),
-          [t0] "=&v"(t0), [t1] "=&v"(t1), [kc] "+s"(kc), [kn] "+s"(kn), [pairs] "+s"(pairs)
-        : [sx] "s"(sx), [sw] "s"(sw), [xo] "v"(xo), [wo] "v"(wo), [rs] "s"(rs), [mb] "s"(mb), [kmax] "s"(kmax),
+          [kc] "+s"(kc), [kn] "+s"(kn), [pairs] "+s"(pairs)
+        : [sx] "s"(sx), [sw] "s"(sw), [o0] "v"(o[0]), [o1] "v"(o[1]), [o2] "v"(o[2]), [o3] "v"(o[3]),
+          [o4] "v"(o[4]), [o5] "v"(o[5]), [o6] "v"(o[6]), [o7] "v"(o[7]), [mb] "s"(mb), [kmax] "s"(kmax),
           [pw0] "v"(pw[0]), [pw1] "v"(pw[1]), [px0] "v"(px[0]), [px1] "v"(px[1])
         : "m0", "scc", "memory");
 
