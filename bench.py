@@ -509,13 +509,15 @@ def h3_step_leg(steps, warmup, fp8=False):
             "setup_s": round(setup, 1)}
 
 
-def probe():
+def probe(scale=0.5):
     """Launches for HBM-traffic counters: attention twice (config 2 inputs),
     then a plain device-to-device copy of exactly 2^30 bytes, whose FETCH_SIZE
-    and WRITE_SIZE readings calibrate the counters (2^30 bytes each way)."""
+    and WRITE_SIZE readings calibrate the counters (2^30 bytes each way).
+    scale multiplies the N(0,1) inputs; 0 gives all-zero operands (for the
+    clock the same kernel reaches at a lower power draw)."""
     from h3cli_amd.runtime import Gpu
     with Gpu() as gpu:
-        w = Workload(gpu, SEQ, HEADS, seed=2, scale=0.5, rope=False)
+        w = Workload(gpu, SEQ, HEADS, seed=2, scale=scale, rope=False)
         gpu.begin()
         for _ in range(2):
             gpu.check(w.call(), "attention")
@@ -532,12 +534,13 @@ def probe():
     log("[probe] 2 attention launches (S=32400, H=40) + 1 GiB device copy done")
 
 
-def probe_gemm(which, m=32400, k=5120, n=15360):
+def probe_gemm(which, m=32400, k=5120, n=15360, x_scale=1.0):
     """Launches for SQ counters on config 4's QKV shape, nothing timed: this
     library's W8A16 projection twice (dequantization + GEMM), or, as the
     calibration point, hipBLASLt's BF16 GEMM (torch.matmul on BF16 weights of
     the same shape) twice. The hipBLASLt probe never loads this library (two
-    HIP runtimes in one process do not share the device)."""
+    HIP runtimes in one process do not share the device). x_scale multiplies
+    this library's N(0,1) activations (0: all-zero X)."""
     if which == "hipblaslt":
         import torch
         x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
@@ -552,7 +555,7 @@ def probe_gemm(which, m=32400, k=5120, n=15360):
         lib = gpu.lib
         x = gpu.empty(m * k)
         gpu.begin()
-        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, 64, 1.0, m * k), "fill")
+        gpu.check(lib.h3_hip_fill_normal_bf16(gpu.handle, x.handle, 64, x_scale, m * k), "fill")
         gpu.submit()
         rng = np.random.default_rng(4)
         codes = rng.integers(-127, 128, size=n * k, dtype=np.int8)
@@ -594,6 +597,8 @@ def main():
     ap.add_argument("--probe", action="store_true",
                     help="counter probe for rocprofv3 --pmc: two attention launches and one 1 GiB device copy "
                          "(the calibration kernel), nothing timed")
+    ap.add_argument("--probe-scale", type=float, default=None,
+                    help="with --probe or --probe-gemm h3: scale of the N(0,1) inputs (0: all-zero operands)")
     ap.add_argument("--probe-gemm", choices=["h3", "hipblaslt"],
                     help="counter probe: config 4's QKV projection twice, this library's or hipBLASLt's BF16 GEMM")
     ap.add_argument("--profile-step", action="store_true",
@@ -605,11 +610,11 @@ def main():
         sys.exit(2)
 
     if args.probe_gemm:
-        probe_gemm(args.probe_gemm)
+        probe_gemm(args.probe_gemm, x_scale=1.0 if args.probe_scale is None else args.probe_scale)
         return
     from h3cli_amd.runtime import Gpu
     if args.probe:
-        probe()
+        probe(0.5 if args.probe_scale is None else args.probe_scale)
         return
     if args.profile_step:
         profile_step()
