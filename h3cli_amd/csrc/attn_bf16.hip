@@ -164,7 +164,7 @@ void attn_bf16_kernel(Args a) {
     unsigned count;
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        count = __builtin_amdgcn_readfirstlane(a.kv_count[qb]);
+        count = __builtin_amdgcn_readfirstlane(load_uniform(a.kv_count + qb));
         list = a.kv_list + (size_t)qb * a.list_stride;
     } else {
         count = (a.seq + BN - 1) / BN;
@@ -322,8 +322,8 @@ void attn_bf16_kernel(Args a) {
     // next iteration's loads.
     unsigned tile = 0, next = 1;
     if constexpr (SPARSE) {
-        if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
-        if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
+        if (count) tile = __builtin_amdgcn_readfirstlane(load_uniform(list));
+        if (count > 1) next = __builtin_amdgcn_readfirstlane(load_uniform(list + 1));
     }
     if (count) load_tile(tile, 0);
     wait_vm_loads();
@@ -333,7 +333,7 @@ void attn_bf16_kernel(Args a) {
         const int cur = it & 1;
         if (it + 1 < count) load_tile(next, cur ^ 1);
         uint32_t later = it + 2;
-        if constexpr (SPARSE) later = it + 2 < count ? list[it + 2] : 0u;
+        if constexpr (SPARSE) later = it + 2 < count ? load_uniform(list + it + 2) : 0u;
         const uint8_t *ks = smem + cur * STAGE_BYTES;
         process(ks, ks + K_BYTES, tile);
         wait_vm_loads();

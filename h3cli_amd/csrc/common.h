@@ -73,6 +73,14 @@ __device__ inline bool bf16_vec_nonfinite(const V &v) {
     return bad;
 }
 
+// A wave-uniform load from memory no kernel writes while this one runs,
+// through the constant address space: hipcc then issues a scalar load
+// (s_load, counted by lgkmcnt). A vector load of the same value is counted by
+// vmcnt, and the wait for it also waits for every earlier direct global->LDS
+// tile load, which ends the prefetch of the next tile early.
+template <typename T> __device__ inline T load_uniform(const T *p) {
+    return *(const __attribute__((address_space(4))) T *)p;
+}
 // Wait for this wave's outstanding vector-memory loads, including direct
 // global->LDS loads, before a barrier publishes their LDS contents.
 __device__ inline void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }

@@ -297,7 +297,7 @@ void sage_attn_kernel(SArgs a) {
     unsigned count;
     const uint32_t *list = nullptr;
     if constexpr (SPARSE) {
-        count = __builtin_amdgcn_readfirstlane(a.kv_count[qb]);
+        count = __builtin_amdgcn_readfirstlane(load_uniform(a.kv_count + qb));
         list = a.kv_list + (size_t)qb * a.list_stride;
     } else count = ntiles;
 
@@ -401,7 +401,7 @@ void sage_attn_kernel(SArgs a) {
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        const float c = qs * a.k_scale[head * a.blocks + min(tile, a.blocks - 1)];
+        const float c = qs * load_uniform(a.k_scale + head * a.blocks + min(tile, a.blocks - 1));
         const bool masked = !FULL && tile * BN + BN > a.seq;
         if (masked) {
 #pragma unroll
@@ -477,8 +477,8 @@ void sage_attn_kernel(SArgs a) {
     // BF16 kernel): the id load completes under the tile-load wait.
     unsigned tile = 0, next = 1;
     if constexpr (SPARSE) {
-        if (count) tile = __builtin_amdgcn_readfirstlane(list[0]);
-        if (count > 1) next = __builtin_amdgcn_readfirstlane(list[1]);
+        if (count) tile = __builtin_amdgcn_readfirstlane(load_uniform(list));
+        if (count > 1) next = __builtin_amdgcn_readfirstlane(load_uniform(list + 1));
     }
     if (count) load_tile(tile, 0, std::false_type{});
     wait_vm_loads();
@@ -490,7 +490,7 @@ void sage_attn_kernel(SArgs a) {
         const int cur = it & 1;
         if (it + 1 < count) load_tile(next, cur ^ 1, full_tag);
         uint32_t later = it + 2;
-        if constexpr (SPARSE) later = it + 2 < count ? list[it + 2] : 0u;
+        if constexpr (SPARSE) later = it + 2 < count ? load_uniform(list + it + 2) : 0u;
         const uint8_t *ks = lds + cur * SAGE_TILE;
         process(ks, ks + Q8_TILE, tile, full_tag);
         wait_vm_loads();
