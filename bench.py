@@ -534,6 +534,21 @@ def probe(scale=0.5):
     log("[probe] 2 attention launches (S=32400, H=40) + 1 GiB device copy done")
 
 
+def probe_sage(scale=1.0):
+    """Two Sage attention calls on config 3's inputs (N(0,1) times scale, the
+    +4.0 channel bias when scale > 0), for counters; nothing timed. scale 0
+    gives all-zero int8 and fp8 operands."""
+    from h3cli_amd.runtime import Gpu
+    with Gpu() as gpu:
+        gpu.check(gpu.lib.h3_gpu_dit_attention_configure(gpu.handle, 1), "configure sage2++")
+        w = Workload(gpu, SEQ, HEADS, seed=3, scale=scale, rope=False, k_bias=scale > 0)
+        gpu.begin()
+        for _ in range(2):
+            gpu.check(w.call(), "sage attention")
+        gpu.submit()
+    log(f"[probe-sage] 2 Sage attention calls (S={SEQ}, H={HEADS}, input scale {scale})")
+
+
 def probe_gemm(which, m=32400, k=5120, n=15360, x_scale=1.0):
     """Launches for SQ counters on config 4's QKV shape, nothing timed: this
     library's W8A16 projection twice (dequantization + GEMM), or, as the
@@ -597,8 +612,10 @@ def main():
     ap.add_argument("--probe", action="store_true",
                     help="counter probe for rocprofv3 --pmc: two attention launches and one 1 GiB device copy "
                          "(the calibration kernel), nothing timed")
+    ap.add_argument("--probe-sage", action="store_true",
+                    help="counter probe: two Sage attention calls on config 3's inputs")
     ap.add_argument("--probe-scale", type=float, default=None,
-                    help="with --probe or --probe-gemm h3: scale of the N(0,1) inputs (0: all-zero operands)")
+                    help="with --probe, --probe-sage or --probe-gemm h3: scale of the N(0,1) inputs (0: all-zero operands)")
     ap.add_argument("--probe-gemm", choices=["h3", "hipblaslt"],
                     help="counter probe: config 4's QKV projection twice, this library's or hipBLASLt's BF16 GEMM")
     ap.add_argument("--profile-step", action="store_true",
@@ -615,6 +632,9 @@ def main():
     from h3cli_amd.runtime import Gpu
     if args.probe:
         probe(0.5 if args.probe_scale is None else args.probe_scale)
+        return
+    if args.probe_sage:
+        probe_sage(1.0 if args.probe_scale is None else args.probe_scale)
         return
     if args.profile_step:
         profile_step()
