@@ -478,11 +478,11 @@ int launch_staged(h3_gpu *g, const GemmArgs &a) {
 // N % 256 == 0, M * K * 2 < 2^31 and N * K * 2 < 2^31 (32-bit offsets).
 constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
 
-// Load step t of a K tile into stage ST: 1 KB LDS block wave + 4 (t % 8) of X
-// (t < 8) or W (t >= 8), from the lane offset o<t % 8> (row 8 wave + lane / 8
-// + 32 (t % 8), precomputed: the loop holds no VALU instruction besides the
-// MFMAs, since with one wave per SIMD each one delays the next MFMA); kc is
-// the tile's K byte offset.
+// Load T (0..7) of a K tile's X (PIPE_LD_X) or W (PIPE_LD_W) into stage ST:
+// LDS block wave + 4 T (1 KB), rows 8 wave + lane / 8 + 32 T from the lane
+// offset o<T>. The offsets are precomputed so that the loop holds no VALU
+// instruction besides the MFMAs (with one wave per SIMD each one delays the
+// next MFMA); kc is the tile's K byte offset.
 #define PIPE_LD_X(ST, T) "s_add_u32 m0, %[mb], 32768*" #ST "+4096*" #T "\n"                                  \
     "buffer_load_dwordx4 %[o" #T "], %[sx], %[kc] offen lds\n"
 #define PIPE_LD_W(ST, T) "s_add_u32 m0, %[mb], 65536+32768*" #ST "+4096*" #T "\n"                            \
