@@ -92,6 +92,50 @@ def test_masked_sage_large_logit_scale():
         g.close()
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_masked_list_lengths(mode):
+    """Tile lists of every length the kernels can meet: a query block with no
+    kept block (its rows are zeros), one with only the last block (one tile
+    with keys, one wholly past S: S = 960 ends on a tile boundary), one with
+    only the first block, one with the first and the last; the other rows
+    random. BF16 (mode 0) against the masked oracle; Sage (mode 1) against
+    the masked quantized-operand oracle (rows that see only 128 or 256 keys
+    have outputs near 1, where the int8/fp8 operands alone put the quantized
+    oracle up to 0.057 from the FP32 one), with the same cosine gate against
+    the FP32 oracle as the other masked Sage tests."""
+    seq, heads = 960, 2
+    print(f"[sparse list lengths] mode={mode} seq={seq}", flush=True)
+    nb = (seq + 127) // 128
+    rng = np.random.default_rng(5)
+    mask = (rng.random((nb, nb)) < 0.3).astype(np.uint8)
+    mask[0, :] = 0
+    mask[1, :] = 0; mask[1, nb - 1] = 1
+    mask[2, :] = 0; mask[2, 0] = 1
+    mask[3, :] = 0; mask[3, 0] = 1; mask[3, nb - 1] = 1
+    g = make_gpu(mode)
+    try:
+        bind_mask(g, mask)
+        if mode == 1:
+            q, k, v = sage_inputs(seq, heads, seed=17)
+        else:
+            q, k, v = synth.attention_inputs(seq, heads, seed=17, scale=1.0)
+        out = bf16(sdpa(g, q, k, v, seq, heads))
+        assert np.all(out[:128] == 0.0)
+        scale = scale_bf16(1 / math.sqrt(128))
+        ref = oracle.attention(bf16(q), bf16(k), bf16(v), seq, heads, scale, mask=mask, block=128)
+        m = metrics(out, ref)
+        if mode == 0:
+            assert m["max_abs"] <= ATTN_MAX_ABS and m["cosine"] >= ATTN_COSINE, m
+            return
+        assert m["cosine"] >= ATTN_COSINE, m
+        refq = oracle.sage_attention(oracle.sage_pack(q, k, v, seq, heads), seq, heads, scale, mask=mask, block=128)
+        mq = metrics(out, refq)
+        bound = ATTN_MAX_ABS * max(1.0, float(np.abs(refq).max()))
+        assert mq["cosine"] >= 0.9995 and mq["max_abs"] <= bound, (mq, bound)
+    finally:
+        g.close()
+
+
 def test_masked_sage_global_load_path(monkeypatch):
     """The block-sparse Sage kernel's buffer-load path and its global-load path
     (attention variant 13, what operands of 4 GiB and more take) agree bit for
