@@ -69,6 +69,8 @@ def synthetic_q8(seed, n, k, group):
     (513, 1024, 512, 64, True, False),      # reference q8 recipe (group 64) + bias
     (256, 768, 768, 768, False, True),      # fused GELU-tanh epilogue
     (33, 256, 256, 256, False, False),      # M smaller than a tile
+    (300, 1024, 512, 1024, True, False),    # hand-scheduled GEMM, bias epilogue
+    (300, 1024, 512, 1024, True, True),     # hand-scheduled GEMM, bias + GELU-tanh epilogue
     (50, 100, 30, 100, True, False),        # unaligned shape: small-GEMM path
 ])
 def test_w8a16_linear(gpu, m, k, n, group, bias, gelu):
