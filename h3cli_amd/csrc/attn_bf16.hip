@@ -776,8 +776,8 @@ int launch_wide(h3_gpu *g, const Args &a, unsigned groups) {
 // exponential. V^T fragments of sub-tile j are read under S1(j), K fragments
 // of sub-tile j + 1 under PV0(j). Groups of 128 keys (two sub-tiles) share a
 // barrier, placed after the last V^T read of the group; the tiles two groups
-// ahead are loaded (buffer_load ... lds) right after it into the stage just
-// released. The loop body holds two groups, one per stage, so every LDS
+// ahead are loaded (buffer_load ... lds) into the stage just released, the
+// first right after the barrier, the second in the next group's first phase. The loop body holds two groups, one per stage, so every LDS
 // address is a base register plus a constant; K rows past S are caught by
 // the buffer's bounds check on the per-lane offset (tile base + row), which
 // makes the loads the same for every group. Running max, the row-sum test that raises it, the recomputation
@@ -924,6 +924,14 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
     AP_B(1, 1, 0, 2), U(1, 1, 0, 3, J), AP_B(1, 1, 0, 3), U(1, 1, 1, 0, J), AP_B(1, 1, 1, 0), U(1, 1, 1, 1, J),        \
     AP_B(1, 1, 1, 1), U(1, 1, 1, 2, J), AP_B(1, 1, 1, 2), U(1, 1, 1, 3, J), AP_B(1, 1, 1, 3) AP_FIN(1)
 #define AP_X1_NONE "", "", "", "", "", "", "", "", "", "", "", "", "", "", "", ""
+// Phase 1 with the second tile's loads of the previous group (B0..B7, one
+// after each part A).
+#define AP_X1L(U, J, B0, B1, B2, B3, B4, B5, B6, B7)                                                              \
+    U(1, 1, 0, 0, J) B0, AP_B(1, 1, 0, 0), U(1, 1, 0, 1, J) B1, AP_B(1, 1, 0, 1), U(1, 1, 0, 2, J) B2,                  \
+    AP_B(1, 1, 0, 2), U(1, 1, 0, 3, J) B3, AP_B(1, 1, 0, 3), U(1, 1, 1, 0, J) B4, AP_B(1, 1, 1, 0),                     \
+    U(1, 1, 1, 1, J) B5, AP_B(1, 1, 1, 1), U(1, 1, 1, 2, J) B6, AP_B(1, 1, 1, 2), U(1, 1, 1, 3, J) B7,                  \
+    AP_B(1, 1, 1, 3) AP_FIN(1)
+#define AP_X1L_EXP(...) AP_X1L(__VA_ARGS__)
 // Phase 2: G (group end of block 0 or nothing), block 0's softmax, half 0.
 #define AP_X2(G, U, J) G U(0, 0, 0, 0, J), AP_B(0, 0, 0, 0), U(0, 0, 0, 1, J), AP_B(0, 0, 0, 1), U(0, 0, 0, 2, J),    \
     AP_B(0, 0, 0, 2), U(0, 0, 0, 3, J), AP_B(0, 0, 0, 3), U(0, 0, 1, 0, J), AP_B(0, 0, 1, 0), U(0, 0, 1, 1, J),        \
@@ -948,10 +956,16 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
     AP_RK(6, 0, KJ, KS) AP_RK(6, 1, KJ, KS) U(1, 0, 1, 0, J), AP_RK(7, 0, KJ, KS) L4 AP_B(1, 0, 1, 0),                \
     AP_RK(7, 1, KJ, KS) U(1, 0, 1, 1, J), L5 AP_B(1, 0, 1, 1), U(1, 0, 1, 2, J), L6 AP_B(1, 0, 1, 2),                 \
     U(1, 0, 1, 3, J), L7 AP_B(1, 0, 1, 3)
-#define AP_L4(ST) AP_LTILE AP_LK(ST, 0, 0, tl0) AP_LV(ST, 0, 0), AP_LK(ST, 0, 1, tl1) AP_LV(ST, 0, 1),                   \
-    AP_LK(ST, 0, 2, tl0) AP_LV(ST, 0, 2), AP_LK(ST, 0, 3, tl1) AP_LV(ST, 0, 3),                                        \
-    AP_LTILE AP_LK(ST, 1, 0, tl0) AP_LV(ST, 1, 0), AP_LK(ST, 1, 1, tl1) AP_LV(ST, 1, 1),                               \
-    AP_LK(ST, 1, 2, tl0) AP_LV(ST, 1, 2), AP_LK(ST, 1, 3, tl1) AP_LV(ST, 1, 3)
+// The loads of one tile J (eight 1 KB blocks per wave: four of K, four of
+// V^T) as eight slots. A group's two tiles are loaded in two phases: tile 0
+// in its last phase (AP_L4), tile 1 in the next group's first (AP_LB), so
+// that the four waves, which leave the barrier together, do not queue
+// sixteen loads each at once behind the texture unit. The next group's
+// barrier waits for both.
+#define AP_LT(ST, J) AP_LTILE AP_LK(ST, J, 0, tl0), AP_LV(ST, J, 0), AP_LK(ST, J, 1, tl1), AP_LV(ST, J, 1),               \
+    AP_LK(ST, J, 2, tl0), AP_LV(ST, J, 2), AP_LK(ST, J, 3, tl1), AP_LV(ST, J, 3)
+#define AP_L4(ST) AP_LT(ST, 0)
+#define AP_LB(ST) AP_LT(ST, 1)
 #define AP_L4_NONE "", "", "", "", "", "", "", ""
 #define AP_LNONE(ST) AP_L4_NONE
 #define AP_X4_EXP(...) AP_X4(__VA_ARGS__)
@@ -961,9 +975,10 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
 // One group (sub-tiles 0 and 1) in stage ST, the next group in stage OT. U0 /
 // U1: the part-A macro for the softmax of sub-tiles 0 and 1 (AP_MA masks with
 // lim0 / lim1), UP: for block 1's previous sub-tile in phase 1 of sub-tile 0
-// (the last sub-tile of the previous group); LD: AP_L4 or AP_LNONE.
-#define AP_GROUP(UP, JP, U0, U1, L, ST, OT, LD)                                                                   \
-    AP_PH_EXP(AP_SMFMA(0), AP_X1(UP, JP))                                                                         \
+// (the last sub-tile of the previous group); LD: AP_L4 or AP_LNONE; LP: AP_LB
+// (the previous group's second tile, loaded in the first phase) or AP_LNONE.
+#define AP_GROUP(UP, JP, U0, U1, L, ST, OT, LD, LP)                                                               \
+    AP_PH_EXP(AP_SMFMA(0), AP_X1L_EXP(UP, JP, LP(OT)))                                                            \
     AP_PH_EXP(AP_PVMFMA(1), AP_X2(AP_GEND(0, L##a), U0, 0))                                                       \
     AP_PH_EXP(AP_SMFMA(1), AP_X3(AP_GEND(1, L##b), U0, 0, ST))                                                    \
     AP_WAIT_LDS                                                                                                   \
@@ -1154,11 +1169,11 @@ void attn_bf16_pipe(Args a) {
         "s_cmp_eq_u32 %[gl], 0\n"
         "s_cbranch_scc1 ap_loop_end_%=\n"
         "ap_loop_%=:\n"
-        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gp, 1, 0, AP_L4)
+        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gp, 1, 0, AP_L4, AP_LB)
         "s_sub_u32 %[gl], %[gl], 1\n"
         "s_cmp_eq_u32 %[gl], 0\n"
         "s_cbranch_scc1 ap_loop_end_%=\n"
-        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gq, 0, 1, AP_L4)
+        AP_GROUP(AP_UA, 0, AP_UA, AP_UA, gq, 0, 1, AP_L4, AP_LB)
         "s_sub_u32 %[gl], %[gl], 1\n"
         "s_cmp_lg_u32 %[gl], 0\n"
         "s_cbranch_scc1 ap_loop_%=\n"
@@ -1167,7 +1182,7 @@ void attn_bf16_pipe(Args a) {
         "s_cbranch_scc1 ap_last0_%=\n"
         AP_BASE1
         "ap_last0_%=:\n"
-        AP_GROUP(AP_UA, 0, AP_MA, AP_MA, gl, 0, 1, AP_LNONE)
+        AP_GROUP(AP_UA, 0, AP_MA, AP_MA, gl, 0, 1, AP_LNONE, AP_LNONE)
         AP_TAIL
         : [o00] "+{v[64:79]}"(o0[0]), [o01] "+{v[80:95]}"(o0[1]), [o02] "+{v[96:111]}"(o0[2]),
           [o03] "+{v[112:127]}"(o0[3]), [o10] "+{v[128:143]}"(o1[0]), [o11] "+{v[144:159]}"(o1[1]),
