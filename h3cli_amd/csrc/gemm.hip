@@ -477,6 +477,10 @@ int launch_staged(h3_gpu *g, const GemmArgs &a) {
 // of swz(). Requirements: K % 128 == 0 (tiles come in stage pairs),
 // N % 256 == 0, M * K * 2 < 2^31 and N * K * 2 < 2^31 (32-bit offsets).
 constexpr int PIPE_LDS = 4 * TILE_BYTES;     // 128 KB
+// Tile rows per grouped band of the pipe kernel: an XCD's 32 resident
+// workgroups then cover 4 row tiles x 8 column tiles (measured on the config-4
+// shapes: 4 and 8 within 1% of each other, 4 ahead; 16 rows 13% slower).
+constexpr int PIPE_GROUP_M = 4;
 
 // Load T (0..7) of a K tile's X (PIPE_LD_X) or W (PIPE_LD_W) into stage ST:
 // LDS block wave + 4 T (1 KB), rows 8 wave + lane / 8 + 32 T from the lane
@@ -554,10 +558,10 @@ void gemm_bf16_pipe(GemmArgs a) {
     const unsigned wm = wave / 2, wn = wave % 2;
     const unsigned tiles_m = (a.m + TM - 1) / TM, tiles_n = a.n / TN;
     const unsigned pid = xcd_remap(blockIdx.x, gridDim.x);
-    const unsigned band = pid / (GROUP_M * tiles_n), first_m = band * GROUP_M;
-    const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)GROUP_M);
-    const unsigned tm = first_m + (pid % (GROUP_M * tiles_n)) % rows_in_band;
-    const unsigned tn = (pid % (GROUP_M * tiles_n)) / rows_in_band;
+    const unsigned band = pid / (PIPE_GROUP_M * tiles_n), first_m = band * PIPE_GROUP_M;
+    const unsigned rows_in_band = min(tiles_m - first_m, (unsigned)PIPE_GROUP_M);
+    const unsigned tm = first_m + (pid % (PIPE_GROUP_M * tiles_n)) % rows_in_band;
+    const unsigned tn = (pid % (PIPE_GROUP_M * tiles_n)) / rows_in_band;
     const unsigned m0 = __builtin_amdgcn_readfirstlane(tm * TM), n0 = __builtin_amdgcn_readfirstlane(tn * TN);
     const unsigned ksteps = a.k / TK;
 
