@@ -925,11 +925,11 @@ constexpr int PIPE_STAGE = 2 * (K_BYTES + V_BYTES);   // 64 KB: two 64-key tiles
     AP_B(1, 1, 1, 1), U(1, 1, 1, 2, J), AP_B(1, 1, 1, 2), U(1, 1, 1, 3, J), AP_B(1, 1, 1, 3) AP_FIN(1)
 #define AP_X1_NONE "", "", "", "", "", "", "", "", "", "", "", "", "", "", "", ""
 // Phase 1 with the second tile's loads of the previous group (B0..B7, one
-// after each part A).
+// ahead of each part A: memory instructions go before the exponentials).
 #define AP_X1L(U, J, B0, B1, B2, B3, B4, B5, B6, B7)                                                              \
-    U(1, 1, 0, 0, J) B0, AP_B(1, 1, 0, 0), U(1, 1, 0, 1, J) B1, AP_B(1, 1, 0, 1), U(1, 1, 0, 2, J) B2,                  \
-    AP_B(1, 1, 0, 2), U(1, 1, 0, 3, J) B3, AP_B(1, 1, 0, 3), U(1, 1, 1, 0, J) B4, AP_B(1, 1, 1, 0),                     \
-    U(1, 1, 1, 1, J) B5, AP_B(1, 1, 1, 1), U(1, 1, 1, 2, J) B6, AP_B(1, 1, 1, 2), U(1, 1, 1, 3, J) B7,                  \
+    B0 U(1, 1, 0, 0, J), AP_B(1, 1, 0, 0), B1 U(1, 1, 0, 1, J), AP_B(1, 1, 0, 1), B2 U(1, 1, 0, 2, J),                  \
+    AP_B(1, 1, 0, 2), B3 U(1, 1, 0, 3, J), AP_B(1, 1, 0, 3), B4 U(1, 1, 1, 0, J), AP_B(1, 1, 1, 0),                     \
+    B5 U(1, 1, 1, 1, J), AP_B(1, 1, 1, 1), B6 U(1, 1, 1, 2, J), AP_B(1, 1, 1, 2), B7 U(1, 1, 1, 3, J),                  \
     AP_B(1, 1, 1, 3) AP_FIN(1)
 #define AP_X1L_EXP(...) AP_X1L(__VA_ARGS__)
 // Phase 2: G (group end of block 0 or nothing), block 0's softmax, half 0.

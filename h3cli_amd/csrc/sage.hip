@@ -596,10 +596,12 @@ constexpr int SP_LDS = 4 * SP_STAGE;
 #define SP_NOMFMA5 "", "", "", "", ""
 #define SP_NONE8 "", "", "", "", "", "", "", ""
 #define SP_NONE5 "", "", "", "", ""
-// Phases: MFMA M_k, then extra E_k (and a second extra list F_k).
+// Phases: MFMA M_k, then the memory slot F_k (LDS reads, tile loads, scale
+// loads), then the VALU slot E_k. Issuing the memory instructions ahead of
+// the exponentials measured 2% faster than after them.
 #define SP_PH8(M0, M1, M2, M3, M4, M5, M6, M7, E0, E1, E2, E3, E4, E5, E6, E7, F0, F1, F2, F3, F4, F5, F6, F7)  \
-    M0 E0 F0 M1 E1 F1 M2 E2 F2 M3 E3 F3 M4 E4 F4 M5 E5 F5 M6 E6 F6 M7 E7 F7
-#define SP_PH5(M0, M1, M2, M3, M4, E0, E1, E2, E3, E4, F0, F1, F2, F3, F4) M0 E0 F0 M1 E1 F1 M2 E2 F2 M3 E3 F3 M4 E4 F4
+    M0 F0 E0 M1 F1 E1 M2 F2 E2 M3 F3 E3 M4 F4 E4 M5 F5 E5 M6 F6 E6 M7 F7 E7
+#define SP_PH5(M0, M1, M2, M3, M4, E0, E1, E2, E3, E4, F0, F1, F2, F3, F4) M0 F0 E0 M1 F1 E1 M2 F2 E2 M3 F3 E3 M4 F4 E4
 #define SP_PH8_EXP(...) SP_PH8(__VA_ARGS__)
 #define SP_PH5_EXP(...) SP_PH5(__VA_ARGS__)
 
