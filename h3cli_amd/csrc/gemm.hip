@@ -38,6 +38,8 @@
 
 namespace {
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int TM = 256, TN = 256, TK = 64;
 constexpr int ROW_BYTES = TK * 2;               // 128 B per BF16 tile row
 constexpr int TILE_BYTES = 256 * ROW_BYTES;     // 32 KB per operand tile
@@ -631,32 +633,45 @@ void gemm_bf16_pipe(GemmArgs a) {
         : "m0", "scc", "memory");
 
     // Block (i, j): lane holds output row m0 + wm*128 + j*16 + n16 and columns
-    // n0 + wn*128 + i*16 + 4*q4 + 0..3.
+    // n0 + wn*128 + i*16 + 4*q4 + 0..3. Blocks i and i + 1 go out together
+    // as 16-byte stores: v_permlane16_swap hands the odd lane rows' block-i
+    // values to the even rows and the even rows' block-(i+1) values to the
+    // odd rows, so each lane holds eight consecutive columns.
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const unsigned row = m0 + wm * 128 + j * 16 + n16;
         if (row >= a.m) continue;
         uint16_t *dst = a.y + (size_t)row * a.n;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const unsigned col = n0 + wn * 128 + i * 16 + 4 * q4;
-            u16x4 out;
-            u16x4 bias4 = {};
-            if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
+        for (int ip = 0; ip < 4; ip++) {
+            unsigned w[2][2];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float x = c[i][j][e];
-                if constexpr (EPI & 4) x *= a.alpha[0];
-                if constexpr (EPI & 1) x += bf16_to_f32(bias4[e]);
-                uint16_t b = f32_to_bf16(x);
-                if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
-                out[e] = b;
+            for (int h = 0; h < 2; h++) {
+                const int i = 2 * ip + h;
+                const unsigned col = n0 + wn * 128 + i * 16 + 4 * q4;
+                u16x4 out;
+                u16x4 bias4 = {};
+                if constexpr (EPI & 1) bias4 = *reinterpret_cast<const u16x4 *>(a.bias + col);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = c[i][j][e];
+                    if constexpr (EPI & 4) x *= a.alpha[0];
+                    if constexpr (EPI & 1) x += bf16_to_f32(bias4[e]);
+                    uint16_t b = f32_to_bf16(x);
+                    if constexpr (EPI & 2) b = f32_to_bf16(gelu_tanh(bf16_to_f32(b)));
+                    out[e] = b;
+                }
+                w[h][0] = out[0] | ((unsigned)out[1] << 16);
+                w[h][1] = out[2] | ((unsigned)out[3] << 16);
             }
-            *reinterpret_cast<u16x4 *>(dst + col) = out;
+            const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+            const unsigned col = n0 + wn * 128 + 2 * ip * 16 + ((q4 & 1) ? 16 + 4 * (q4 - 1) : 4 * q4);
+            u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+            *reinterpret_cast<u32x4 *>(dst + col) = v;
         }
     }
 }
-
 template <int EPI>
 int launch_pipe(h3_gpu *g, const GemmArgs &a, bool timed = true) {
     constexpr size_t shared = PIPE_LDS;
